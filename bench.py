@@ -1,0 +1,285 @@
+#!/usr/bin/env python3
+"""Benchmark of the fused per-layer op set on one MI355X.
+
+Headline step: one fused residual-add + RMSNorm launch over 16384 x 4096 f32
+(Llama-3-8B width, eps 1e-5) — x and residual in, normed rows and the updated
+residual out, every input resident in HBM before timing starts. The printed
+JSON line reports that kernel's achieved HBM bandwidth (algorithmic bytes /
+average launch time, HIP events on the launch stream) against MI355X's 8 TB/s,
+the single-thread CPU oracle on a bounded sample of the same workload, and
+(``ops``) the same measurement for every other op at its configuration shape.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-ops] [--cpu-seconds S]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import re
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "fused-op HBM GB/s & % of 8 TB/s peak (RMSNorm/RoPE/SwiGLU/embed)"
+PEAK_GBS = 8000.0
+PROFILES = ROOT / "profiles"
+
+
+def parse():
+    p = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=50)
+    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--no-ops", action="store_true", help="skip the per-op table")
+    p.add_argument("--only", default=None, help="comma list of op names for the per-op table")
+    p.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU-baseline time budget")
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    p.add_argument("--profile-run", action="store_true",
+                   help="launch only the headline kernel (warmup + steps), print nothing else: for rocprofv3")
+    return p.parse_args()
+
+
+# ───────────────────────────── timing helpers ─────────────────────────────
+def time_launches(torch, fn, sets, warmup: int, steps: int):
+    """Run fn(set) over rotating buffer sets; return per-launch ms (HIP events on
+    the current stream, the stream every op is enqueued on)."""
+    stream = torch.cuda.current_stream()
+    for i in range(warmup):
+        fn(sets[i % len(sets)])
+    torch.cuda.synchronize()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    t0 = time.perf_counter()
+    for i in range(steps):
+        s, e = evs[i]
+        s.record(stream)
+        fn(sets[i % len(sets)])
+        e.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    per = [s.elapsed_time(e) for s, e in evs]
+    return per, wall
+
+
+def median(xs):
+    return float(np.median(np.asarray(xs)))
+
+
+def cpu_time(fn, budget_s: float, min_reps: int = 1):
+    """Repeat fn until the budget is spent; return (seconds per call, reps)."""
+    fn()  # first touch of the output pages
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        reps += 1
+        el = time.perf_counter() - t0
+        if reps >= min_reps and el >= budget_s:
+            return el / reps, reps
+
+
+def committed_traffic(kernel_tag: str):
+    """HBM bytes per launch of the headline kernel from the committed rocprofv3
+    --pmc summary (FETCH_SIZE + WRITE_SIZE, calibrated), or None."""
+    f = PROFILES / f"{kernel_tag}_pmc.md"
+    if not f.exists():
+        return None
+    m = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", f.read_text())
+    return float(m.group(1)) if m else None
+
+
+# ───────────────────────────── workloads ─────────────────────────────
+def gen(torch, shape, seed, dev, dtype, std=1.0, mean=0.0):
+    g = torch.Generator(device=dev).manual_seed(seed)
+    return (torch.randn(shape, generator=g, device=dev) * std + mean).to(dtype)
+
+
+def headline(torch, ops, dev, args):
+    rows, dim = 16384, 4096
+    f32 = torch.float32
+    w = gen(torch, (dim,), 3, dev, f32, 0.1, 1.0)
+    # two buffer sets (2 x 805 MB) so no launch can be served by the 256 MB Infinity Cache
+    sets = [(gen(torch, (rows, dim), 10 + i, dev, f32), gen(torch, (rows, dim), 20 + i, dev, f32),
+             torch.empty(rows, dim, device=dev)) for i in range(2)]
+
+    def fn(s):
+        ops.add_rms_norm(s[0], s[1], w, 1e-5, out=s[2])
+
+    per, wall = time_launches(torch, fn, sets, args.warmup, args.steps)
+    alg_bytes = 4 * rows * dim * 4 + dim * 4  # read x, residual, weight; write y, residual
+    return rows, dim, alg_bytes, per, wall
+
+
+def op_table(torch, ops, dev, only=None):
+    """Per-op GB/s at each configuration shape (median of 20 launches after 3 warm-ups)."""
+    import sapient_amd._lib as L
+    f32, f16, bf16 = torch.float32, torch.float16, torch.bfloat16
+    res = []
+
+    def run(name, shape_desc, dtype_s, alg_bytes, units, unit_name, make_sets, fn, latency_bound=False):
+        if only and name.split()[0] not in only:
+            return
+        sets = make_sets()
+        per, _ = time_launches(torch, fn, sets, 3, 20)
+        ms = median(per)
+        gbs = alg_bytes / (ms * 1e-3) / 1e9
+        res.append({"op": name, "shape": shape_desc, "dtype": dtype_s, "us": round(ms * 1e3, 2),
+                    "GB/s": round(gbs, 1), "pct_peak": round(100 * gbs / PEAK_GBS, 1),
+                    f"{unit_name}/s": round(units / (ms * 1e-3), 1), "alg_bytes": alg_bytes,
+                    "latency_bound": latency_bound})
+        del sets
+        torch.cuda.empty_cache()
+
+    # C2: fused add + RMSNorm at Llama-3-8B width, half precision
+    rows, dim = 16384, 4096
+    for dt, tag in ((f16, "f16"), (bf16, "bf16")):
+        w = gen(torch, (dim,), 3, dev, f32, 0.1, 1.0)
+        run("add_rms_norm", f"{rows}x{dim}", tag + " (f32 w)", 4 * rows * dim * 2 + dim * 4, rows, "rows",
+            lambda dt=dt: [(gen(torch, (rows, dim), 30 + i, dev, dt), gen(torch, (rows, dim), 40 + i, dev, dt),
+                            torch.empty(rows, dim, device=dev, dtype=dt)) for i in range(3)],
+            lambda s, w=w: ops.add_rms_norm(s[0], s[1], w, 1e-5, out=s[2]))
+    # C3: RoPE, Q 32 + K 8 heads, T 8192, head_dim 128, in place
+    T, D = 8192, 128
+    for dt, tag in ((f32, "f32"), (f16, "f16")):
+        for il in (False, True):
+            pos = torch.arange(T, dtype=torch.int32, device=dev)
+            n_el = (32 + 8) * T * D
+            run("rope_" + ("interleaved" if il else "neox"), f"q32+k8 x {T} x {D}", tag, 2 * n_el * (4 if dt == f32 else 2),
+                T, "tokens",
+                lambda dt=dt: [(gen(torch, (1, 32, T, D), 50 + i, dev, dt), gen(torch, (1, 8, T, D), 60 + i, dev, dt))
+                               for i in range(4 if dt == f16 else 2)],
+                lambda s, il=il, pos=pos: ops.rope_(s[0], s[1], pos, 5e5, interleaved=il))
+    # C4: SwiGLU [8192, 14336] f16, GELU-tanh [8192, 10240] f16
+    n = 8192 * 14336
+    run("swiglu", "8192x14336", "f16", 3 * n * 2, 8192, "rows",
+        lambda: [(gen(torch, (8192, 14336), 70 + i, dev, f16, 2.0), gen(torch, (8192, 14336), 80 + i, dev, f16, 2.0),
+                  torch.empty(8192, 14336, device=dev, dtype=f16)) for i in range(2)],
+        lambda s: ops.swiglu(s[0], s[1], out=s[2]))
+    ops.init(dev)
+    n = 8192 * 10240
+    run("gelu_tanh", "8192x10240", "f16", 2 * n * 2, 8192, "rows",
+        lambda: [(gen(torch, (8192, 10240), 90 + i, dev, f16, 2.0), torch.empty(8192, 10240, device=dev, dtype=f16))
+                 for i in range(3)],
+        lambda s: ops.gelu_tanh(s[0], out=s[1]))
+    # C5: Q4_K embedding gather, 128256 x 4096 table, 65536 ids (uniform, Zipf 1.1)
+    vocab, hidden, n_ids = 128256, 4096, 65536
+    nb = vocab * hidden // 256
+    g = torch.Generator(device=dev).manual_seed(7)
+    table = torch.randint(0, 256, (nb, 144), generator=g, device=dev, dtype=torch.int32).to(torch.uint8)
+    dd = (torch.rand((nb, 2), generator=g, device=dev) * (0.02 - 0.0005) + 0.0005).to(f16)
+    table[:, 0:4] = dd.view(torch.uint8).view(nb, 4)
+    table = table.reshape(-1)
+    rng = np.random.default_rng(8)
+    p = 1.0 / np.arange(1, vocab + 1) ** 1.1
+    zipf = rng.permutation(vocab)[np.minimum(np.searchsorted(np.cumsum(p / p.sum()), rng.random(n_ids)), vocab - 1)]
+    for dist, ids_np in (("uniform", rng.integers(0, vocab, n_ids)), ("zipf1.1", zipf)):
+        ids = torch.from_numpy(ids_np.astype(np.int32)).to(dev)
+        run(f"embed_q4_k {dist}", f"{vocab}x{hidden} -> {n_ids} ids", "q4_k->f32",
+            n_ids * (2304 + 4 + hidden * 4), n_ids, "rows",
+            lambda: [torch.empty(n_ids, hidden, device=dev) for _ in range(2)],
+            lambda o, ids=ids: ops.embed(table, L.Q4_K, vocab, hidden, ids, out=o))
+    del table
+    # C1: Qwen2.5-0.5B layer ops (latency-bound, reported only)
+    H = 896
+    for T1 in (1, 512):
+        w = gen(torch, (H,), 3, dev, f32, 0.1, 1.0)
+        run(f"rms_norm qwen T={T1}", f"{T1}x{H}", "f32", T1 * H * 8 + H * 4, T1, "rows",
+            lambda T1=T1: [(gen(torch, (T1, H), 100 + i, dev, f32), torch.empty(T1, H, device=dev)) for i in range(2)],
+            lambda s, w=w: ops.rms_norm(s[0], w, 1e-6, out=s[1]), latency_bound=True)
+        pos = torch.arange(T1, dtype=torch.int32, device=dev)
+        run(f"rope_neox qwen T={T1}", f"q14+k2 x {T1} x 64", "f32", 2 * 16 * T1 * 64 * 4, T1, "tokens",
+            lambda T1=T1: [(gen(torch, (1, 14, T1, 64), 110 + i, dev, f32), gen(torch, (1, 2, T1, 64), 120 + i, dev, f32))
+                           for i in range(2)],
+            lambda s, pos=pos: ops.rope_(s[0], s[1], pos, 1e6), latency_bound=True)
+        run(f"swiglu qwen T={T1}", f"{T1}x4864", "f32", 3 * T1 * 4864 * 4, T1, "rows",
+            lambda T1=T1: [(gen(torch, (T1, 4864), 130 + i, dev, f32), gen(torch, (T1, 4864), 140 + i, dev, f32),
+                            torch.empty(T1, 4864, device=dev)) for i in range(2)],
+            lambda s: ops.swiglu(s[0], s[1], out=s[2]), latency_bound=True)
+    vocab_q, hid_q = 151936, 896
+    nbq = vocab_q * hid_q // 32
+    tq = torch.randint(-127, 128, (nbq, 34), generator=g, device=dev, dtype=torch.int32).to(torch.int8).view(torch.uint8)
+    dq = (torch.rand((nbq, 1), generator=g, device=dev) * (0.05 - 0.001) + 0.001).to(f16)
+    tq[:, 0:2] = dq.view(torch.uint8).view(nbq, 2)
+    tq = tq.reshape(-1)
+    for T1 in (1, 512):
+        ids = torch.from_numpy(rng.integers(0, vocab_q, T1).astype(np.int32)).to(dev)
+        run(f"embed_q8_0 qwen T={T1}", f"{vocab_q}x{hid_q} -> {T1} ids", "q8_0->f32", T1 * (952 + 4 + hid_q * 4),
+            T1, "rows", lambda T1=T1: [torch.empty(T1, hid_q, device=dev) for _ in range(2)],
+            lambda o, ids=ids: ops.embed(tq, L.Q8_0, vocab_q, hid_q, ids, out=o), latency_bound=True)
+    return res
+
+
+def main():
+    args = parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: every op here is row- or token-independent, so a multi-GPU run is "
+              "N copies of the one-GPU kernel on 1/N of the rows (no exchange step). Run with --gpus 1.",
+              file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    import sapient_amd
+    import sapient_amd.ops as ops
+
+    if not sapient_amd.LIB_PATH.exists():
+        from sapient_amd import build
+        build.build(verbose=False)
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+
+    rows, dim, alg_bytes, per, wall = headline(torch, ops, dev, args)
+    if args.profile_run:
+        return
+    avg_ms = float(np.mean(per))
+    achieved = alg_bytes / (avg_ms * 1e-3) / 1e9
+    value = alg_bytes * args.steps / (sum(per) * 1e-3) / 1e9
+
+    cpu = None
+    if not args.no_cpu:
+        import oracle
+        n_rows = 2048  # an eighth of the rows; repeated for the time budget
+        rng = np.random.default_rng(0)
+        xs = rng.standard_normal((n_rows, dim), dtype=np.float32)
+        rs = rng.standard_normal((n_rows, dim), dtype=np.float32)
+        ws = (rng.standard_normal(dim, dtype=np.float32) * np.float32(0.1) + np.float32(1.0))
+        sec, reps = cpu_time(lambda: oracle.add_rms_norm(xs, rs, ws, 1e-5), args.cpu_seconds)
+        sample_bytes = 4 * n_rows * dim * 4 + dim * 4
+        cpu = {"value": round(sample_bytes / sec / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+               "sample": f"oracle add_rms_norm on {n_rows}x{dim} f32 rows (1/8 of the workload), {reps} reps "
+                         f"in {args.cpu_seconds:.0f} s, 1 thread, {os.cpu_count()} host cores visible",
+               "rows_per_s": round(n_rows / sec, 1)}
+
+    line = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(sum(per) / args.steps, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded torch.randn ~N(0,1) inputs/residual, weight ~N(1,0.1))",
+        "config": {"workload": "fused residual-add + RMSNorm, Llama-3-8B width", "rows": rows, "dim": dim,
+                   "eps": 1e-5, "io": "x, residual in; normed + updated residual out (f32)",
+                   "rows_per_s": round(rows / (avg_ms * 1e-3), 1), "pct_of_peak": round(100 * value / PEAK_GBS, 1)},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / PEAK_GBS, 4), "traffic": committed_traffic("add_rms_norm_f32_16384x4096"),
+                     "kernel": "rms_rows_vec<float,float,float,fused,16>", "alg_bytes_per_launch": alg_bytes,
+                     "avg_launch_us": round(avg_ms * 1e3, 2)},
+        "cpu_baseline": cpu,
+    }
+    if not args.no_ops:
+        only = set(args.only.split(",")) if args.only else None
+        line["ops"] = op_table(torch, ops, dev, only)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,141 @@
+/*
+ * sapient_hip.h — C ABI of the MI355X (gfx950) fused per-layer op set.
+ *
+ * This is the drop-in boundary: a Rust backend crate (or any FFI caller)
+ * binds these symbols and wraps them behind sapient's op traits. Every
+ * function:
+ *   - takes raw DEVICE pointers, explicit sizes and a HIP stream
+ *     (`stream` is a hipStream_t passed as void*; NULL = the default stream);
+ *   - enqueues its kernels on that stream and returns without synchronizing;
+ *   - never allocates or frees memory (all buffers are caller-owned and must
+ *     outlive the queued work);
+ *   - returns SPH_OK (0) or a negative status; sph_status_string() names it.
+ * Functions are reentrant and hold no per-call state; ordering is per stream.
+ *
+ * Numerics: every op computes in f32 from inputs widened exactly (f16/bf16
+ * → f32), as the reference's CPU kernels do; half-precision outputs are the
+ * f32 result rounded once, to nearest-even.
+ *
+ * Citations name the reference interface each entry point replaces
+ * (paths relative to the sapient workspace root).
+ */
+#ifndef SAPIENT_HIP_H
+#define SAPIENT_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SPH_ABI_VERSION 1
+
+/* Status codes. */
+#define SPH_OK 0
+#define SPH_EINVAL (-1)  /* null pointer, unsupported dtype, bad shape or alignment */
+#define SPH_EHIP (-2)    /* the HIP runtime reported an error while enqueueing */
+#define SPH_ERANGE (-3)  /* a token id is outside [0, vocab) */
+#define SPH_ENODEV (-4)  /* no usable gfx950 device is current */
+
+/* Element / table types. The values are GGUF tensor type ids
+ * (crates/sapient-io/src/gguf.rs:90-104), so a caller can pass them through. */
+#define SPH_F32 0
+#define SPH_F16 1
+#define SPH_Q8_0 8
+#define SPH_Q4_K 12
+#define SPH_Q6_K 14
+#define SPH_BF16 30
+
+/* RoPE pair layouts. */
+#define SPH_ROPE_NEOX 0        /* rotate_half: pairs (i, i + rotary_dim/2) */
+#define SPH_ROPE_INTERLEAVED 1 /* ggml NORM: pairs (2i, 2i + 1) */
+
+/* Library identity and diagnostics. */
+int sph_abi_version(void);
+const char* sph_status_string(int status);
+
+/* One-time per-device set-up (the GELU lookup tables). Optional: the first
+ * sph_gelu_tanh call on a device does it lazily; call it first when later
+ * calls will be captured into a HIP graph. Synchronizes `stream` once. */
+int sph_init(void* stream);
+
+/* RMSNorm over the last dimension, `rows` rows of `dim` elements:
+ *   y = x * (1 / sqrt(mean(x^2) + eps)) * weight.
+ * Replaces LlmBackend::rms_norm (crates/sapient-models/src/forward/backend.rs:72)
+ * → kernels::layernorm::rms_norm (crates/sapient-backends/cpu/src/kernels/layernorm.rs:75-106),
+ * and the wgpu analog WgpuContext::rms_norm (crates/sapient-backends/wgpu/src/resident.rs:237).
+ * x_dtype ∈ {F32, F16, BF16}; w_dtype ∈ {F32, x_dtype}; out_dtype ∈ {F32, x_dtype}.
+ * `weight` may be NULL (unit weight, as the kernel's Option<&Tensor>). */
+int sph_rms_norm(const void* x, int x_dtype, const void* weight, int w_dtype, void* out,
+                 int out_dtype, int64_t rows, int64_t dim, float eps, void* stream);
+
+/* Fused residual add + RMSNorm: r = x + residual (written back into
+ * `residual`, rounded to `dtype`), out = rms_norm(r) computed from the f32 sum.
+ * Replaces the pair LlmBackend::add → LlmBackend::rms_norm
+ * (crates/sapient-models/src/forward/llama.rs:508 then :515; wgpu analog
+ * crates/sapient-models/src/forward/wgpu_engine.rs:469 then :472).
+ * dtype ∈ {F32, F16, BF16} for x and residual; w_dtype ∈ {F32, dtype};
+ * out_dtype ∈ {F32, dtype}. `out` must not alias x or residual. */
+int sph_add_rms_norm(const void* x, void* residual, int dtype, const void* weight, int w_dtype,
+                     void* out, int out_dtype, int64_t rows, int64_t dim, float eps, void* stream);
+
+/* Element-wise a + b and a * b with the reference's broadcast rule: same
+ * length, or either operand of length 1 (elementwise.rs:27-57, :61-69).
+ * Replaces LlmBackend::add / LlmBackend::mul (backend.rs:82-83). `out` has
+ * max(na, nb) elements and may alias a full-length input. */
+int sph_add(const void* a, int64_t na, const void* b, int64_t nb, void* out, int dtype, void* stream);
+int sph_mul(const void* a, int64_t na, const void* b, int64_t nb, void* out, int dtype, void* stream);
+
+/* SiLU: x / (1 + exp(-x)). Replaces LlmBackend::silu (backend.rs:80)
+ * → elementwise::silu (crates/sapient-backends/cpu/src/kernels/elementwise.rs:141-143). */
+int sph_silu(const void* x, void* out, int dtype, int64_t n, void* stream);
+
+/* SwiGLU: silu(gate) * up, fused. Replaces LlmBackend::silu then ::mul
+ * (llama.rs:531-532) and the wgpu analog WgpuContext::swiglu (resident.rs:409).
+ * `out` may alias `gate` or `up`. */
+int sph_swiglu(const void* gate, const void* up, void* out, int dtype, int64_t n, void* stream);
+
+/* GELU, tanh approximation: 0.5 x (1 + tanh(0.79788456 (x + 0.044715 x^3))).
+ * Replaces LlmBackend::gelu (backend.rs:81) → elementwise::gelu
+ * (elementwise.rs:120-127). Bit-exact with the reference on glibc: tanh is
+ * evaluated by glibc's own tanhf algorithm. `out` may alias `x`. */
+int sph_gelu_tanh(const void* x, void* out, int dtype, int64_t n, void* stream);
+
+/* Rotary position embedding, in place, on up to two tensors sharing positions
+ * (Q and K). Each tensor is [batch, heads, seq, head_dim] contiguous (the
+ * reference's rank-4 layout, rope.rs:18-26). Channels [0, rotary_dim) rotate,
+ * the rest pass through; the angle of pair i at position p is
+ *   (p / pos_scale) / powf(base, 2i / rotary_dim).
+ * Replaces LlmBackend::apply_rope_positions (backend.rs:84) → rope::apply_rope
+ * (crates/sapient-backends/cpu/src/kernels/rope.rs:18-62, rotary_dim = head_dim,
+ * pos_scale = 1), LlmBackend::apply_rope_partial (backend.rs:89-97) →
+ * rope::apply_rope_partial_scaled (rope.rs:83-136), and WgpuContext::rope
+ * (resident.rs:467). layout = SPH_ROPE_INTERLEAVED rotates (2i, 2i+1) pairs
+ * instead (the layout the reference reaches by permuting GGUF q/k rows,
+ * crates/sapient-models/src/gguf_weights.rs:111-115).
+ * `k` may be NULL (n_k_heads ignored). positions: device int32[seq], >= 0.
+ * dtype ∈ {F32, F16, BF16}; head_dim even; rotary_dim even, 2..min(head_dim, 512). */
+int sph_rope(void* q, int64_t n_q_heads, void* k, int64_t n_k_heads, int dtype, int layout,
+             const int32_t* positions, int64_t batch, int64_t seq, int64_t head_dim,
+             int64_t rotary_dim, float base, float pos_scale, void* stream);
+
+/* Token-embedding gather with on-the-fly row dequantization into f32:
+ * out[t, :] = dequant(table[ids[t], :]). The table is the raw GGUF tensor
+ * data, rows of byte_count(hidden) bytes, consumed verbatim (no repacking).
+ * Replaces common::embed_tokens (crates/sapient-models/src/forward/common.rs:164-217)
+ * and WgpuContext::embed / embed_q8_0 / embed_q4_k (resident.rs:714,
+ * quant.rs:445, quant.rs:273). table_dtype ∈ {F32, F16, BF16, Q8_0, Q4_K, Q6_K};
+ * hidden a multiple of the block width (32 for Q8_0, 256 for K-quants).
+ * ids: device uint32[n_ids]. An id >= vocab never reads the table: its
+ * output row is zero-filled and, if `bad_id_flag` (device int32) is not NULL,
+ * 1 is stored there. Callers holding the ids on the host validate them first,
+ * as the reference does (common.rs:171-173). */
+int sph_embed(const void* table, int table_dtype, int64_t vocab, int64_t hidden,
+              const uint32_t* ids, int64_t n_ids, float* out, int32_t* bad_id_flag, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SAPIENT_HIP_H */

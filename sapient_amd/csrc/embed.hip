@@ -1,0 +1,212 @@
+// embed.hip — token-embedding gather with in-register GGUF row dequantization, gfx950.
+//
+// Reference: common::embed_tokens → gather_row_f32
+// (crates/sapient-models/src/forward/common.rs:164-217) and the dequant arms of
+// Tensor::to_f32_vec (crates/sapient-core/src/tensor.rs:378-398, Q4_K
+// :504-527 with get_scale_min_k4 :567-576, Q6_K :534-565):
+//   Q8_0 (34-byte block of 32): y = f32(i8 q) · f32(d)
+//   Q4_K (144-byte block of 256): y = (d·sc)·q − dmin·m, 6-bit (sc, m) unpacked per
+//        32-element sub-block, low nibbles then high nibbles per 64 elements
+//   Q6_K (210-byte block of 256): y = (d·sc)·(q − 32)
+// Every product above is exact in f32 (≤ 21 significant bits) except Q6_K's
+// last one, which is rounded in the reference's order; Q4_K's single rounding
+// is the final subtraction, which one FMA performs identically (d·sc·q is
+// exact). The gather is therefore bit-exact.
+//
+// Design (write-dominated: 16 KiB of f32 out per 2.3 KiB Q4_K row in):
+//  - One wave64 per token; each lane produces 4 consecutive outputs per step,
+//    so every store instruction writes 1 KiB contiguous (16 bytes per lane).
+//  - The packed blocks are read in place — no repacking. Q4_K: each step covers
+//    one 256-element super-block; a lane reads the 16-byte header (d, dmin,
+//    12 scale bytes; the same address for all lanes, one cache line) and the
+//    dword of nibbles it needs, and unpacks its (sc, m) pair in registers.
+//  - Q8_0 / Q6_K blocks are 2-byte aligned only (34 / 210 bytes), so lanes read
+//    them in 16-bit pieces.
+//  - An id >= vocab zero-fills its row and raises `bad_id_flag`; the table is
+//    never read out of bounds.
+#include "sph_common.h"
+
+namespace sph {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kWave = 64;
+constexpr int kTokPerBlock = kThreads / kWave;
+
+__device__ __forceinline__ float f16_at(const uint8_t* p) {
+    return widen(f16{*reinterpret_cast<const uint16_t*>(p)});
+}
+
+__device__ __forceinline__ void store4(float* p, float a, float b, float c, float d) {
+    f32x4 v = {a, b, c, d};
+    *reinterpret_cast<f32x4*>(p) = v;
+}
+
+// Dequantize elements [4e, 4e + 4) of one row into `o`.
+template <int DT>
+__device__ __forceinline__ void dequant4(const uint8_t* __restrict__ row, int e4, float (&o)[4]);
+
+template <>
+__device__ __forceinline__ void dequant4<SPH_F32>(const uint8_t* __restrict__ row, int e4, float (&o)[4]) {
+    const f32x4 v = reinterpret_cast<const f32x4*>(row)[e4];
+    o[0] = v.x; o[1] = v.y; o[2] = v.z; o[3] = v.w;
+}
+
+template <>
+__device__ __forceinline__ void dequant4<SPH_F16>(const uint8_t* __restrict__ row, int e4, float (&o)[4]) {
+    const u32x2 v = reinterpret_cast<const u32x2*>(row)[e4];
+    o[0] = widen(f16{(uint16_t)v.x}); o[1] = widen(f16{(uint16_t)(v.x >> 16)});
+    o[2] = widen(f16{(uint16_t)v.y}); o[3] = widen(f16{(uint16_t)(v.y >> 16)});
+}
+
+template <>
+__device__ __forceinline__ void dequant4<SPH_BF16>(const uint8_t* __restrict__ row, int e4, float (&o)[4]) {
+    const u32x2 v = reinterpret_cast<const u32x2*>(row)[e4];
+    o[0] = __uint_as_float(v.x << 16); o[1] = __uint_as_float(v.x & 0xFFFF0000u);
+    o[2] = __uint_as_float(v.y << 16); o[3] = __uint_as_float(v.y & 0xFFFF0000u);
+}
+
+template <>
+__device__ __forceinline__ void dequant4<SPH_Q8_0>(const uint8_t* __restrict__ row, int e4, float (&o)[4]) {
+    const int blk = e4 >> 3;            // 8 groups of 4 per 32-element block
+    const int j = (e4 & 7) * 4;
+    const uint8_t* b = row + blk * 34;
+    const float d = f16_at(b);
+    const uint16_t* q = reinterpret_cast<const uint16_t*>(b + 2 + j);  // 2-byte aligned
+    const uint32_t lo = q[0], hi = q[1];
+    o[0] = (float)(int8_t)(lo & 0xFF) * d;
+    o[1] = (float)(int8_t)(lo >> 8) * d;
+    o[2] = (float)(int8_t)(hi & 0xFF) * d;
+    o[3] = (float)(int8_t)(hi >> 8) * d;
+}
+
+template <>
+__device__ __forceinline__ void dequant4<SPH_Q6_K>(const uint8_t* __restrict__ row, int e4, float (&o)[4]) {
+    const int blk = e4 >> 6;            // 64 groups of 4 per 256-element super-block
+    const int e = (e4 & 63) * 4;        // element within the super-block
+    const int n = e >> 7;               // 128-element half
+    const int g = (e & 127) >> 5;       // quarter within the half (0..3)
+    const int l = e & 31;               // 4 consecutive l
+    const uint8_t* b = row + blk * 210;
+    const float d = f16_at(b + 208);
+    const uint16_t* ql = reinterpret_cast<const uint16_t*>(b + 64 * n + 32 * (g & 1) + l);
+    const uint16_t* qh = reinterpret_cast<const uint16_t*>(b + 128 + 32 * n + l);
+    const uint32_t qlw = (uint32_t)ql[0] | ((uint32_t)ql[1] << 16);
+    const uint32_t qhw = (uint32_t)qh[0] | ((uint32_t)qh[1] << 16);
+    const float dsc = d * (float)(int8_t)b[192 + 8 * n + (l >> 4) + 2 * g];
+    const int lshift = (g >> 1) * 4;    // quarters 2, 3 use the high nibbles
+    const int hshift = 2 * g;           // qh bits 2g..2g+1
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        const int ql4 = (qlw >> (8 * c + lshift)) & 0xF;
+        const int qh2 = (qhw >> (8 * c + hshift)) & 0x3;
+        o[c] = dsc * (float)((ql4 | (qh2 << 4)) - 32);
+    }
+}
+
+// Q4_K: a lane handles elements [4l, 4l + 4) of super-block `blk`, l = lane.
+__device__ __forceinline__ void dequant_q4k_lane(const uint8_t* __restrict__ row, int blk, int lane, float (&o)[4]) {
+    const uint8_t* b = row + blk * 144;
+    const u32x4 hdr = *reinterpret_cast<const u32x4*>(b);  // d, dmin, scales[0..12)
+    const int sb = lane >> 3;            // 32-element sub-block 0..7
+    const uint32_t qw = reinterpret_cast<const uint32_t*>(b + 16 + 32 * (sb >> 1))[lane & 7];
+    const float d = widen(f16{(uint16_t)hdr.x});
+    const float dmin = widen(f16{(uint16_t)(hdr.x >> 16)});
+    const int k = sb & 3, sh = 8 * k;
+    const uint32_t A = (hdr.y >> sh) & 0xFF;  // scales[k]
+    const uint32_t B = (hdr.z >> sh) & 0xFF;  // scales[k + 4]
+    const uint32_t C = (hdr.w >> sh) & 0xFF;  // scales[k + 8]
+    uint32_t sc, m;
+    if (sb < 4) {
+        sc = A & 63;
+        m = B & 63;
+    } else {
+        sc = (C & 0x0F) | ((A >> 6) << 4);
+        m = (C >> 4) | ((B >> 6) << 4);
+    }
+    const float d1 = d * (float)sc;
+    const float m1 = dmin * (float)m;
+    const uint32_t nib = (sb & 1) ? (qw >> 4) & 0x0F0F0F0Fu : qw & 0x0F0F0F0Fu;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) o[c] = __builtin_fmaf(d1, (float)((nib >> (8 * c)) & 0xFF), -m1);
+}
+
+template <int DT>
+__global__ __launch_bounds__(kThreads) void embed_rows(const uint8_t* __restrict__ table, int64_t vocab,
+                                                       int hidden, int64_t row_bytes, const uint32_t* __restrict__ ids,
+                                                       int64_t n_ids, float* __restrict__ out, int32_t* bad_id_flag) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int64_t t = (int64_t)blockIdx.x * kTokPerBlock + (threadIdx.x / kWave);
+    if (t >= n_ids) return;
+    const uint32_t id = ids[t];
+    float* dst = out + (size_t)t * (size_t)hidden;
+    const int n4 = hidden / 4;
+    if ((int64_t)id >= vocab) {
+        for (int e4 = lane; e4 < n4; e4 += kWave) store4(dst + 4 * e4, 0.f, 0.f, 0.f, 0.f);
+        if (lane == 0 && bad_id_flag != nullptr) *bad_id_flag = 1;
+        return;
+    }
+    const uint8_t* row = table + (size_t)id * (size_t)row_bytes;
+    if constexpr (DT == SPH_Q4_K) {
+        const int nblk = hidden / 256;
+        for (int blk = 0; blk < nblk; ++blk) {
+            float o[4];
+            dequant_q4k_lane(row, blk, lane, o);
+            store4(dst + 256 * blk + 4 * lane, o[0], o[1], o[2], o[3]);
+        }
+    } else {
+        for (int e4 = lane; e4 < n4; e4 += kWave) {
+            float o[4];
+            dequant4<DT>(row, e4, o);
+            store4(dst + 4 * e4, o[0], o[1], o[2], o[3]);
+        }
+    }
+}
+
+template <int DT>
+int launch_embed(const void* table, int64_t vocab, int64_t hidden, int64_t row_bytes, const uint32_t* ids,
+                 int64_t n_ids, float* out, int32_t* flag, hipStream_t stream) {
+    constexpr int64_t kChunk = int64_t(1) << 24;  // tokens per launch
+    for (int64_t t0 = 0; t0 < n_ids; t0 += kChunk) {
+        const int64_t nt = n_ids - t0 < kChunk ? n_ids - t0 : kChunk;
+        const dim3 grid((unsigned)((nt + kTokPerBlock - 1) / kTokPerBlock));
+        embed_rows<DT><<<grid, kThreads, 0, stream>>>(static_cast<const uint8_t*>(table), vocab, (int)hidden, row_bytes,
+                                                      ids + t0, nt, out + (size_t)t0 * (size_t)hidden, flag);
+        const int st = launch_status();
+        if (st != SPH_OK) return st;
+    }
+    return SPH_OK;
+}
+
+}  // namespace
+}  // namespace sph
+
+extern "C" int sph_embed(const void* table, int table_dtype, int64_t vocab, int64_t hidden, const uint32_t* ids,
+                         int64_t n_ids, float* out, int32_t* bad_id_flag, void* stream) {
+    using namespace sph;
+    if (vocab < 0 || hidden <= 0 || n_ids < 0 || hidden > INT32_MAX / 4) return SPH_EINVAL;
+    int64_t row_bytes = 0;
+    size_t align = 16;
+    switch (table_dtype) {
+    case SPH_F32: row_bytes = hidden * 4; if (hidden % 4) return SPH_EINVAL; break;
+    case SPH_F16:
+    case SPH_BF16: row_bytes = hidden * 2; align = 8; if (hidden % 4) return SPH_EINVAL; break;
+    case SPH_Q8_0: if (hidden % 32) return SPH_EINVAL; row_bytes = hidden / 32 * 34; align = 2; break;
+    case SPH_Q4_K: if (hidden % 256) return SPH_EINVAL; row_bytes = hidden / 256 * 144; break;
+    case SPH_Q6_K: if (hidden % 256) return SPH_EINVAL; row_bytes = hidden / 256 * 210; align = 2; break;
+    default: return SPH_EINVAL;
+    }
+    if (n_ids == 0) return SPH_OK;
+    if (ids == nullptr || out == nullptr || (vocab > 0 && table == nullptr)) return SPH_EINVAL;
+    if (!aligned(table, align) || !aligned(out, 16) || !aligned(ids, 4)) return SPH_EINVAL;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    switch (table_dtype) {
+    case SPH_F32: return launch_embed<SPH_F32>(table, vocab, hidden, row_bytes, ids, n_ids, out, bad_id_flag, s);
+    case SPH_F16: return launch_embed<SPH_F16>(table, vocab, hidden, row_bytes, ids, n_ids, out, bad_id_flag, s);
+    case SPH_BF16: return launch_embed<SPH_BF16>(table, vocab, hidden, row_bytes, ids, n_ids, out, bad_id_flag, s);
+    case SPH_Q8_0: return launch_embed<SPH_Q8_0>(table, vocab, hidden, row_bytes, ids, n_ids, out, bad_id_flag, s);
+    case SPH_Q4_K: return launch_embed<SPH_Q4_K>(table, vocab, hidden, row_bytes, ids, n_ids, out, bad_id_flag, s);
+    case SPH_Q6_K: return launch_embed<SPH_Q6_K>(table, vocab, hidden, row_bytes, ids, n_ids, out, bad_id_flag, s);
+    }
+    return SPH_EINVAL;
+}

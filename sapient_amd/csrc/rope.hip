@@ -1,0 +1,181 @@
+// rope.hip — rotary position embedding (NEOX and interleaved), in place, gfx950.
+//
+// Reference math (crates/sapient-backends/cpu/src/kernels/rope.rs:48-57, :123-129):
+//   freq = (pos as f32 / pos_scale) / powf(base, 2i / rotary_dim)
+//   o[a] = x[a]·cos(freq) − x[b]·sin(freq);   o[b] = x[b]·cos(freq) + x[a]·sin(freq)
+// with (a, b) = (i, i + rotary_dim/2) for NEOX and (2i, 2i + 1) for the
+// interleaved layout (gguf_weights.rs:111-115 defines the permutation between them).
+//
+// Design:
+//  - A thread owns P consecutive pairs (i0 .. i0+P) of one token and walks a
+//    group of heads of Q and K: sin/cos are computed once per (position, pair)
+//    and reused for every head (40 at the Llama-3-8B shape), so the
+//    transcendental cost is amortised and the loop over heads is pure
+//    16-byte load / FMA-free arithmetic / 16-byte store.
+//  - Parity: the d/2 denominators powf(base, 2i/d) come from the host's libm
+//    (the call the reference makes, passed in as kernel arguments); the
+//    division by them is IEEE f32 in-kernel; sin and cos are evaluated in f64
+//    and rounded once to f32 (correctly rounded except in vanishingly rare
+//    double-rounding cases); the rotation rounds each product before the
+//    add/subtract (-ffp-contract=off), exactly as the reference.
+//  - grid.x covers tokens, grid.y splits the heads into groups so that even
+//    short sequences put enough waves on the 256 CUs.
+#include <math.h>
+
+#include "sph_common.h"
+
+namespace sph {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kMaxHalf = 256;  // rotary_dim <= 512
+
+struct DenTable {
+    float v[kMaxHalf];
+};
+
+template <typename T, int P, bool INTERLEAVED>
+__global__ __launch_bounds__(kThreads) void rope_kernel(T* q, int nq, T* k, int nk, const int32_t* __restrict__ pos,
+                                                        int64_t ntok, int64_t seq, int head_dim, int half,
+                                                        int lanes_per_tok, int toks_per_block, int heads_per_group,
+                                                        float pos_scale, DenTable den) {
+    const int tib = threadIdx.x / lanes_per_tok;
+    const int lit = threadIdx.x - tib * lanes_per_tok;
+    if (tib >= toks_per_block) return;
+    const int64_t t = (int64_t)blockIdx.x * toks_per_block + tib;
+    if (t >= ntok) return;
+    const int i0 = lit * P;
+    const int64_t b = t / seq;
+    const int64_t s = t - b * seq;
+
+    const float p = (float)pos[s] / pos_scale;
+    float cs[P], sn[P];
+#pragma unroll
+    for (int j = 0; j < P; ++j) {
+        const float freq = p / den.v[i0 + j];
+        double sd, cd;
+        sincos((double)freq, &sd, &cd);
+        sn[j] = (float)sd;
+        cs[j] = (float)cd;
+    }
+
+    const int h_begin = blockIdx.y * heads_per_group;
+    int h_end = h_begin + heads_per_group;
+    if (h_end > nq + nk) h_end = nq + nk;
+    for (int hh = h_begin; hh < h_end; ++hh) {
+        T* row = hh < nq ? q + ((size_t)(b * nq + hh) * (size_t)seq + (size_t)s) * (size_t)head_dim
+                         : k + ((size_t)(b * nk + (hh - nq)) * (size_t)seq + (size_t)s) * (size_t)head_dim;
+        if constexpr (!INTERLEAVED) {
+            float x0[P], x1[P];
+            if constexpr (P == 1) {
+                x0[0] = widen(row[i0]);
+                x1[0] = widen(row[i0 + half]);
+            } else {
+                load_f32<T, P>(row + i0, x0);
+                load_f32<T, P>(row + i0 + half, x1);
+            }
+            float o0[P], o1[P];
+#pragma unroll
+            for (int j = 0; j < P; ++j) {
+                o0[j] = x0[j] * cs[j] - x1[j] * sn[j];
+                o1[j] = x1[j] * cs[j] + x0[j] * sn[j];
+            }
+            if constexpr (P == 1) {
+                row[i0] = narrow<T>(o0[0]);
+                row[i0 + half] = narrow<T>(o1[0]);
+            } else {
+                store_f32<T, P>(row + i0, o0);
+                store_f32<T, P>(row + i0 + half, o1);
+            }
+        } else {
+            float x[2 * P];
+            load_f32<T, 2 * P>(row + 2 * i0, x);
+            float o[2 * P];
+#pragma unroll
+            for (int j = 0; j < P; ++j) {
+                o[2 * j] = x[2 * j] * cs[j] - x[2 * j + 1] * sn[j];
+                o[2 * j + 1] = x[2 * j + 1] * cs[j] + x[2 * j] * sn[j];
+            }
+            store_f32<T, 2 * P>(row + 2 * i0, o);
+        }
+    }
+}
+
+template <typename T, int P, bool IL>
+int launch_rope_p(T* q, int nq, T* k, int nk, const int32_t* pos, int64_t ntok, int64_t seq, int head_dim,
+                  int half, float pos_scale, const DenTable& den, hipStream_t stream) {
+    const int lanes_per_tok = half / P;
+    const int toks_per_block = kThreads / lanes_per_tok;
+    const int64_t blocks_x = (ntok + toks_per_block - 1) / toks_per_block;
+    const int heads = nq + nk;
+    // Aim for >= 2048 blocks in total (8 per CU), never fewer than 1 head per group.
+    int groups = (int)((2048 + blocks_x - 1) / blocks_x);
+    if (groups > heads) groups = heads;
+    if (groups < 1) groups = 1;
+    const int heads_per_group = (heads + groups - 1) / groups;
+    groups = (heads + heads_per_group - 1) / heads_per_group;
+    if (blocks_x > INT32_MAX) return SPH_EINVAL;
+    const dim3 grid((unsigned)blocks_x, (unsigned)groups);
+    rope_kernel<T, P, IL><<<grid, kThreads, 0, stream>>>(q, nq, k, nk, pos, ntok, seq, head_dim, half, lanes_per_tok,
+                                                         toks_per_block, heads_per_group, pos_scale, den);
+    return launch_status();
+}
+
+template <typename T>
+int launch_rope(void* qv, int nq, void* kv, int nk, int layout, const int32_t* pos, int64_t batch, int64_t seq,
+                int head_dim, int rotary_dim, float base, float pos_scale, hipStream_t stream) {
+    T* q = static_cast<T*>(qv);
+    T* k = static_cast<T*>(kv);
+    const int half = rotary_dim / 2;
+    // The reference's denominators: base.powf(2.0 * i as f32 / rotary_dim as f32), host libm.
+    DenTable den;
+    for (int i = 0; i < kMaxHalf; ++i)
+        den.v[i] = i < half ? powf(base, 2.0f * (float)i / (float)rotary_dim) : 1.0f;
+    const int64_t ntok = batch * seq;
+    auto ok = [&](int P, int elems_per_access) {
+        const size_t bytes = (size_t)elems_per_access * sizeof(T);
+        if (half % P != 0 || head_dim % elems_per_access != 0) return false;
+        if (elems_per_access > 1 && bytes % 4 != 0) return false;
+        return aligned(q, bytes < 16 ? bytes : 16) && (k == nullptr || aligned(k, bytes < 16 ? bytes : 16));
+    };
+    constexpr int V = vec16<T>::n;  // elements per 16-byte access
+    if (layout == SPH_ROPE_NEOX) {
+        if (ok(V, V)) return launch_rope_p<T, V, false>(q, nq, k, nk, pos, ntok, seq, head_dim, half, pos_scale, den, stream);
+        if (ok(V / 2, V / 2)) return launch_rope_p<T, V / 2, false>(q, nq, k, nk, pos, ntok, seq, head_dim, half, pos_scale, den, stream);
+        if constexpr (V / 4 >= 2) {
+            if (ok(V / 4, V / 4)) return launch_rope_p<T, V / 4, false>(q, nq, k, nk, pos, ntok, seq, head_dim, half, pos_scale, den, stream);
+        }
+        return launch_rope_p<T, 1, false>(q, nq, k, nk, pos, ntok, seq, head_dim, half, pos_scale, den, stream);
+    }
+    if (ok(V / 2, V)) return launch_rope_p<T, V / 2, true>(q, nq, k, nk, pos, ntok, seq, head_dim, half, pos_scale, den, stream);
+    if constexpr (V / 4 >= 1) {
+        if (ok(V / 4, V / 2)) return launch_rope_p<T, V / 4, true>(q, nq, k, nk, pos, ntok, seq, head_dim, half, pos_scale, den, stream);
+    }
+    return launch_rope_p<T, 1, true>(q, nq, k, nk, pos, ntok, seq, head_dim, half, pos_scale, den, stream);
+}
+
+}  // namespace
+}  // namespace sph
+
+extern "C" int sph_rope(void* q, int64_t n_q_heads, void* k, int64_t n_k_heads, int dtype, int layout,
+                        const int32_t* positions, int64_t batch, int64_t seq, int64_t head_dim,
+                        int64_t rotary_dim, float base, float pos_scale, void* stream) {
+    if (layout != SPH_ROPE_NEOX && layout != SPH_ROPE_INTERLEAVED) return SPH_EINVAL;
+    if (!sph::is_float_dtype(dtype)) return SPH_EINVAL;
+    if (k == nullptr) n_k_heads = 0;
+    if (n_q_heads < 0 || n_k_heads < 0 || batch < 0 || seq < 0) return SPH_EINVAL;
+    if (head_dim <= 0 || head_dim % 2 != 0 || head_dim > INT32_MAX) return SPH_EINVAL;
+    if (rotary_dim <= 0 || rotary_dim % 2 != 0 || rotary_dim > head_dim || rotary_dim / 2 > sph::kMaxHalf)
+        return SPH_EINVAL;
+    if (n_q_heads + n_k_heads > INT32_MAX) return SPH_EINVAL;
+    const int64_t heads = n_q_heads + n_k_heads;
+    if (batch == 0 || seq == 0 || heads == 0) return SPH_OK;
+    if (positions == nullptr || (n_q_heads > 0 && q == nullptr)) return SPH_EINVAL;
+    if (!(pos_scale == pos_scale) || pos_scale == 0.0f) return SPH_EINVAL;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    return sph::with_float_type(dtype, [&](auto t) -> int {
+        using T = decltype(t);
+        return sph::launch_rope<T>(q, (int)n_q_heads, k, (int)n_k_heads, layout, positions, batch, seq, (int)head_dim,
+                                   (int)rotary_dim, base, pos_scale, s);
+    });
+}

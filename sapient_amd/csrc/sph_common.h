@@ -1,0 +1,143 @@
+// sph_common.h — device helpers shared by the gfx950 kernels: storage types,
+// exact widening / round-to-nearest-even narrowing, 16-byte vector access,
+// wave64 reductions, and host-side launch plumbing.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "sapient_hip.h"
+
+namespace sph {
+
+// ───────────────────────────── storage types ─────────────────────────────
+// f16 and bf16 travel as raw 16-bit patterns; arithmetic is always f32.
+struct f16 { uint16_t bits; };
+struct bf16 { uint16_t bits; };
+static_assert(sizeof(f16) == 2 && sizeof(bf16) == 2, "half storage must be 2 bytes");
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float widen(float v) { return v; }
+__device__ __forceinline__ float widen(f16 v) {
+    // v_cvt_f32_f16: exact, f16 subnormals included (f16 denormals are on by default).
+    return (float)__builtin_bit_cast(_Float16, v.bits);
+}
+__device__ __forceinline__ float widen(bf16 v) { return __uint_as_float((uint32_t)v.bits << 16); }
+
+template <typename T> __device__ __forceinline__ T narrow(float v);
+template <> __device__ __forceinline__ float narrow<float>(float v) { return v; }
+template <> __device__ __forceinline__ f16 narrow<f16>(float v) {
+    // v_cvt_f16_f32 rounds to nearest-even (default MODE), keeps subnormals.
+    return f16{__builtin_bit_cast(uint16_t, (_Float16)v)};
+}
+template <> __device__ __forceinline__ bf16 narrow<bf16>(float v) {
+    uint32_t x = __float_as_uint(v);
+    if ((x & 0x7FFFFFFFu) > 0x7F800000u) return bf16{(uint16_t)((x >> 16) | 0x40u)};
+    // round to nearest, ties to even: add 0x7FFF plus the kept lsb
+    x += 0x7FFFu + ((x >> 16) & 1u);
+    return bf16{(uint16_t)(x >> 16)};
+}
+
+// Elements of T that fill one 16-byte access.
+template <typename T> struct vec16 { static constexpr int n = 16 / (int)sizeof(T); };
+
+// Load N consecutive elements of T (N * sizeof(T) a multiple of 4 bytes and
+// the address aligned to min(16, N * sizeof(T))) into f32 registers.
+template <typename T, int N>
+__device__ __forceinline__ void load_f32(const T* __restrict__ p, float (&v)[N]) {
+    constexpr int bytes = N * (int)sizeof(T);
+    static_assert(bytes % 4 == 0, "vector access must be whole dwords");
+    uint32_t raw[bytes / 4];
+    if constexpr (bytes % 16 == 0) {
+#pragma unroll
+        for (int c = 0; c < bytes / 16; ++c) {
+            u32x4 q = reinterpret_cast<const u32x4*>(p)[c];
+            raw[4 * c] = q.x; raw[4 * c + 1] = q.y; raw[4 * c + 2] = q.z; raw[4 * c + 3] = q.w;
+        }
+    } else if constexpr (bytes % 8 == 0) {
+#pragma unroll
+        for (int c = 0; c < bytes / 8; ++c) {
+            u32x2 q = reinterpret_cast<const u32x2*>(p)[c];
+            raw[2 * c] = q.x; raw[2 * c + 1] = q.y;
+        }
+    } else {
+#pragma unroll
+        for (int c = 0; c < bytes / 4; ++c) raw[c] = reinterpret_cast<const uint32_t*>(p)[c];
+    }
+    if constexpr (sizeof(T) == 4) {
+#pragma unroll
+        for (int i = 0; i < N; ++i) v[i] = __uint_as_float(raw[i]);
+    } else {
+#pragma unroll
+        for (int i = 0; i < N; ++i) {
+            uint16_t h = (uint16_t)(raw[i / 2] >> (16 * (i & 1)));
+            v[i] = widen(T{h});
+        }
+    }
+}
+
+// Store N f32 values as consecutive elements of T (same alignment rule).
+template <typename T, int N>
+__device__ __forceinline__ void store_f32(T* __restrict__ p, const float (&v)[N]) {
+    constexpr int bytes = N * (int)sizeof(T);
+    static_assert(bytes % 4 == 0, "vector access must be whole dwords");
+    uint32_t raw[bytes / 4];
+    if constexpr (sizeof(T) == 4) {
+#pragma unroll
+        for (int i = 0; i < N; ++i) raw[i] = __float_as_uint(v[i]);
+    } else {
+#pragma unroll
+        for (int i = 0; i < N; i += 2)
+            raw[i / 2] = (uint32_t)narrow<T>(v[i]).bits | ((uint32_t)narrow<T>(v[i + 1]).bits << 16);
+    }
+    if constexpr (bytes % 16 == 0) {
+#pragma unroll
+        for (int c = 0; c < bytes / 16; ++c) {
+            u32x4 q = {raw[4 * c], raw[4 * c + 1], raw[4 * c + 2], raw[4 * c + 3]};
+            reinterpret_cast<u32x4*>(p)[c] = q;
+        }
+    } else if constexpr (bytes % 8 == 0) {
+#pragma unroll
+        for (int c = 0; c < bytes / 8; ++c) {
+            u32x2 q = {raw[2 * c], raw[2 * c + 1]};
+            reinterpret_cast<u32x2*>(p)[c] = q;
+        }
+    } else {
+#pragma unroll
+        for (int c = 0; c < bytes / 4; ++c) reinterpret_cast<uint32_t*>(p)[c] = raw[c];
+    }
+}
+
+// Butterfly sum over the 64 lanes of a wave. Every lane ends with the same
+// bits: each step adds the same two operands in either order.
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int m = 32; m > 0; m >>= 1) v += __shfl_xor(v, m, 64);
+    return v;
+}
+
+// ─────────────────────────────── host side ───────────────────────────────
+inline bool aligned(const void* p, size_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
+inline bool is_float_dtype(int dt) { return dt == SPH_F32 || dt == SPH_F16 || dt == SPH_BF16; }
+inline size_t dtype_size(int dt) { return dt == SPH_F32 ? 4 : 2; }
+
+inline int launch_status() {
+    hipError_t e = hipGetLastError();
+    return e == hipSuccess ? SPH_OK : SPH_EHIP;
+}
+
+// Dispatch a functor templated on the storage type of a float dtype code.
+template <typename F>
+inline int with_float_type(int dt, F&& f) {
+    switch (dt) {
+    case SPH_F32: return f(float{});
+    case SPH_F16: return f(f16{});
+    case SPH_BF16: return f(bf16{});
+    default: return SPH_EINVAL;
+    }
+}
+
+}  // namespace sph

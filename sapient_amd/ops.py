@@ -1,0 +1,177 @@
+"""Device-resident op calls on torch tensors, through the C ABI.
+
+torch supplies device memory and the current HIP stream; every op runs in the
+HIP kernels of ``libsapient_hip.so``. Inputs must be contiguous device
+tensors. Errors from the ABI raise :class:`SapientHipError`.
+"""
+from __future__ import annotations
+
+from typing import Optional, Tuple
+
+import torch
+
+from . import _lib
+from ._lib import check, lib
+
+_DT = {torch.float32: _lib.F32, torch.float16: _lib.F16, torch.bfloat16: _lib.BF16}
+
+
+def dtype_code(t: torch.dtype) -> int:
+    try:
+        return _DT[t]
+    except KeyError:
+        raise TypeError(f"unsupported dtype {t}") from None
+
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _dev(t: torch.Tensor, name: str) -> torch.Tensor:
+    if not t.is_cuda:
+        raise ValueError(f"{name} must be a device tensor")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    return t
+
+
+def init(device: Optional[torch.device] = None) -> None:
+    """Per-device set-up (GELU tables); optional, done lazily otherwise."""
+    with torch.cuda.device(device or torch.cuda.current_device()):
+        check(lib().sph_init(torch.cuda.current_stream().cuda_stream), "init")
+
+
+def rms_norm(x: torch.Tensor, weight: Optional[torch.Tensor], eps: float,
+             out: Optional[torch.Tensor] = None, out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
+    """RMSNorm over the last dim (layernorm.rs:75-106). out_dtype: f32 (the
+    reference's output type) or x's dtype; defaults to x's dtype."""
+    _dev(x, "x")
+    dim = x.shape[-1] if x.dim() else 1
+    rows = x.numel() // dim if dim else 0
+    od = out_dtype or (out.dtype if out is not None else x.dtype)
+    if out is None:
+        out = torch.empty(x.shape, dtype=od, device=x.device)
+    _dev(out, "out")
+    w = _dev(weight, "weight") if weight is not None else None
+    check(lib().sph_rms_norm(x.data_ptr(), dtype_code(x.dtype),
+                             None if w is None else w.data_ptr(), dtype_code(w.dtype) if w is not None else 0,
+                             out.data_ptr(), dtype_code(out.dtype), rows, dim, float(eps), _stream(x)),
+          "rms_norm")
+    return out
+
+
+def add_rms_norm(x: torch.Tensor, residual: torch.Tensor, weight: Optional[torch.Tensor], eps: float,
+                 out: Optional[torch.Tensor] = None,
+                 out_dtype: Optional[torch.dtype] = None) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Fused add (llama.rs:508) + rms_norm (llama.rs:515). `residual` is
+    updated in place with x + residual; returns (normed, residual)."""
+    _dev(x, "x")
+    _dev(residual, "residual")
+    if residual.shape != x.shape or residual.dtype != x.dtype:
+        raise ValueError("x and residual must share shape and dtype")
+    dim = x.shape[-1]
+    rows = x.numel() // dim if dim else 0
+    od = out_dtype or (out.dtype if out is not None else x.dtype)
+    if out is None:
+        out = torch.empty(x.shape, dtype=od, device=x.device)
+    _dev(out, "out")
+    w = _dev(weight, "weight") if weight is not None else None
+    check(lib().sph_add_rms_norm(x.data_ptr(), residual.data_ptr(), dtype_code(x.dtype),
+                                 None if w is None else w.data_ptr(), dtype_code(w.dtype) if w is not None else 0,
+                                 out.data_ptr(), dtype_code(out.dtype), rows, dim, float(eps), _stream(x)),
+          "add_rms_norm")
+    return out, residual
+
+
+def _binary(fn, name, a, b, out):
+    _dev(a, "a")
+    _dev(b, "b")
+    if a.dtype != b.dtype:
+        raise ValueError("operands must share dtype")
+    big = a if a.numel() >= b.numel() else b
+    if out is None:
+        out = torch.empty(big.shape, dtype=a.dtype, device=a.device)
+    _dev(out, "out")
+    check(fn(a.data_ptr(), a.numel(), b.data_ptr(), b.numel(), out.data_ptr(), dtype_code(a.dtype), _stream(a)), name)
+    return out
+
+
+def add(a: torch.Tensor, b: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """a + b with the reference's length-1 broadcast (elementwise.rs:27-63)."""
+    return _binary(lib().sph_add, "add", a, b, out)
+
+
+def mul(a: torch.Tensor, b: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """a * b with the reference's length-1 broadcast (elementwise.rs:27-57, :67-69)."""
+    return _binary(lib().sph_mul, "mul", a, b, out)
+
+
+def silu(x: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    _dev(x, "x")
+    out = torch.empty_like(x) if out is None else _dev(out, "out")
+    check(lib().sph_silu(x.data_ptr(), out.data_ptr(), dtype_code(x.dtype), x.numel(), _stream(x)), "silu")
+    return out
+
+
+def swiglu(gate: torch.Tensor, up: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """silu(gate) * up, fused (llama.rs:531-532)."""
+    _dev(gate, "gate")
+    _dev(up, "up")
+    if gate.shape != up.shape or gate.dtype != up.dtype:
+        raise ValueError("gate and up must share shape and dtype")
+    out = torch.empty_like(gate) if out is None else _dev(out, "out")
+    check(lib().sph_swiglu(gate.data_ptr(), up.data_ptr(), out.data_ptr(), dtype_code(gate.dtype), gate.numel(),
+                           _stream(gate)), "swiglu")
+    return out
+
+
+def gelu_tanh(x: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """GELU tanh form (elementwise.rs:120-127), bit-exact with the reference."""
+    _dev(x, "x")
+    out = torch.empty_like(x) if out is None else _dev(out, "out")
+    check(lib().sph_gelu_tanh(x.data_ptr(), out.data_ptr(), dtype_code(x.dtype), x.numel(), _stream(x)), "gelu")
+    return out
+
+
+def rope_(q: torch.Tensor, k: Optional[torch.Tensor], positions: torch.Tensor, base: float,
+          rotary_dim: Optional[int] = None, pos_scale: float = 1.0, interleaved: bool = False) -> None:
+    """RoPE in place on q [B, Hq, S, D] and optionally k [B, Hk, S, D]
+    (rope.rs:18-62 / :83-136). positions: int32 device tensor [S]."""
+    _dev(q, "q")
+    if q.dim() != 4:
+        raise ValueError("q must be [batch, heads, seq, head_dim]")
+    B, Hq, S, D = q.shape
+    Hk = 0
+    if k is not None:
+        _dev(k, "k")
+        if k.dim() != 4 or k.shape[0] != B or k.shape[2] != S or k.shape[3] != D or k.dtype != q.dtype:
+            raise ValueError("k must be [batch, kv_heads, seq, head_dim] like q")
+        Hk = k.shape[1]
+    _dev(positions, "positions")
+    if positions.dtype != torch.int32 or positions.numel() != S:
+        raise ValueError("positions must be int32 with seq_len entries")
+    rd = D if rotary_dim is None else rotary_dim
+    layout = _lib.ROPE_INTERLEAVED if interleaved else _lib.ROPE_NEOX
+    check(lib().sph_rope(q.data_ptr(), Hq, None if k is None else k.data_ptr(), Hk, dtype_code(q.dtype), layout,
+                         positions.data_ptr(), B, S, D, rd, float(base), float(pos_scale), _stream(q)), "rope")
+
+
+def embed(table: torch.Tensor, table_dtype: int, vocab: int, hidden: int, ids: torch.Tensor,
+          out: Optional[torch.Tensor] = None, bad_id_flag: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Row gather + dequant of a raw GGUF table (common.rs:164-217) into f32
+    [n_ids, hidden]. `table` holds the raw tensor bytes (any dtype, contiguous);
+    ids: int32/uint32 device tensor (ids are read as uint32)."""
+    _dev(table, "table")
+    _dev(ids, "ids")
+    if ids.dtype not in (torch.int32, torch.uint32):
+        raise ValueError("ids must be 32-bit")
+    n = ids.numel()
+    if out is None:
+        out = torch.empty((n, hidden), dtype=torch.float32, device=ids.device)
+    _dev(out, "out")
+    flag = None
+    if bad_id_flag is not None:
+        flag = _dev(bad_id_flag, "bad_id_flag")
+    check(lib().sph_embed(table.data_ptr(), table_dtype, vocab, hidden, ids.data_ptr(), n, out.data_ptr(),
+                          None if flag is None else flag.data_ptr(), _stream(ids)), "embed")
+    return out

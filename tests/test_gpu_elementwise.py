@@ -1,0 +1,161 @@
+"""GPU parity: add, mul, SiLU, SwiGLU and GELU-tanh against the oracle.
+
+Reference: crates/sapient-backends/cpu/src/kernels/elementwise.rs:27-69 (add/mul and
+broadcast), :120-127 (gelu), :141-143 (silu); SwiGLU = silu then mul (llama.rs:531-532).
+
+Tolerances:
+  add / mul          bit-exact (one IEEE operation, same rounding)
+  SiLU / SwiGLU f32  ≤ 1e-5 relative (hardware exp2 / reciprocal vs glibc expf)
+  SiLU / SwiGLU half ≤ 1 ulp of the output format vs the f32 oracle rounded
+  GELU (every dtype) bit-exact: the kernel evaluates glibc's own tanhf algorithm
+"""
+import numpy as np
+import pytest
+import torch
+
+from helpers import assert_bits_equal, max_rel, narrow_bits, to_np, ulp_diff16, widen
+from refvec import WgpuLcg
+
+import sapient_amd.ops as ops
+
+pytestmark = pytest.mark.gpu
+DTYPES = [torch.float32, torch.float16, torch.bfloat16]
+IDS = lambda d: str(d).split(".")[-1]
+
+
+def _gen(shape, seed, dev, std=1.0, dtype=torch.float32):
+    g = torch.Generator(device=dev).manual_seed(seed)
+    return (torch.randn(shape, generator=g, device=dev) * std).to(dtype)
+
+
+SPECIALS = np.array([0.0, -0.0, 1.0, -1.0, 0.5, -0.5, 3.0, -3.0, 5.0, -5.0, 8.0, -8.0, 10.0, -10.0, 20.0,
+                     -20.0, 40.0, -40.0, 79.9, -79.9, -80.0, -80.1, 87.3, -87.3, 88.7, -88.7, -88.73, 89.0,
+                     -89.0, 100.0, -100.0, 1e-20, -1e-20, 1e-40, -1e-40, 3.4e38, -3.4e38, np.inf, -np.inf,
+                     np.nan], np.float32)
+
+
+def _check(out, ref32, orc, rtol, what):
+    if out.dtype == torch.float32:
+        r = max_rel(to_np(out), ref32, floor=1e-37)
+        assert r <= rtol, f"{what}: max rel err {r:.3e}"
+    else:
+        d = ulp_diff16(to_np(out), narrow_bits(ref32, out.dtype, orc), out.dtype)
+        assert int(d.max()) <= 1, f"{what}: max {int(d.max())} ulp"
+
+
+def test_swiglu_and_add_match_wgpu_test_vectors(dev, orc):
+    """resident.rs:103-124: n = 4096, lcg 0x9E3779B9; add ≤ 1e-5, swiglu ≤ 1e-4 abs there."""
+    nxt = WgpuLcg()
+    a, b = nxt.take(4096), nxt.take(4096)
+    ta, tb = torch.from_numpy(a).to(dev), torch.from_numpy(b).to(dev)
+    print("case add/swiglu wgpu-vectors", flush=True)
+    assert_bits_equal(to_np(ops.add(ta, tb)), orc.add(a, b), "add")
+    sg = to_np(ops.swiglu(ta, tb))
+    assert max_rel(sg, orc.swiglu(a, b), floor=1e-37) <= 1e-5
+    silu = a.astype(np.float64) / (1 + np.exp(-a.astype(np.float64)))
+    assert np.abs(sg - silu * b).max() < 1e-4
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=IDS)
+@pytest.mark.parametrize("n", [1, 3, 8, 31, 4096, 4096 * 4864 + 7])
+def test_add_mul_bit_exact(dev, orc, dtype, n):
+    print(f"case add/mul {dtype} n={n}", flush=True)
+    a, b = _gen((n,), 3, dev, dtype=dtype), _gen((n,), 4, dev, dtype=dtype)
+    a32, b32 = widen(a, orc), widen(b, orc)
+    for fn, ref in ((ops.add, orc.add), (ops.mul, orc.mul)):
+        got = fn(a, b)
+        want = ref(a32, b32)
+        if dtype == torch.float32:
+            assert_bits_equal(to_np(got), want, fn.__name__)
+        else:
+            assert np.array_equal(to_np(got), narrow_bits(want, dtype, orc)), fn.__name__
+
+
+def test_add_mul_scalar_broadcast(dev, orc):
+    """elementwise.rs:41-48 and the test at :226-231: [1,2,3] * [2] = [2,4,6]."""
+    a = torch.tensor([1.0, 2.0, 3.0], device=dev)
+    s = torch.tensor([2.0], device=dev)
+    assert ops.mul(a, s).cpu().tolist() == [2.0, 4.0, 6.0]
+    assert ops.mul(s, a).cpu().tolist() == [2.0, 4.0, 6.0]
+    assert ops.add(a, s).cpu().tolist() == [3.0, 4.0, 5.0]
+    x = _gen((1000,), 5, dev)
+    assert_bits_equal(to_np(ops.add(x, s)), orc.add(to_np(x), np.float32([2.0])), "add broadcast")
+    from sapient_amd._lib import EINVAL, SapientHipError
+    with pytest.raises(SapientHipError) as e:
+        ops.add(a, torch.zeros(2, device=dev))
+    assert e.value.status == EINVAL
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=IDS)
+@pytest.mark.parametrize("n", [1, 5, 4864, 512 * 4864, 1 << 20])
+def test_silu_swiglu(dev, orc, dtype, n):
+    print(f"case silu/swiglu {dtype} n={n}", flush=True)
+    g, u = _gen((n,), 6, dev, 2.0, dtype), _gen((n,), 7, dev, 2.0, dtype)
+    g32, u32 = widen(g, orc), widen(u, orc)
+    _check(ops.silu(g), orc.silu(g32), orc, 1e-5, f"silu {dtype}")
+    _check(ops.swiglu(g, u), orc.swiglu(g32, u32), orc, 1e-5, f"swiglu {dtype}")
+
+
+def test_silu_special_values(dev, orc):
+    x = torch.from_numpy(SPECIALS).to(dev)
+    got = to_np(ops.silu(x))
+    want = orc.silu(SPECIALS)
+    assert max_rel(got, want, floor=1e-37) <= 1e-5, list(zip(SPECIALS, got, want))
+    assert np.array_equal(np.signbit(got[want == 0]), np.signbit(want[want == 0]))
+
+
+def test_swiglu_llama3_8b_full(dev, orc):
+    """SwiGLU on [8192, 14336] f16, inputs ~N(0, 2): ≤ 1 f16 ulp everywhere."""
+    shape = (8192, 14336)
+    print("case swiglu full f16", flush=True)
+    g, u = _gen(shape, 51, dev, 2.0, torch.float16), _gen(shape, 52, dev, 2.0, torch.float16)
+    out = ops.swiglu(g, u)
+    torch.cuda.synchronize()
+    want = orc.swiglu(widen(g, orc), widen(u, orc))
+    d = ulp_diff16(to_np(out), narrow_bits(want, torch.float16, orc), torch.float16)
+    assert int(d.max()) <= 1, f"max {int(d.max())} ulp"
+
+
+def test_swiglu_in_place(dev, orc):
+    g, u = _gen((4099,), 8, dev, 2.0), _gen((4099,), 9, dev, 2.0)
+    want = orc.swiglu(to_np(g), to_np(u))
+    ops.swiglu(g, u, out=g)
+    assert max_rel(to_np(g), want, floor=1e-37) <= 1e-5
+
+
+def test_gelu_f32_bit_exact(dev, orc):
+    """f32 GELU reproduces glibc's tanhf bits, so the result equals the oracle exactly."""
+    x = torch.cat([_gen((1 << 20,), 10, dev, 2.0), _gen((1 << 16,), 11, dev, 8.0), torch.from_numpy(SPECIALS).to(dev)])
+    print("case gelu f32", flush=True)
+    assert_bits_equal(to_np(ops.gelu_tanh(x)), orc.gelu(to_np(x)), "gelu f32")
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=IDS)
+def test_gelu_half_exhaustive_bit_exact(dev, orc, dtype):
+    """Every one of the 65536 f16 / bf16 inputs: output bits equal RNE(oracle(widen(x)))."""
+    bits = torch.arange(0, 65536, dtype=torch.int32).to(torch.int16).view(dtype)
+    x = bits.to(dev)
+    print(f"case gelu exhaustive {dtype}", flush=True)
+    got = to_np(ops.gelu_tanh(x))
+    want = narrow_bits(orc.gelu(widen(x, orc)), dtype, orc)
+    nan = np.isnan(orc.gelu(widen(x, orc)))
+    assert np.array_equal(got[~nan], want[~nan])
+    assert (ulp_diff16(got[nan], want[nan], dtype) == 0).all()
+    # unaligned / tail path gives the same bits
+    got2 = to_np(ops.gelu_tanh(x[3:]))
+    assert np.array_equal(got2, got[3:])
+
+
+def test_gelu_phi2_full(dev, orc):
+    """GELU-tanh on [8192, 10240] f16 (phi-2 FFN), inputs ~N(0, 2): bit-exact."""
+    x = _gen((8192, 10240), 61, dev, 2.0, torch.float16)
+    print("case gelu full f16", flush=True)
+    out = ops.gelu_tanh(x)
+    torch.cuda.synchronize()
+    want = narrow_bits(orc.gelu(widen(x, orc)), torch.float16, orc)
+    assert np.array_equal(to_np(out), want)
+
+
+def test_gelu_kat(dev):
+    """elementwise.rs:206-210: gelu(0) = 0."""
+    assert ops.gelu_tanh(torch.zeros(1, device=dev)).item() == 0.0

@@ -1,0 +1,195 @@
+"""GPU parity: token-embedding gather with GGUF row dequantization — bit-exact.
+
+Reference: crates/sapient-models/src/forward/common.rs:164-217 (embed_tokens /
+gather_row_f32), crates/sapient-core/src/tensor.rs:378-398, :504-527, :534-576
+(Q8_0 / Q4_K / Q6_K dequant). Every dequantized value must equal the oracle's
+bits (NaN table entries: NaN-ness only).
+"""
+import numpy as np
+import pytest
+import torch
+
+from helpers import assert_bits_equal, to_np
+from refvec import (WgpuLcg, f16_bits, gather_test_values, quantize_q8_0_blocks, random_q4_k_blocks,
+                    random_q6_k_blocks)
+
+import sapient_amd.ops as ops
+from sapient_amd._lib import BF16, F16, F32, Q4_K, Q6_K, Q8_0
+
+pytestmark = pytest.mark.gpu
+
+
+def _dev_bytes(a: np.ndarray, dev) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(a).view(np.uint8).reshape(-1).copy()).to(dev)
+
+
+def _ids(ids, dev) -> torch.Tensor:
+    return torch.from_numpy(np.asarray(ids, np.uint32).view(np.int32).copy()).to(dev)
+
+
+def _gather(dev, table_bytes: np.ndarray, dt: int, vocab: int, hidden: int, ids) -> np.ndarray:
+    out = ops.embed(_dev_bytes(table_bytes, dev), dt, vocab, hidden, _ids(ids, dev))
+    return to_np(out)
+
+
+def test_embed_q8_0_matches_wgpu_test_vectors(dev, orc):
+    """resident.rs:565-592: vocab 100 x 320, lcg 0x9E3779B9, ids [7, 0, 99, 42]."""
+    vocab, dim = 100, 320
+    table = WgpuLcg().take(vocab * dim)
+    blocks, deq = quantize_q8_0_blocks(table)
+    ids = [7, 0, 99, 42]
+    print("case embed q8_0 wgpu-vectors", flush=True)
+    got = _gather(dev, blocks, Q8_0, vocab, dim, ids)
+    want = deq.reshape(vocab, dim)[ids]
+    assert_bits_equal(got, want, "embed_q8_0 vs test restatement")
+    assert_bits_equal(got, orc.embed_tokens(blocks, Q8_0, vocab, dim, ids), "embed_q8_0 vs oracle")
+
+
+def test_embed_q4_k_matches_wgpu_test_vectors(dev, orc):
+    """resident.rs:678-705: vocab 50 x 512, random_q4_k_blocks, ids [3, 0, 49, 21]."""
+    vocab, dim = 50, 512
+    blocks, deq = random_q4_k_blocks(vocab * dim // 256, WgpuLcg())
+    ids = [3, 0, 49, 21]
+    print("case embed q4_k wgpu-vectors", flush=True)
+    got = _gather(dev, blocks, Q4_K, vocab, dim, ids)
+    assert_bits_equal(got, deq.reshape(vocab, dim)[ids], "embed_q4_k vs test restatement")
+
+
+def test_embed_q6_k_matches_wgpu_test_vectors(dev, orc):
+    """resident.rs:712-804 data generator (random_q6_k_blocks), vocab 40 x 512."""
+    vocab, dim = 40, 512
+    blocks, deq = random_q6_k_blocks(vocab * dim // 256, WgpuLcg())
+    ids = [39, 0, 17, 5, 17]
+    print("case embed q6_k wgpu-vectors", flush=True)
+    got = _gather(dev, blocks, Q6_K, vocab, dim, ids)
+    assert_bits_equal(got, deq.reshape(vocab, dim)[ids], "embed_q6_k vs test restatement")
+
+
+def test_embed_row_gather_matches_full_dequant(dev, orc):
+    """common.rs:678-718: vocab 17 x 256, LCG seed 0xABCD, ids [0, 7, 16, 3], F32 / F16 / Q8_0 tables."""
+    vocab, hidden = 17, 256
+    data = gather_test_values(vocab, hidden)
+    ids = [0, 7, 16, 3]
+    q8 = orc.quantize_q8_0(data)
+    for dt, table, full in ((F32, data, data.reshape(-1)),
+                            (F16, f16_bits(data), orc.f16_bits_to_f32(f16_bits(data))),
+                            (Q8_0, q8, orc.dequant(q8, Q8_0, vocab * hidden))):
+        print(f"case embed gather-vs-full dtype {dt}", flush=True)
+        got = _gather(dev, table, dt, vocab, hidden, ids)
+        assert_bits_equal(got, full.reshape(vocab, hidden)[ids], f"dtype {dt}")
+
+
+@pytest.mark.parametrize("dt", [F16, BF16])
+def test_embed_half_tables_all_bit_patterns(dev, orc, dt):
+    """Every 16-bit pattern once: widening is exact (NaN payload aside)."""
+    vocab, hidden = 256, 256
+    table = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    ids = list(range(vocab))[::-1]
+    print(f"case embed all-bit-patterns {dt}", flush=True)
+    got = _gather(dev, table, dt, vocab, hidden, ids)
+    assert_bits_equal(got, orc.embed_tokens(table, dt, vocab, hidden, ids), f"widen {dt}")
+
+
+def test_embed_q4_k_both_scale_branches_and_subnormal_scales(dev, orc):
+    """Hand-built blocks: every 6-bit (sc, m) on both get_scale_min_k4 branches
+    (j < 4 and j >= 4 with the high bits), with subnormal, tiny and large f16 d/dmin."""
+    rng = np.random.default_rng(5)
+    nb = 64
+    blocks = rng.integers(0, 256, (nb, 144), dtype=np.uint8)
+    dvals = np.array([0x0001, 0x03FF, 0x0400, 0x3C00, 0x7BFF, 0x1234], np.uint16)
+    for b in range(nb):
+        blocks[b, 0:2] = np.array([dvals[b % 6]], np.uint16).view(np.uint8)
+        blocks[b, 2:4] = np.array([dvals[(b + 3) % 6]], np.uint16).view(np.uint8)
+        blocks[b, 4:16] = (np.arange(12) * 21 + b * 7) % 256
+    vocab, dim = nb // 4, 1024
+    ids = list(range(vocab))
+    got = _gather(dev, blocks, Q4_K, vocab, dim, ids)
+    assert_bits_equal(got, orc.embed_tokens(blocks, Q4_K, vocab, dim, ids), "q4_k hand-built")
+
+
+def test_embed_q8_0_every_quant_value(dev, orc):
+    """All 256 int8 quants under f16 scales incl. subnormal / max / negative."""
+    scales = np.array([0x0001, 0x0200, 0x3C00, 0xBC00, 0x7BFF, 0x2E66, 0x1000, 0x8001], np.uint16)
+    blocks = np.zeros((8, 8, 34), np.uint8)  # 8 rows of 8 blocks: each row sweeps all 256 quants
+    for r in range(8):
+        for b in range(8):
+            blocks[r, b, 0:2] = np.array([scales[(r + b) % 8]], np.uint16).view(np.uint8)
+            blocks[r, b, 2:] = np.arange(32 * b, 32 * b + 32) % 256
+    ids = [7, 3, 0, 5]
+    got = _gather(dev, blocks, Q8_0, 8, 256, ids)
+    assert_bits_equal(got, orc.embed_tokens(blocks, Q8_0, 8, 256, ids), "q8_0 sweep")
+
+
+def _q4k_table(vocab, hidden, seed, dev):
+    """Synthetic Q4_K table on the device: d, dmin ~U(0.0005, 0.02) as f16, scales and
+    nibbles uniform random bytes."""
+    g = torch.Generator(device=dev).manual_seed(seed)
+    nb = vocab * hidden // 256
+    t = torch.randint(0, 256, (nb, 144), generator=g, device=dev, dtype=torch.int32).to(torch.uint8)
+    d = (torch.rand((nb, 2), generator=g, device=dev) * (0.02 - 0.0005) + 0.0005).to(torch.float16)
+    t[:, 0:4] = d.view(torch.uint8).view(nb, 4)
+    return t.reshape(-1)
+
+
+def test_embed_q8_0_qwen_shape(dev, orc):
+    """Qwen2.5-0.5B table 151936 x 896 Q8_0, T = 512 uniform ids (and T = 1)."""
+    vocab, hidden = 151936, 896
+    g = torch.Generator(device=dev).manual_seed(71)
+    nb = vocab * hidden // 32
+    t = torch.randint(-127, 128, (nb, 34), generator=g, device=dev, dtype=torch.int32).to(torch.int8).view(torch.uint8)
+    d = (torch.rand((nb, 1), generator=g, device=dev) * (0.05 - 0.001) + 0.001).to(torch.float16)
+    t[:, 0:2] = d.view(torch.uint8).view(nb, 2)
+    table = t.reshape(-1).contiguous()
+    tab_np = to_np(table)
+    for T in (1, 512):
+        ids = np.random.default_rng(T).integers(0, vocab, T).astype(np.uint32)
+        print(f"case embed q8_0 qwen T={T}", flush=True)
+        got = to_np(ops.embed(table, Q8_0, vocab, hidden, _ids(ids, dev)))
+        assert_bits_equal(got, orc.embed_tokens(tab_np, Q8_0, vocab, hidden, ids), f"q8_0 T={T}")
+
+
+@pytest.mark.parametrize("dist", ["uniform", "zipf"])
+def test_embed_q4_k_llama3_full(dev, orc, dist):
+    """128256 x 4096 Q4_K table, 65536 ids (uniform and Zipf s = 1.1): every row bit-exact."""
+    vocab, hidden, n = 128256, 4096, 65536
+    table = _q4k_table(vocab, hidden, 81, dev)
+    rng = np.random.default_rng(82)
+    if dist == "uniform":
+        ids = rng.integers(0, vocab, n).astype(np.uint32)
+    else:
+        p = 1.0 / np.arange(1, vocab + 1) ** 1.1
+        ranks = np.searchsorted(np.cumsum(p / p.sum()), rng.random(n))
+        ids = rng.permutation(vocab)[np.minimum(ranks, vocab - 1)].astype(np.uint32)
+    print(f"case embed q4_k full {dist}", flush=True)
+    out = ops.embed(table, Q4_K, vocab, hidden, _ids(ids, dev))
+    torch.cuda.synchronize()
+    assert_bits_equal(to_np(out), orc.embed_tokens(to_np(table), Q4_K, vocab, hidden, ids), f"q4_k {dist}")
+
+
+def test_embed_out_of_range_id_sets_flag_and_zero_fills(dev, orc):
+    """common.rs:171-173 rejects ids >= vocab; the device path never reads the table for them."""
+    vocab, hidden = 17, 256
+    data = gather_test_values(vocab, hidden)
+    flag = torch.zeros(1, dtype=torch.int32, device=dev)
+    out = ops.embed(_dev_bytes(data, dev), F32, vocab, hidden, _ids([3, 17, 0xFFFFFFFF, 5], dev), bad_id_flag=flag)
+    o = to_np(out)
+    assert flag.item() == 1
+    assert (o[1] == 0).all() and (o[2] == 0).all()
+    assert_bits_equal(o[[0, 3]], data[[3, 5]], "valid rows")
+    from oracle import ERANGE, OracleError
+    with pytest.raises(OracleError) as e:
+        orc.embed_tokens(data, F32, vocab, hidden, [17])
+    assert e.value.status == ERANGE
+
+
+def test_embed_rejects_bad_arguments(dev):
+    from sapient_amd._lib import EINVAL, lib
+    L = lib()
+    t = torch.zeros(1024, dtype=torch.uint8, device=dev)
+    ids = torch.zeros(2, dtype=torch.int32, device=dev)
+    out = torch.zeros(2, 512, device=dev)
+    s = torch.cuda.current_stream().cuda_stream
+    assert L.sph_embed(t.data_ptr(), Q8_0, 1, 48, ids.data_ptr(), 2, out.data_ptr(), None, s) == EINVAL  # 48 % 32
+    assert L.sph_embed(t.data_ptr(), Q4_K, 1, 300, ids.data_ptr(), 2, out.data_ptr(), None, s) == EINVAL  # % 256
+    assert L.sph_embed(t.data_ptr(), 2, 1, 256, ids.data_ptr(), 2, out.data_ptr(), None, s) == EINVAL    # Q4_0
+    assert L.sph_embed(t.data_ptr() + 1, Q4_K, 1, 256, ids.data_ptr(), 2, out.data_ptr(), None, s) == EINVAL

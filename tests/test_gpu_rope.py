@@ -1,0 +1,157 @@
+"""GPU parity: rotary position embedding (NEOX and interleaved), in place.
+
+Reference: crates/sapient-backends/cpu/src/kernels/rope.rs:18-62 (apply_rope),
+:83-136 (apply_rope_partial_scaled); interleaved pairs per the GGUF q/k row
+permutation (crates/sapient-models/src/gguf_weights.rs:111-115).
+
+Tolerance: each output element within 1e-5 of the norm of the input pair it
+came from (x0·cos − x1·sin cancels, so a pure relative bound is meaningless
+near zero). Half outputs: ≤ 1 ulp against the f32 oracle rounded to nearest-even.
+"""
+import numpy as np
+import pytest
+import torch
+
+from helpers import narrow_bits, to_np, ulp_diff16, widen
+from refvec import WgpuLcg
+
+import sapient_amd.ops as ops
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-5
+
+
+def _gen(shape, seed, dev, dtype=torch.float32):
+    g = torch.Generator(device=dev).manual_seed(seed)
+    return torch.randn(shape, generator=g, device=dev).to(dtype)
+
+
+def _pair_norm(x: np.ndarray, rotary_dim: int, interleaved: bool) -> np.ndarray:
+    """Per element, the norm of the input pair it belongs to (|x| outside the rotary part)."""
+    pn = np.abs(x).astype(np.float64)
+    half = rotary_dim // 2
+    if interleaved:
+        a, b = x[..., 0:rotary_dim:2], x[..., 1:rotary_dim:2]
+        n = np.sqrt(a.astype(np.float64) ** 2 + b.astype(np.float64) ** 2)
+        pn[..., 0:rotary_dim:2] = n
+        pn[..., 1:rotary_dim:2] = n
+    else:
+        a, b = x[..., :half], x[..., half:rotary_dim]
+        n = np.sqrt(a.astype(np.float64) ** 2 + b.astype(np.float64) ** 2)
+        pn[..., :half] = n
+        pn[..., half:rotary_dim] = n
+    return pn
+
+
+def _check(out: torch.Tensor, ref32: np.ndarray, x32: np.ndarray, rotary_dim, interleaved, orc, what):
+    if out.dtype == torch.float32:
+        got = to_np(out).astype(np.float64)
+        err = np.abs(got - ref32) / np.maximum(_pair_norm(x32, rotary_dim, interleaved), 1e-30)
+        err = np.where(got == ref32, 0.0, err)
+        assert float(err.max()) <= TOL, f"{what}: max pair-relative err {float(err.max()):.3e}"
+    else:
+        d = ulp_diff16(to_np(out), narrow_bits(ref32, out.dtype, orc), out.dtype)
+        assert int(d.max()) <= 1, f"{what}: max {int(d.max())} ulp"
+
+
+def _run(dev, orc, dtype, B, Hq, Hk, S, D, rd, base, positions, interleaved, pos_scale=1.0, seed=0):
+    q = _gen((B, Hq, S, D), 100 + seed, dev, dtype)
+    k = _gen((B, Hk, S, D), 200 + seed, dev, dtype) if Hk else None
+    q32 = widen(q, orc).reshape(B, Hq, S, D)
+    k32 = widen(k, orc).reshape(B, Hk, S, D) if Hk else None
+    pos = torch.tensor(positions, dtype=torch.int32, device=dev)
+    ops.rope_(q, k, pos, base, rotary_dim=rd, pos_scale=pos_scale, interleaved=interleaved)
+    torch.cuda.synchronize()
+    what = f"rope {'il' if interleaved else 'neox'} {dtype} B{B} Hq{Hq} Hk{Hk} S{S} D{D} rd{rd}"
+    ref_q = orc.apply_rope_partial_scaled(q32, positions, base, rd, pos_scale, interleaved)
+    _check(q, ref_q, q32, rd, interleaved, orc, what + " q")
+    if Hk:
+        ref_k = orc.apply_rope_partial_scaled(k32, positions, base, rd, pos_scale, interleaved)
+        _check(k, ref_k, k32, rd, interleaved, orc, what + " k")
+
+
+@pytest.mark.parametrize("H,S,D,rd", [(4, 7, 80, 32), (3, 5, 64, 64)])
+def test_rope_matches_wgpu_test_vectors(dev, orc, H, S, D, rd):
+    """resident.rs:152-187: lcg 0x9E3779B9 data, positions s + 11, base 1e4."""
+    nxt = WgpuLcg()
+    data = nxt.take(H * S * D).reshape(1, H, S, D)
+    positions = [s + 11 for s in range(S)]
+    x = torch.from_numpy(data.copy()).to(dev)
+    print(f"case rope wgpu-vectors {H},{S},{D},{rd}", flush=True)
+    ops.rope_(x, None, torch.tensor(positions, dtype=torch.int32, device=dev), 1e4, rotary_dim=rd)
+    ref = orc.apply_rope_partial_scaled(data, positions, 1e4, rd)
+    _check(x, ref, data, rd, False, orc, "rope wgpu vectors")
+    assert np.abs(to_np(x) - ref).max() < 1e-4  # the reference test's own bound
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16], ids=lambda d: str(d).split(".")[-1])
+@pytest.mark.parametrize("interleaved", [False, True], ids=["neox", "interleaved"])
+@pytest.mark.parametrize("B,Hq,Hk,S,D,rd", [
+    (1, 14, 2, 1, 64, 64),       # Qwen2.5-0.5B decode (T = 1)
+    (1, 14, 2, 512, 64, 64),     # Qwen2.5-0.5B prefill (T = 512)
+    (2, 4, 2, 9, 128, 128),
+    (1, 3, 0, 5, 80, 32),        # Phi partial rotary
+    (1, 2, 1, 3, 6, 6),          # odd half: scalar path
+    (1, 2, 2, 4, 12, 8),
+])
+def test_rope_shapes(dev, orc, dtype, interleaved, B, Hq, Hk, S, D, rd):
+    positions = [int(p) for p in np.random.default_rng(S).integers(0, 8192, S)] if S > 1 else [4095]
+    base = 1e6 if D == 64 else 5e5
+    print(f"case rope {dtype} il={interleaved} {B},{Hq},{Hk},{S},{D},{rd}", flush=True)
+    _run(dev, orc, dtype, B, Hq, Hk, S, D, rd, base, positions, interleaved)
+
+
+def test_rope_linear_position_scale(dev, orc):
+    """rope.rs:123-124: effective position pos / pos_scale (Gemma3 uses 8)."""
+    _run(dev, orc, torch.float32, 1, 4, 2, 33, 128, 128, 1e6, list(range(100, 133)), False, pos_scale=8.0)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16], ids=["float32", "float16"])
+@pytest.mark.parametrize("interleaved", [False, True], ids=["neox", "interleaved"])
+def test_rope_llama3_8b_full(dev, orc, dtype, interleaved):
+    """Q 32 heads + K 8 heads, T = 8192 contiguous positions, head_dim 128, theta 5e5."""
+    print(f"case rope full {dtype} il={interleaved}", flush=True)
+    _run(dev, orc, dtype, 1, 32, 8, 8192, 128, 128, 5e5, list(range(8192)), interleaved, seed=7)
+
+
+def test_rope_position_zero_is_identity(dev):
+    """rope.rs:196-206: at position 0 the vector is unchanged."""
+    x = torch.tensor([1.0, 2.0, 3.0, 4.0], device=dev).view(1, 1, 1, 4)
+    ops.rope_(x, None, torch.zeros(1, dtype=torch.int32, device=dev), 1e4)
+    assert x.flatten().cpu().tolist() == [1.0, 2.0, 3.0, 4.0]
+
+
+def test_rope_partial_leaves_tail_unchanged(dev):
+    """rope.rs:168-182: head_dim 8, rotary_dim 4, position 3."""
+    data = torch.arange(1, 9, dtype=torch.float32, device=dev).view(1, 1, 1, 8)
+    x = data.clone()
+    ops.rope_(x, None, torch.tensor([3], dtype=torch.int32, device=dev), 1e4, rotary_dim=4)
+    assert torch.equal(x[..., 4:], data[..., 4:])
+    assert (x[..., :4] - data[..., :4]).abs().max() > 1e-6
+
+
+def test_rope_interleaved_is_permuted_neox(dev, orc):
+    """interleaved(P x) = P neox(x) for the GGUF row permutation P, bit for bit on the GPU."""
+    H, S, D = 3, 17, 64
+    x = _gen((1, H, S, D), 300, dev)
+    pos = torch.arange(S, dtype=torch.int32, device=dev) + 5
+    xn = x.clone()
+    ops.rope_(xn, None, pos, 1e4)
+    # P maps HF channel a*D/2 + b to interleaved channel 2b + a (gguf_weights.rs:111-115)
+    perm = torch.tensor([(c % 2) * (D // 2) + c // 2 for c in range(D)], device=dev)
+    xi = x[..., perm].contiguous()
+    ops.rope_(xi, None, pos, 1e4, interleaved=True)
+    assert torch.equal(xi, xn[..., perm])
+
+
+def test_rope_rejects_bad_arguments(dev):
+    from sapient_amd._lib import EINVAL, lib
+    L = lib()
+    x = torch.zeros(1, 2, 3, 8, device=dev)
+    pos = torch.zeros(3, dtype=torch.int32, device=dev)
+    s = torch.cuda.current_stream().cuda_stream
+    args = lambda D, rd, layout=0: (x.data_ptr(), 2, None, 0, 0, layout, pos.data_ptr(), 1, 3, D, rd, 1e4, 1.0, s)
+    assert L.sph_rope(*args(7, 7)) == EINVAL      # odd head_dim
+    assert L.sph_rope(*args(8, 10)) == EINVAL     # rotary_dim > head_dim
+    assert L.sph_rope(*args(8, 3)) == EINVAL      # odd rotary_dim
+    assert L.sph_rope(*args(8, 8, 2)) == EINVAL   # unknown layout
