@@ -27,6 +27,9 @@ ARCH = "gfx950"
 #  -ffp-contract=off      no a*b+c fusion: products and sums round as in the reference
 #  correctly-rounded f32 divide/sqrt, f32 denormals kept (both HIP defaults, stated)
 #  -packed-fp32-ops off   no v_pk_{add,mul,fma}_f32 generation
+#  -fma-mix/-mad-mix off  no v_fma_mix*/v_mad_mix*: the backend folds f32 products
+#                         into these f16-result ops, which round differently from
+#                         "round to f32, then to f16" and give +0 for -0 products
 HIPCC_FLAGS = [
     f"--offload-arch={ARCH}",
     "-O3",
@@ -36,6 +39,8 @@ HIPCC_FLAGS = [
     "-fhip-fp32-correctly-rounded-divide-sqrt",
     "-fno-gpu-flush-denormals-to-zero",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Xclang", "-target-feature", "-Xclang", "-fma-mix-insts",
+    "-Xclang", "-target-feature", "-Xclang", "-mad-mix-insts",
     "-Wall",
     "-Wno-unused-function",
 ]

@@ -8,12 +8,14 @@
 //   gelu 0.5 v (1 + tanh(0.79788456 (v + 0.044715 v v v)))   (:120-127)
 //
 // Design: all streams are HBM-bound. Each thread moves 16-byte vectors, four
-// in flight per operand per loop trip (a grid-stride loop over ~2K blocks).
+// in flight per operand per loop trip (a grid-stride loop over ~2K blocks),
+// with non-temporal loads and stores (every byte is touched once).
 //  - SiLU evaluates exp(-v) with the hardware exp2 on a split-precision
 //    argument and 1/(1+e) with the hardware reciprocal: ≤ ~4 f32 ulp from the
 //    reference, no cancellation anywhere, ~12 VALU ops per element. Inputs
 //    below -80 (where 1/(1+e) would be subnormal) take the IEEE expf / divide
-//    path, which also reproduces the reference's -0 once expf(-v) overflows.
+//    path, which also reproduces the reference's -0 once expf(-v) overflows;
+//    inputs above 64 return v, exactly as the reference does.
 //  - GELU: the reference's 1 + tanh(z) cancels for z < -3, so its result there
 //    is glibc's rounding of tanh; only glibc's own algorithm reproduces it (see
 //    glibc_tanhf.h). For f16 / bf16 inputs the op is a function of 16 bits, so
@@ -36,7 +38,10 @@ enum Op { OP_ADD = 0, OP_MUL = 1, OP_SILU = 2, OP_SWIGLU = 3, OP_GELU = 4 };
 enum Bcast { B_NONE = 0, B_SCALAR_B = 1, B_SCALAR_A = 2 };
 
 __device__ __forceinline__ float silu_f(float g) {
-    if (g < -80.0f) return g / (1.0f + expf(-g));
+    // Below -80 (and NaN): IEEE path. Above 64: exp(-g) < 2^-92, so 1 + e
+    // rounds to 1 and the reference returns g itself (also for +inf).
+    if (!(g >= -80.0f)) return g / (1.0f + expf(-g));
+    if (g > 64.0f) return g;
     const float kL2eHi = 1.44269502162933349609375f;  // f32(log2 e)
     const float kL2eLo = 1.925963033500011e-08f;      // log2 e - kL2eHi
     const float kLn2 = 0.693147180559945309f;
@@ -77,8 +82,8 @@ __global__ __launch_bounds__(kThreads) void ew_vec(const T* a, const T* b, T* ou
         for (int u = 0; u < kUnroll; ++u) {
             const int64_t i = base + (int64_t)u * kThreads;
             if (i < nvec) {
-                if constexpr (BC != B_SCALAR_A) load_f32<T, E>(a + i * E, va[u]);
-                if constexpr (binary_op<OP>() && BC != B_SCALAR_B) load_f32<T, E>(b + i * E, vb[u]);
+                if constexpr (BC != B_SCALAR_A) load_f32<T, E, true>(a + i * E, va[u]);
+                if constexpr (binary_op<OP>() && BC != B_SCALAR_B) load_f32<T, E, true>(b + i * E, vb[u]);
             }
         }
 #pragma unroll
@@ -92,7 +97,7 @@ __global__ __launch_bounds__(kThreads) void ew_vec(const T* a, const T* b, T* ou
                     const float y = BC == B_SCALAR_B ? sb : vb[u][e];
                     o[e] = apply_op<OP>(x, y);
                 }
-                store_f32<T, E>(out + i * E, o);
+                store_f32<T, E, true>(out + i * E, o);
             }
         }
     }
@@ -200,7 +205,7 @@ __global__ __launch_bounds__(kLutThreads) void gelu_lut_apply(const uint16_t* in
 #pragma unroll
         for (int u = 0; u < kUnroll; ++u) {
             const int64_t i = base + (int64_t)u * kLutThreads;
-            if (i < nvec) q[u] = vin[i];
+            if (i < nvec) q[u] = vload<true>(vin + i);
         }
 #pragma unroll
         for (int u = 0; u < kUnroll; ++u) {
@@ -212,7 +217,7 @@ __global__ __launch_bounds__(kLutThreads) void gelu_lut_apply(const uint16_t* in
                     const uint32_t w = q[u][c];
                     r[c] = (uint32_t)tab[w & 0xFFFFu] | ((uint32_t)tab[w >> 16] << 16);
                 }
-                vout[i] = r;
+                vstore<true>(vout + i, r);
             }
         }
     }

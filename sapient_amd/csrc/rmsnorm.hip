@@ -7,16 +7,20 @@
 // RMSNorm of the f32 sum.
 //
 // Design (HBM-bound, ≈0.2 flop/byte):
-//  - One wave64 per row. Each lane owns every 64th 16-byte vector of the row
-//    and keeps its slice of r in registers, so every input byte crosses HBM
-//    once and the row is never re-read: the wave sums r², reduces with a
-//    butterfly of cross-lane shuffles (no LDS, no barrier), then scales and
-//    stores from registers.
-//  - All accesses are 16 bytes per lane, 1 KiB contiguous per wave instruction.
+//  - A row is split across W wave64s (W = 1, 2, 4, 8 or 16, chosen so every
+//    lane holds ~16 values); each lane owns every (64·W)-th 16-byte vector of
+//    the row and keeps its slice of r in registers, so every input byte
+//    crosses HBM once and the row is never re-read. Small W keeps the register
+//    footprint at ~64 VGPRs, i.e. the full 8 waves per SIMD of occupancy.
+//  - Each wave sums its r² with a butterfly of cross-lane shuffles; the W
+//    partial sums meet in LDS and every wave adds them in the same fixed order.
+//  - All row traffic is 16 bytes per lane (1 KiB contiguous per wave
+//    instruction) and non-temporal: x, residual and y are touched once, and
+//    streaming them past the caches measured ~+20 % achieved bandwidth on
+//    MI355X. The weight row uses ordinary loads (it is re-read by every row).
 //  - The residual store is issued before the reduction, overlapping it.
-//  - Rows wider than 128 values per lane (8192 elements), or rows whose
-//    pointers / width do not allow 16-byte access, take a block-per-row
-//    two-pass kernel.
+//  - Rows wider than 16 waves x 16 values, or whose pointers / width do not
+//    allow 16-byte access, take a block-per-row two-pass kernel.
 //
 // Parity: x·x, the division by dim, sqrt and 1/· are IEEE-rounded f32 exactly
 // as in the reference; the products y = (r·inv)·w round in the same order (the
@@ -28,56 +32,72 @@ namespace sph {
 namespace {
 
 constexpr int kWave = 64;
-constexpr int kRowsPerBlock = 4;  // 256 threads, one row per wave
 
-template <typename TX, typename TW, typename TO, bool FUSED, int VPT>
-__global__ __launch_bounds__(256) void rms_rows_vec(const TX* __restrict__ x, TX* __restrict__ residual,
-                                                   const TW* __restrict__ w, TO* __restrict__ out,
-                                                   int64_t rows, int dim, float eps) {
+// W waves per row, VPT 16-byte vectors per lane, RPB rows per block.
+template <typename TX, typename TW, typename TO, bool FUSED, int W, int VPT>
+__global__ __launch_bounds__(W >= 4 ? 64 * W : 256) void rms_rows_vec(const TX* __restrict__ x, TX* __restrict__ residual,
+                                                                   const TW* __restrict__ w, TO* __restrict__ out,
+                                                                   int64_t rows, int dim, float eps) {
     constexpr int E = vec16<TX>::n;  // elements per 16-byte access of x
+    constexpr int WPB = W >= 4 ? W : 4;
+    constexpr int RPB = WPB / W;
+    __shared__ float partial[WPB];
     const int lane = threadIdx.x & (kWave - 1);
-    const int64_t row = (int64_t)blockIdx.x * kRowsPerBlock + (threadIdx.x / kWave);
-    if (row >= rows) return;  // whole wave leaves together
+    const int wv = threadIdx.x / kWave;
+    const int sub = wv % W;  // this wave's share of the row
+    const int64_t row = (int64_t)blockIdx.x * RPB + wv / W;
+    const bool live = row < rows;
     const int nvec = dim / E;
     const size_t base = (size_t)row * (size_t)dim;
 
     float r[VPT][E];
     float ss = 0.0f;
+    if (live) {
 #pragma unroll
-    for (int j = 0; j < VPT; ++j) {
-        const int v = lane + kWave * j;
-        if (v < nvec) {
-            load_f32<TX, E>(x + base + (size_t)v * E, r[j]);
-            if constexpr (FUSED) {
-                float b[E];
-                load_f32<TX, E>(residual + base + (size_t)v * E, b);
+        for (int j = 0; j < VPT; ++j) {
+            const int v = (sub + W * j) * kWave + lane;
+            if (v < nvec) {
+                load_f32<TX, E, true>(x + base + (size_t)v * E, r[j]);
+                if constexpr (FUSED) {
+                    float b[E];
+                    load_f32<TX, E, true>(residual + base + (size_t)v * E, b);
 #pragma unroll
-                for (int e = 0; e < E; ++e) r[j][e] = r[j][e] + b[e];
-                store_f32<TX, E>(residual + base + (size_t)v * E, r[j]);
+                    for (int e = 0; e < E; ++e) r[j][e] = r[j][e] + b[e];
+                    store_f32<TX, E, true>(residual + base + (size_t)v * E, r[j]);
+                }
+#pragma unroll
+                for (int e = 0; e < E; ++e) ss = ss + r[j][e] * r[j][e];
             }
-#pragma unroll
-            for (int e = 0; e < E; ++e) ss = ss + r[j][e] * r[j][e];
         }
     }
     ss = wave_sum(ss);
+    if constexpr (W > 1) {
+        if (lane == 0) partial[wv] = ss;
+        __syncthreads();
+        float tot = 0.0f;
+#pragma unroll
+        for (int k = 0; k < W; ++k) tot = tot + partial[(wv / W) * W + k];
+        ss = tot;
+    }
+    if (!live) return;
     const float ms = ss / (float)dim;
     const float inv = 1.0f / sqrtf(ms + eps);
 
 #pragma unroll
     for (int j = 0; j < VPT; ++j) {
-        const int v = lane + kWave * j;
+        const int v = (sub + W * j) * kWave + lane;
         if (v < nvec) {
-            float wv[E];
+            float wv_[E];
             if (w != nullptr) {
-                load_f32<TW, E>(w + (size_t)v * E, wv);
+                load_f32<TW, E>(w + (size_t)v * E, wv_);
             } else {
 #pragma unroll
-                for (int e = 0; e < E; ++e) wv[e] = 1.0f;
+                for (int e = 0; e < E; ++e) wv_[e] = 1.0f;
             }
             float y[E];
 #pragma unroll
-            for (int e = 0; e < E; ++e) y[e] = (r[j][e] * inv) * wv[e];
-            store_f32<TO, E>(out + base + (size_t)v * E, y);
+            for (int e = 0; e < E; ++e) y[e] = (r[j][e] * inv) * wv_[e];
+            store_f32<TO, E, true>(out + base + (size_t)v * E, y);
         }
     }
 }
@@ -123,9 +143,14 @@ int launch_rms(const void* x, void* residual, const void* w, void* out, int64_t 
                float eps, hipStream_t stream) {
     if (rows == 0 || dim == 0) return SPH_OK;
     constexpr int E = vec16<TX>::n;
+    // Vector path: ~16 values per lane, W waves per row (W <= 16).
+    constexpr int VPT = 16 / E;
+    const int64_t nvec = dim / E;
+    int W = 1;
+    while (W < 16 && nvec > (int64_t)kWave * VPT * W) W *= 2;
     const bool vec_ok = dim % E == 0 && aligned(x, 16) && aligned(out, 16) &&
                         (!FUSED || aligned(residual, 16)) && (w == nullptr || aligned(w, 16)) &&
-                        dim / E <= kWave * (128 / E) && dim <= INT32_MAX;
+                        nvec <= (int64_t)kWave * VPT * W && dim <= INT32_MAX;
     // A launch covers at most 2^22 rows, keeping grid x block below 2^32 work-items.
     constexpr int64_t kChunk = int64_t(1) << 22;
     for (int64_t r0 = 0; r0 < rows; r0 += kChunk) {
@@ -136,16 +161,17 @@ int launch_rms(const void* x, void* residual, const void* w, void* out, int64_t 
         const TW* wp = static_cast<const TW*>(w);
         TO* op = static_cast<TO*>(out) + off;
         if (vec_ok) {
-            const int64_t nvec = dim / E;
-            const dim3 grid((unsigned)((nr + kRowsPerBlock - 1) / kRowsPerBlock));
+            const int rpb = W >= 4 ? 1 : 4 / W;
+            const dim3 grid((unsigned)((nr + rpb - 1) / rpb));
+            const int threads = W >= 4 ? kWave * W : 256;
             const int d = (int)dim;
-            // Per-lane register slice: up to 16, 64 or 128 f32 values.
-            if (nvec <= kWave * 4)
-                rms_rows_vec<TX, TW, TO, FUSED, 4><<<grid, 256, 0, stream>>>(xp, rp, wp, op, nr, d, eps);
-            else if (nvec <= kWave * (64 / E))
-                rms_rows_vec<TX, TW, TO, FUSED, 64 / E><<<grid, 256, 0, stream>>>(xp, rp, wp, op, nr, d, eps);
-            else
-                rms_rows_vec<TX, TW, TO, FUSED, 128 / E><<<grid, 256, 0, stream>>>(xp, rp, wp, op, nr, d, eps);
+            switch (W) {
+            case 1: rms_rows_vec<TX, TW, TO, FUSED, 1, VPT><<<grid, threads, 0, stream>>>(xp, rp, wp, op, nr, d, eps); break;
+            case 2: rms_rows_vec<TX, TW, TO, FUSED, 2, VPT><<<grid, threads, 0, stream>>>(xp, rp, wp, op, nr, d, eps); break;
+            case 4: rms_rows_vec<TX, TW, TO, FUSED, 4, VPT><<<grid, threads, 0, stream>>>(xp, rp, wp, op, nr, d, eps); break;
+            case 8: rms_rows_vec<TX, TW, TO, FUSED, 8, VPT><<<grid, threads, 0, stream>>>(xp, rp, wp, op, nr, d, eps); break;
+            default: rms_rows_vec<TX, TW, TO, FUSED, 16, VPT><<<grid, threads, 0, stream>>>(xp, rp, wp, op, nr, d, eps); break;
+            }
         } else {
             rms_rows_generic<TX, TW, TO, FUSED><<<dim3((unsigned)nr), 256, 0, stream>>>(xp, rp, wp, op, nr, dim, eps);
         }

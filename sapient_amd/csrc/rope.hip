@@ -11,7 +11,8 @@
 //    group of heads of Q and K: sin/cos are computed once per (position, pair)
 //    and reused for every head (40 at the Llama-3-8B shape), so the
 //    transcendental cost is amortised and the loop over heads is pure
-//    16-byte load / FMA-free arithmetic / 16-byte store.
+//    16-byte load / FMA-free arithmetic / 16-byte store, non-temporal (each
+//    element is read once and written once).
 //  - Parity: the d/2 denominators powf(base, 2i/d) come from the host's libm
 //    (the call the reference makes, passed in as kernel arguments); the
 //    division by them is IEEE f32 in-kernel; sin and cos are evaluated in f64
@@ -71,8 +72,8 @@ __global__ __launch_bounds__(kThreads) void rope_kernel(T* q, int nq, T* k, int 
                 x0[0] = widen(row[i0]);
                 x1[0] = widen(row[i0 + half]);
             } else {
-                load_f32<T, P>(row + i0, x0);
-                load_f32<T, P>(row + i0 + half, x1);
+                load_f32<T, P, true>(row + i0, x0);
+                load_f32<T, P, true>(row + i0 + half, x1);
             }
             float o0[P], o1[P];
 #pragma unroll
@@ -84,19 +85,19 @@ __global__ __launch_bounds__(kThreads) void rope_kernel(T* q, int nq, T* k, int 
                 row[i0] = narrow<T>(o0[0]);
                 row[i0 + half] = narrow<T>(o1[0]);
             } else {
-                store_f32<T, P>(row + i0, o0);
-                store_f32<T, P>(row + i0 + half, o1);
+                store_f32<T, P, true>(row + i0, o0);
+                store_f32<T, P, true>(row + i0 + half, o1);
             }
         } else {
             float x[2 * P];
-            load_f32<T, 2 * P>(row + 2 * i0, x);
+            load_f32<T, 2 * P, true>(row + 2 * i0, x);
             float o[2 * P];
 #pragma unroll
             for (int j = 0; j < P; ++j) {
                 o[2 * j] = x[2 * j] * cs[j] - x[2 * j + 1] * sn[j];
                 o[2 * j + 1] = x[2 * j + 1] * cs[j] + x[2 * j] * sn[j];
             }
-            store_f32<T, 2 * P>(row + 2 * i0, o);
+            store_f32<T, 2 * P, true>(row + 2 * i0, o);
         }
     }
 }

@@ -78,3 +78,26 @@ def assert_bits_equal(got: np.ndarray, want: np.ndarray, what: str) -> None:
         i = int(np.flatnonzero(bad)[0])
         raise AssertionError(f"{what}: {int(bad.sum())} of {g.size} differ; first at {i}: "
                              f"got {g[i]!r} ({gb[i]:#010x}) want {w[i]!r} ({wb[i]:#010x})")
+
+
+def assert_bits16_equal(got: np.ndarray, want: np.ndarray, what: str) -> None:
+    """Bit-exact comparison of f16/bf16 bit arrays, reporting the first mismatches."""
+    g = np.asarray(got, np.uint16).reshape(-1)
+    w = np.asarray(want, np.uint16).reshape(-1)
+    assert g.shape == w.shape, f"{what}: shape {g.shape} vs {w.shape}"
+    bad = np.flatnonzero(g != w)
+    if bad.size:
+        ex = ", ".join(f"[{i}] got {g[i]:#06x} want {w[i]:#06x}" for i in bad[:6])
+        raise AssertionError(f"{what}: {bad.size} of {g.size} differ: {ex}")
+
+
+def assert_ulp16(got: np.ndarray, want: np.ndarray, dtype, max_ulp: int, what: str) -> None:
+    """f16/bf16 bits within max_ulp representable values, reporting the worst elements."""
+    g = np.asarray(got, np.uint16).reshape(-1)
+    w = np.asarray(want, np.uint16).reshape(-1)
+    d = ulp_diff16(g, w, dtype)
+    bad = np.flatnonzero(d > max_ulp)
+    if bad.size:
+        worst = bad[np.argsort(-d[bad])][:6]
+        ex = ", ".join(f"[{i}] got {g[i]:#06x} want {w[i]:#06x} ({int(d[i])} ulp)" for i in worst)
+        raise AssertionError(f"{what}: {bad.size} of {g.size} beyond {max_ulp} ulp: {ex}")

@@ -13,7 +13,7 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import assert_bits_equal, max_rel, narrow_bits, to_np, ulp_diff16, widen
+from helpers import assert_ulp16, assert_bits16_equal, assert_bits_equal, max_rel, narrow_bits, to_np, ulp_diff16, widen
 from refvec import WgpuLcg
 
 import sapient_amd.ops as ops
@@ -39,8 +39,7 @@ def _check(out, ref32, orc, rtol, what):
         r = max_rel(to_np(out), ref32, floor=1e-37)
         assert r <= rtol, f"{what}: max rel err {r:.3e}"
     else:
-        d = ulp_diff16(to_np(out), narrow_bits(ref32, out.dtype, orc), out.dtype)
-        assert int(d.max()) <= 1, f"{what}: max {int(d.max())} ulp"
+        assert_ulp16(to_np(out), narrow_bits(ref32, out.dtype, orc), out.dtype, 1, what)
 
 
 def test_swiglu_and_add_match_wgpu_test_vectors(dev, orc):
@@ -68,7 +67,7 @@ def test_add_mul_bit_exact(dev, orc, dtype, n):
         if dtype == torch.float32:
             assert_bits_equal(to_np(got), want, fn.__name__)
         else:
-            assert np.array_equal(to_np(got), narrow_bits(want, dtype, orc)), fn.__name__
+            assert_bits16_equal(to_np(got), narrow_bits(want, dtype, orc), f"{fn.__name__} {dtype}")
 
 
 def test_add_mul_scalar_broadcast(dev, orc):
@@ -112,8 +111,7 @@ def test_swiglu_llama3_8b_full(dev, orc):
     out = ops.swiglu(g, u)
     torch.cuda.synchronize()
     want = orc.swiglu(widen(g, orc), widen(u, orc))
-    d = ulp_diff16(to_np(out), narrow_bits(want, torch.float16, orc), torch.float16)
-    assert int(d.max()) <= 1, f"max {int(d.max())} ulp"
+    assert_ulp16(to_np(out), narrow_bits(want, torch.float16, orc), torch.float16, 1, "swiglu full f16")
 
 
 def test_swiglu_in_place(dev, orc):
@@ -139,7 +137,7 @@ def test_gelu_half_exhaustive_bit_exact(dev, orc, dtype):
     got = to_np(ops.gelu_tanh(x))
     want = narrow_bits(orc.gelu(widen(x, orc)), dtype, orc)
     nan = np.isnan(orc.gelu(widen(x, orc)))
-    assert np.array_equal(got[~nan], want[~nan])
+    assert_bits16_equal(got[~nan], want[~nan], f"gelu {dtype}")
     assert (ulp_diff16(got[nan], want[nan], dtype) == 0).all()
     # unaligned / tail path gives the same bits
     got2 = to_np(ops.gelu_tanh(x[3:]))
@@ -153,7 +151,7 @@ def test_gelu_phi2_full(dev, orc):
     out = ops.gelu_tanh(x)
     torch.cuda.synchronize()
     want = narrow_bits(orc.gelu(widen(x, orc)), torch.float16, orc)
-    assert np.array_equal(to_np(out), want)
+    assert_bits16_equal(to_np(out), want, "gelu full f16")
 
 
 def test_gelu_kat(dev):

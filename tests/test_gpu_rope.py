@@ -6,7 +6,12 @@ permutation (crates/sapient-models/src/gguf_weights.rs:111-115).
 
 Tolerance: each output element within 1e-5 of the norm of the input pair it
 came from (x0·cos − x1·sin cancels, so a pure relative bound is meaningless
-near zero). Half outputs: ≤ 1 ulp against the f32 oracle rounded to nearest-even.
+near zero). Half outputs: ≤ 1 ulp against the f32 oracle rounded to
+nearest-even, or — where cancellation leaves |o| far below the pair norm, so
+that one f16 ulp of o is finer than the f32 computation itself (glibc's
+sinf/cosf are not correctly rounded; a 1-ulp sin/cos difference moves o by
+~1e-7) — within the f32 bound plus half an output ulp:
+|widen(got) − ref| ≤ 1e-5·|pair| + ½·ulp(ref).
 """
 import numpy as np
 import pytest
@@ -50,8 +55,20 @@ def _check(out: torch.Tensor, ref32: np.ndarray, x32: np.ndarray, rotary_dim, in
         err = np.where(got == ref32, 0.0, err)
         assert float(err.max()) <= TOL, f"{what}: max pair-relative err {float(err.max()):.3e}"
     else:
-        d = ulp_diff16(to_np(out), narrow_bits(ref32, out.dtype, orc), out.dtype)
-        assert int(d.max()) <= 1, f"{what}: max {int(d.max())} ulp"
+        got16, want16 = to_np(out), narrow_bits(ref32, out.dtype, orc)
+        d = ulp_diff16(got16, want16, out.dtype).reshape(ref32.shape)
+        got32 = widen(out, orc).reshape(ref32.shape).astype(np.float64)
+        mant = 10 if out.dtype == torch.float16 else 7
+        emin = -14 if out.dtype == torch.float16 else -126
+        e = np.floor(np.log2(np.maximum(np.abs(ref32.astype(np.float64)), 2.0 ** emin)))
+        half_ulp = 0.5 * 2.0 ** (e - mant)
+        bound = TOL * _pair_norm(x32, rotary_dim, interleaved) + half_ulp
+        ok = (d <= 1) | (np.abs(got32 - ref32) <= bound)
+        if not ok.all():
+            i = np.flatnonzero(~ok.reshape(-1))[:5]
+            raise AssertionError(f"{what}: {int((~ok).sum())} elements fail; first {i.tolist()}: "
+                                 f"got {got32.reshape(-1)[i]} want {ref32.reshape(-1)[i]} "
+                                 f"bound {bound.reshape(-1)[i]}")
 
 
 def _run(dev, orc, dtype, B, Hq, Hk, S, D, rd, base, positions, interleaved, pos_scale=1.0, seed=0):
