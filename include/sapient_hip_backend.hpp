@@ -1,0 +1,119 @@
+// sapient_hip_backend.hpp — C++ host-side mirror of sapient's LlmBackend op
+// surface on the MI355X kernels of sapient_hip.h.
+//
+// The reference trait (crates/sapient-models/src/forward/backend.rs:57-115)
+// takes host tensors and returns new host tensors; this class does the same —
+// upload, run the HIP kernels through the C ABI on its own stream, download —
+// with the reference's argument meaning, validation and error messages. It is
+// what a Rust `HipLlmBackend` wrapper does over FFI, written in C++ because the
+// reference is compiled code. There is no CPU fallback: a failed HIP call
+// raises sapient_hip::Error.
+#pragma once
+
+#include <cstddef>
+#include <cstdint>
+#include <mutex>
+#include <stdexcept>
+#include <string>
+#include <utility>
+#include <vector>
+
+#include "sapient_hip.h"
+
+namespace sapient_hip {
+
+// Tensor dtypes of the op set (values are GGUF type ids, as in sapient_hip.h).
+enum class DType : int { F32 = SPH_F32, F16 = SPH_F16, BF16 = SPH_BF16, Q8_0 = SPH_Q8_0, Q4_K = SPH_Q4_K, Q6_K = SPH_Q6_K };
+
+const char* dtype_name(DType dt);
+bool is_quantized(DType dt);
+// Bytes of `numel` elements (crates/sapient-core/src/dtype.rs:136-145).
+size_t byte_count(DType dt, size_t numel);
+
+class Error : public std::runtime_error {
+ public:
+    using std::runtime_error::runtime_error;
+};
+
+// A contiguous host tensor: shape, dtype and little-endian bytes — the data
+// model of sapient_core::Tensor (crates/sapient-core/src/tensor.rs:22-29).
+class Tensor {
+ public:
+    Tensor() = default;
+    static Tensor from_f32(const std::vector<float>& data, std::vector<size_t> shape);
+    static Tensor from_f16_bytes(std::vector<uint8_t> bytes, std::vector<size_t> shape);
+    static Tensor from_bf16_bytes(std::vector<uint8_t> bytes, std::vector<size_t> shape);
+    // Packed GGUF blocks; the byte count must equal byte_count(dt, numel)
+    // (tensor.rs:143-169).
+    static Tensor from_quant_bytes(std::vector<uint8_t> bytes, std::vector<size_t> shape, DType dt);
+
+    const std::vector<size_t>& shape() const { return shape_; }
+    DType dtype() const { return dtype_; }
+    size_t numel() const;
+    const std::vector<uint8_t>& bytes() const { return bytes_; }
+    // The values of an F32 tensor (as_f32_slice); throws for other dtypes.
+    std::vector<float> as_f32() const;
+
+ private:
+    Tensor(std::vector<size_t> shape, DType dt, std::vector<uint8_t> bytes)
+        : shape_(std::move(shape)), dtype_(dt), bytes_(std::move(bytes)) {}
+    std::vector<size_t> shape_;
+    DType dtype_ = DType::F32;
+    std::vector<uint8_t> bytes_;
+};
+
+class HipLlmBackend {
+ public:
+    // Binds the current HIP device and creates one stream (default priority).
+    HipLlmBackend();
+    ~HipLlmBackend();
+    HipLlmBackend(const HipLlmBackend&) = delete;
+    HipLlmBackend& operator=(const HipLlmBackend&) = delete;
+
+    // A gfx950 device is present and the library answers.
+    static bool is_available();
+    const char* name() const { return "hip"; }
+
+    // LlmBackend::rms_norm (backend.rs:72 → layernorm.rs:75-106): f32 output.
+    Tensor rms_norm(const Tensor& x, const Tensor& weight, float eps);
+    // LlmBackend::silu / gelu (elementwise.rs:141-143, :120-127): F32 input only.
+    Tensor silu(const Tensor& x);
+    Tensor gelu(const Tensor& x);
+    // LlmBackend::add / mul (elementwise.rs:27-69): same length or a length-1 side.
+    Tensor add(const Tensor& a, const Tensor& b);
+    Tensor mul(const Tensor& a, const Tensor& b);
+    // LlmBackend::apply_rope_positions (rope.rs:18-62): x [B, H, S, D].
+    Tensor apply_rope_positions(const Tensor& x, const std::vector<size_t>& positions, float base);
+    // LlmBackend::apply_rope_partial (rope.rs:71-78, :83-136).
+    Tensor apply_rope_partial(const Tensor& x, const std::vector<size_t>& positions, float base, size_t rotary_dim);
+
+    // Fused / layout extensions (default trait methods composing the above).
+    std::pair<Tensor, Tensor> add_rms_norm(const Tensor& x, const Tensor& residual, const Tensor& weight, float eps);
+    Tensor swiglu(const Tensor& gate, const Tensor& up);
+    Tensor apply_rope_interleaved(const Tensor& x, const std::vector<size_t>& positions, float base);
+
+    // common::embed_tokens (common.rs:164-179): weight [vocab, hidden] →
+    // [1, ids.size(), hidden] f32; an id >= vocab is an error.
+    Tensor embed_tokens(const Tensor& weight, const std::vector<uint32_t>& ids);
+
+ private:
+    struct DeviceBuf {
+        void* ptr = nullptr;
+        size_t bytes = 0;
+    };
+    DeviceBuf upload(const void* host, size_t bytes);
+    DeviceBuf alloc(size_t bytes);
+    void release(DeviceBuf& b);
+    void download(const DeviceBuf& b, void* host, size_t bytes);
+    Tensor f32_input(const Tensor& t) const;  // exact widening of f16/bf16 (tensor.rs:331-361)
+    Tensor binary(const Tensor& a, const Tensor& b, bool mul);
+    Tensor unary_f32(const Tensor& x, const char* op);
+    Tensor rope(const Tensor& x, const std::vector<size_t>& positions, float base, size_t rotary_dim, int layout,
+                bool partial);
+    void check(int status, const char* op) const;
+
+    void* stream_ = nullptr;
+    std::mutex mu_;
+};
+
+}  // namespace sapient_hip

@@ -1,8 +1,10 @@
 """Build the gfx950 shared library ``sapient_amd/libsapient_hip.so``.
 
-Each ``csrc/*.hip`` / ``csrc/*.cpp`` translation unit is compiled by hipcc
-(in parallel) into ``sapient_amd/_build/`` and linked into one shared library
-that exports the C ABI declared in ``include/sapient_hip.h``.
+Each ``csrc/*.hip`` / ``csrc/*.cpp`` kernel translation unit and the C++
+host layer (``host/*.cpp``) is compiled by hipcc (in parallel) into
+``sapient_amd/_build/`` and linked into one shared library that exports the C
+ABI declared in ``include/sapient_hip.h`` and the C++ API of
+``include/sapient_hip_backend.hpp``.
 
 Usage: ``python -m sapient_amd.build`` (or ``__graft_entry__.build()``).
 """
@@ -54,7 +56,7 @@ def hipcc() -> str:
 
 
 def sources() -> list[Path]:
-    return sorted(list(CSRC.glob("*.hip")) + list(CSRC.glob("*.cpp")))
+    return sorted(list(CSRC.glob("*.hip")) + list(CSRC.glob("*.cpp")) + list((PKG / "host").glob("*.cpp")))
 
 
 def _compile(src: Path) -> Path:

@@ -18,8 +18,9 @@
 //    so every store instruction writes 1 KiB contiguous (16 bytes per lane).
 //  - The packed blocks are read in place — no repacking. Q4_K: each step covers
 //    one 256-element super-block; a lane reads the 16-byte header (d, dmin,
-//    12 scale bytes; the same address for all lanes, one cache line) and the
-//    dword of nibbles it needs, and unpacks its (sc, m) pair in registers.
+//    12 scale bytes; wave-uniform, so a scalar load) and the dword of nibbles
+//    it needs, and unpacks its (sc, m) pair in registers. A row's loads are
+//    all issued before the first is consumed (16 super-blocks per batch).
 //  - Q8_0 / Q6_K blocks are 2-byte aligned only (34 / 210 bytes), so lanes read
 //    them in 16-bit pieces.
 //  - An id >= vocab zero-fills its row and raises `bad_id_flag`; the table is
@@ -104,12 +105,11 @@ __device__ __forceinline__ void dequant4<SPH_Q6_K>(const uint8_t* __restrict__ r
     }
 }
 
-// Q4_K: a lane handles elements [4l, 4l + 4) of super-block `blk`, l = lane.
-__device__ __forceinline__ void dequant_q4k_lane(const uint8_t* __restrict__ row, int blk, int lane, float (&o)[4]) {
-    const uint8_t* b = row + blk * 144;
-    const u32x4 hdr = *reinterpret_cast<const u32x4*>(b);  // d, dmin, scales[0..12)
+// Q4_K: a lane handles elements [4l, 4l + 4) of a super-block, l = lane.
+// `hdr` is the block's first 16 bytes (d, dmin, scales[0..12)), `qw` the
+// dword of nibbles this lane needs.
+__device__ __forceinline__ void dequant_q4k_lane(const u32x4 hdr, uint32_t qw, int lane, float (&o)[4]) {
     const int sb = lane >> 3;            // 32-element sub-block 0..7
-    const uint32_t qw = reinterpret_cast<const uint32_t*>(b + 16 + 32 * (sb >> 1))[lane & 7];
     const float d = widen(f16{(uint16_t)hdr.x});
     const float dmin = widen(f16{(uint16_t)(hdr.x >> 16)});
     const int k = sb & 3, sh = 8 * k;
@@ -131,6 +131,11 @@ __device__ __forceinline__ void dequant_q4k_lane(const uint8_t* __restrict__ row
     for (int c = 0; c < 4; ++c) o[c] = __builtin_fmaf(d1, (float)((nib >> (8 * c)) & 0xFF), -m1);
 }
 
+// Super-blocks of one Q4_K row handled per batch: all their loads are issued
+// before any is consumed, so a wave has 2 x kQ4kBatch requests in flight
+// instead of one dependent load per step.
+constexpr int kQ4kBatch = 16;
+
 template <int DT>
 __global__ __launch_bounds__(kThreads) void embed_rows(const uint8_t* __restrict__ table, int64_t vocab,
                                                        int hidden, int64_t row_bytes, const uint32_t* __restrict__ ids,
@@ -138,7 +143,9 @@ __global__ __launch_bounds__(kThreads) void embed_rows(const uint8_t* __restrict
     const int lane = threadIdx.x & (kWave - 1);
     const int64_t t = (int64_t)blockIdx.x * kTokPerBlock + (threadIdx.x / kWave);
     if (t >= n_ids) return;
-    const uint32_t id = ids[t];
+    // The token is wave-uniform: broadcast its id so the row base (and every
+    // block header address) lives in scalar registers.
+    const uint32_t id = __builtin_amdgcn_readfirstlane(ids[t]);
     float* dst = out + (size_t)t * (size_t)hidden;
     const int n4 = hidden / 4;
     if ((int64_t)id >= vocab) {
@@ -149,10 +156,26 @@ __global__ __launch_bounds__(kThreads) void embed_rows(const uint8_t* __restrict
     const uint8_t* row = table + (size_t)id * (size_t)row_bytes;
     if constexpr (DT == SPH_Q4_K) {
         const int nblk = hidden / 256;
-        for (int blk = 0; blk < nblk; ++blk) {
-            float o[4];
-            dequant_q4k_lane(row, blk, lane, o);
-            store4(dst + 256 * blk + 4 * lane, o[0], o[1], o[2], o[3]);
+        const int qoff = 16 + 32 * (lane >> 4) + 4 * (lane & 7);  // this lane's nibble dword in a block
+        for (int b0 = 0; b0 < nblk; b0 += kQ4kBatch) {
+            u32x4 hdr[kQ4kBatch];
+            uint32_t qw[kQ4kBatch];
+#pragma unroll
+            for (int j = 0; j < kQ4kBatch; ++j) {
+                if (b0 + j < nblk) {
+                    const uint8_t* b = row + (size_t)(b0 + j) * 144;
+                    hdr[j] = *reinterpret_cast<const u32x4*>(b);
+                    qw[j] = *reinterpret_cast<const uint32_t*>(b + qoff);
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < kQ4kBatch; ++j) {
+                if (b0 + j < nblk) {
+                    float o[4];
+                    dequant_q4k_lane(hdr[j], qw[j], lane, o);
+                    store4(dst + 256 * (b0 + j) + 4 * lane, o[0], o[1], o[2], o[3]);
+                }
+            }
         }
     } else {
         for (int e4 = lane; e4 < n4; e4 += kWave) {

@@ -1,0 +1,374 @@
+// hip_llm_backend.cpp — the C++ host-side mirror of sapient's LlmBackend op
+// surface (crates/sapient-models/src/forward/backend.rs:57-115) over the C ABI.
+//
+// Each op uploads its host inputs, runs the HIP kernels on this backend's
+// stream, waits, and downloads a new host tensor — the round trip the
+// reference's MLX backend makes per op (backend.rs:520-600). Weights are
+// uploaded per call too: a host tensor's address can be reused once it is
+// freed, so caching by pointer (as the MLX backend does, backend.rs:483-508,
+// where Arc lifetimes make it safe) would risk a stale device copy here.
+// Output dtypes, validation and error messages follow the reference's CPU
+// kernels.
+#include "sapient_hip_backend.hpp"
+
+#include <hip/hip_runtime.h>
+
+#include <cstring>
+#include <string>
+
+namespace sapient_hip {
+
+const char* dtype_name(DType dt) {
+    switch (dt) {
+    case DType::F32: return "f32";
+    case DType::F16: return "f16";
+    case DType::BF16: return "bf16";
+    case DType::Q8_0: return "q8_0";
+    case DType::Q4_K: return "q4_k";
+    case DType::Q6_K: return "q6_k";
+    }
+    return "?";
+}
+
+bool is_quantized(DType dt) { return dt == DType::Q8_0 || dt == DType::Q4_K || dt == DType::Q6_K; }
+
+size_t byte_count(DType dt, size_t numel) {
+    switch (dt) {
+    case DType::F32: return numel * 4;
+    case DType::F16:
+    case DType::BF16: return numel * 2;
+    case DType::Q8_0: return numel / 32 * 34;
+    case DType::Q4_K: return numel / 256 * 144;
+    case DType::Q6_K: return numel / 256 * 210;
+    }
+    return 0;
+}
+
+static size_t product(const std::vector<size_t>& s) {
+    size_t n = 1;
+    for (size_t d : s) n *= d;
+    return n;
+}
+
+static std::string shape_str(const std::vector<size_t>& s) {
+    std::string r = "[";
+    for (size_t i = 0; i < s.size(); ++i) r += (i ? ", " : "") + std::to_string(s[i]);
+    return r + "]";
+}
+
+// ─────────────────────────────── Tensor ───────────────────────────────
+size_t Tensor::numel() const { return product(shape_); }
+
+Tensor Tensor::from_f32(const std::vector<float>& data, std::vector<size_t> shape) {
+    if (product(shape) != data.size())
+        throw Error("shape mismatch: expected " + std::to_string(product(shape)) + " elements, got " +
+                    std::to_string(data.size()));
+    std::vector<uint8_t> b(data.size() * 4);
+    if (!data.empty()) std::memcpy(b.data(), data.data(), b.size());
+    return Tensor(std::move(shape), DType::F32, std::move(b));
+}
+
+Tensor Tensor::from_f16_bytes(std::vector<uint8_t> bytes, std::vector<size_t> shape) {
+    if (bytes.size() != product(shape) * 2)
+        throw Error("shape mismatch: expected " + std::to_string(product(shape) * 2) + " bytes, got " +
+                    std::to_string(bytes.size()));
+    return Tensor(std::move(shape), DType::F16, std::move(bytes));
+}
+
+Tensor Tensor::from_bf16_bytes(std::vector<uint8_t> bytes, std::vector<size_t> shape) {
+    if (bytes.size() != product(shape) * 2)
+        throw Error("shape mismatch: expected " + std::to_string(product(shape) * 2) + " bytes, got " +
+                    std::to_string(bytes.size()));
+    return Tensor(std::move(shape), DType::BF16, std::move(bytes));
+}
+
+Tensor Tensor::from_quant_bytes(std::vector<uint8_t> bytes, std::vector<size_t> shape, DType dt) {
+    if (!is_quantized(dt))
+        throw Error(std::string("type mismatch: expected a quantized dtype (Q8_0, Q4_K, Q6_K), got ") + dtype_name(dt));
+    const size_t expected = byte_count(dt, product(shape));
+    if (bytes.size() != expected)
+        throw Error("shape mismatch: expected " + std::to_string(expected) + " bytes, got " + std::to_string(bytes.size()));
+    return Tensor(std::move(shape), dt, std::move(bytes));
+}
+
+std::vector<float> Tensor::as_f32() const {
+    if (dtype_ != DType::F32) throw Error(std::string("type mismatch: expected f32, got ") + dtype_name(dtype_));
+    std::vector<float> v(numel());
+    if (!v.empty()) std::memcpy(v.data(), bytes_.data(), v.size() * 4);
+    return v;
+}
+
+// ─────────────────────────────── backend ───────────────────────────────
+static void hip_ok(hipError_t e, const char* what) {
+    if (e != hipSuccess) throw Error(std::string("hip: ") + what + ": " + hipGetErrorString(e));
+}
+
+bool HipLlmBackend::is_available() {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n == 0) return false;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return false;
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, dev) != hipSuccess) return false;
+    return std::strncmp(prop.gcnArchName, "gfx950", 6) == 0 && sph_abi_version() == SPH_ABI_VERSION;
+}
+
+HipLlmBackend::HipLlmBackend() {
+    if (!is_available()) throw Error("hip: no gfx950 device available");
+    hipStream_t s = nullptr;
+    hip_ok(hipStreamCreate(&s), "stream create");  // default priority
+    stream_ = s;
+}
+
+HipLlmBackend::~HipLlmBackend() {
+    if (stream_) (void)hipStreamDestroy(static_cast<hipStream_t>(stream_));
+}
+
+void HipLlmBackend::check(int status, const char* op) const {
+    if (status != SPH_OK)
+        throw Error(std::string("hip backend: ") + op + ": " + sph_status_string(status) + " (" +
+                    std::to_string(status) + ")");
+}
+
+HipLlmBackend::DeviceBuf HipLlmBackend::alloc(size_t bytes) {
+    DeviceBuf b;
+    b.bytes = bytes;
+    hip_ok(hipMalloc(&b.ptr, bytes ? bytes : 16), "malloc");
+    return b;
+}
+
+HipLlmBackend::DeviceBuf HipLlmBackend::upload(const void* host, size_t bytes) {
+    DeviceBuf b = alloc(bytes);
+    if (bytes) hip_ok(hipMemcpyAsync(b.ptr, host, bytes, hipMemcpyHostToDevice, static_cast<hipStream_t>(stream_)), "upload");
+    return b;
+}
+
+void HipLlmBackend::download(const DeviceBuf& b, void* host, size_t bytes) {
+    if (bytes) hip_ok(hipMemcpyAsync(host, b.ptr, bytes, hipMemcpyDeviceToHost, static_cast<hipStream_t>(stream_)), "download");
+    hip_ok(hipStreamSynchronize(static_cast<hipStream_t>(stream_)), "synchronize");
+}
+
+void HipLlmBackend::release(DeviceBuf& b) {
+    if (b.ptr) (void)hipFree(b.ptr);
+    b.ptr = nullptr;
+}
+
+// Tensor::to_f32_cow for the float dtypes (tensor.rs:331-361): exact widening.
+Tensor HipLlmBackend::f32_input(const Tensor& t) const {
+    if (t.dtype() == DType::F32) return t;
+    if (t.dtype() != DType::F16 && t.dtype() != DType::BF16)
+        throw Error(std::string("type mismatch: expected a float tensor, got ") + dtype_name(t.dtype()));
+    std::vector<float> v(t.numel());
+    const uint8_t* b = t.bytes().data();
+    for (size_t i = 0; i < v.size(); ++i) {
+        const uint16_t h = (uint16_t)(b[2 * i] | (b[2 * i + 1] << 8));
+        uint32_t u;
+        if (t.dtype() == DType::BF16) {
+            u = (uint32_t)((h & 0x7FFFu) > 0x7F80u ? (h | 0x40u) : h) << 16;
+        } else {
+            const uint32_t sign = (uint32_t)(h & 0x8000u) << 16, exp = (h >> 10) & 0x1Fu, man = h & 0x3FFu;
+            if (exp == 0x1F) {
+                u = sign | 0x7F800000u | (man ? 0x400000u | (man << 13) : 0u);
+            } else if (exp == 0) {
+                float f = (float)man * 0x1p-24f;
+                std::memcpy(&u, &f, 4);
+                u |= sign;
+            } else {
+                u = sign | ((exp + 112u) << 23) | (man << 13);
+            }
+        }
+        std::memcpy(&v[i], &u, 4);
+    }
+    return Tensor::from_f32(v, t.shape());
+}
+
+Tensor HipLlmBackend::rms_norm(const Tensor& x, const Tensor& weight_t, float eps) {
+    std::lock_guard<std::mutex> lock(mu_);
+    const auto& s = x.shape();
+    const size_t dim = s.empty() ? 1 : s.back();
+    const size_t rows = dim ? x.numel() / dim : 0;
+    if (x.dtype() != DType::F32 && x.dtype() != DType::F16 && x.dtype() != DType::BF16)
+        throw Error(std::string("type mismatch: expected a float tensor, got ") + dtype_name(x.dtype()));
+    // The device kernel takes an f32 weight or one of x's type (widened exactly on the host otherwise).
+    const Tensor wt = (weight_t.dtype() == DType::F32 || weight_t.dtype() == x.dtype()) ? weight_t : f32_input(weight_t);
+    if (wt.numel() != dim) throw Error("shape mismatch: weight " + shape_str(wt.shape()) + " for rows of " + std::to_string(dim));
+    DeviceBuf xd = upload(x.bytes().data(), x.bytes().size());
+    DeviceBuf wd = upload(wt.bytes().data(), wt.bytes().size());
+    DeviceBuf od = alloc(x.numel() * 4);
+    const int st = sph_rms_norm(xd.ptr, (int)x.dtype(), wd.ptr, (int)wt.dtype(), od.ptr, SPH_F32, (int64_t)rows,
+                                (int64_t)dim, eps, stream_);
+    std::vector<float> out(x.numel());
+    if (st == SPH_OK) download(od, out.data(), out.size() * 4);
+    release(xd);
+    release(wd);
+    release(od);
+    check(st, "rms_norm");
+    return Tensor::from_f32(out, s);
+}
+
+std::pair<Tensor, Tensor> HipLlmBackend::add_rms_norm(const Tensor& x, const Tensor& residual, const Tensor& weight_t,
+                                                      float eps) {
+    const Tensor xf = f32_input(x), rf = f32_input(residual);
+    if (xf.shape() != rf.shape())
+        throw Error("shape mismatch: " + shape_str(xf.shape()) + " vs " + shape_str(rf.shape()));
+    std::lock_guard<std::mutex> lock(mu_);
+    const size_t dim = xf.shape().empty() ? 1 : xf.shape().back();
+    const size_t rows = dim ? xf.numel() / dim : 0;
+    const Tensor wt = weight_t.dtype() == DType::F32 ? weight_t : f32_input(weight_t);
+    if (wt.numel() != dim) throw Error("shape mismatch: weight " + shape_str(wt.shape()) + " for rows of " + std::to_string(dim));
+    DeviceBuf xd = upload(xf.bytes().data(), xf.bytes().size());
+    DeviceBuf rd = upload(rf.bytes().data(), rf.bytes().size());
+    DeviceBuf wd = upload(wt.bytes().data(), wt.bytes().size());
+    DeviceBuf od = alloc(xf.numel() * 4);
+    const int st = sph_add_rms_norm(xd.ptr, rd.ptr, SPH_F32, wd.ptr, SPH_F32, od.ptr, SPH_F32, (int64_t)rows,
+                                    (int64_t)dim, eps, stream_);
+    std::vector<float> normed(xf.numel()), sum(xf.numel());
+    if (st == SPH_OK) {
+        download(od, normed.data(), normed.size() * 4);
+        download(rd, sum.data(), sum.size() * 4);
+    }
+    release(xd);
+    release(rd);
+    release(wd);
+    release(od);
+    check(st, "add_rms_norm");
+    return {Tensor::from_f32(normed, xf.shape()), Tensor::from_f32(sum, xf.shape())};
+}
+
+// binary_f32 (elementwise.rs:27-57): both sides widened to f32; same length or
+// a length-1 side broadcast; anything else is a ShapeMismatch.
+Tensor HipLlmBackend::binary(const Tensor& a0, const Tensor& b0, bool mul) {
+    const Tensor a = f32_input(a0), b = f32_input(b0);
+    const size_t na = a.numel(), nb = b.numel();
+    if (!(na == nb || nb == 1 || na == 1))
+        throw Error("shape mismatch: expected " + shape_str(a.shape()) + ", got " + shape_str(b.shape()));
+    const std::vector<size_t> shape = (na == nb || nb == 1) ? a.shape() : b.shape();
+    const size_t n = (na == nb || nb == 1) ? na : nb;
+    std::lock_guard<std::mutex> lock(mu_);
+    DeviceBuf ad = upload(a.bytes().data(), a.bytes().size());
+    DeviceBuf bd = upload(b.bytes().data(), b.bytes().size());
+    DeviceBuf od = alloc(n * 4);
+    const int st = mul ? sph_mul(ad.ptr, (int64_t)na, bd.ptr, (int64_t)nb, od.ptr, SPH_F32, stream_)
+                       : sph_add(ad.ptr, (int64_t)na, bd.ptr, (int64_t)nb, od.ptr, SPH_F32, stream_);
+    std::vector<float> out(n);
+    if (st == SPH_OK) download(od, out.data(), n * 4);
+    release(ad);
+    release(bd);
+    release(od);
+    check(st, mul ? "mul" : "add");
+    return Tensor::from_f32(out, shape);
+}
+
+Tensor HipLlmBackend::add(const Tensor& a, const Tensor& b) { return binary(a, b, false); }
+Tensor HipLlmBackend::mul(const Tensor& a, const Tensor& b) { return binary(a, b, true); }
+
+// unary_f32 (elementwise.rs:15-24): only F32 input is accepted.
+Tensor HipLlmBackend::unary_f32(const Tensor& x, const char* op) {
+    if (x.dtype() != DType::F32) throw Error(std::string("type mismatch: expected f32, got ") + dtype_name(x.dtype()));
+    std::lock_guard<std::mutex> lock(mu_);
+    DeviceBuf xd = upload(x.bytes().data(), x.bytes().size());
+    DeviceBuf od = alloc(x.numel() * 4);
+    const int st = std::strcmp(op, "silu") == 0 ? sph_silu(xd.ptr, od.ptr, SPH_F32, (int64_t)x.numel(), stream_)
+                                                 : sph_gelu_tanh(xd.ptr, od.ptr, SPH_F32, (int64_t)x.numel(), stream_);
+    std::vector<float> out(x.numel());
+    if (st == SPH_OK) download(od, out.data(), out.size() * 4);
+    release(xd);
+    release(od);
+    check(st, op);
+    return Tensor::from_f32(out, x.shape());
+}
+
+Tensor HipLlmBackend::silu(const Tensor& x) { return unary_f32(x, "silu"); }
+Tensor HipLlmBackend::gelu(const Tensor& x) { return unary_f32(x, "gelu"); }
+
+Tensor HipLlmBackend::swiglu(const Tensor& gate, const Tensor& up) {
+    if (gate.dtype() != DType::F32 || up.dtype() != DType::F32)
+        throw Error(std::string("type mismatch: expected f32, got ") + dtype_name(gate.dtype() != DType::F32 ? gate.dtype() : up.dtype()));
+    if (gate.numel() != up.numel())
+        throw Error("shape mismatch: expected " + shape_str(gate.shape()) + ", got " + shape_str(up.shape()));
+    std::lock_guard<std::mutex> lock(mu_);
+    DeviceBuf gd = upload(gate.bytes().data(), gate.bytes().size());
+    DeviceBuf ud = upload(up.bytes().data(), up.bytes().size());
+    DeviceBuf od = alloc(gate.numel() * 4);
+    const int st = sph_swiglu(gd.ptr, ud.ptr, od.ptr, SPH_F32, (int64_t)gate.numel(), stream_);
+    std::vector<float> out(gate.numel());
+    if (st == SPH_OK) download(od, out.data(), out.size() * 4);
+    release(gd);
+    release(ud);
+    release(od);
+    check(st, "swiglu");
+    return Tensor::from_f32(out, gate.shape());
+}
+
+// rope.rs:18-62 / :83-136: x [batch, n_heads, seq_len, head_dim] → new f32 tensor.
+Tensor HipLlmBackend::rope(const Tensor& x0, const std::vector<size_t>& positions, float base, size_t rotary_dim,
+                           int layout, bool partial) {
+    const auto& d = x0.shape();
+    if (d.size() != 4) throw Error("rank mismatch: expected 4, got " + std::to_string(d.size()));
+    const size_t batch = d[0], n_heads = d[1], seq = d[2], head_dim = d[3];
+    if (partial) {
+        if (rotary_dim == 0 || rotary_dim > head_dim) throw Error("rotary_dim must be in 1..=head_dim");
+        if (rotary_dim % 2 != 0) throw Error("RoPE requires even rotary_dim");
+    } else if (head_dim % 2 != 0) {
+        throw Error("RoPE requires even head_dim");
+    }
+    if (positions.size() != seq) throw Error("positions length must match seq_len");
+    std::vector<int32_t> pos(seq);
+    for (size_t i = 0; i < seq; ++i) {
+        if (positions[i] > (size_t)INT32_MAX) throw Error("position out of the supported range (< 2^31)");
+        pos[i] = (int32_t)positions[i];
+    }
+    const Tensor x = f32_input(x0);
+    std::lock_guard<std::mutex> lock(mu_);
+    DeviceBuf xd = upload(x.bytes().data(), x.bytes().size());
+    DeviceBuf pd = upload(pos.data(), pos.size() * 4);
+    const int st = sph_rope(xd.ptr, (int64_t)n_heads, nullptr, 0, SPH_F32, layout, static_cast<const int32_t*>(pd.ptr),
+                            (int64_t)batch, (int64_t)seq, (int64_t)head_dim, (int64_t)rotary_dim, base, 1.0f, stream_);
+    std::vector<float> out(x.numel());
+    if (st == SPH_OK) download(xd, out.data(), out.size() * 4);
+    release(xd);
+    release(pd);
+    check(st, "rope");
+    return Tensor::from_f32(out, d);
+}
+
+Tensor HipLlmBackend::apply_rope_positions(const Tensor& x, const std::vector<size_t>& positions, float base) {
+    const size_t head_dim = x.shape().size() == 4 ? x.shape()[3] : 0;
+    return rope(x, positions, base, head_dim, SPH_ROPE_NEOX, false);
+}
+
+Tensor HipLlmBackend::apply_rope_partial(const Tensor& x, const std::vector<size_t>& positions, float base,
+                                         size_t rotary_dim) {
+    return rope(x, positions, base, rotary_dim, SPH_ROPE_NEOX, true);
+}
+
+Tensor HipLlmBackend::apply_rope_interleaved(const Tensor& x, const std::vector<size_t>& positions, float base) {
+    const size_t head_dim = x.shape().size() == 4 ? x.shape()[3] : 0;
+    return rope(x, positions, base, head_dim, SPH_ROPE_INTERLEAVED, false);
+}
+
+// common.rs:164-217: every id is checked against vocab before any row is read.
+Tensor HipLlmBackend::embed_tokens(const Tensor& w, const std::vector<uint32_t>& ids) {
+    const auto& d = w.shape();
+    if (d.size() != 2) throw Error("embedding table must be [vocab, hidden], got " + shape_str(d));
+    const size_t vocab = d[0], hidden = d[1];
+    for (uint32_t id : ids)
+        if ((size_t)id >= vocab) throw Error("token id " + std::to_string(id) + " out of vocab range");
+    std::lock_guard<std::mutex> lock(mu_);
+    DeviceBuf td = upload(w.bytes().data(), w.bytes().size());
+    DeviceBuf idd = upload(ids.data(), ids.size() * 4);
+    DeviceBuf od = alloc(ids.size() * hidden * 4);
+    const int st = sph_embed(td.ptr, (int)w.dtype(), (int64_t)vocab, (int64_t)hidden,
+                             static_cast<const uint32_t*>(idd.ptr), (int64_t)ids.size(), static_cast<float*>(od.ptr),
+                             nullptr, stream_);
+    std::vector<float> out(ids.size() * hidden);
+    if (st == SPH_OK) download(od, out.data(), out.size() * 4);
+    release(td);
+    release(idd);
+    release(od);
+    if (st == SPH_EINVAL) throw Error(std::string("unsupported embedding dtype ") + dtype_name(w.dtype()));
+    check(st, "embed_tokens");
+    return Tensor::from_f32(out, {1, ids.size(), hidden});
+}
+
+}  // namespace sapient_hip

@@ -1,0 +1,29 @@
+"""Builds the native test programs of tests/native/ into tests/native/_build/:
+
+- test_hip_llm_backend: GPU tests of the C++ LlmBackend mirror, linked against the
+  in-tree libsapient_hip.so (rpath relative to the binary, so the tree can move);
+- check_glibc_tanhf: the host-side exhaustive check of glibc_tanhf.h.
+"""
+import shutil
+import subprocess
+from pathlib import Path
+
+HERE = Path(__file__).resolve().parent
+ROOT = HERE.parents[1]
+OUT = HERE / "_build"
+
+
+def build() -> None:
+    gxx = shutil.which("g++") or "g++"
+    OUT.mkdir(exist_ok=True)
+    subprocess.run([gxx, "-std=c++17", "-O1", "-Wall", f"-I{ROOT / 'include'}", str(HERE / "test_hip_llm_backend.cpp"),
+                    "-o", str(OUT / "test_hip_llm_backend"), f"-L{ROOT / 'sapient_amd'}", "-lsapient_hip",
+                    "-Wl,-rpath,$ORIGIN/../../../sapient_amd", "-Wl,-rpath,/opt/rocm/lib"], check=True)
+    subprocess.run([gxx, "-O2", "-std=c++17", "-ffp-contract=off", "-fno-fast-math", "-D__HIP_PLATFORM_AMD__",
+                    "-I/opt/rocm/include", f"-I{ROOT / 'sapient_amd' / 'csrc'}", f"-I{ROOT / 'include'}",
+                    str(HERE / "check_glibc_tanhf.cpp"), "-o", str(OUT / "check_glibc_tanhf"), "-lpthread", "-lm"],
+                   check=True)
+
+
+if __name__ == "__main__":
+    build()

@@ -1,0 +1,303 @@
+// GPU tests of the C++ LlmBackend mirror (include/sapient_hip_backend.hpp),
+// written after the reference's own unit tests so they read the same way:
+//   layernorm.rs:113-149, elementwise.rs:176-232, rope.rs:155-206,
+//   common.rs:669-718, and the trait's validation errors (rope.rs:19-35,
+//   elementwise.rs:15-21, common.rs:171-173).
+// Prints "test <name> ... ok|FAILED: <why>" per test; exits 1 if any failed.
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <functional>
+#include <string>
+#include <vector>
+
+#include "sapient_hip_backend.hpp"
+
+using sapient_hip::DType;
+using sapient_hip::Error;
+using sapient_hip::HipLlmBackend;
+using sapient_hip::Tensor;
+
+struct Failure {
+    std::string why;
+};
+
+#define ASSERT(cond, msg) \
+    do {                  \
+        if (!(cond)) throw Failure{std::string(msg) + " [" #cond "]"}; \
+    } while (0)
+
+template <typename F>
+static std::string expect_error(F&& f) {
+    try {
+        f();
+    } catch (const Error& e) {
+        return e.what();
+    }
+    throw Failure{"expected an error"};
+}
+
+// ── helpers the reference tests use ──────────────────────────────────────────
+static uint16_t f16_from_f32(float f) {  // half::f16::from_f32 (nearest-even)
+    uint32_t x;
+    std::memcpy(&x, &f, 4);
+    const uint32_t sign = (x >> 16) & 0x8000u, exp = (x >> 23) & 0xFFu, man = x & 0x7FFFFFu;
+    if (exp == 0xFF) return (uint16_t)(sign | 0x7C00u | (man ? 0x200u | (man >> 13) : 0u));
+    const int e = (int)exp - 112;
+    if (e >= 0x1F) return (uint16_t)(sign | 0x7C00u);
+    if (e <= 0) {
+        if (e < -10) return (uint16_t)sign;
+        const uint32_t m = man | 0x800000u, sh = (uint32_t)(14 - e);
+        uint32_t h = m >> sh;
+        const uint32_t rb = 1u << (sh - 1);
+        if ((m & rb) && ((m & (rb - 1)) || (h & 1))) ++h;
+        return (uint16_t)(sign | h);
+    }
+    uint32_t h = sign | ((uint32_t)e << 10) | (man >> 13);
+    if ((man & 0x1000u) && (man & 0x2FFFu)) ++h;
+    return (uint16_t)h;
+}
+
+static float f16_to_f32(uint16_t h) {
+    const uint32_t sign = (uint32_t)(h & 0x8000u) << 16, exp = (h >> 10) & 0x1Fu, man = h & 0x3FFu;
+    uint32_t u;
+    if (exp == 0x1F) u = sign | 0x7F800000u | (man << 13);
+    else if (exp == 0) {
+        float f = (float)man * 0x1p-24f;
+        std::memcpy(&u, &f, 4);
+        u |= sign;
+    } else u = sign | ((exp + 112u) << 23) | (man << 13);
+    float f;
+    std::memcpy(&f, &u, 4);
+    return f;
+}
+
+// quantize_q8_0_block (crates/sapient-backends/cpu/src/kernels/quant.rs:223-235)
+static std::vector<uint8_t> quantize_q8_0(const std::vector<float>& x) {
+    std::vector<uint8_t> out;
+    for (size_t b = 0; b < x.size() / 32; ++b) {
+        float max_abs = 0.0f;
+        for (int i = 0; i < 32; ++i) max_abs = std::fmax(max_abs, std::fabs(x[b * 32 + i]));
+        const float scale = max_abs / 127.0f;
+        const uint16_t d = f16_from_f32(scale);
+        const float inv = scale > 0.0f ? 1.0f / scale : 0.0f;
+        out.push_back((uint8_t)(d & 0xFF));
+        out.push_back((uint8_t)(d >> 8));
+        for (int i = 0; i < 32; ++i) {
+            float q = std::round(x[b * 32 + i] * inv);
+            q = q < -127.0f ? -127.0f : (q > 127.0f ? 127.0f : q);
+            out.push_back((uint8_t)(int8_t)q);
+        }
+    }
+    return out;
+}
+
+// ── tests ────────────────────────────────────────────────────────────────────
+static void rmsnorm_identity_weight(HipLlmBackend& bk) {  // layernorm.rs:125-149
+    const Tensor x = Tensor::from_f32({3.0f, 4.0f}, {1, 2});
+    const Tensor w = Tensor::from_f32({1.0f, 1.0f}, {2});
+    const std::vector<float> d = bk.rms_norm(x, w, 0.0f).as_f32();
+    const float e0 = 3.0f / std::sqrt(12.5f), e1 = 4.0f / std::sqrt(12.5f);
+    ASSERT(std::fabs(d[0] - e0) < 1e-5f && std::fabs(d[1] - e1) < 1e-5f, "rms_norm [3,4]");
+}
+
+static void rmsnorm_half_input_outputs_f32(HipLlmBackend& bk) {  // to_f32_cow upcast, f32 result
+    std::vector<uint8_t> b;
+    for (float v : {3.0f, 4.0f}) {
+        const uint16_t h = f16_from_f32(v);
+        b.push_back((uint8_t)(h & 0xFF));
+        b.push_back((uint8_t)(h >> 8));
+    }
+    const Tensor y = bk.rms_norm(Tensor::from_f16_bytes(b, {1, 2}), Tensor::from_f32({1.0f, 1.0f}, {2}), 0.0f);
+    ASSERT(y.dtype() == DType::F32, "f32 output");
+    ASSERT(std::fabs(y.as_f32()[1] - 4.0f / std::sqrt(12.5f)) < 1e-5f, "value");
+}
+
+static void test_add(HipLlmBackend& bk) {  // elementwise.rs:184-194
+    const std::vector<float> r = bk.add(Tensor::from_f32({1.0f, 2.0f}, {2}), Tensor::from_f32({3.0f, 4.0f}, {2})).as_f32();
+    ASSERT(std::fabs(r[0] - 4.0f) < 1e-6f && r[1] == 6.0f, "add");
+}
+
+static void test_scalar_broadcast(HipLlmBackend& bk) {  // elementwise.rs:225-231
+    const Tensor a = Tensor::from_f32({1.0f, 2.0f, 3.0f}, {3});
+    const Tensor b = Tensor::from_f32({2.0f}, {1});
+    ASSERT(bk.mul(a, b).as_f32() == std::vector<float>({2.0f, 4.0f, 6.0f}), "mul broadcast b");
+    ASSERT(bk.mul(b, a).as_f32() == std::vector<float>({2.0f, 4.0f, 6.0f}), "mul broadcast a");
+    const std::string e = expect_error([&] { bk.add(a, Tensor::from_f32({1.0f, 2.0f}, {2})); });
+    ASSERT(e.find("shape mismatch") != std::string::npos, "mismatch error");
+}
+
+static void test_gelu(HipLlmBackend& bk) {  // elementwise.rs:206-210
+    ASSERT(std::fabs(bk.gelu(Tensor::from_f32({0.0f}, {1})).as_f32()[0]) < 1e-5f, "gelu(0)");
+}
+
+static void test_silu_and_swiglu(HipLlmBackend& bk) {  // silu(0) = 0, silu(x) = x·sigmoid(x)
+    const std::vector<float> s = bk.silu(Tensor::from_f32({0.0f, 1.0f, -2.0f}, {3})).as_f32();
+    ASSERT(s[0] == 0.0f, "silu(0)");
+    ASSERT(std::fabs(s[1] - 1.0f / (1.0f + std::exp(-1.0f))) < 1e-6f, "silu(1)");
+    ASSERT(std::fabs(s[2] + 2.0f / (1.0f + std::exp(2.0f))) < 1e-6f, "silu(-2)");
+    const Tensor g = Tensor::from_f32({0.5f, -1.5f, 3.0f}, {3});
+    const Tensor u = Tensor::from_f32({2.0f, 0.25f, -1.0f}, {3});
+    const std::vector<float> sw = bk.swiglu(g, u).as_f32();
+    const std::vector<float> composed = bk.mul(bk.silu(g), u).as_f32();
+    ASSERT(sw == composed, "swiglu == mul(silu(g), u) bit for bit");
+}
+
+static void unary_rejects_non_f32(HipLlmBackend& bk) {  // elementwise.rs:15-21
+    const Tensor h = Tensor::from_f16_bytes({0, 0, 0, 0}, {2});
+    ASSERT(expect_error([&] { bk.silu(h); }).find("type mismatch") != std::string::npos, "silu");
+    ASSERT(expect_error([&] { bk.gelu(h); }).find("type mismatch") != std::string::npos, "gelu");
+}
+
+static void rope_output_shape(HipLlmBackend& bk) {  // rope.rs:159-165
+    const Tensor x = Tensor::from_f32(std::vector<float>(64, 0.1f), {1, 2, 4, 8});
+    ASSERT(bk.apply_rope_positions(x, {0, 1, 2, 3}, 10000.0f).shape() == std::vector<size_t>({1, 2, 4, 8}), "shape");
+}
+
+static void rope_partial_leaves_tail_unchanged(HipLlmBackend& bk) {  // rope.rs:167-181
+    std::vector<float> data;
+    for (int v = 1; v <= 8; ++v) data.push_back((float)v);
+    const std::vector<float> o = bk.apply_rope_partial(Tensor::from_f32(data, {1, 1, 1, 8}), {3}, 10000.0f, 4).as_f32();
+    for (int i = 4; i < 8; ++i) ASSERT(std::fabs(o[i] - data[i]) < 1e-6f, "tail channel changed");
+    bool any = false;
+    for (int i = 0; i < 4; ++i) any |= std::fabs(o[i] - data[i]) > 1e-6f;
+    ASSERT(any, "rotary channels changed");
+}
+
+static void rope_partial_full_matches_apply_rope(HipLlmBackend& bk) {  // rope.rs:183-193
+    std::vector<float> data;
+    for (int v = 0; v < 16; ++v) data.push_back((float)v * 0.1f);
+    const Tensor x = Tensor::from_f32(data, {1, 1, 2, 8});
+    const std::vector<float> full = bk.apply_rope_positions(x, {2, 5}, 10000.0f).as_f32();
+    const std::vector<float> part = bk.apply_rope_partial(x, {2, 5}, 10000.0f, 8).as_f32();
+    for (size_t i = 0; i < full.size(); ++i) ASSERT(std::fabs(full[i] - part[i]) < 1e-6f, "partial == full");
+}
+
+static void rope_position_zero_is_identity(HipLlmBackend& bk) {  // rope.rs:195-205
+    const std::vector<float> data = {1.0f, 2.0f, 3.0f, 4.0f};
+    const std::vector<float> o = bk.apply_rope_positions(Tensor::from_f32(data, {1, 1, 1, 4}), {0}, 10000.0f).as_f32();
+    for (int i = 0; i < 4; ++i) ASSERT(std::fabs(o[i] - data[i]) < 1e-6f, "position 0 should be identity");
+}
+
+static void rope_rejects_bad_arguments(HipLlmBackend& bk) {  // rope.rs:19-35, :99-109
+    const Tensor x3 = Tensor::from_f32(std::vector<float>(8, 1.0f), {1, 1, 8});
+    ASSERT(expect_error([&] { bk.apply_rope_positions(x3, {0}, 1e4f); }).find("rank mismatch") != std::string::npos, "rank");
+    const Tensor odd = Tensor::from_f32(std::vector<float>(5, 1.0f), {1, 1, 1, 5});
+    ASSERT(expect_error([&] { bk.apply_rope_positions(odd, {0}, 1e4f); }).find("even head_dim") != std::string::npos, "odd");
+    const Tensor x = Tensor::from_f32(std::vector<float>(16, 1.0f), {1, 1, 2, 8});
+    ASSERT(expect_error([&] { bk.apply_rope_positions(x, {0}, 1e4f); }).find("positions length") != std::string::npos, "len");
+    ASSERT(expect_error([&] { bk.apply_rope_partial(x, {0, 1}, 1e4f, 10); }).find("rotary_dim") != std::string::npos, "rd");
+}
+
+static void rope_interleaved_is_permuted_neox(HipLlmBackend& bk) {  // gguf_weights.rs:111-115
+    const size_t D = 16;
+    std::vector<float> x(2 * 3 * D);
+    for (size_t i = 0; i < x.size(); ++i) x[i] = std::sin(0.37f * (float)i);
+    std::vector<float> xp(x.size());
+    for (size_t r = 0; r < x.size() / D; ++r)
+        for (size_t c = 0; c < D; ++c) xp[r * D + c] = x[r * D + (c % 2) * (D / 2) + c / 2];
+    const std::vector<float> n = bk.apply_rope_positions(Tensor::from_f32(x, {1, 2, 3, D}), {4, 9, 77}, 1e4f).as_f32();
+    const std::vector<float> i = bk.apply_rope_interleaved(Tensor::from_f32(xp, {1, 2, 3, D}), {4, 9, 77}, 1e4f).as_f32();
+    for (size_t r = 0; r < x.size() / D; ++r)
+        for (size_t c = 0; c < D; ++c) ASSERT(i[r * D + c] == n[r * D + (c % 2) * (D / 2) + c / 2], "P neox(x)");
+}
+
+static void add_rms_norm_is_add_then_rms_norm(HipLlmBackend& bk) {  // llama.rs:508 → :515
+    std::vector<float> a(3 * 64), b(3 * 64), w(64);
+    for (size_t i = 0; i < a.size(); ++i) a[i] = std::cos(0.1f * (float)i), b[i] = std::sin(0.3f * (float)i);
+    for (size_t i = 0; i < w.size(); ++i) w[i] = 1.0f + 0.01f * (float)i;
+    const Tensor x = Tensor::from_f32(a, {3, 64}), r = Tensor::from_f32(b, {3, 64}), wt = Tensor::from_f32(w, {64});
+    const auto fused = bk.add_rms_norm(x, r, wt, 1e-5f);
+    const Tensor sum = bk.add(r, x);
+    ASSERT(fused.second.as_f32() == sum.as_f32(), "residual == add");
+    ASSERT(fused.first.as_f32() == bk.rms_norm(sum, wt, 1e-5f).as_f32(), "normed == rms_norm(add)");
+}
+
+static void embed_row_gather_matches_full_dequant(HipLlmBackend& bk) {  // common.rs:674-718
+    const size_t vocab = 17, hidden = 256;
+    uint64_t s = 0xABCD;
+    std::vector<float> data(vocab * hidden);
+    for (float& v : data) {
+        s = s * 6364136223846793005ull + 1442695040888963407ull;
+        v = ((float)(s >> 40) / (float)(1u << 24)) * 2.0f - 1.0f;
+    }
+    const Tensor f32_t = Tensor::from_f32(data, {vocab, hidden});
+    std::vector<uint8_t> f16b;
+    std::vector<float> f16_full;
+    for (float v : data) {
+        const uint16_t h = f16_from_f32(v);
+        f16b.push_back((uint8_t)(h & 0xFF));
+        f16b.push_back((uint8_t)(h >> 8));
+        f16_full.push_back(f16_to_f32(h));
+    }
+    const Tensor f16_t = Tensor::from_f16_bytes(f16b, {vocab, hidden});
+    const std::vector<uint8_t> q8 = quantize_q8_0(data);
+    std::vector<float> q8_full;  // Tensor::to_f32_vec, Q8_0 arm (tensor.rs:378-389)
+    for (size_t b = 0; b < q8.size() / 34; ++b) {
+        const float d = f16_to_f32((uint16_t)(q8[b * 34] | (q8[b * 34 + 1] << 8)));
+        for (int j = 0; j < 32; ++j) q8_full.push_back((float)(int8_t)q8[b * 34 + 2 + j] * d);
+    }
+    const Tensor q8_t = Tensor::from_quant_bytes(q8, {vocab, hidden}, DType::Q8_0);
+    const std::vector<uint32_t> ids = {0, 7, 16, 3};
+    const std::pair<const Tensor*, const std::vector<float>*> tables[] = {{&f32_t, &data}, {&f16_t, &f16_full}, {&q8_t, &q8_full}};
+    for (const auto& [table, full] : tables) {
+        const Tensor got = bk.embed_tokens(*table, ids);
+        ASSERT(got.shape() == std::vector<size_t>({1, ids.size(), hidden}), "shape [1, seq, hidden]");
+        const std::vector<float> g = got.as_f32();
+        for (size_t i = 0; i < ids.size(); ++i)
+            ASSERT(std::memcmp(&g[i * hidden], &(*full)[ids[i] * hidden], hidden * 4) == 0,
+                   std::string("row gather differs from full dequant (dtype ") + sapient_hip::dtype_name(table->dtype()) + ")");
+    }
+    // Out-of-range id still errors.
+    const std::string e = expect_error([&] { bk.embed_tokens(f32_t, {(uint32_t)vocab}); });
+    ASSERT(e.find("token id 17 out of vocab range") != std::string::npos, "OOR error");
+}
+
+static void quant_bytes_are_validated(HipLlmBackend&) {  // tensor.rs:143-169
+    ASSERT(expect_error([] { Tensor::from_quant_bytes(std::vector<uint8_t>(33), {32}, DType::Q8_0); })
+               .find("shape mismatch") != std::string::npos, "byte count");
+}
+
+int main() {
+    if (!HipLlmBackend::is_available()) {
+        std::printf("no gfx950 device\n");
+        return 1;
+    }
+    HipLlmBackend bk;
+    const std::pair<const char*, void (*)(HipLlmBackend&)> tests[] = {
+        {"rmsnorm_identity_weight", rmsnorm_identity_weight},
+        {"rmsnorm_half_input_outputs_f32", rmsnorm_half_input_outputs_f32},
+        {"test_add", test_add},
+        {"test_scalar_broadcast", test_scalar_broadcast},
+        {"test_gelu", test_gelu},
+        {"test_silu_and_swiglu", test_silu_and_swiglu},
+        {"unary_rejects_non_f32", unary_rejects_non_f32},
+        {"rope_output_shape", rope_output_shape},
+        {"rope_partial_leaves_tail_unchanged", rope_partial_leaves_tail_unchanged},
+        {"rope_partial_full_matches_apply_rope", rope_partial_full_matches_apply_rope},
+        {"rope_position_zero_is_identity", rope_position_zero_is_identity},
+        {"rope_rejects_bad_arguments", rope_rejects_bad_arguments},
+        {"rope_interleaved_is_permuted_neox", rope_interleaved_is_permuted_neox},
+        {"add_rms_norm_is_add_then_rms_norm", add_rms_norm_is_add_then_rms_norm},
+        {"embed_row_gather_matches_full_dequant", embed_row_gather_matches_full_dequant},
+        {"quant_bytes_are_validated", quant_bytes_are_validated},
+    };
+    int failed = 0;
+    for (const auto& [name, fn] : tests) {
+        std::printf("test %s ... ", name);
+        std::fflush(stdout);
+        try {
+            fn(bk);
+            std::printf("ok\n");
+        } catch (const Failure& f) {
+            std::printf("FAILED: %s\n", f.why.c_str());
+            ++failed;
+        } catch (const std::exception& e) {
+            std::printf("FAILED (exception): %s\n", e.what());
+            ++failed;
+        }
+        std::fflush(stdout);
+    }
+    std::printf("%d failed\n", failed);
+    return failed ? 1 : 0;
+}

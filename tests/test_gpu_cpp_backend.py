@@ -1,0 +1,25 @@
+"""GPU: the C++ LlmBackend mirror (include/sapient_hip_backend.hpp) passes its
+native test program (tests/native/test_hip_llm_backend.cpp), which restates the
+reference's own unit tests against the HIP backend."""
+import subprocess
+from pathlib import Path
+
+import pytest
+
+pytestmark = pytest.mark.gpu
+NATIVE = Path(__file__).resolve().parent / "native"
+
+
+def test_cpp_llm_backend_mirror():
+    exe = NATIVE / "_build" / "test_hip_llm_backend"
+    if not exe.exists():
+        import importlib.util
+        spec = importlib.util.spec_from_file_location("native_build", NATIVE / "build.py")
+        mod = importlib.util.module_from_spec(spec)
+        spec.loader.exec_module(mod)
+        mod.build()
+    print("case native test_hip_llm_backend", flush=True)
+    res = subprocess.run([str(exe)], capture_output=True, text=True, timeout=300)
+    print(res.stdout)
+    assert res.returncode == 0, res.stdout + res.stderr
+    assert res.stdout.strip().endswith("0 failed")
