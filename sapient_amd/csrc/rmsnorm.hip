@@ -8,10 +8,11 @@
 //
 // Design (HBM-bound, ≈0.2 flop/byte):
 //  - A row is split across W wave64s (W = 1, 2, 4, 8 or 16, chosen so every
-//    lane holds ~16 values); each lane owns every (64·W)-th 16-byte vector of
-//    the row and keeps its slice of r in registers, so every input byte
-//    crosses HBM once and the row is never re-read. Small W keeps the register
-//    footprint at ~64 VGPRs, i.e. the full 8 waves per SIMD of occupancy.
+//    lane holds ~16 values); wave w owns the w-th contiguous 1/W of the row
+//    (VPT runs of 64 16-byte vectors; contiguous chunks measured ~5 % faster
+//    than interleaving the waves) and keeps its slice of r in registers, so
+//    every input byte crosses HBM once and the row is never re-read. The
+//    register footprint stays at ~64 VGPRs: the full 8 waves per SIMD.
 //  - Each wave sums its r² with a butterfly of cross-lane shuffles; the W
 //    partial sums meet in LDS and every wave adds them in the same fixed order.
 //  - All row traffic is 16 bytes per lane (1 KiB contiguous per wave
@@ -55,7 +56,7 @@ __global__ __launch_bounds__(W >= 4 ? 64 * W : 256) void rms_rows_vec(const TX* 
     if (live) {
 #pragma unroll
         for (int j = 0; j < VPT; ++j) {
-            const int v = (sub + W * j) * kWave + lane;
+            const int v = (sub * VPT + j) * kWave + lane;
             if (v < nvec) {
                 load_f32<TX, E, true>(x + base + (size_t)v * E, r[j]);
                 if constexpr (FUSED) {
@@ -85,7 +86,7 @@ __global__ __launch_bounds__(W >= 4 ? 64 * W : 256) void rms_rows_vec(const TX* 
 
 #pragma unroll
     for (int j = 0; j < VPT; ++j) {
-        const int v = (sub + W * j) * kWave + lane;
+        const int v = (sub * VPT + j) * kWave + lane;
         if (v < nvec) {
             float wv_[E];
             if (w != nullptr) {
