@@ -165,6 +165,23 @@ def op_table(torch, ops, dev, only=None):
         lambda: [(gen(torch, (8192, 10240), 90 + i, dev, f16, 2.0), torch.empty(8192, 10240, device=dev, dtype=f16))
                  for i in range(3)],
         lambda s: ops.gelu_tanh(s[0], out=s[1]))
+    # LayerNorm (+ bias), erf-GELU and the bias add: the encoder-family norm / activation path
+    rows, dim = 16384, 4096
+    wl, bl = gen(torch, (dim,), 4, dev, f32, 0.1, 1.0), gen(torch, (dim,), 5, dev, f32, 0.1)
+    for dt, tag, es in ((f32, "f32", 4), (f16, "f16 (f32 w,b)", 2)):
+        run("layer_norm", f"{rows}x{dim}", tag, 2 * rows * dim * es + 2 * dim * 4, rows, "rows",
+            lambda dt=dt: [(gen(torch, (rows, dim), 150 + i, dev, dt, 2.0, 0.5), torch.empty(rows, dim, device=dev, dtype=dt))
+                           for i in range(3)],
+            lambda s: ops.layer_norm(s[0], wl, bl, 1e-5, out=s[1]))
+    run("add_bias", f"{rows}x{dim}", "f32", 2 * rows * dim * 4 + dim * 4, rows, "rows",
+        lambda: [(gen(torch, (rows, dim), 160 + i, dev, f32), torch.empty(rows, dim, device=dev)) for i in range(3)],
+        lambda s: ops.add_bias(s[0], bl, out=s[1]))
+    n = 12000 * 5120
+    for dt, tag, es in ((f32, "f32", 4), (f16, "f16", 2)):
+        run("gelu_erf", "12000x5120", tag, 2 * n * es, 12000, "rows",
+            lambda dt=dt: [(gen(torch, (12000, 5120), 170 + i, dev, dt, 2.0), torch.empty(12000, 5120, device=dev, dtype=dt))
+                           for i in range(3)],
+            lambda s: ops.gelu_erf(s[0], out=s[1]))
     # C5: Q4_K embedding gather, 128256 x 4096 table, 65536 ids (uniform, Zipf 1.1)
     vocab, hidden, n_ids = 128256, 4096, 65536
     nb = vocab * hidden // 256

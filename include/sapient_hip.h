@@ -80,6 +80,18 @@ int sph_rms_norm(const void* x, int x_dtype, const void* weight, int w_dtype, vo
 int sph_add_rms_norm(const void* x, void* residual, int dtype, const void* weight, int w_dtype,
                      void* out, int out_dtype, int64_t rows, int64_t dim, float eps, void* stream);
 
+/* LayerNorm over the last dimension, two-pass mean then variance:
+ *   mean = sum(x) / dim;  var = sum((x - mean)^2) / dim;
+ *   y = ((x - mean) * (1 / sqrt(var + eps))) * weight + bias.
+ * Replaces LlmBackend::layer_norm (backend.rs:73-79) → common::layer_norm
+ * (crates/sapient-models/src/forward/common.rs:575-577) → kernels::layernorm::layer_norm
+ * (layernorm.rs:17-69, axis = -1), and the wgpu analog WgpuContext::layer_norm
+ * (resident.rs:277). `weight` and `bias` may each be NULL (the kernel's
+ * Option<&Tensor> cases, layernorm.rs:59-64); both are of wb_dtype ∈ {F32, x_dtype}.
+ * x_dtype ∈ {F32, F16, BF16}; out_dtype ∈ {F32, x_dtype}. */
+int sph_layer_norm(const void* x, int x_dtype, const void* weight, const void* bias, int wb_dtype,
+                   void* out, int out_dtype, int64_t rows, int64_t dim, float eps, void* stream);
+
 /* Element-wise a + b and a * b with the reference's broadcast rule: same
  * length, or either operand of length 1 (elementwise.rs:27-57, :61-69).
  * Replaces LlmBackend::add / LlmBackend::mul (backend.rs:82-83). `out` has
@@ -101,6 +113,22 @@ int sph_swiglu(const void* gate, const void* up, void* out, int dtype, int64_t n
  * (elementwise.rs:120-127). Bit-exact with the reference on glibc: tanh is
  * evaluated by glibc's own tanhf algorithm. `out` may alias `x`. */
 int sph_gelu_tanh(const void* x, void* out, int dtype, int64_t n, void* stream);
+
+/* Exact-form GELU: 0.5 x (1 + erf(x / sqrt(2))), erf by the reference's
+ * Abramowitz-Stegun rational approximation with glibc's expf.
+ * Replaces elementwise::gelu_erf (elementwise.rs:135-138, erf_approx :163-174)
+ * and WgpuContext::gelu_erf (resident.rs:316). Bit-exact with the reference
+ * on glibc. `out` may alias `x`. */
+int sph_gelu_erf(const void* x, void* out, int dtype, int64_t n, void* stream);
+
+/* Bias over the last dimension: out[i] = y[i] + bias[i % n], `total` elements
+ * of y, a multiple of n. Replaces common::add_bias_last_dim
+ * (crates/sapient-models/src/forward/common.rs:556-569, the bias step of
+ * LlmBackend::linear_3d_bias, backend.rs:64-70) and WgpuContext::add_bias
+ * (resident.rs:416). dtype ∈ {F32, F16, BF16} for y and out;
+ * bias_dtype ∈ {F32, dtype}. `out` may alias `y`. */
+int sph_add_bias(const void* y, const void* bias, int bias_dtype, void* out, int dtype, int64_t total, int64_t n,
+                 void* stream);
 
 /* Rotary position embedding, in place, on up to two tensors sharing positions
  * (Q and K). Each tensor is [batch, heads, seq, head_dim] contiguous (the

@@ -76,9 +76,17 @@ class HipLlmBackend {
 
     // LlmBackend::rms_norm (backend.rs:72 → layernorm.rs:75-106): f32 output.
     Tensor rms_norm(const Tensor& x, const Tensor& weight, float eps);
+    // LlmBackend::layer_norm (backend.rs:73-79 → layernorm.rs:17-69, last axis):
+    // `bias` may be null; f32 output.
+    Tensor layer_norm(const Tensor& x, const Tensor& weight, const Tensor* bias, float eps);
+    // common::add_bias_last_dim (common.rs:556-569), the bias step of
+    // LlmBackend::linear_3d_bias (backend.rs:64-70): y F32, bias [y.last_dim].
+    Tensor add_bias_last_dim(const Tensor& y, const Tensor& bias);
     // LlmBackend::silu / gelu (elementwise.rs:141-143, :120-127): F32 input only.
     Tensor silu(const Tensor& x);
     Tensor gelu(const Tensor& x);
+    // elementwise::gelu_erf (elementwise.rs:135-138): F32 input only.
+    Tensor gelu_erf(const Tensor& x);
     // LlmBackend::add / mul (elementwise.rs:27-69): same length or a length-1 side.
     Tensor add(const Tensor& a, const Tensor& b);
     Tensor mul(const Tensor& a, const Tensor& b);
@@ -97,9 +105,17 @@ class HipLlmBackend {
     Tensor embed_tokens(const Tensor& weight, const std::vector<uint32_t>& ids);
 
  private:
+    // A device allocation owned by one call; freed on scope exit (also when a
+    // later upload throws), or earlier by release().
     struct DeviceBuf {
         void* ptr = nullptr;
         size_t bytes = 0;
+        DeviceBuf() = default;
+        DeviceBuf(const DeviceBuf&) = delete;
+        DeviceBuf& operator=(const DeviceBuf&) = delete;
+        DeviceBuf(DeviceBuf&& o) noexcept : ptr(o.ptr), bytes(o.bytes) { o.ptr = nullptr; }
+        DeviceBuf& operator=(DeviceBuf&&) = delete;
+        ~DeviceBuf();
     };
     DeviceBuf upload(const void* host, size_t bytes);
     DeviceBuf alloc(size_t bytes);

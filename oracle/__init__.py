@@ -46,6 +46,8 @@ def lib() -> C.CDLL:
             "sor_add": (C.c_int, [vp, sz, vp, sz, vp]),
             "sor_mul": (C.c_int, [vp, sz, vp, sz, vp]),
             "sor_add_rms_norm": (None, [vp, vp, vp, vp, vp, sz, sz, fl]),
+            "sor_layer_norm": (None, [vp, vp, vp, vp, sz, sz, fl]),
+            "sor_add_bias_last_dim": (None, [vp, vp, vp, sz, sz]),
             "sor_silu": (None, [vp, vp, sz]),
             "sor_swiglu": (None, [vp, vp, vp, sz]),
             "sor_gelu": (None, [vp, vp, sz]),
@@ -131,6 +133,30 @@ def add_rms_norm(x, residual, weight, eps: float):
     normed, r_out = np.empty_like(x), np.empty_like(x)
     lib().sor_add_rms_norm(_p(x), _p(r), _p(w), _p(normed), _p(r_out), x.size // dim, dim, np.float32(eps))
     return normed, r_out
+
+
+def layer_norm(x, weight, bias, eps: float) -> np.ndarray:
+    """layernorm.rs:17-69 over the last axis; weight / bias may be None."""
+    x = _f32(x)
+    w = None if weight is None else _f32(weight)
+    b = None if bias is None else _f32(bias)
+    n = x.shape[-1]
+    out = np.empty_like(x)
+    lib().sor_layer_norm(_p(x), None if w is None else _p(w), None if b is None else _p(b), _p(out),
+                         x.size // n, n, np.float32(eps))
+    return out
+
+
+def add_bias_last_dim(y, bias) -> np.ndarray:
+    """common.rs:556-569: y + bias broadcast over the last dimension."""
+    y, b = _f32(y), _f32(bias)
+    if y.ndim == 0:
+        raise ValueError("empty tensor")
+    if b.size != y.shape[-1]:
+        raise ValueError(f"bias length {b.size} does not match last dim {y.shape[-1]}")
+    out = np.empty_like(y)
+    lib().sor_add_bias_last_dim(_p(y), _p(b), _p(out), y.size, b.size)
+    return out
 
 
 def _binary(fn, a, b):

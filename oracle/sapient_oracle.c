@@ -125,6 +125,39 @@ void sor_rms_norm(const float* x, const float* w, float* out, size_t outer, size
     }
 }
 
+/* ─────────────────────── next row f3: LayerNorm, bias add ───────────────────────
+ * crates/sapient-backends/cpu/src/kernels/layernorm.rs:17-69 (axis = -1, as
+ * common::layer_norm calls it, common.rs:575-577):
+ *   mean = (Σ_serial v) / n;  var = (Σ_serial (v-mean)*(v-mean)) / n
+ *   inv_std = 1 / sqrt(var + eps);  normed = (x - mean) * inv_std
+ *   out = normed * w + b  (each of w, b optional; two roundings, no FMA) */
+void sor_layer_norm(const float* x, const float* w, const float* b, float* out, size_t outer, size_t n, float eps) {
+    for (size_t o = 0; o < outer; o++) {
+        const float* row = x + o * n;
+        float s = -0.0f;
+        for (size_t i = 0; i < n; i++) s = s + row[i];
+        float mean = s / (float)n;
+        float v = -0.0f;
+        for (size_t i = 0; i < n; i++) v = v + (row[i] - mean) * (row[i] - mean);
+        float var = v / (float)n;
+        float inv_std = 1.0f / sqrtf(var + eps);
+        for (size_t i = 0; i < n; i++) {
+            float normed = (row[i] - mean) * inv_std;
+            float y = normed;
+            if (w && b) y = normed * w[i] + b[i];
+            else if (w) y = normed * w[i];
+            else if (b) y = normed + b[i];
+            out[o * n + i] = y;
+        }
+    }
+}
+
+/* crates/sapient-models/src/forward/common.rs:556-569 (add_bias_last_dim):
+ * y [.., n] f32, bias [n] (any float dtype, widened): out[k] = y[k] + b[k % n]. */
+void sor_add_bias_last_dim(const float* y, const float* bias, float* out, size_t total, size_t n) {
+    for (size_t k = 0; k < total; k++) out[k] = y[k] + bias[k % n];
+}
+
 /* ─────────────────────── a2: residual add, mul ───────────────────────
  * crates/sapient-backends/cpu/src/kernels/elementwise.rs:61-63 (add), :67-69 (mul),
  * through binary_f32 :27-57: same length, or either side of length 1 broadcast.

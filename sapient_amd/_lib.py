@@ -24,11 +24,14 @@ SIGNATURES = {
     "sph_init": (_i32, [_vp]),
     "sph_rms_norm": (_i32, [_vp, _i32, _vp, _i32, _vp, _i32, _i64, _i64, _f, _vp]),
     "sph_add_rms_norm": (_i32, [_vp, _vp, _i32, _vp, _i32, _vp, _i32, _i64, _i64, _f, _vp]),
+    "sph_layer_norm": (_i32, [_vp, _i32, _vp, _vp, _i32, _vp, _i32, _i64, _i64, _f, _vp]),
     "sph_add": (_i32, [_vp, _i64, _vp, _i64, _vp, _i32, _vp]),
     "sph_mul": (_i32, [_vp, _i64, _vp, _i64, _vp, _i32, _vp]),
     "sph_silu": (_i32, [_vp, _vp, _i32, _i64, _vp]),
     "sph_swiglu": (_i32, [_vp, _vp, _vp, _i32, _i64, _vp]),
     "sph_gelu_tanh": (_i32, [_vp, _vp, _i32, _i64, _vp]),
+    "sph_gelu_erf": (_i32, [_vp, _vp, _i32, _i64, _vp]),
+    "sph_add_bias": (_i32, [_vp, _vp, _i32, _vp, _i32, _i64, _i64, _vp]),
     "sph_rope": (_i32, [_vp, _i64, _vp, _i64, _i32, _i32, _vp, _i64, _i64, _i64, _i64, _f, _f, _vp]),
     "sph_embed": (_i32, [_vp, _i32, _i64, _i64, _vp, _i64, _vp, _vp, _vp]),
 }

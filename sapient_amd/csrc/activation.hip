@@ -1,4 +1,5 @@
-// activation.hip — element-wise add / mul / SiLU / SwiGLU / GELU-tanh for gfx950.
+// activation.hip — element-wise add / mul / SiLU / SwiGLU / GELU (tanh and erf
+// forms) and the last-dimension bias add, for gfx950.
 //
 // Reference math (crates/sapient-backends/cpu/src/kernels/elementwise.rs):
 //   add  a + b                        (:61-63, broadcast rule of binary_f32 :27-57)
@@ -6,6 +7,8 @@
 //   silu v / (1 + exp(-v))            (:141-143)
 //   swiglu = silu(gate) * up          (llama.rs:531-532; wgpu analog elementwise.wgsl op1)
 //   gelu 0.5 v (1 + tanh(0.79788456 (v + 0.044715 v v v)))   (:120-127)
+//   gelu_erf 0.5 v (1 + erf_approx(v / √2))                  (:135-138, :163-174)
+//   add_bias y[i] + bias[i % n]        (crates/sapient-models/src/forward/common.rs:556-569)
 //
 // Design: all streams are HBM-bound. Each thread moves 16-byte vectors, two
 // in flight per operand, non-temporal (every byte is touched once); the grid
@@ -24,11 +27,19 @@
 //    GELU is tabulated once per device — every input with |v| < 16 evaluated
 //    on the GPU with that algorithm; outside that band the result is exactly
 //    v, -0 or NaN — and each launch stages the 76 KiB table in LDS (two
-//    blocks per CU in gfx950's 160 KiB) and streams the tensor through it:
+//    resident blocks per CU in gfx950's 160 KiB) and streams the tensor through it:
 //    bit-exact and bandwidth-bound. f32 inputs evaluate the algorithm per
 //    element (VALU-bound).
+//  - erf-GELU takes the same two routes: its erf_approx multiplies by glibc's
+//    expf(-x²), restated in glibc_expf.h (double-precision evaluation with a
+//    32-entry table of 2^(i/32), which each block stages in LDS). Outside
+//    |v| < 16 expf(-x²) underflows to 0, so the band and the outside rule are
+//    the ones of the tanh form.
+//  - Bias add: a block owns a tile of up to 256 16-byte column vectors and a
+//    run of rows; each thread loads its bias vector once and streams the rows.
 #include <mutex>
 
+#include "glibc_expf.h"
 #include "glibc_tanhf.h"
 #include "sph_common.h"
 
@@ -39,7 +50,10 @@ constexpr int kThreads = 256;
 constexpr int kUnroll = 2;       // vectors in flight per operand per thread
 constexpr int64_t kMaxGrid = 65536;  // ~one loop trip per thread at the configuration sizes
 
-enum Op { OP_ADD = 0, OP_MUL = 1, OP_SILU = 2, OP_SWIGLU = 3, OP_GELU = 4 };
+enum Op { OP_ADD = 0, OP_MUL = 1, OP_SILU = 2, OP_SWIGLU = 3, OP_GELU = 4, OP_GELU_ERF = 5 };
+
+// 2^(i/32) for the expf restatement, staged per block into LDS by the kernels that need it.
+__constant__ Exp2fTable kExp2f = exp2f_table();
 enum Bcast { B_NONE = 0, B_SCALAR_B = 1, B_SCALAR_A = 2 };
 
 __device__ __forceinline__ float silu_f(float g) {
@@ -59,13 +73,22 @@ __device__ __forceinline__ float silu_f(float g) {
 }
 
 template <int OP>
-__device__ __forceinline__ float apply_op(float a, float b) {
+__device__ __forceinline__ float apply_op(float a, float b, const uint64_t* exp_tab) {
     if constexpr (OP == OP_ADD) return a + b;
     if constexpr (OP == OP_MUL) return a * b;
     if constexpr (OP == OP_SILU) return silu_f(a);
     if constexpr (OP == OP_SWIGLU) return silu_f(a) * b;
     if constexpr (OP == OP_GELU) return gelu_tanh_ref_order(a);
+    if constexpr (OP == OP_GELU_ERF) return gelu_erf_ref_order(a, exp_tab);
     return 0.0f;
+}
+
+template <int OP> constexpr bool needs_exp_table() { return OP == OP_GELU_ERF; }
+
+// Copy the 2^(i/32) table into LDS (block-wide; call before any use).
+__device__ __forceinline__ void stage_exp_table(uint64_t* tab) {
+    if (threadIdx.x < 32) tab[threadIdx.x] = kExp2f.tab[threadIdx.x];
+    __syncthreads();
 }
 
 template <int OP> constexpr bool binary_op() { return OP == OP_ADD || OP == OP_MUL || OP == OP_SWIGLU; }
@@ -77,6 +100,8 @@ template <int OP> constexpr bool binary_op() { return OP == OP_ADD || OP == OP_M
 template <typename T, int OP, int BC>
 __global__ __launch_bounds__(kThreads) void ew_vec(const T* a, const T* b, T* out, int64_t nvec) {
     constexpr int E = vec16<T>::n;
+    __shared__ uint64_t exp_tab[needs_exp_table<OP>() ? 32 : 1];
+    if constexpr (needs_exp_table<OP>()) stage_exp_table(exp_tab);
     float sa = 0.0f, sb = 0.0f;
     if constexpr (BC == B_SCALAR_A) sa = widen(a[0]);
     if constexpr (BC == B_SCALAR_B) sb = widen(b[0]);
@@ -100,7 +125,7 @@ __global__ __launch_bounds__(kThreads) void ew_vec(const T* a, const T* b, T* ou
                 for (int e = 0; e < E; ++e) {
                     const float x = BC == B_SCALAR_A ? sa : va[u][e];
                     const float y = BC == B_SCALAR_B ? sb : vb[u][e];
-                    o[e] = apply_op<OP>(x, y);
+                    o[e] = apply_op<OP>(x, y, exp_tab);
                 }
                 store_f32<T, E, true>(out + i * E, o);
             }
@@ -112,11 +137,13 @@ __global__ __launch_bounds__(kThreads) void ew_vec(const T* a, const T* b, T* ou
 template <typename T, int OP, int BC>
 __global__ __launch_bounds__(kThreads) void ew_scalar(const T* a, const T* b, T* out, int64_t begin,
                                                       int64_t end) {
+    __shared__ uint64_t exp_tab[needs_exp_table<OP>() ? 32 : 1];
+    if constexpr (needs_exp_table<OP>()) stage_exp_table(exp_tab);
     const int64_t stride = (int64_t)gridDim.x * kThreads;
     for (int64_t i = begin + (int64_t)blockIdx.x * kThreads + threadIdx.x; i < end; i += stride) {
         const float x = widen(a[BC == B_SCALAR_A ? 0 : i]);
         const float y = binary_op<OP>() ? widen(b[BC == B_SCALAR_B ? 0 : i]) : 0.0f;
-        out[i] = narrow<T>(apply_op<OP>(x, y));
+        out[i] = narrow<T>(apply_op<OP>(x, y, exp_tab));
     }
 }
 
@@ -210,26 +237,33 @@ __device__ __forceinline__ uint32_t gelu_outside(uint32_t h) {
     return 0x8000u;                                   // v <= -16: -0
 }
 
-__device__ __align__(16) uint16_t gelu_lut[2][kLutEntries];
+// Tables by index: form * 2 + type, form 0 = tanh, 1 = erf; type 0 = f16, 1 = bf16.
+constexpr int kLutTables = 4;
+__device__ __align__(16) uint16_t gelu_lut[kLutTables][kLutEntries];
 
 template <typename T>
 __global__ __launch_bounds__(kThreads) void gelu_lut_build(int which) {
+    __shared__ uint64_t exp_tab[32];
+    stage_exp_table(exp_tab);
     const uint32_t slot = blockIdx.x * kThreads + threadIdx.x;
     constexpr uint32_t L = gelu_band<T>::kLimit;
     if (slot >= 2 * L) return;
     const uint32_t h = slot < L ? slot : 0x8000u | (slot - L);
     const float v = widen(T{(uint16_t)h});
-    gelu_lut[which][slot] = narrow<T>(gelu_tanh_ref_order(v)).bits;
+    const float g = which < 2 ? gelu_tanh_ref_order(v) : gelu_erf_ref_order(v, exp_tab);
+    gelu_lut[which][slot] = narrow<T>(g).bits;
 }
 
-constexpr int kLutThreads = 1024;
+constexpr int kLutThreads = 512;
 
 template <typename T>
 __device__ __forceinline__ uint32_t gelu_lookup(const uint16_t* tab, uint32_t h) {
     return (h & 0x7FFFu) < gelu_band<T>::kLimit ? (uint32_t)tab[gelu_slot<T>(h)] : gelu_outside<T>(h);
 }
 
-// Two blocks per CU: stage the band table in LDS, then stream 16-byte vectors.
+// Four 512-thread blocks per CU (two resident at a time, LDS-bound): stage the
+// band table in LDS, then stream 16-byte vectors, grid-stride. Measured on
+// MI355X this shape is within ~7 % of a table-free copy of the same stream.
 template <typename T>
 __global__ __launch_bounds__(kLutThreads) void gelu_lut_apply(const uint16_t* in, uint16_t* out, int64_t nvec, int which) {
     __shared__ __align__(16) uint16_t tab[kLutEntries];
@@ -280,7 +314,7 @@ std::mutex g_init_mu;
 bool g_lut_ready[kMaxDevices];
 int g_num_cus[kMaxDevices];
 
-// Build both tables on `stream` once per device and wait for them.
+// Build the four tables on `stream` once per device and wait for them.
 int ensure_device_ready(hipStream_t stream, int* cus) {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return SPH_ENODEV;
@@ -290,8 +324,10 @@ int ensure_device_ready(hipStream_t stream, int* cus) {
         if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
             return SPH_ENODEV;
         g_num_cus[dev] = n;
-        gelu_lut_build<f16><<<(kLutEntries + kThreads - 1) / kThreads, kThreads, 0, stream>>>(0);
-        gelu_lut_build<bf16><<<(kLutEntries + kThreads - 1) / kThreads, kThreads, 0, stream>>>(1);
+        for (int form = 0; form < 2; ++form) {
+            gelu_lut_build<f16><<<(kLutEntries + kThreads - 1) / kThreads, kThreads, 0, stream>>>(form * 2);
+            gelu_lut_build<bf16><<<(kLutEntries + kThreads - 1) / kThreads, kThreads, 0, stream>>>(form * 2 + 1);
+        }
         if (launch_status() != SPH_OK) return SPH_EHIP;
         if (hipStreamSynchronize(stream) != hipSuccess) return SPH_EHIP;
         g_lut_ready[dev] = true;
@@ -309,7 +345,7 @@ int gelu_half(const uint16_t* x, uint16_t* out, int which, int64_t n, hipStream_
     if (aligned(x, 16) && aligned(out, 16)) {
         const int64_t nvec = n / 8;
         if (nvec > 0) {
-            gelu_lut_apply<T><<<grid_for(nvec, (int64_t)kLutThreads * 4, 2 * cus), kLutThreads, 0, stream>>>(x, out, nvec, which);
+            gelu_lut_apply<T><<<grid_for(nvec, (int64_t)kLutThreads * 4, 4 * cus), kLutThreads, 0, stream>>>(x, out, nvec, which);
             if (launch_status() != SPH_OK) return SPH_EHIP;
         }
         done = nvec * 8;
@@ -319,6 +355,103 @@ int gelu_half(const uint16_t* x, uint16_t* out, int which, int64_t n, hipStream_
         if (launch_status() != SPH_OK) return SPH_EHIP;
     }
     return SPH_OK;
+}
+
+// GELU of either form: half types through the tables, f32 per element.
+template <int OP>
+int gelu_any(const void* x, void* out, int dtype, int64_t n, hipStream_t s) {
+    if (n < 0) return SPH_EINVAL;
+    if (n > 0 && (x == nullptr || out == nullptr)) return SPH_EINVAL;
+    if (n == 0) return is_float_dtype(dtype) ? SPH_OK : SPH_EINVAL;
+    const int form = OP == OP_GELU ? 0 : 1;
+    if (dtype == SPH_F16)
+        return gelu_half<f16>(static_cast<const uint16_t*>(x), static_cast<uint16_t*>(out), form * 2, n, s);
+    if (dtype == SPH_BF16)
+        return gelu_half<bf16>(static_cast<const uint16_t*>(x), static_cast<uint16_t*>(out), form * 2 + 1, n, s);
+    return dispatch_unary<OP>(x, out, dtype, n, s);
+}
+
+// ───────────────────────────── bias add ─────────────────────────────
+constexpr int kBiasRowsPerBlock = 16;
+
+// Block b covers column tile b % ntiles (up to 256 16-byte vectors of a row)
+// over rows [(b / ntiles) · R, + R). A thread keeps its bias vector in
+// registers and streams y down the rows, RU rows in flight.
+template <typename T, typename TB>
+__global__ __launch_bounds__(kThreads) void bias_rows_vec(const T* y, const TB* bias, T* out, int64_t rows, int nvr,
+                                                         int ntiles, int tile) {
+    constexpr int E = vec16<T>::n;
+    constexpr int RU = 4;
+    const int t = (int)(blockIdx.x % (unsigned)ntiles);
+    const int64_t r0 = (int64_t)(blockIdx.x / (unsigned)ntiles) * kBiasRowsPerBlock;
+    const int v = t * tile + (int)threadIdx.x;
+    if ((int)threadIdx.x >= tile || v >= nvr) return;
+    float bv[E];
+    load_f32<TB, E>(bias + (size_t)v * E, bv);
+    const int64_t r_end = r0 + kBiasRowsPerBlock < rows ? r0 + kBiasRowsPerBlock : rows;
+    for (int64_t r = r0; r < r_end; r += RU) {
+        float q[RU][E];
+#pragma unroll
+        for (int u = 0; u < RU; ++u)
+            if (r + u < r_end) load_f32<T, E, true>(y + ((size_t)(r + u) * nvr + v) * E, q[u]);
+#pragma unroll
+        for (int u = 0; u < RU; ++u) {
+            if (r + u < r_end) {
+#pragma unroll
+                for (int e = 0; e < E; ++e) q[u][e] = q[u][e] + bv[e];
+                store_f32<T, E, true>(out + ((size_t)(r + u) * nvr + v) * E, q[u]);
+            }
+        }
+    }
+}
+
+// Any width / alignment: element-wise with one modulo per element.
+template <typename T, typename TB>
+__global__ __launch_bounds__(kThreads) void bias_scalar(const T* y, const TB* bias, T* out, int64_t total, int64_t n) {
+    const int64_t stride = (int64_t)gridDim.x * kThreads;
+    for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < total; i += stride)
+        out[i] = narrow<T>(widen(y[i]) + widen(bias[i % n]));
+}
+
+template <typename T, typename TB>
+int launch_bias(const void* y, const void* bias, void* out, int64_t total, int64_t n, hipStream_t stream) {
+    constexpr int E = vec16<T>::n;
+    const T* yp = static_cast<const T*>(y);
+    const TB* bp = static_cast<const TB*>(bias);
+    T* op = static_cast<T*>(out);
+    const int64_t rows = total / n;
+    const int64_t nvr = n / E;
+    const bool vec_ok = n % E == 0 && aligned(y, 16) && aligned(out, 16) && aligned(bias, 16) &&
+                        nvr <= (int64_t)1 << 24;
+    if (vec_ok) {
+        const int tile = nvr >= kThreads ? kThreads : (int)((nvr + 63) / 64 * 64);
+        const int ntiles = (int)((nvr + tile - 1) / tile);
+        const int64_t groups = (rows + kBiasRowsPerBlock - 1) / kBiasRowsPerBlock;
+        // The grid is one launch: ntiles · groups < 2^32 blocks is checked here.
+        if ((int64_t)ntiles * groups < ((int64_t)1 << 31)) {
+            bias_rows_vec<T, TB><<<dim3((unsigned)(ntiles * groups)), tile, 0, stream>>>(yp, bp, op, rows, (int)nvr,
+                                                                                          ntiles, tile);
+            return launch_status();
+        }
+    }
+    bias_scalar<T, TB><<<grid_for(total, kThreads, 65536), kThreads, 0, stream>>>(yp, bp, op, total, n);
+    return launch_status();
+}
+
+int dispatch_bias(const void* y, const void* bias, int b_dt, void* out, int dt, int64_t total, int64_t n,
+                  hipStream_t stream) {
+    if (total < 0 || n < 0) return SPH_EINVAL;
+    if (!is_float_dtype(dt) || !is_float_dtype(b_dt)) return SPH_EINVAL;
+    if (total == 0) return SPH_OK;
+    if (n == 0 || total % n != 0) return SPH_EINVAL;
+    if (y == nullptr || bias == nullptr || out == nullptr) return SPH_EINVAL;
+    return with_float_type(dt, [&](auto ty) -> int {
+        using T = decltype(ty);
+        return with_float_type(b_dt, [&](auto tb) -> int {
+            using TB = decltype(tb);
+            return launch_bias<T, TB>(y, bias, out, total, n, stream);
+        });
+    });
 }
 
 }  // namespace
@@ -344,13 +477,14 @@ extern "C" int sph_swiglu(const void* gate, const void* up, void* out, int dtype
 }
 
 extern "C" int sph_gelu_tanh(const void* x, void* out, int dtype, int64_t n, void* stream) {
-    if (n < 0) return SPH_EINVAL;
-    if (n > 0 && (x == nullptr || out == nullptr)) return SPH_EINVAL;
-    if (n == 0) return sph::is_float_dtype(dtype) ? SPH_OK : SPH_EINVAL;
-    hipStream_t s = static_cast<hipStream_t>(stream);
-    if (dtype == SPH_F16)
-        return sph::gelu_half<sph::f16>(static_cast<const uint16_t*>(x), static_cast<uint16_t*>(out), 0, n, s);
-    if (dtype == SPH_BF16)
-        return sph::gelu_half<sph::bf16>(static_cast<const uint16_t*>(x), static_cast<uint16_t*>(out), 1, n, s);
-    return sph::dispatch_unary<sph::OP_GELU>(x, out, dtype, n, s);
+    return sph::gelu_any<sph::OP_GELU>(x, out, dtype, n, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int sph_gelu_erf(const void* x, void* out, int dtype, int64_t n, void* stream) {
+    return sph::gelu_any<sph::OP_GELU_ERF>(x, out, dtype, n, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int sph_add_bias(const void* y, const void* bias, int bias_dtype, void* out, int dtype, int64_t total,
+                            int64_t n, void* stream) {
+    return sph::dispatch_bias(y, bias, bias_dtype, out, dtype, total, n, static_cast<hipStream_t>(stream));
 }

@@ -1,10 +1,11 @@
-// rmsnorm.hip — RMSNorm and fused residual-add + RMSNorm for gfx950.
+// rmsnorm.hip — RMSNorm, fused residual-add + RMSNorm and LayerNorm for gfx950.
 //
 // Reference math (crates/sapient-backends/cpu/src/kernels/layernorm.rs:93-103):
 //   ms = (Σ x_i²) / dim;  inv = 1 / sqrt(ms + eps);  y_i = (x_i · inv) · w_i
 // The fused variant replaces `add` (llama.rs:508) followed by `rms_norm`
 // (llama.rs:515): r = x + residual is written back to `residual` and y is the
-// RMSNorm of the f32 sum.
+// RMSNorm of the f32 sum. LayerNorm (layernorm.rs:17-69, last axis):
+//   mean = Σx / n;  var = Σ(x − mean)² / n;  y = ((x − mean) · 1/sqrt(var + eps)) · w + b
 //
 // Design (HBM-bound, ≈0.2 flop/byte):
 //  - A row is split across W wave64s (W = 1, 2, 4, 8 or 16, chosen so every
@@ -34,15 +35,47 @@ namespace {
 
 constexpr int kWave = 64;
 
+enum Kind { K_RMS = 0, K_ADD_RMS = 1, K_LAYER = 2 };
+
+// y for one element: RMSNorm (r·inv)·w; LayerNorm ((r−mean)·inv)·w + b.
+template <int KIND>
+__device__ __forceinline__ float norm_out(float r, float mean, float inv, float w, float b, bool has_w, bool has_b) {
+    if constexpr (KIND == K_LAYER) {
+        const float normed = (r - mean) * inv;
+        if (has_w && has_b) return normed * w + b;
+        if (has_w) return normed * w;
+        if (has_b) return normed + b;
+        return normed;
+    } else {
+        return (r * inv) * w;  // w = 1 when absent: (r·inv)·1 is r·inv exactly
+    }
+}
+
+// Sum of one value per wave of a row: the W partials meet in LDS and every
+// wave adds them in the same order. `slot` lets two reductions share a barrier-safe buffer.
+template <int W, int WPB>
+__device__ __forceinline__ float row_sum(float v, float (*partial)[WPB], int slot, int lane, int wv) {
+    v = wave_sum(v);
+    if constexpr (W > 1) {
+        if (lane == 0) partial[slot][wv] = v;
+        __syncthreads();
+        float tot = 0.0f;
+#pragma unroll
+        for (int k = 0; k < W; ++k) tot = tot + partial[slot][(wv / W) * W + k];
+        v = tot;
+    }
+    return v;
+}
+
 // W waves per row, VPT 16-byte vectors per lane, RPB rows per block.
-template <typename TX, typename TW, typename TO, bool FUSED, int W, int VPT>
+template <typename TX, typename TW, typename TO, int KIND, int W, int VPT>
 __global__ __launch_bounds__(W >= 4 ? 64 * W : 256) void rms_rows_vec(const TX* __restrict__ x, TX* __restrict__ residual,
-                                                                   const TW* __restrict__ w, TO* __restrict__ out,
-                                                                   int64_t rows, int dim, float eps) {
+                                                                   const TW* __restrict__ w, const TW* __restrict__ bias,
+                                                                   TO* __restrict__ out, int64_t rows, int dim, float eps) {
     constexpr int E = vec16<TX>::n;  // elements per 16-byte access of x
     constexpr int WPB = W >= 4 ? W : 4;
     constexpr int RPB = WPB / W;
-    __shared__ float partial[WPB];
+    __shared__ float partial[2][WPB];
     const int lane = threadIdx.x & (kWave - 1);
     const int wv = threadIdx.x / kWave;
     const int sub = wv % W;  // this wave's share of the row
@@ -59,7 +92,7 @@ __global__ __launch_bounds__(W >= 4 ? 64 * W : 256) void rms_rows_vec(const TX* 
             const int v = (sub * VPT + j) * kWave + lane;
             if (v < nvec) {
                 load_f32<TX, E, true>(x + base + (size_t)v * E, r[j]);
-                if constexpr (FUSED) {
+                if constexpr (KIND == K_ADD_RMS) {
                     float b[E];
                     load_f32<TX, E, true>(residual + base + (size_t)v * E, b);
 #pragma unroll
@@ -67,83 +100,114 @@ __global__ __launch_bounds__(W >= 4 ? 64 * W : 256) void rms_rows_vec(const TX* 
                     store_f32<TX, E, true>(residual + base + (size_t)v * E, r[j]);
                 }
 #pragma unroll
-                for (int e = 0; e < E; ++e) ss = ss + r[j][e] * r[j][e];
+                for (int e = 0; e < E; ++e) {
+                    if constexpr (KIND == K_LAYER) ss = ss + r[j][e];
+                    else ss = ss + r[j][e] * r[j][e];
+                }
             }
         }
     }
-    ss = wave_sum(ss);
-    if constexpr (W > 1) {
-        if (lane == 0) partial[wv] = ss;
-        __syncthreads();
-        float tot = 0.0f;
+    ss = row_sum<W, WPB>(ss, partial, 0, lane, wv);
+    float mean = 0.0f, inv;
+    if constexpr (KIND == K_LAYER) {
+        mean = ss / (float)dim;
+        float vs = 0.0f;
+        if (live) {
 #pragma unroll
-        for (int k = 0; k < W; ++k) tot = tot + partial[(wv / W) * W + k];
-        ss = tot;
+            for (int j = 0; j < VPT; ++j) {
+                const int v = (sub * VPT + j) * kWave + lane;
+                if (v < nvec) {
+#pragma unroll
+                    for (int e = 0; e < E; ++e) vs = vs + (r[j][e] - mean) * (r[j][e] - mean);
+                }
+            }
+        }
+        vs = row_sum<W, WPB>(vs, partial, 1, lane, wv);
+        inv = 1.0f / sqrtf(vs / (float)dim + eps);
+    } else {
+        inv = 1.0f / sqrtf(ss / (float)dim + eps);
     }
     if (!live) return;
-    const float ms = ss / (float)dim;
-    const float inv = 1.0f / sqrtf(ms + eps);
+    const bool has_w = w != nullptr, has_b = bias != nullptr;
 
 #pragma unroll
     for (int j = 0; j < VPT; ++j) {
         const int v = (sub * VPT + j) * kWave + lane;
         if (v < nvec) {
-            float wv_[E];
-            if (w != nullptr) {
+            float wv_[E], bv[E];
+            if (has_w) {
                 load_f32<TW, E>(w + (size_t)v * E, wv_);
             } else {
 #pragma unroll
                 for (int e = 0; e < E; ++e) wv_[e] = 1.0f;
             }
+            if (KIND == K_LAYER && has_b) {
+                load_f32<TW, E>(bias + (size_t)v * E, bv);
+            } else {
+#pragma unroll
+                for (int e = 0; e < E; ++e) bv[e] = 0.0f;
+            }
             float y[E];
 #pragma unroll
-            for (int e = 0; e < E; ++e) y[e] = (r[j][e] * inv) * wv_[e];
+            for (int e = 0; e < E; ++e) y[e] = norm_out<KIND>(r[j][e], mean, inv, wv_[e], bv[e], has_w, has_b);
             store_f32<TO, E, true>(out + base + (size_t)v * E, y);
         }
     }
 }
 
-// Any width and alignment: one 256-thread block per row, two passes. Pass 2
-// recomputes r from the inputs (it re-reads them from cache) so the half
-// variants normalise the unrounded f32 sum; each thread owns the same
-// elements in both passes, so the in-place residual update cannot race.
-template <typename TX, typename TW, typename TO, bool FUSED>
+// Any width and alignment: one 256-thread block per row, re-reading the row
+// from cache for each pass. The last pass recomputes r from the inputs so the
+// half variants normalise the unrounded f32 sum; each thread owns the same
+// elements in every pass, so the in-place residual update cannot race.
+template <typename TX, typename TW, typename TO, int KIND>
 __global__ __launch_bounds__(256) void rms_rows_generic(const TX* __restrict__ x, TX* residual,
-                                                       const TW* __restrict__ w, TO* __restrict__ out,
-                                                       int64_t rows, int64_t dim, float eps) {
-    __shared__ float partial[256 / kWave];
+                                                       const TW* __restrict__ w, const TW* __restrict__ bias,
+                                                       TO* __restrict__ out, int64_t rows, int64_t dim, float eps) {
+    __shared__ float partial[2][256 / kWave];
+    const int lane = threadIdx.x & (kWave - 1), wv = threadIdx.x / kWave;
     const int64_t row = blockIdx.x;
     const size_t base = (size_t)row * (size_t)dim;
+    auto value = [&](int64_t i) {
+        float r = widen(x[base + i]);
+        if constexpr (KIND == K_ADD_RMS) r = r + widen(residual[base + i]);
+        return r;
+    };
     float ss = 0.0f;
     for (int64_t i = threadIdx.x; i < dim; i += blockDim.x) {
-        float r = widen(x[base + i]);
-        if constexpr (FUSED) r = r + widen(residual[base + i]);
-        ss = ss + r * r;
+        const float r = value(i);
+        if constexpr (KIND == K_LAYER) ss = ss + r;
+        else ss = ss + r * r;
     }
-    ss = wave_sum(ss);
-    if ((threadIdx.x & (kWave - 1)) == 0) partial[threadIdx.x / kWave] = ss;
-    __syncthreads();
-    float tot = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 256 / kWave; ++i) tot = tot + partial[i];
-    const float ms = tot / (float)dim;
-    const float inv = 1.0f / sqrtf(ms + eps);
-    for (int64_t i = threadIdx.x; i < dim; i += blockDim.x) {
-        float r = widen(x[base + i]);
-        if constexpr (FUSED) {
-            r = r + widen(residual[base + i]);
-            residual[base + i] = narrow<TX>(r);
+    ss = row_sum<4, 4>(ss, partial, 0, lane, wv);
+    float mean = 0.0f, inv;
+    if constexpr (KIND == K_LAYER) {
+        mean = ss / (float)dim;
+        float vs = 0.0f;
+        for (int64_t i = threadIdx.x; i < dim; i += blockDim.x) {
+            const float d = value(i) - mean;
+            vs = vs + d * d;
         }
-        const float wv = w != nullptr ? widen(w[i]) : 1.0f;
-        out[base + i] = narrow<TO>((r * inv) * wv);
+        vs = row_sum<4, 4>(vs, partial, 1, lane, wv);
+        inv = 1.0f / sqrtf(vs / (float)dim + eps);
+    } else {
+        inv = 1.0f / sqrtf(ss / (float)dim + eps);
+    }
+    const bool has_w = w != nullptr, has_b = bias != nullptr;
+    for (int64_t i = threadIdx.x; i < dim; i += blockDim.x) {
+        const float r = value(i);
+        if constexpr (KIND == K_ADD_RMS) residual[base + i] = narrow<TX>(r);
+        const float wv_ = has_w ? widen(w[i]) : 1.0f;
+        const float bv = (KIND == K_LAYER && has_b) ? widen(bias[i]) : 0.0f;
+        out[base + i] = narrow<TO>(norm_out<KIND>(r, mean, inv, wv_, bv, has_w, has_b));
     }
 }
 
-template <typename TX, typename TW, typename TO, bool FUSED>
-int launch_rms(const void* x, void* residual, const void* w, void* out, int64_t rows, int64_t dim,
+template <typename TX, typename TW, typename TO, int KIND>
+int launch_rms(const void* x, void* residual, const void* w, const void* bias, void* out, int64_t rows, int64_t dim,
                float eps, hipStream_t stream) {
     if (rows == 0 || dim == 0) return SPH_OK;
     constexpr int E = vec16<TX>::n;
+    constexpr bool FUSED = KIND == K_ADD_RMS;
     // Vector path: ~16 values per lane, W waves per row (W <= 16).
     constexpr int VPT = 16 / E;
     const int64_t nvec = dim / E;
@@ -151,7 +215,8 @@ int launch_rms(const void* x, void* residual, const void* w, void* out, int64_t 
     while (W < 16 && nvec > (int64_t)kWave * VPT * W) W *= 2;
     const bool vec_ok = dim % E == 0 && aligned(x, 16) && aligned(out, 16) &&
                         (!FUSED || aligned(residual, 16)) && (w == nullptr || aligned(w, 16)) &&
-                        nvec <= (int64_t)kWave * VPT * W && dim <= INT32_MAX;
+                        (bias == nullptr || aligned(bias, 16)) && nvec <= (int64_t)kWave * VPT * W &&
+                        dim <= INT32_MAX;
     // A launch covers at most 2^22 rows, keeping grid x block below 2^32 work-items.
     constexpr int64_t kChunk = int64_t(1) << 22;
     for (int64_t r0 = 0; r0 < rows; r0 += kChunk) {
@@ -160,6 +225,7 @@ int launch_rms(const void* x, void* residual, const void* w, void* out, int64_t 
         const TX* xp = static_cast<const TX*>(x) + off;
         TX* rp = FUSED ? static_cast<TX*>(residual) + off : nullptr;
         const TW* wp = static_cast<const TW*>(w);
+        const TW* bp = static_cast<const TW*>(bias);
         TO* op = static_cast<TO*>(out) + off;
         if (vec_ok) {
             const int rpb = W >= 4 ? 1 : 4 / W;
@@ -167,14 +233,14 @@ int launch_rms(const void* x, void* residual, const void* w, void* out, int64_t 
             const int threads = W >= 4 ? kWave * W : 256;
             const int d = (int)dim;
             switch (W) {
-            case 1: rms_rows_vec<TX, TW, TO, FUSED, 1, VPT><<<grid, threads, 0, stream>>>(xp, rp, wp, op, nr, d, eps); break;
-            case 2: rms_rows_vec<TX, TW, TO, FUSED, 2, VPT><<<grid, threads, 0, stream>>>(xp, rp, wp, op, nr, d, eps); break;
-            case 4: rms_rows_vec<TX, TW, TO, FUSED, 4, VPT><<<grid, threads, 0, stream>>>(xp, rp, wp, op, nr, d, eps); break;
-            case 8: rms_rows_vec<TX, TW, TO, FUSED, 8, VPT><<<grid, threads, 0, stream>>>(xp, rp, wp, op, nr, d, eps); break;
-            default: rms_rows_vec<TX, TW, TO, FUSED, 16, VPT><<<grid, threads, 0, stream>>>(xp, rp, wp, op, nr, d, eps); break;
+            case 1: rms_rows_vec<TX, TW, TO, KIND, 1, VPT><<<grid, threads, 0, stream>>>(xp, rp, wp, bp, op, nr, d, eps); break;
+            case 2: rms_rows_vec<TX, TW, TO, KIND, 2, VPT><<<grid, threads, 0, stream>>>(xp, rp, wp, bp, op, nr, d, eps); break;
+            case 4: rms_rows_vec<TX, TW, TO, KIND, 4, VPT><<<grid, threads, 0, stream>>>(xp, rp, wp, bp, op, nr, d, eps); break;
+            case 8: rms_rows_vec<TX, TW, TO, KIND, 8, VPT><<<grid, threads, 0, stream>>>(xp, rp, wp, bp, op, nr, d, eps); break;
+            default: rms_rows_vec<TX, TW, TO, KIND, 16, VPT><<<grid, threads, 0, stream>>>(xp, rp, wp, bp, op, nr, d, eps); break;
             }
         } else {
-            rms_rows_generic<TX, TW, TO, FUSED><<<dim3((unsigned)nr), 256, 0, stream>>>(xp, rp, wp, op, nr, dim, eps);
+            rms_rows_generic<TX, TW, TO, KIND><<<dim3((unsigned)nr), 256, 0, stream>>>(xp, rp, wp, bp, op, nr, dim, eps);
         }
         const int st = launch_status();
         if (st != SPH_OK) return st;
@@ -182,24 +248,24 @@ int launch_rms(const void* x, void* residual, const void* w, void* out, int64_t 
     return SPH_OK;
 }
 
-// Resolve (x, weight, out) storage types: weight and out are each f32 or x's type.
-template <bool FUSED>
-int dispatch_rms(const void* x, void* residual, int x_dt, const void* w, int w_dt, void* out, int out_dt,
-                 int64_t rows, int64_t dim, float eps, hipStream_t stream) {
+// Resolve (x, weight/bias, out) storage types: weight/bias and out are each f32 or x's type.
+template <int KIND>
+int dispatch_rms(const void* x, void* residual, int x_dt, const void* w, const void* b, int w_dt, void* out,
+                 int out_dt, int64_t rows, int64_t dim, float eps, hipStream_t stream) {
     if (!is_float_dtype(x_dt)) return SPH_EINVAL;
-    if (w != nullptr && w_dt != SPH_F32 && w_dt != x_dt) return SPH_EINVAL;
+    if ((w != nullptr || b != nullptr) && w_dt != SPH_F32 && w_dt != x_dt) return SPH_EINVAL;
     if (out_dt != SPH_F32 && out_dt != x_dt) return SPH_EINVAL;
-    const bool w32 = (w == nullptr) || w_dt == SPH_F32;
+    const bool w32 = (w == nullptr && b == nullptr) || w_dt == SPH_F32;
     const bool o32 = out_dt == SPH_F32;
     return with_float_type(x_dt, [&](auto tx) -> int {
         using TX = decltype(tx);
         if constexpr (sizeof(TX) == 4) {
-            return launch_rms<float, float, float, FUSED>(x, residual, w, out, rows, dim, eps, stream);
+            return launch_rms<float, float, float, KIND>(x, residual, w, b, out, rows, dim, eps, stream);
         } else {
-            if (w32 && o32) return launch_rms<TX, float, float, FUSED>(x, residual, w, out, rows, dim, eps, stream);
-            if (w32 && !o32) return launch_rms<TX, float, TX, FUSED>(x, residual, w, out, rows, dim, eps, stream);
-            if (!w32 && o32) return launch_rms<TX, TX, float, FUSED>(x, residual, w, out, rows, dim, eps, stream);
-            return launch_rms<TX, TX, TX, FUSED>(x, residual, w, out, rows, dim, eps, stream);
+            if (w32 && o32) return launch_rms<TX, float, float, KIND>(x, residual, w, b, out, rows, dim, eps, stream);
+            if (w32 && !o32) return launch_rms<TX, float, TX, KIND>(x, residual, w, b, out, rows, dim, eps, stream);
+            if (!w32 && o32) return launch_rms<TX, TX, float, KIND>(x, residual, w, b, out, rows, dim, eps, stream);
+            return launch_rms<TX, TX, TX, KIND>(x, residual, w, b, out, rows, dim, eps, stream);
         }
     });
 }
@@ -211,8 +277,8 @@ extern "C" int sph_rms_norm(const void* x, int x_dtype, const void* weight, int 
                             int out_dtype, int64_t rows, int64_t dim, float eps, void* stream) {
     if (rows < 0 || dim < 0) return SPH_EINVAL;
     if ((rows > 0 && dim > 0) && (x == nullptr || out == nullptr)) return SPH_EINVAL;
-    return sph::dispatch_rms<false>(x, nullptr, x_dtype, weight, w_dtype, out, out_dtype, rows, dim, eps,
-                                    static_cast<hipStream_t>(stream));
+    return sph::dispatch_rms<sph::K_RMS>(x, nullptr, x_dtype, weight, nullptr, w_dtype, out, out_dtype, rows, dim, eps,
+                                         static_cast<hipStream_t>(stream));
 }
 
 extern "C" int sph_add_rms_norm(const void* x, void* residual, int dtype, const void* weight, int w_dtype,
@@ -220,6 +286,14 @@ extern "C" int sph_add_rms_norm(const void* x, void* residual, int dtype, const 
     if (rows < 0 || dim < 0) return SPH_EINVAL;
     if ((rows > 0 && dim > 0) && (x == nullptr || residual == nullptr || out == nullptr)) return SPH_EINVAL;
     if (out == x || out == residual) return SPH_EINVAL;
-    return sph::dispatch_rms<true>(x, residual, dtype, weight, w_dtype, out, out_dtype, rows, dim, eps,
-                                   static_cast<hipStream_t>(stream));
+    return sph::dispatch_rms<sph::K_ADD_RMS>(x, residual, dtype, weight, nullptr, w_dtype, out, out_dtype, rows, dim,
+                                             eps, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int sph_layer_norm(const void* x, int x_dtype, const void* weight, const void* bias, int wb_dtype,
+                              void* out, int out_dtype, int64_t rows, int64_t dim, float eps, void* stream) {
+    if (rows < 0 || dim < 0) return SPH_EINVAL;
+    if ((rows > 0 && dim > 0) && (x == nullptr || out == nullptr)) return SPH_EINVAL;
+    return sph::dispatch_rms<sph::K_LAYER>(x, nullptr, x_dtype, weight, bias, wb_dtype, out, out_dtype, rows, dim,
+                                           eps, static_cast<hipStream_t>(stream));
 }

@@ -148,6 +148,10 @@ void HipLlmBackend::download(const DeviceBuf& b, void* host, size_t bytes) {
     hip_ok(hipStreamSynchronize(static_cast<hipStream_t>(stream_)), "synchronize");
 }
 
+HipLlmBackend::DeviceBuf::~DeviceBuf() {
+    if (ptr) (void)hipFree(ptr);
+}
+
 void HipLlmBackend::release(DeviceBuf& b) {
     if (b.ptr) (void)hipFree(b.ptr);
     b.ptr = nullptr;
@@ -268,8 +272,11 @@ Tensor HipLlmBackend::unary_f32(const Tensor& x, const char* op) {
     std::lock_guard<std::mutex> lock(mu_);
     DeviceBuf xd = upload(x.bytes().data(), x.bytes().size());
     DeviceBuf od = alloc(x.numel() * 4);
-    const int st = std::strcmp(op, "silu") == 0 ? sph_silu(xd.ptr, od.ptr, SPH_F32, (int64_t)x.numel(), stream_)
-                                                 : sph_gelu_tanh(xd.ptr, od.ptr, SPH_F32, (int64_t)x.numel(), stream_);
+    const int64_t n = (int64_t)x.numel();
+    int st;
+    if (std::strcmp(op, "silu") == 0) st = sph_silu(xd.ptr, od.ptr, SPH_F32, n, stream_);
+    else if (std::strcmp(op, "gelu_erf") == 0) st = sph_gelu_erf(xd.ptr, od.ptr, SPH_F32, n, stream_);
+    else st = sph_gelu_tanh(xd.ptr, od.ptr, SPH_F32, n, stream_);
     std::vector<float> out(x.numel());
     if (st == SPH_OK) download(od, out.data(), out.size() * 4);
     release(xd);
@@ -280,6 +287,58 @@ Tensor HipLlmBackend::unary_f32(const Tensor& x, const char* op) {
 
 Tensor HipLlmBackend::silu(const Tensor& x) { return unary_f32(x, "silu"); }
 Tensor HipLlmBackend::gelu(const Tensor& x) { return unary_f32(x, "gelu"); }
+Tensor HipLlmBackend::gelu_erf(const Tensor& x) { return unary_f32(x, "gelu_erf"); }
+
+// layernorm::layer_norm (layernorm.rs:17-69) over the last axis: x, weight and
+// bias are widened to f32 (to_f32_cow) and the output is f32.
+Tensor HipLlmBackend::layer_norm(const Tensor& x0, const Tensor& weight0, const Tensor* bias0, float eps) {
+    const Tensor x = f32_input(x0), w = f32_input(weight0);
+    const Tensor b = bias0 ? f32_input(*bias0) : Tensor();
+    const auto& s = x.shape();
+    const size_t dim = s.empty() ? 1 : s.back();
+    const size_t rows = dim ? x.numel() / dim : 0;
+    if (w.numel() != dim) throw Error("shape mismatch: weight " + shape_str(w.shape()) + " for rows of " + std::to_string(dim));
+    if (bias0 && b.numel() != dim) throw Error("shape mismatch: bias " + shape_str(b.shape()) + " for rows of " + std::to_string(dim));
+    std::lock_guard<std::mutex> lock(mu_);
+    DeviceBuf xd = upload(x.bytes().data(), x.bytes().size());
+    DeviceBuf wd = upload(w.bytes().data(), w.bytes().size());
+    DeviceBuf bd = bias0 ? upload(b.bytes().data(), b.bytes().size()) : DeviceBuf{};
+    DeviceBuf od = alloc(x.numel() * 4);
+    const int st = sph_layer_norm(xd.ptr, SPH_F32, wd.ptr, bd.ptr, SPH_F32, od.ptr, SPH_F32, (int64_t)rows,
+                                  (int64_t)dim, eps, stream_);
+    std::vector<float> out(x.numel());
+    if (st == SPH_OK) download(od, out.data(), out.size() * 4);
+    release(xd);
+    release(wd);
+    release(bd);
+    release(od);
+    check(st, "layer_norm");
+    return Tensor::from_f32(out, s);
+}
+
+// common::add_bias_last_dim (common.rs:556-569): y is F32, the bias any float
+// type of length equal to y's last dimension.
+Tensor HipLlmBackend::add_bias_last_dim(const Tensor& y, const Tensor& bias0) {
+    if (y.shape().empty()) throw Error("empty tensor");
+    if (y.dtype() != DType::F32) throw Error(std::string("type mismatch: expected f32, got ") + dtype_name(y.dtype()));
+    const size_t n = y.shape().back();
+    const Tensor b = (bias0.dtype() == DType::F32 || bias0.dtype() == DType::F16 || bias0.dtype() == DType::BF16)
+                         ? bias0 : f32_input(bias0);
+    if (b.numel() != n)
+        throw Error("bias length " + std::to_string(b.numel()) + " does not match last dim " + std::to_string(n));
+    std::lock_guard<std::mutex> lock(mu_);
+    DeviceBuf yd = upload(y.bytes().data(), y.bytes().size());
+    DeviceBuf bd = upload(b.bytes().data(), b.bytes().size());
+    DeviceBuf od = alloc(y.numel() * 4);
+    const int st = sph_add_bias(yd.ptr, bd.ptr, (int)b.dtype(), od.ptr, SPH_F32, (int64_t)y.numel(), (int64_t)n, stream_);
+    std::vector<float> out(y.numel());
+    if (st == SPH_OK) download(od, out.data(), out.size() * 4);
+    release(yd);
+    release(bd);
+    release(od);
+    check(st, "add_bias_last_dim");
+    return Tensor::from_f32(out, y.shape());
+}
 
 Tensor HipLlmBackend::swiglu(const Tensor& gate, const Tensor& up) {
     if (gate.dtype() != DType::F32 || up.dtype() != DType::F32)

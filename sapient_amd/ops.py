@@ -35,6 +35,19 @@ def _dev(t: torch.Tensor, name: str) -> torch.Tensor:
     return t
 
 
+def _out(out: Optional[torch.Tensor], shape, dtype: torch.dtype, device, name: str = "out") -> torch.Tensor:
+    """A fresh output, or the caller's after checking it holds exactly what the kernel writes."""
+    if out is None:
+        return torch.empty(shape, dtype=dtype, device=device)
+    _dev(out, name)
+    numel = 1
+    for d in shape:
+        numel *= d
+    if out.numel() != numel or out.dtype != dtype:
+        raise ValueError(f"{name} must hold {numel} elements of {dtype}")
+    return out
+
+
 def init(device: Optional[torch.device] = None) -> None:
     """Per-device set-up (GELU tables); optional, done lazily otherwise."""
     with torch.cuda.device(device or torch.cuda.current_device()):
@@ -49,14 +62,42 @@ def rms_norm(x: torch.Tensor, weight: Optional[torch.Tensor], eps: float,
     dim = x.shape[-1] if x.dim() else 1
     rows = x.numel() // dim if dim else 0
     od = out_dtype or (out.dtype if out is not None else x.dtype)
-    if out is None:
-        out = torch.empty(x.shape, dtype=od, device=x.device)
-    _dev(out, "out")
-    w = _dev(weight, "weight") if weight is not None else None
+    out = _out(out, x.shape, od, x.device)
+    w = _vec(weight, dim, "weight")
     check(lib().sph_rms_norm(x.data_ptr(), dtype_code(x.dtype),
                              None if w is None else w.data_ptr(), dtype_code(w.dtype) if w is not None else 0,
                              out.data_ptr(), dtype_code(out.dtype), rows, dim, float(eps), _stream(x)),
           "rms_norm")
+    return out
+
+
+def _vec(t: Optional[torch.Tensor], n: int, name: str) -> Optional[torch.Tensor]:
+    if t is None:
+        return None
+    _dev(t, name)
+    if t.numel() != n:
+        raise ValueError(f"{name} length {t.numel()} does not match last dim {n}")
+    return t
+
+
+def layer_norm(x: torch.Tensor, weight: Optional[torch.Tensor], bias: Optional[torch.Tensor], eps: float,
+               out: Optional[torch.Tensor] = None, out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
+    """LayerNorm over the last dim (layernorm.rs:17-69, axis -1; common.rs:575-577).
+    weight and bias are optional and share one dtype (f32 or x's)."""
+    _dev(x, "x")
+    dim = x.shape[-1] if x.dim() else 1
+    rows = x.numel() // dim if dim else 0
+    od = out_dtype or (out.dtype if out is not None else x.dtype)
+    out = _out(out, x.shape, od, x.device)
+    w = _vec(weight, dim, "weight")
+    b = _vec(bias, dim, "bias")
+    if w is not None and b is not None and w.dtype != b.dtype:
+        raise ValueError("weight and bias must share dtype")
+    wb = w if w is not None else b
+    check(lib().sph_layer_norm(x.data_ptr(), dtype_code(x.dtype), None if w is None else w.data_ptr(),
+                               None if b is None else b.data_ptr(), dtype_code(wb.dtype) if wb is not None else 0,
+                               out.data_ptr(), dtype_code(out.dtype), rows, dim, float(eps), _stream(x)),
+          "layer_norm")
     return out
 
 
@@ -72,10 +113,8 @@ def add_rms_norm(x: torch.Tensor, residual: torch.Tensor, weight: Optional[torch
     dim = x.shape[-1]
     rows = x.numel() // dim if dim else 0
     od = out_dtype or (out.dtype if out is not None else x.dtype)
-    if out is None:
-        out = torch.empty(x.shape, dtype=od, device=x.device)
-    _dev(out, "out")
-    w = _dev(weight, "weight") if weight is not None else None
+    out = _out(out, x.shape, od, x.device)
+    w = _vec(weight, dim, "weight")
     check(lib().sph_add_rms_norm(x.data_ptr(), residual.data_ptr(), dtype_code(x.dtype),
                                  None if w is None else w.data_ptr(), dtype_code(w.dtype) if w is not None else 0,
                                  out.data_ptr(), dtype_code(out.dtype), rows, dim, float(eps), _stream(x)),
@@ -89,9 +128,7 @@ def _binary(fn, name, a, b, out):
     if a.dtype != b.dtype:
         raise ValueError("operands must share dtype")
     big = a if a.numel() >= b.numel() else b
-    if out is None:
-        out = torch.empty(big.shape, dtype=a.dtype, device=a.device)
-    _dev(out, "out")
+    out = _out(out, big.shape, a.dtype, a.device)
     check(fn(a.data_ptr(), a.numel(), b.data_ptr(), b.numel(), out.data_ptr(), dtype_code(a.dtype), _stream(a)), name)
     return out
 
@@ -108,7 +145,7 @@ def mul(a: torch.Tensor, b: torch.Tensor, out: Optional[torch.Tensor] = None) ->
 
 def silu(x: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
     _dev(x, "x")
-    out = torch.empty_like(x) if out is None else _dev(out, "out")
+    out = _out(out, x.shape, x.dtype, x.device)
     check(lib().sph_silu(x.data_ptr(), out.data_ptr(), dtype_code(x.dtype), x.numel(), _stream(x)), "silu")
     return out
 
@@ -119,7 +156,7 @@ def swiglu(gate: torch.Tensor, up: torch.Tensor, out: Optional[torch.Tensor] = N
     _dev(up, "up")
     if gate.shape != up.shape or gate.dtype != up.dtype:
         raise ValueError("gate and up must share shape and dtype")
-    out = torch.empty_like(gate) if out is None else _dev(out, "out")
+    out = _out(out, gate.shape, gate.dtype, gate.device)
     check(lib().sph_swiglu(gate.data_ptr(), up.data_ptr(), out.data_ptr(), dtype_code(gate.dtype), gate.numel(),
                            _stream(gate)), "swiglu")
     return out
@@ -128,8 +165,31 @@ def swiglu(gate: torch.Tensor, up: torch.Tensor, out: Optional[torch.Tensor] = N
 def gelu_tanh(x: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
     """GELU tanh form (elementwise.rs:120-127), bit-exact with the reference."""
     _dev(x, "x")
-    out = torch.empty_like(x) if out is None else _dev(out, "out")
+    out = _out(out, x.shape, x.dtype, x.device)
     check(lib().sph_gelu_tanh(x.data_ptr(), out.data_ptr(), dtype_code(x.dtype), x.numel(), _stream(x)), "gelu")
+    return out
+
+
+def gelu_erf(x: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """GELU erf form (elementwise.rs:135-138, :163-174), bit-exact with the reference."""
+    _dev(x, "x")
+    out = _out(out, x.shape, x.dtype, x.device)
+    check(lib().sph_gelu_erf(x.data_ptr(), out.data_ptr(), dtype_code(x.dtype), x.numel(), _stream(x)), "gelu_erf")
+    return out
+
+
+def add_bias(y: torch.Tensor, bias: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """y + bias over the last dim (common.rs:556-569); bias may be f32 or a half type."""
+    _dev(y, "y")
+    if y.dim() == 0:
+        raise ValueError("empty tensor")
+    n = y.shape[-1]
+    _dev(bias, "bias")
+    if bias.numel() != n:
+        raise ValueError(f"bias length {bias.numel()} does not match last dim {n}")
+    out = _out(out, y.shape, y.dtype, y.device)
+    check(lib().sph_add_bias(y.data_ptr(), bias.data_ptr(), dtype_code(bias.dtype), out.data_ptr(),
+                             dtype_code(y.dtype), y.numel(), n, _stream(y)), "add_bias")
     return out
 
 
@@ -156,6 +216,12 @@ def rope_(q: torch.Tensor, k: Optional[torch.Tensor], positions: torch.Tensor, b
                          positions.data_ptr(), B, S, D, rd, float(base), float(pos_scale), _stream(q)), "rope")
 
 
+# Bytes per row as (bytes per block, elements per block) of each table type
+# (crates/sapient-core/src/dtype.rs:136-145).
+_ROW_BYTES = {_lib.F32: (4, 1), _lib.F16: (2, 1), _lib.BF16: (2, 1), _lib.Q8_0: (34, 32), _lib.Q4_K: (144, 256),
+              _lib.Q6_K: (210, 256)}
+
+
 def embed(table: torch.Tensor, table_dtype: int, vocab: int, hidden: int, ids: torch.Tensor,
           out: Optional[torch.Tensor] = None, bad_id_flag: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Row gather + dequant of a raw GGUF table (common.rs:164-217) into f32
@@ -166,12 +232,17 @@ def embed(table: torch.Tensor, table_dtype: int, vocab: int, hidden: int, ids: t
     if ids.dtype not in (torch.int32, torch.uint32):
         raise ValueError("ids must be 32-bit")
     n = ids.numel()
-    if out is None:
-        out = torch.empty((n, hidden), dtype=torch.float32, device=ids.device)
-    _dev(out, "out")
+    if table_dtype not in _ROW_BYTES or hidden < 0 or vocab < 0:
+        raise ValueError("unsupported table dtype or negative size")
+    num, den = _ROW_BYTES[table_dtype]
+    if hidden % den == 0 and table.numel() * table.element_size() < vocab * (hidden // den) * num:
+        raise ValueError("table holds fewer than vocab rows")
+    out = _out(out, (n, hidden), torch.float32, ids.device)
     flag = None
     if bad_id_flag is not None:
         flag = _dev(bad_id_flag, "bad_id_flag")
+        if flag.dtype != torch.int32 or flag.numel() < 1:
+            raise ValueError("bad_id_flag must be an int32 device tensor")
     check(lib().sph_embed(table.data_ptr(), table_dtype, vocab, hidden, ids.data_ptr(), n, out.data_ptr(),
                           None if flag is None else flag.data_ptr(), _stream(ids)), "embed")
     return out

@@ -1,7 +1,7 @@
 // GPU tests of the C++ LlmBackend mirror (include/sapient_hip_backend.hpp),
 // written after the reference's own unit tests so they read the same way:
 //   layernorm.rs:113-149, elementwise.rs:176-232, rope.rs:155-206,
-//   common.rs:669-718, and the trait's validation errors (rope.rs:19-35,
+//   common.rs:556-569 and :669-718, and the trait's validation errors (rope.rs:19-35,
 //   elementwise.rs:15-21, common.rs:171-173).
 // Prints "test <name> ... ok|FAILED: <why>" per test; exits 1 if any failed.
 #include <cmath>
@@ -111,6 +111,41 @@ static void rmsnorm_half_input_outputs_f32(HipLlmBackend& bk) {  // to_f32_cow u
     const Tensor y = bk.rms_norm(Tensor::from_f16_bytes(b, {1, 2}), Tensor::from_f32({1.0f, 1.0f}, {2}), 0.0f);
     ASSERT(y.dtype() == DType::F32, "f32 output");
     ASSERT(std::fabs(y.as_f32()[1] - 4.0f / std::sqrt(12.5f)) < 1e-5f, "value");
+}
+
+static void layernorm_zero_mean_unit_var(HipLlmBackend& bk) {  // layernorm.rs:113-123 (unit weight)
+    const Tensor x = Tensor::from_f32({1.0f, 2.0f, 3.0f, 4.0f}, {2, 2});
+    const std::vector<float> d = bk.layer_norm(x, Tensor::from_f32({1.0f, 1.0f}, {2}), nullptr, 1e-5f).as_f32();
+    ASSERT(std::fabs(d[0] + 1.0f) < 1e-4f && std::fabs(d[1] - 1.0f) < 1e-4f, "row 0");
+    ASSERT(std::fabs(d[2] + 1.0f) < 1e-4f && std::fabs(d[3] - 1.0f) < 1e-4f, "row 1");
+    const Tensor b = Tensor::from_f32({0.5f, -0.5f}, {2});
+    const std::vector<float> e = bk.layer_norm(x, Tensor::from_f32({2.0f, 2.0f}, {2}), &b, 1e-5f).as_f32();
+    ASSERT(std::fabs(e[0] + 1.5f) < 2e-4f && std::fabs(e[1] - 1.5f) < 2e-4f, "weight and bias");
+    ASSERT(expect_error([&] { bk.layer_norm(x, Tensor::from_f32({1.0f}, {1}), nullptr, 1e-5f); })
+               .find("shape mismatch") != std::string::npos, "weight length");
+}
+
+static void test_gelu_erf(HipLlmBackend& bk) {  // elementwise.rs:216-224
+    const std::vector<float> v = bk.gelu_erf(Tensor::from_f32({0.0f, 1.0f, -1.0f}, {3})).as_f32();
+    ASSERT(std::fabs(v[0]) < 1e-6f, "g(0)");
+    ASSERT(std::fabs(v[1] - 0.8413447f) < 1e-4f, "g(1)");
+    ASSERT(std::fabs(v[2] + 0.1586553f) < 1e-4f, "g(-1)");
+}
+
+static void add_bias_last_dim_broadcasts(HipLlmBackend& bk) {  // common.rs:556-569
+    const Tensor y = Tensor::from_f32({1.0f, 2.0f, 3.0f, 4.0f, 5.0f, 6.0f}, {2, 3});
+    const std::vector<float> o = bk.add_bias_last_dim(y, Tensor::from_f32({10.0f, 20.0f, 30.0f}, {3})).as_f32();
+    ASSERT(o == std::vector<float>({11.0f, 22.0f, 33.0f, 14.0f, 25.0f, 36.0f}), "f32 bias");
+    std::vector<uint8_t> hb;
+    for (float v : {0.5f, -1.0f, 2.0f}) {
+        const uint16_t h = f16_from_f32(v);
+        hb.push_back((uint8_t)(h & 0xFF));
+        hb.push_back((uint8_t)(h >> 8));
+    }
+    const std::vector<float> h = bk.add_bias_last_dim(y, Tensor::from_f16_bytes(hb, {3})).as_f32();
+    ASSERT(h == std::vector<float>({1.5f, 1.0f, 5.0f, 4.5f, 4.0f, 8.0f}), "f16 bias");
+    const std::string e = expect_error([&] { bk.add_bias_last_dim(y, Tensor::from_f32({1.0f, 2.0f}, {2})); });
+    ASSERT(e.find("bias length 2 does not match last dim 3") != std::string::npos, "length error");
 }
 
 static void test_add(HipLlmBackend& bk) {  // elementwise.rs:184-194
@@ -267,6 +302,9 @@ int main() {
     const std::pair<const char*, void (*)(HipLlmBackend&)> tests[] = {
         {"rmsnorm_identity_weight", rmsnorm_identity_weight},
         {"rmsnorm_half_input_outputs_f32", rmsnorm_half_input_outputs_f32},
+        {"layernorm_zero_mean_unit_var", layernorm_zero_mean_unit_var},
+        {"test_gelu_erf", test_gelu_erf},
+        {"add_bias_last_dim_broadcasts", add_bias_last_dim_broadcasts},
         {"test_add", test_add},
         {"test_scalar_broadcast", test_scalar_broadcast},
         {"test_gelu", test_gelu},

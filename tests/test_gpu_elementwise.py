@@ -1,13 +1,18 @@
-"""GPU parity: add, mul, SiLU, SwiGLU and GELU-tanh against the oracle.
+"""GPU parity: add, mul, SiLU, SwiGLU, GELU (tanh and erf forms) and the
+last-dimension bias add against the oracle.
 
 Reference: crates/sapient-backends/cpu/src/kernels/elementwise.rs:27-69 (add/mul and
-broadcast), :120-127 (gelu), :141-143 (silu); SwiGLU = silu then mul (llama.rs:531-532).
+broadcast), :120-127 (gelu), :135-138 with :163-174 (gelu_erf), :141-143 (silu);
+SwiGLU = silu then mul (llama.rs:531-532); bias add
+crates/sapient-models/src/forward/common.rs:556-569.
 
 Tolerances:
   add / mul          bit-exact (one IEEE operation, same rounding)
   SiLU / SwiGLU f32  ≤ 1e-5 relative (hardware exp2 / reciprocal vs glibc expf)
   SiLU / SwiGLU half ≤ 1 ulp of the output format vs the f32 oracle rounded
   GELU (every dtype) bit-exact: the kernel evaluates glibc's own tanhf algorithm
+  erf-GELU (every dtype) bit-exact: glibc's own expf algorithm
+  bias add           bit-exact (one IEEE add)
 """
 import numpy as np
 import pytest
@@ -157,3 +162,113 @@ def test_gelu_phi2_full(dev, orc):
 def test_gelu_kat(dev):
     """elementwise.rs:206-210: gelu(0) = 0."""
     assert ops.gelu_tanh(torch.zeros(1, device=dev)).item() == 0.0
+
+
+def test_gelu_erf_f32_bit_exact(dev, orc):
+    """f32 erf-GELU reproduces glibc's expf bits, so the result equals the oracle exactly."""
+    x = torch.cat([_gen((1 << 20,), 12, dev, 2.0), _gen((1 << 16,), 13, dev, 8.0), torch.from_numpy(SPECIALS).to(dev)])
+    print("case gelu_erf f32", flush=True)
+    assert_bits_equal(to_np(ops.gelu_erf(x)), orc.gelu_erf(to_np(x)), "gelu_erf f32")
+
+
+def test_gelu_erf_matches_wgpu_test_vectors(dev, orc):
+    """wgpu tests/resident.rs:909-930: n = 4096 + 37, lcg · 4; the reference test's bound is 1e-5."""
+    x = WgpuLcg().take(4096 + 37) * np.float32(4.0)
+    got = to_np(ops.gelu_erf(torch.from_numpy(x).to(dev)))
+    assert_bits_equal(got, orc.gelu_erf(x), "gelu_erf wgpu vectors")
+    from math import erf
+    want = np.array([0.5 * t * (1 + erf(t / np.sqrt(2))) for t in x.astype(np.float64)])
+    assert np.abs(got - want).max() < 1e-5
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=IDS)
+def test_gelu_erf_half_exhaustive_bit_exact(dev, orc, dtype):
+    """Every one of the 65536 f16 / bf16 inputs: output bits equal RNE(oracle(widen(x)))."""
+    bits = torch.arange(0, 65536, dtype=torch.int32).to(torch.int16).view(dtype)
+    x = bits.to(dev)
+    print(f"case gelu_erf exhaustive {dtype}", flush=True)
+    got = to_np(ops.gelu_erf(x))
+    ref = orc.gelu_erf(widen(x, orc))
+    want = narrow_bits(ref, dtype, orc)
+    nan = np.isnan(ref)
+    assert_bits16_equal(got[~nan], want[~nan], f"gelu_erf {dtype}")
+    assert (ulp_diff16(got[nan], want[nan], dtype) == 0).all()
+    got2 = to_np(ops.gelu_erf(x[3:]))
+    assert np.array_equal(got2, got[3:])
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=IDS)
+def test_gelu_erf_whisper_full(dev, orc, dtype):
+    """erf-GELU on [1500 · 8, 5120] (Whisper-large FFN width, 8 utterances), inputs ~N(0, 2): bit-exact."""
+    x = _gen((12000, 5120), 62, dev, 2.0, dtype)
+    print(f"case gelu_erf full {dtype}", flush=True)
+    out = ops.gelu_erf(x)
+    torch.cuda.synchronize()
+    ref = orc.gelu_erf(widen(x, orc))
+    if dtype == torch.float32:
+        assert_bits_equal(to_np(out), ref, "gelu_erf full f32")
+    else:
+        assert_bits16_equal(to_np(out), narrow_bits(ref, dtype, orc), f"gelu_erf full {dtype}")
+
+
+def test_gelu_erf_kat(dev):
+    """elementwise.rs:216-224: g(0) = 0, g(1) = 0.8413447, g(-1) = -0.1586553 within 1e-4."""
+    v = ops.gelu_erf(torch.tensor([0.0, 1.0, -1.0], device=dev)).cpu().numpy()
+    assert abs(v[0]) < 1e-6 and abs(v[1] - 0.8413447) < 1e-4 and abs(v[2] + 0.1586553) < 1e-4
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=IDS)
+@pytest.mark.parametrize("bdtype", DTYPES, ids=IDS)
+@pytest.mark.parametrize("rows,n", [(13, 320), (1, 1), (5, 3), (7, 100), (64, 1280), (3, 4096), (2, 8200),
+                                    (1, 65536)])
+def test_add_bias_bit_exact(dev, orc, dtype, bdtype, rows, n):
+    print(f"case add_bias {dtype} bias {bdtype} {rows}x{n}", flush=True)
+    y = _gen((rows, n), 20 + n, dev, dtype=dtype)
+    bias = _gen((n,), 21, dev, dtype=bdtype)
+    got = ops.add_bias(y, bias)
+    want = orc.add_bias_last_dim(widen(y, orc), widen(bias, orc))
+    if dtype == torch.float32:
+        assert_bits_equal(to_np(got), want, "add_bias")
+    else:
+        assert_bits16_equal(to_np(got), narrow_bits(want, dtype, orc), f"add_bias {dtype}")
+
+
+def test_add_bias_matches_wgpu_test_vectors(dev, orc):
+    """wgpu tests/resident.rs:933-951: 13 x 320, lcg; the reference test's bound is 1e-5."""
+    nxt = WgpuLcg()
+    x = nxt.take(13 * 320).reshape(13, 320)
+    bias = nxt.take(320)
+    got = to_np(ops.add_bias(torch.from_numpy(x).to(dev), torch.from_numpy(bias).to(dev)))
+    assert_bits_equal(got, orc.add_bias_last_dim(x, bias), "add_bias wgpu vectors")
+    assert np.abs(got - (x + bias)).max() < 1e-5
+
+
+def test_add_bias_full_in_place_and_unaligned(dev, orc):
+    """16384 x 4096 f32 with an f16 bias (the reference's F32-y / half-bias case), in place; then
+    4-byte-offset views through the scalar path."""
+    y = _gen((16384, 4096), 31, dev)
+    bias = _gen((4096,), 32, dev, dtype=torch.float16)
+    want = orc.add_bias_last_dim(to_np(y), widen(bias, orc))
+    ops.add_bias(y, bias, out=y)
+    torch.cuda.synchronize()
+    assert_bits_equal(to_np(y), want, "add_bias full in place")
+    base = _gen((3 * 640 + 1,), 33, dev)
+    yv = base[1:].view(3, 640)
+    bb = _gen((641,), 34, dev)[1:]
+    got = ops.add_bias(yv, bb)
+    assert_bits_equal(to_np(got), orc.add_bias_last_dim(to_np(yv), to_np(bb)), "add_bias unaligned")
+
+
+def test_add_bias_rejects_bad_arguments(dev):
+    from sapient_amd._lib import EINVAL, lib
+    L = lib()
+    y = torch.zeros(4, 8, device=dev)
+    s = torch.cuda.current_stream().cuda_stream
+    p = y.data_ptr()
+    assert L.sph_add_bias(p, p, 0, p, 0, 32, 5, s) == EINVAL    # total not a multiple of n
+    assert L.sph_add_bias(p, p, 0, p, 0, 32, 0, s) == EINVAL    # n = 0 with data
+    assert L.sph_add_bias(p, p, 8, p, 0, 32, 8, s) == EINVAL    # bias dtype
+    assert L.sph_add_bias(p, None, 0, p, 0, 32, 8, s) == EINVAL  # null bias
+    assert L.sph_add_bias(p, p, 0, p, 0, 0, 8, s) == 0           # empty is a no-op
+    with pytest.raises(ValueError, match="does not match last dim"):
+        ops.add_bias(y, torch.zeros(7, device=dev))

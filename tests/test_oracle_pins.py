@@ -128,6 +128,89 @@ def test_rms_norm_matches_wgpu_test_restatement():
     assert np.abs(oracle.rms_norm(x, w, 1e-5) - want).max() < 1e-4
 
 
+def test_layer_norm_kat():
+    """layernorm.rs:113-123: [[1, 2], [3, 4]], no weight / bias, eps 1e-5 → ±1 within 1e-4."""
+    y = oracle.layer_norm(np.array([[1.0, 2.0], [3.0, 4.0]], np.float32), None, None, 1e-5)
+    assert np.abs(y - np.array([[-1, 1], [-1, 1]], np.float32)).max() < 1e-4
+
+
+def test_layer_norm_serial_two_pass_bit_exact():
+    """Bit-exact against a numpy restatement of the reference's op order: f32
+    serial folds of x and of (x - mean)^2, each / n, 1/sqrt(var + eps), then
+    (x - mean) * inv * w + b."""
+    rng = np.random.default_rng(11)
+    x = (rng.standard_normal((16, 768)) * 3 + 0.5).astype(np.float32)
+    w = (np.float32(0.5) + np.abs(rng.standard_normal(768))).astype(np.float32)
+    b = (rng.standard_normal(768) * 0.1).astype(np.float32)
+    n = np.float32(768)
+    mean = np.add.accumulate(x, axis=1, dtype=np.float32)[:, -1] / n
+    d = (x - mean[:, None]).astype(np.float32)
+    var = np.add.accumulate((d * d).astype(np.float32), axis=1, dtype=np.float32)[:, -1] / n
+    inv = (np.float32(1.0) / np.sqrt((var + np.float32(1e-5)).astype(np.float32))).astype(np.float32)
+    normed = (d * inv[:, None]).astype(np.float32)
+    assert np.array_equal(_bits(oracle.layer_norm(x, w, b, 1e-5)), _bits(((normed * w).astype(np.float32) + b)))
+    assert np.array_equal(_bits(oracle.layer_norm(x, w, None, 1e-5)), _bits((normed * w).astype(np.float32)))
+    assert np.array_equal(_bits(oracle.layer_norm(x, None, b, 1e-5)), _bits((normed + b).astype(np.float32)))
+    assert np.array_equal(_bits(oracle.layer_norm(x, None, None, 1e-5)), _bits(normed))
+
+
+def test_layer_norm_closed_form_and_invariants():
+    """Against float64 math (population variance, eps inside the root); shift
+    invariance; unit weight gives rows of mean 0 and variance 1 / (1 + eps/var)."""
+    rng = np.random.default_rng(12)
+    x = (rng.standard_normal((32, 4096)) * 2 + 3).astype(np.float32)
+    w = rng.standard_normal(4096).astype(np.float32)
+    b = rng.standard_normal(4096).astype(np.float32)
+    x64 = x.astype(np.float64)
+    mu = x64.mean(axis=1, keepdims=True)
+    var = x64.var(axis=1, keepdims=True)  # population variance, divides by n
+    want = (x64 - mu) / np.sqrt(var + 1e-5) * w + b
+    y = oracle.layer_norm(x, w, b, 1e-5).astype(np.float64)
+    # The serial f32 sums move mean and variance by ~1e-6 relative: an error of
+    # |w| · 2e-5 · (1 + |normed|) at most. A variance divided by n - 1 would
+    # shift normed by 1.2e-4 · |normed| and fail.
+    normed = np.abs((x64 - mu) / np.sqrt(var))
+    assert (np.abs(y - want) <= np.abs(w) * 2e-5 * (1 + normed) + np.abs(b) * 2.0 ** -22).all()
+    n1 = (x64 - mu) / np.sqrt(x64.var(axis=1, ddof=1, keepdims=True) + 1e-5) * w + b
+    assert not (np.abs(n1 - want) <= np.abs(w) * 2e-5 * (1 + normed) + np.abs(b) * 2.0 ** -22).all()
+    # a large eps is visible (pins where eps enters)
+    big = (x64 - mu) / np.sqrt(var + 4.0)
+    assert np.abs(oracle.layer_norm(x, None, None, 4.0) - big).max() < 1e-5
+    # unit weight, zero bias: mean 0, variance var / (var + eps)
+    u = oracle.layer_norm(x, None, None, 1e-5).astype(np.float64)
+    assert np.abs(u.mean(axis=1)).max() < 1e-5
+    assert np.allclose(u.var(axis=1), (var / (var + 1e-5))[:, 0], atol=1e-5)
+
+
+def test_layer_norm_matches_wgpu_test_restatement():
+    """wgpu tests/resident.rs:860-886: 7 x 1536, lcg * 3, w = 0.5 + |next()|, b = next() * 0.1, eps 1e-5,
+    max |Δ| < 1e-4 against the test's own f32 restatement (:838-857)."""
+    nxt = WgpuLcg()
+    x = (nxt.take(7 * 1536) * np.float32(3.0)).reshape(7, 1536)
+    w = np.float32(0.5) + np.abs(nxt.take(1536))
+    b = nxt.take(1536) * np.float32(0.1)
+    mean = x.sum(axis=1, dtype=np.float32) / np.float32(1536)
+    var = ((x - mean[:, None]) ** 2).sum(axis=1, dtype=np.float32) / np.float32(1536)
+    want = (x - mean[:, None]) * (np.float32(1.0) / np.sqrt(var + np.float32(1e-5)))[:, None] * w + b
+    assert np.abs(oracle.layer_norm(x, w, b, 1e-5) - want).max() < 1e-4
+
+
+def test_add_bias_last_dim():
+    """common.rs:556-569: bias[i % n] added to every row, exactly (integer-valued
+    data makes every sum exact); a length mismatch is an error; wgpu
+    tests/resident.rs:933-951 data (13 x 320) within 1e-5."""
+    y = np.arange(12, dtype=np.float32).reshape(2, 2, 3)
+    out = oracle.add_bias_last_dim(y, np.float32([100, 200, 300]))
+    assert np.array_equal(out, y + np.float32([100, 200, 300]))
+    with pytest.raises(ValueError, match="does not match last dim"):
+        oracle.add_bias_last_dim(y, np.float32([1, 2]))
+    nxt = WgpuLcg()
+    x = nxt.take(13 * 320).reshape(13, 320)
+    bias = nxt.take(320)
+    assert np.abs(oracle.add_bias_last_dim(x, bias) - (x + bias)).max() < 1e-5
+    assert np.array_equal(_bits(oracle.add_bias_last_dim(x, bias)), _bits((x + bias).astype(np.float32)))
+
+
 def test_add_rms_norm_is_add_then_rms_norm():
     rng = np.random.default_rng(3)
     x, r = rng.standard_normal((2, 8, 256), dtype=np.float32)
@@ -202,6 +285,22 @@ def test_gelu_closed_form_including_cancellation():
     assert np.max(np.abs(y - y64)[calm] / np.maximum(np.abs(y64[calm]), 1e-30)) < 1e-6
     bound = np.abs(0.5 * v64) * 2.0 ** -22 + np.abs(y64) * 2.0 ** -22 + 1e-45
     assert (np.abs(y - y64)[~calm] <= bound[~calm]).all()
+
+
+def test_gelu_erf_abramowitz_stegun_bound():
+    """erf_approx is A&S 7.1.26 (max error 1.5e-7): against float64 erf over a
+    dense grid the oracle stays within 0.5|v| (1.5e-7 + 8 ulp(1)) + 2 ulp(y); a
+    wrong coefficient or a dropped term breaks the bound by orders of magnitude.
+    Odd symmetry of erf: gelu_erf(v) - gelu_erf(-v) = v up to rounding."""
+    from math import erf
+    v = np.linspace(-6, 6, 200001, dtype=np.float32)
+    y = oracle.gelu_erf(v).astype(np.float64)
+    v64 = v.astype(np.float64)
+    want = 0.5 * v64 * (1 + np.array([erf(t / np.sqrt(2)) for t in v64]))
+    bound = 0.5 * np.abs(v64) * (1.5e-7 + 8 * 2.0 ** -23) + np.abs(want) * 2.0 ** -22 + 1e-45
+    assert (np.abs(y - want) <= bound).all()
+    ym = oracle.gelu_erf(-v).astype(np.float64)
+    assert np.max(np.abs((y - ym) - v64)) < 1e-5 * 6
 
 
 def test_gelu_erf_matches_wgpu_test_bound():
