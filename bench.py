@@ -297,7 +297,7 @@ def main():
                    "rows_per_s": round(rows / (avg_ms * 1e-3), 1), "pct_of_peak": round(100 * value / PEAK_GBS, 1)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / PEAK_GBS, 4), "traffic": committed_traffic("add_rms_norm_f32_16384x4096"),
-                     "kernel": "rms_rows_vec<float, float, float, true, 4, 4>", "alg_bytes_per_launch": alg_bytes,
+                     "kernel": "rms_rows_vec<float, float, float, 1, 8, 2, false>", "alg_bytes_per_launch": alg_bytes,
                      "avg_launch_us": round(avg_ms * 1e3, 2)},
         "cpu_baseline": cpu,
     }

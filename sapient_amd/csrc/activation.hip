@@ -35,8 +35,8 @@
 //    32-entry table of 2^(i/32), which each block stages in LDS). Outside
 //    |v| < 16 expf(-x²) underflows to 0, so the band and the outside rule are
 //    the ones of the tanh form.
-//  - Bias add: a block owns a tile of up to 256 16-byte column vectors and a
-//    run of rows; each thread loads its bias vector once and streams the rows.
+//  - Bias add: a block owns a tile of up to 256 16-byte column vectors over
+//    two rows; each thread loads its bias vector once and adds it to both.
 #include <mutex>
 
 #include "glibc_expf.h"
@@ -372,7 +372,9 @@ int gelu_any(const void* x, void* out, int dtype, int64_t n, hipStream_t s) {
 }
 
 // ───────────────────────────── bias add ─────────────────────────────
-constexpr int kBiasRowsPerBlock = 16;
+// Two rows per block, both in flight: measured on MI355X at 16384 x 4096 f32
+// this runs at the speed of a plain two-stream add (16 rows per block: -15 %).
+constexpr int kBiasRowsPerBlock = 2;
 
 // Block b covers column tile b % ntiles (up to 256 16-byte vectors of a row)
 // over rows [(b / ntiles) · R, + R). A thread keeps its bias vector in
@@ -381,7 +383,7 @@ template <typename T, typename TB>
 __global__ __launch_bounds__(kThreads) void bias_rows_vec(const T* y, const TB* bias, T* out, int64_t rows, int nvr,
                                                          int ntiles, int tile) {
     constexpr int E = vec16<T>::n;
-    constexpr int RU = 4;
+    constexpr int RU = 2;
     const int t = (int)(blockIdx.x % (unsigned)ntiles);
     const int64_t r0 = (int64_t)(blockIdx.x / (unsigned)ntiles) * kBiasRowsPerBlock;
     const int v = t * tile + (int)threadIdx.x;

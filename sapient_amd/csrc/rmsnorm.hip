@@ -67,90 +67,166 @@ __device__ __forceinline__ float row_sum(float v, float (*partial)[WPB], int slo
     return v;
 }
 
+// 16 bytes of T as f32 values.
+template <typename T, int E>
+__device__ __forceinline__ void unpack16(const u32x4& q, float (&v)[E]) {
+    const uint32_t raw[4] = {q.x, q.y, q.z, q.w};
+    if constexpr (sizeof(T) == 4) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = __uint_as_float(raw[i]);
+    } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = widen(T{(uint16_t)(raw[i / 2] >> (16 * (i & 1)))});
+    }
+}
+
 // W waves per row, VPT 16-byte vectors per lane, RPB rows per block.
-template <typename TX, typename TW, typename TO, int KIND, int W, int VPT>
+//  LOOP = false: block b owns row b·RPB + wave/W; weight and bias are read at
+//    the output stage (the lowest register footprint).
+//  LOOP = true: block b walks rows b·RPB, + step, ... (step = gridDim.x · RPB)
+//    with weight and bias held in registers across its rows and the next
+//    row's raw vectors loaded before the current row is reduced. Used where a
+//    grid of a few blocks per CU re-reads the weights less than one block per
+//    row would (LayerNorm: weight and bias rows).
+template <typename TX, typename TW, typename TO, int KIND, int W, int VPT, bool LOOP>
 __global__ __launch_bounds__(W >= 4 ? 64 * W : 256) void rms_rows_vec(const TX* __restrict__ x, TX* __restrict__ residual,
                                                                    const TW* __restrict__ w, const TW* __restrict__ bias,
                                                                    TO* __restrict__ out, int64_t rows, int dim, float eps) {
     constexpr int E = vec16<TX>::n;  // elements per 16-byte access of x
     constexpr int WPB = W >= 4 ? W : 4;
     constexpr int RPB = WPB / W;
-    __shared__ float partial[2][WPB];
+    // Two buffers, alternating by row: a wave still reading row i's partials
+    // cannot be overtaken by row i + 2's writes (row i + 1's barrier lies between).
+    __shared__ float partial[2][2][WPB];
     const int lane = threadIdx.x & (kWave - 1);
     const int wv = threadIdx.x / kWave;
     const int sub = wv % W;  // this wave's share of the row
-    const int64_t row = (int64_t)blockIdx.x * RPB + wv / W;
-    const bool live = row < rows;
     const int nvec = dim / E;
-    const size_t base = (size_t)row * (size_t)dim;
+    const bool has_w = w != nullptr, has_b = bias != nullptr;
 
-    float r[VPT][E];
-    float ss = 0.0f;
-    if (live) {
+    auto load_wb = [&](int j, float (&wj)[E], float (&bj)[E]) {
+        const int v = (sub * VPT + j) * kWave + lane;
+        if (v < nvec && has_w) {
+            load_f32<TW, E>(w + (size_t)v * E, wj);
+        } else {
+#pragma unroll
+            for (int e = 0; e < E; ++e) wj[e] = 1.0f;
+        }
+        if (v < nvec && KIND == K_LAYER && has_b) {
+            load_f32<TW, E>(bias + (size_t)v * E, bj);
+        } else {
+#pragma unroll
+            for (int e = 0; e < E; ++e) bj[e] = 0.0f;
+        }
+    };
+    auto fetch = [&](int64_t row, u32x4 (&vx)[VPT], u32x4 (&vres)[VPT]) {
+        if (row >= rows) return;
+        const size_t base = (size_t)row * (size_t)dim;
 #pragma unroll
         for (int j = 0; j < VPT; ++j) {
             const int v = (sub * VPT + j) * kWave + lane;
             if (v < nvec) {
-                load_f32<TX, E, true>(x + base + (size_t)v * E, r[j]);
-                if constexpr (KIND == K_ADD_RMS) {
-                    float b[E];
-                    load_f32<TX, E, true>(residual + base + (size_t)v * E, b);
-#pragma unroll
-                    for (int e = 0; e < E; ++e) r[j][e] = r[j][e] + b[e];
-                    store_f32<TX, E, true>(residual + base + (size_t)v * E, r[j]);
-                }
-#pragma unroll
-                for (int e = 0; e < E; ++e) {
-                    if constexpr (KIND == K_LAYER) ss = ss + r[j][e];
-                    else ss = ss + r[j][e] * r[j][e];
-                }
+                vx[j] = vload<true>(reinterpret_cast<const u32x4*>(x + base + (size_t)v * E));
+                if constexpr (KIND == K_ADD_RMS)
+                    vres[j] = vload<true>(reinterpret_cast<const u32x4*>(residual + base + (size_t)v * E));
             }
         }
-    }
-    ss = row_sum<W, WPB>(ss, partial, 0, lane, wv);
-    float mean = 0.0f, inv;
-    if constexpr (KIND == K_LAYER) {
-        mean = ss / (float)dim;
-        float vs = 0.0f;
+    };
+    // One row from its raw vectors: sums, reductions, output. `wr`/`br` are
+    // the held weights (LOOP) or unused (weights read at the output stage).
+    auto row_body = [&](int64_t row, const u32x4 (&cx)[VPT], const u32x4 (&cres)[VPT], int par,
+                        const float (*wr)[E], const float (*br)[E]) {
+        const bool live = row < rows;
+        const size_t base = (size_t)row * (size_t)dim;
+        float r[VPT][E];
+        float ss = 0.0f;
         if (live) {
 #pragma unroll
             for (int j = 0; j < VPT; ++j) {
                 const int v = (sub * VPT + j) * kWave + lane;
                 if (v < nvec) {
+                    unpack16<TX, E>(cx[j], r[j]);
+                    if constexpr (KIND == K_ADD_RMS) {
+                        float b[E];
+                        unpack16<TX, E>(cres[j], b);
 #pragma unroll
-                    for (int e = 0; e < E; ++e) vs = vs + (r[j][e] - mean) * (r[j][e] - mean);
+                        for (int e = 0; e < E; ++e) r[j][e] = r[j][e] + b[e];
+                        store_f32<TX, E, true>(residual + base + (size_t)v * E, r[j]);
+                    }
+#pragma unroll
+                    for (int e = 0; e < E; ++e) {
+                        if constexpr (KIND == K_LAYER) ss = ss + r[j][e];
+                        else ss = ss + r[j][e] * r[j][e];
+                    }
                 }
             }
         }
-        vs = row_sum<W, WPB>(vs, partial, 1, lane, wv);
-        inv = 1.0f / sqrtf(vs / (float)dim + eps);
-    } else {
-        inv = 1.0f / sqrtf(ss / (float)dim + eps);
-    }
-    if (!live) return;
-    const bool has_w = w != nullptr, has_b = bias != nullptr;
+        ss = row_sum<W, WPB>(ss, partial[par], 0, lane, wv);
+        float mean = 0.0f, inv;
+        if constexpr (KIND == K_LAYER) {
+            mean = ss / (float)dim;
+            float vs = 0.0f;
+            if (live) {
+#pragma unroll
+                for (int j = 0; j < VPT; ++j) {
+                    const int v = (sub * VPT + j) * kWave + lane;
+                    if (v < nvec) {
+#pragma unroll
+                        for (int e = 0; e < E; ++e) vs = vs + (r[j][e] - mean) * (r[j][e] - mean);
+                    }
+                }
+            }
+            vs = row_sum<W, WPB>(vs, partial[par], 1, lane, wv);
+            inv = 1.0f / sqrtf(vs / (float)dim + eps);
+        } else {
+            inv = 1.0f / sqrtf(ss / (float)dim + eps);
+        }
+        if (!live) return;
+#pragma unroll
+        for (int j = 0; j < VPT; ++j) {
+            const int v = (sub * VPT + j) * kWave + lane;
+            if (v < nvec) {
+                float wj[E], bj[E];
+                if constexpr (LOOP) {
+#pragma unroll
+                    for (int e = 0; e < E; ++e) {
+                        wj[e] = wr[j][e];
+                        bj[e] = br[j][e];
+                    }
+                } else {
+                    load_wb(j, wj, bj);
+                }
+                float y[E];
+#pragma unroll
+                for (int e = 0; e < E; ++e) y[e] = norm_out<KIND>(r[j][e], mean, inv, wj[e], bj[e], has_w, has_b);
+                store_f32<TO, E, true>(out + base + (size_t)v * E, y);
+            }
+        }
+    };
 
+    const int64_t first = (int64_t)blockIdx.x * RPB;
+    if constexpr (!LOOP) {
+        u32x4 cx[VPT], cres[VPT];
+        fetch(first + wv / W, cx, cres);
+        row_body(first + wv / W, cx, cres, 0, nullptr, nullptr);
+    } else {
+        float wr[VPT][E], br[VPT][E];
 #pragma unroll
-    for (int j = 0; j < VPT; ++j) {
-        const int v = (sub * VPT + j) * kWave + lane;
-        if (v < nvec) {
-            float wv_[E], bv[E];
-            if (has_w) {
-                load_f32<TW, E>(w + (size_t)v * E, wv_);
-            } else {
+        for (int j = 0; j < VPT; ++j) load_wb(j, wr[j], br[j]);
+        const int64_t step = (int64_t)gridDim.x * RPB;
+        u32x4 nx[VPT], nres[VPT];
+        fetch(first + wv / W, nx, nres);
+        int par = 0;
+        for (int64_t row0 = first; row0 < rows; row0 += step, par ^= 1) {  // trip count uniform over the block
+            const int64_t row = row0 + wv / W;
+            u32x4 cx[VPT], cres[VPT];
 #pragma unroll
-                for (int e = 0; e < E; ++e) wv_[e] = 1.0f;
+            for (int j = 0; j < VPT; ++j) {
+                cx[j] = nx[j];
+                cres[j] = nres[j];
             }
-            if (KIND == K_LAYER && has_b) {
-                load_f32<TW, E>(bias + (size_t)v * E, bv);
-            } else {
-#pragma unroll
-                for (int e = 0; e < E; ++e) bv[e] = 0.0f;
-            }
-            float y[E];
-#pragma unroll
-            for (int e = 0; e < E; ++e) y[e] = norm_out<KIND>(r[j][e], mean, inv, wv_[e], bv[e], has_w, has_b);
-            store_f32<TO, E, true>(out + base + (size_t)v * E, y);
+            fetch(row + step, nx, nres);
+            row_body(row, cx, cres, par, wr, br);
         }
     }
 }
@@ -202,21 +278,47 @@ __global__ __launch_bounds__(256) void rms_rows_generic(const TX* __restrict__ x
     }
 }
 
+template <typename TX, typename TW, typename TO, int KIND, int VPT, bool LOOP>
+void launch_vec(int W, dim3 grid, int threads, const TX* xp, TX* rp, const TW* wp, const TW* bp, TO* op, int64_t nr, int d,
+                float eps, hipStream_t stream) {
+    switch (W) {
+    case 1: rms_rows_vec<TX, TW, TO, KIND, 1, VPT, LOOP><<<grid, threads, 0, stream>>>(xp, rp, wp, bp, op, nr, d, eps); break;
+    case 2: rms_rows_vec<TX, TW, TO, KIND, 2, VPT, LOOP><<<grid, threads, 0, stream>>>(xp, rp, wp, bp, op, nr, d, eps); break;
+    case 4: rms_rows_vec<TX, TW, TO, KIND, 4, VPT, LOOP><<<grid, threads, 0, stream>>>(xp, rp, wp, bp, op, nr, d, eps); break;
+    case 8: rms_rows_vec<TX, TW, TO, KIND, 8, VPT, LOOP><<<grid, threads, 0, stream>>>(xp, rp, wp, bp, op, nr, d, eps); break;
+    default: rms_rows_vec<TX, TW, TO, KIND, 16, VPT, LOOP><<<grid, threads, 0, stream>>>(xp, rp, wp, bp, op, nr, d, eps); break;
+    }
+}
+
 template <typename TX, typename TW, typename TO, int KIND>
 int launch_rms(const void* x, void* residual, const void* w, const void* bias, void* out, int64_t rows, int64_t dim,
                float eps, hipStream_t stream) {
     if (rows == 0 || dim == 0) return SPH_OK;
     constexpr int E = vec16<TX>::n;
     constexpr bool FUSED = KIND == K_ADD_RMS;
-    // Vector path: ~16 values per lane, W waves per row (W <= 16).
-    constexpr int VPT = 16 / E;
+    // Values per lane (measured at 16384 x 4096 on MI355X): 8 for f32 and for
+    // the fused half kernel, 16 for the other half kernels; twice that for rows
+    // too wide for 16 waves.
+    constexpr int VPT = (sizeof(TX) == 2 && KIND != K_ADD_RMS) ? 2 : 8 / E;
     const int64_t nvec = dim / E;
     int W = 1;
     while (W < 16 && nvec > (int64_t)kWave * VPT * W) W *= 2;
+    const bool wide = nvec > (int64_t)kWave * VPT * W;  // needs 2 VPT at W = 16
     const bool vec_ok = dim % E == 0 && aligned(x, 16) && aligned(out, 16) &&
                         (!FUSED || aligned(residual, 16)) && (w == nullptr || aligned(w, 16)) &&
-                        (bias == nullptr || aligned(bias, 16)) && nvec <= (int64_t)kWave * VPT * W &&
+                        (bias == nullptr || aligned(bias, 16)) && nvec <= (int64_t)kWave * 2 * VPT * 16 &&
                         dim <= INT32_MAX;
+    const int rpb = W >= 4 ? 1 : 4 / W;
+    const int threads = W >= 4 ? kWave * W : 256;
+    // LayerNorm loops each block over rows (16 resident waves per CU), keeping
+    // weight and bias in registers; the RMSNorm kernels give every block one row.
+    constexpr bool kLoop = KIND == K_LAYER;  // the wide variant never loops (register budget)
+    int64_t max_blocks = INT64_MAX;
+    if (kLoop && !wide) {
+        const int cus = device_cu_count();
+        const int waves_per_block = threads / kWave;  // 4, 8 or 16
+        if (cus > 0) max_blocks = (int64_t)cus * (16 / waves_per_block);
+    }
     // A launch covers at most 2^22 rows, keeping grid x block below 2^32 work-items.
     constexpr int64_t kChunk = int64_t(1) << 22;
     for (int64_t r0 = 0; r0 < rows; r0 += kChunk) {
@@ -228,17 +330,13 @@ int launch_rms(const void* x, void* residual, const void* w, const void* bias, v
         const TW* bp = static_cast<const TW*>(bias);
         TO* op = static_cast<TO*>(out) + off;
         if (vec_ok) {
-            const int rpb = W >= 4 ? 1 : 4 / W;
-            const dim3 grid((unsigned)((nr + rpb - 1) / rpb));
-            const int threads = W >= 4 ? kWave * W : 256;
-            const int d = (int)dim;
-            switch (W) {
-            case 1: rms_rows_vec<TX, TW, TO, KIND, 1, VPT><<<grid, threads, 0, stream>>>(xp, rp, wp, bp, op, nr, d, eps); break;
-            case 2: rms_rows_vec<TX, TW, TO, KIND, 2, VPT><<<grid, threads, 0, stream>>>(xp, rp, wp, bp, op, nr, d, eps); break;
-            case 4: rms_rows_vec<TX, TW, TO, KIND, 4, VPT><<<grid, threads, 0, stream>>>(xp, rp, wp, bp, op, nr, d, eps); break;
-            case 8: rms_rows_vec<TX, TW, TO, KIND, 8, VPT><<<grid, threads, 0, stream>>>(xp, rp, wp, bp, op, nr, d, eps); break;
-            default: rms_rows_vec<TX, TW, TO, KIND, 16, VPT><<<grid, threads, 0, stream>>>(xp, rp, wp, bp, op, nr, d, eps); break;
-            }
+            int64_t nb = (nr + rpb - 1) / rpb;
+            if (nb > max_blocks) nb = max_blocks;
+            const dim3 grid((unsigned)nb);
+            if (!wide)
+                launch_vec<TX, TW, TO, KIND, VPT, kLoop>(W, grid, threads, xp, rp, wp, bp, op, nr, (int)dim, eps, stream);
+            else
+                launch_vec<TX, TW, TO, KIND, 2 * VPT, false>(16, grid, threads, xp, rp, wp, bp, op, nr, (int)dim, eps, stream);
         } else {
             rms_rows_generic<TX, TW, TO, KIND><<<dim3((unsigned)nr), 256, 0, stream>>>(xp, rp, wp, bp, op, nr, dim, eps);
         }

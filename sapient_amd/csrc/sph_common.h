@@ -125,15 +125,33 @@ __device__ __forceinline__ void store_f32(T* __restrict__ p, const float (&v)[N]
     }
 }
 
-// Butterfly sum over the 64 lanes of a wave. Every lane ends with the same
-// bits: each step adds the same two operands in either order.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
+}
+
+__device__ __forceinline__ float lane_value(float v, int lane) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
+
+// Sum over the 64 lanes of a wave (all lanes active), returned to every lane.
+// Within each 16-lane row four DPP steps pair lanes symmetrically (xor 1,
+// xor 2, mirror within 8, mirror within 16), so each step adds the same two
+// operands in either order and all 16 lanes hold identical bits; the four
+// row sums are then read as scalars and added in a fixed order. DPP moves are
+// VALU operations, several times quicker than LDS-routed shuffles.
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int m = 32; m > 0; m >>= 1) v += __shfl_xor(v, m, 64);
-    return v;
+    v = v + dpp_mov<0xb1>(v);   // quad_perm [1,0,3,2]
+    v = v + dpp_mov<0x4e>(v);   // quad_perm [2,3,0,1]
+    v = v + dpp_mov<0x141>(v);  // row_half_mirror
+    v = v + dpp_mov<0x140>(v);  // row_mirror
+    return (lane_value(v, 0) + lane_value(v, 16)) + (lane_value(v, 32) + lane_value(v, 48));
 }
 
 // ─────────────────────────────── host side ───────────────────────────────
+// Compute units of the current device (cached per device); 0 if unknown.
+__attribute__((visibility("hidden"))) int device_cu_count();
+
 inline bool aligned(const void* p, size_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
 inline bool is_float_dtype(int dt) { return dt == SPH_F32 || dt == SPH_F16 || dt == SPH_BF16; }
 inline size_t dtype_size(int dt) { return dt == SPH_F32 ? 4 : 2; }
