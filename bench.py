@@ -182,6 +182,17 @@ def op_table(torch, ops, dev, only=None):
             lambda dt=dt: [(gen(torch, (12000, 5120), 170 + i, dev, dt, 2.0), torch.empty(12000, 5120, device=dev, dtype=dt))
                            for i in range(3)],
             lambda s: ops.gelu_erf(s[0], out=s[1]))
+    # Decode-chain helpers: head transpose of a Llama-3-8B prefill Q, KV-cache append of its K
+    T, H, D = 8192, 32, 128
+    for dt, tag, es in ((f32, "f32", 4), (f16, "f16", 2)):
+        run("transpose_heads", f"{T}x{H}x{D}", tag, 2 * T * H * D * es, T, "tokens",
+            lambda dt=dt: [(gen(torch, (T, H, D), 180 + i, dev, dt), torch.empty(H, T, D, device=dev, dtype=dt))
+                           for i in range(3)],
+            lambda s: ops.transpose_heads(s[0], out=s[1]))
+    run("kv_append", f"8x{T}x{D} -> cache 8x{T}x{D}", "f32->f16", 8 * T * D * (4 + 2), T, "tokens",
+        lambda: [(gen(torch, (8, T, D), 190 + i, dev, f32), torch.empty(8, T, D, device=dev, dtype=f16))
+                 for i in range(3)],
+        lambda s: ops.kv_append(s[0], s[1], 0))
     # C5: Q4_K embedding gather, 128256 x 4096 table, 65536 ids (uniform, Zipf 1.1)
     vocab, hidden, n_ids = 128256, 4096, 65536
     nb = vocab * hidden // 256

@@ -35,7 +35,7 @@ extern "C" {
 #define SPH_OK 0
 #define SPH_EINVAL (-1)  /* null pointer, unsupported dtype, bad shape or alignment */
 #define SPH_EHIP (-2)    /* the HIP runtime reported an error while enqueueing */
-#define SPH_ERANGE (-3)  /* a token id is outside [0, vocab) */
+#define SPH_ERANGE (-3)  /* a token id is outside [0, vocab), or cache positions past max_seq */
 #define SPH_ENODEV (-4)  /* no usable gfx950 device is current */
 
 /* Element / table types. The values are GGUF tensor type ids
@@ -161,6 +161,24 @@ int sph_rope(void* q, int64_t n_q_heads, void* k, int64_t n_k_heads, int dtype, 
  * as the reference does (common.rs:171-173). */
 int sph_embed(const void* table, int table_dtype, int64_t vocab, int64_t hidden,
               const uint32_t* ids, int64_t n_ids, float* out, int32_t* bad_id_flag, void* stream);
+
+/* Swap the two leading axes: x [outer, inner, head_dim] → out [inner, outer,
+ * head_dim], head_dim-element rows moving as units (the matmul layout
+ * [seq, heads, hd] ↔ the attention layout [heads, seq, hd]). Replaces
+ * WgpuContext::transpose_heads (crates/sapient-backends/wgpu/src/resident.rs:420-458).
+ * dtype ∈ {F32, F16, BF16}; elements are moved bit for bit. `out` must not
+ * overlap `x`. outer · inner < 2^32. */
+int sph_transpose_heads(const void* x, void* out, int dtype, int64_t outer, int64_t inner, int64_t head_dim,
+                        void* stream);
+
+/* KV-cache append: src [n_kv, seq, head_dim] (heads-major) is written to
+ * positions pos .. pos+seq-1 of cache [n_kv, max_seq, head_dim], converted to
+ * the cache's type (f32 → f16 / bf16 rounds to nearest-even). seq = 1 is a
+ * decode step, seq > 1 a batched prefill. Replaces WgpuContext::kv_append
+ * (resident.rs:645-711). src_dtype, cache_dtype ∈ {F32, F16, BF16};
+ * pos + seq > max_seq returns SPH_ERANGE without writing. */
+int sph_kv_append(const void* src, int src_dtype, void* cache, int cache_dtype, int64_t n_kv, int64_t seq,
+                  int64_t head_dim, int64_t max_seq, int64_t pos, void* stream);
 
 #ifdef __cplusplus
 }

@@ -62,6 +62,8 @@ def lib() -> C.CDLL:
             "sor_row_bytes": (sz, [C.c_int, sz]),
             "sor_embed_tokens": (C.c_int, [vp, C.c_int, sz, sz, vp, sz, vp]),
             "sor_quantize_q8_0": (None, [vp, sz, vp]),
+            "sor_transpose_heads": (None, [vp, vp, sz, sz, sz, sz]),
+            "sor_kv_append": (C.c_int, [vp, vp, C.c_int, sz, sz, sz, sz, sz]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -275,3 +277,29 @@ def quantize_q8_0(x) -> np.ndarray:
     out = np.empty(x.size // 32 * 34, np.uint8)
     lib().sor_quantize_q8_0(_p(x), x.size // 32, _p(out))
     return out
+
+
+def transpose_heads(x, outer: int, inner: int, head_dim: int) -> np.ndarray:
+    """resident.rs:420-458: [outer, inner, hd] -> [inner, outer, hd]; any 2- or
+    4-byte element array (half tensors as uint16 bits) is moved as raw bytes."""
+    x = np.ascontiguousarray(x)
+    if x.size != outer * inner * head_dim or x.itemsize not in (2, 4):
+        raise ValueError("x must hold outer * inner * head_dim 2- or 4-byte elements")
+    out = np.empty((inner, outer, head_dim), x.dtype)
+    lib().sor_transpose_heads(_p(x), _p(out), x.itemsize, outer, inner, head_dim)
+    return out
+
+
+def kv_append(src, cache: np.ndarray, cache_dtype: int, n_kv: int, seq: int, head_dim: int, max_seq: int,
+              pos: int) -> None:
+    """resident.rs:645-711, in place on `cache` ([n_kv, max_seq, hd]; float32, or
+    uint16 bits for F16 / BF16)."""
+    src = _f32(src)
+    if src.size != n_kv * seq * head_dim or cache.size != n_kv * max_seq * head_dim or not cache.flags.c_contiguous:
+        raise ValueError("src / cache sizes do not match the layout")
+    want = np.float32 if cache_dtype == 0 else np.uint16
+    if cache.dtype != want:
+        raise ValueError("cache dtype does not match cache_dtype")
+    st = lib().sor_kv_append(_p(src), _p(cache), cache_dtype, n_kv, seq, head_dim, max_seq, pos)
+    if st != 0:
+        raise OracleError(st, "kv_append")

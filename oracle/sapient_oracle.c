@@ -492,3 +492,38 @@ void sor_quantize_q8_0(const float* x, size_t nblocks, uint8_t* out) {
         }
     }
 }
+
+/* ─────────────── device-resident decode helpers (layout moves) ───────────────
+ * transpose_heads: crates/sapient-backends/wgpu/src/resident.rs:420-458 with
+ * shaders/transpose_heads.wgsl — the two leading axes of [outer, inner, hd]
+ * swapped, hd-element rows moved as units: out[i][o][c] = x[o][i][c]. Elements
+ * are moved as raw bytes (esize 2 or 4), so any element type passes through. */
+void sor_transpose_heads(const void* x, void* out, size_t esize, size_t outer, size_t inner, size_t hd) {
+    const uint8_t* src = (const uint8_t*)x;
+    uint8_t* dst = (uint8_t*)out;
+    for (size_t o = 0; o < outer; o++)
+        for (size_t i = 0; i < inner; i++)
+            memcpy(dst + (i * outer + o) * hd * esize, src + (o * inner + i) * hd * esize, hd * esize);
+}
+
+/* kv_append: resident.rs:645-711 with shaders/kv_append.wgsl and
+ * kv_append_f16.wgsl — src [n_kv, seq, hd] (heads-major) written to positions
+ * pos..pos+seq of the cache [n_kv, max_seq, hd], converted to the cache's
+ * element type: f32 as is, f16 / bf16 rounded to nearest-even (the reference
+ * test's host mirror stores half::f16::from_f32(x), tests/resident.rs:365-371).
+ * pos + seq > max_seq is the reference's debug assertion (:681): SOR_ERANGE. */
+int sor_kv_append(const float* src, void* cache, int cache_dtype, size_t n_kv, size_t seq, size_t hd,
+                  size_t max_seq, size_t pos) {
+    if (pos + seq > max_seq) return SOR_ERANGE;
+    if (cache_dtype != SOR_F32 && cache_dtype != SOR_F16 && cache_dtype != SOR_BF16) return SOR_EINVAL;
+    for (size_t h = 0; h < n_kv; h++)
+        for (size_t s = 0; s < seq; s++)
+            for (size_t c = 0; c < hd; c++) {
+                const float v = src[(h * seq + s) * hd + c];
+                const size_t d = (h * max_seq + pos + s) * hd + c;
+                if (cache_dtype == SOR_F32) ((float*)cache)[d] = v;
+                else if (cache_dtype == SOR_F16) ((uint16_t*)cache)[d] = sor_f32_to_f16(v);
+                else ((uint16_t*)cache)[d] = sor_f32_to_bf16(v);
+            }
+    return SOR_OK;
+}

@@ -11,7 +11,7 @@ extern "C" const char* sph_status_string(int status) {
     case SPH_OK: return "ok";
     case SPH_EINVAL: return "invalid argument (null pointer, dtype, shape or alignment)";
     case SPH_EHIP: return "HIP runtime error while enqueueing work";
-    case SPH_ERANGE: return "token id out of vocab range";
+    case SPH_ERANGE: return "index out of range (token id >= vocab, or cache positions past max_seq)";
     case SPH_ENODEV: return "no usable gfx950 device";
     default: return "unknown status";
     }

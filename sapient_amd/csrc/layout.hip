@@ -1,0 +1,175 @@
+// layout.hip — the device-resident decode helpers: head transposes and the
+// KV-cache append, for gfx950.
+//
+// Reference (crates/sapient-backends/wgpu/src/resident.rs):
+//   transpose_heads  [outer, inner, hd] → [inner, outer, hd]          (:420-458)
+//   kv_append        src [n_kv, seq, hd] → cache[:, pos:pos+seq, :]
+//                    of [n_kv, max_seq, hd], converted to the cache type (:645-711)
+//
+// Both are moves of hd-element rows between two row orders, so one kernel
+// serves both: each thread moves one 16-byte access of the wider side (f32: 4
+// elements, halves: 8; an f32 → half move reads 16 B and writes 8 B),
+// non-temporal, with a per-row index map. The transpose walks 8 × 8 tiles of
+// (outer, inner) rows, so a block's reads cover 8 runs of 8 consecutive
+// source rows and its writes 8 runs of 8 consecutive output rows (measured at
+// [8192, 32, 128] f32: 72 µs walking output rows with two 16-byte accesses per
+// thread, 47.5 µs with one, 45.3 µs with tiles). The append walks source rows
+// (reads contiguous, writes contiguous within each head's run of seq rows).
+// Same-type moves copy raw bits (NaN payloads included); f32 → f16 / bf16
+// rounds to nearest-even, the conversion the reference's host mirror applies
+// (half::f16::from_f32). HBM-bound: read + write once per element.
+#include <type_traits>
+
+#include "sph_common.h"
+
+namespace sph {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr uint32_t kTile = 8;  // transpose tiles: 8 outer x 8 inner rows
+
+enum Map { M_TRANSPOSE = 0, M_KV = 1 };
+
+// Row index map. TRANSPOSE: a = outer, b = inner, row = a tile-ordered row
+// index (see tile_row). KV: walk source rows r = h·seq + s, destination row
+// h·max_seq + pos + s (a = seq, b = max_seq, c = pos).
+struct RowMap {
+    uint32_t a, b;
+    uint64_t c;
+};
+
+// Rows of one call number fewer than 2^32 (checked on the host), so the
+// splits are 32-bit divisions. Returns false for the padding rows of edge tiles.
+template <int MAP>
+__device__ __forceinline__ bool map_row(uint32_t row, const RowMap& m, uint64_t& srow, uint64_t& drow) {
+    if constexpr (MAP == M_TRANSPOSE) {
+        // row = tile · 64 + w; tiles in output order (inner-tile major), and
+        // inside a tile w = wi · 8 + wo, so consecutive rows are consecutive outputs.
+        const uint32_t tiles_o = (m.a + kTile - 1) / kTile;
+        const uint32_t tile = row / (kTile * kTile), w = row % (kTile * kTile);
+        const uint32_t ti = tile / tiles_o, to = tile - ti * tiles_o;
+        const uint32_t o = to * kTile + w % kTile, i = ti * kTile + w / kTile;
+        if (o >= m.a || i >= m.b) return false;
+        srow = (uint64_t)o * m.b + i;
+        drow = (uint64_t)i * m.a + o;
+    } else {
+        const uint32_t hi = row / m.a, lo = row - hi * m.a;
+        srow = row;
+        drow = (uint64_t)hi * m.b + m.c + lo;
+    }
+    return true;
+}
+
+template <typename TS, typename TD>
+struct MoveWidth {
+    static constexpr int n = 16 / (int)(sizeof(TS) > sizeof(TD) ? sizeof(TS) : sizeof(TD));
+};
+
+template <typename TS, typename TD>
+__device__ __forceinline__ void move_chunk(const TS* s, TD* d) {
+    constexpr int E = MoveWidth<TS, TD>::n;
+    if constexpr (std::is_same<TS, TD>::value) {
+        vstore<true>(reinterpret_cast<u32x4*>(d), vload<true>(reinterpret_cast<const u32x4*>(s)));
+    } else {
+        float v[E];
+        load_f32<TS, E, true>(s, v);
+        store_f32<TD, E, true>(d, v);
+    }
+}
+
+// Vector path: hd a multiple of the chunk width, both bases 16-byte aligned;
+// rows [row0, row0 + items / cpr) of this launch, cpr chunks per row.
+template <typename TS, typename TD, int MAP>
+__global__ __launch_bounds__(kThreads) void move_rows_vec(const TS* __restrict__ src, TD* __restrict__ dst,
+                                                          uint32_t items, uint32_t cpr, uint32_t row0, RowMap m) {
+    constexpr int E = MoveWidth<TS, TD>::n;
+    const uint32_t k = blockIdx.x * kThreads + threadIdx.x;
+    if (k >= items) return;
+    const uint32_t r = k / cpr;
+    const uint32_t c = (k - r * cpr) * E;
+    uint64_t srow, drow;
+    if (!map_row<MAP>(row0 + r, m, srow, drow)) return;
+    const uint64_t hd = (uint64_t)cpr * E;
+    move_chunk(src + srow * hd + c, dst + drow * hd + c);
+}
+
+// Any hd / alignment: one element per thread.
+template <typename TS, typename TD, int MAP>
+__global__ __launch_bounds__(kThreads) void move_rows_scalar(const TS* __restrict__ src, TD* __restrict__ dst,
+                                                             uint32_t items, uint32_t hd, uint32_t row0, RowMap m) {
+    const uint32_t k = blockIdx.x * kThreads + threadIdx.x;
+    if (k >= items) return;
+    const uint32_t r = k / hd;
+    const uint32_t c = k - r * hd;
+    uint64_t srow, drow;
+    if (!map_row<MAP>(row0 + r, m, srow, drow)) return;
+    if constexpr (std::is_same<TS, TD>::value) dst[drow * hd + c] = src[srow * hd + c];
+    else dst[drow * hd + c] = narrow<TD>(widen(src[srow * hd + c]));
+}
+
+// `rows` = rows of the walk (the transpose's includes edge-tile padding).
+template <typename TS, typename TD, int MAP>
+int launch_move(const void* src, void* dst, uint64_t rows, uint64_t hd, RowMap m, hipStream_t stream) {
+    if (rows == 0 || hd == 0) return SPH_OK;
+    if (hd > (1u << 24) || rows > UINT32_MAX) return SPH_EINVAL;
+    constexpr int E = MoveWidth<TS, TD>::n;
+    const TS* s = static_cast<const TS*>(src);
+    TD* d = static_cast<TD*>(dst);
+    const bool vec = hd % E == 0 && aligned(src, 16) && aligned(dst, 16);
+    const uint64_t per_row = vec ? hd / E : hd;  // work items per row
+    // Each launch covers whole rows (whole tiles for the transpose) and fewer than 2^31 work items.
+    uint64_t rows_per_launch = ((uint64_t)1 << 31) / per_row;
+    if (MAP == M_TRANSPOSE) rows_per_launch -= rows_per_launch % (kTile * kTile);
+    for (uint64_t r0 = 0; r0 < rows; r0 += rows_per_launch) {
+        const uint64_t nr = rows - r0 < rows_per_launch ? rows - r0 : rows_per_launch;
+        const uint32_t items = (uint32_t)(nr * per_row);
+        const dim3 grid((items + kThreads - 1) / kThreads);
+        if (vec)
+            move_rows_vec<TS, TD, MAP><<<grid, kThreads, 0, stream>>>(s, d, items, (uint32_t)per_row, (uint32_t)r0, m);
+        else
+            move_rows_scalar<TS, TD, MAP><<<grid, kThreads, 0, stream>>>(s, d, items, (uint32_t)hd, (uint32_t)r0, m);
+        const int st = launch_status();
+        if (st != SPH_OK) return st;
+    }
+    return SPH_OK;
+}
+
+}  // namespace
+}  // namespace sph
+
+extern "C" int sph_transpose_heads(const void* x, void* out, int dtype, int64_t outer, int64_t inner,
+                                   int64_t head_dim, void* stream) {
+    if (outer < 0 || inner < 0 || head_dim < 0 || !sph::is_float_dtype(dtype)) return SPH_EINVAL;
+    const uint64_t rows = (uint64_t)outer * (uint64_t)inner;
+    if (rows == 0 || head_dim == 0) return SPH_OK;
+    if (x == nullptr || out == nullptr || x == out) return SPH_EINVAL;
+    if (outer > UINT32_MAX || inner > UINT32_MAX) return SPH_EINVAL;
+    // The walk covers whole 8 x 8 tiles; padding rows are skipped in the kernel.
+    const uint64_t t = sph::kTile;
+    const uint64_t walk = (((uint64_t)outer + t - 1) / t) * (((uint64_t)inner + t - 1) / t) * t * t;
+    const sph::RowMap m{(uint32_t)outer, (uint32_t)inner, 0};
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (dtype == SPH_F32) return sph::launch_move<float, float, sph::M_TRANSPOSE>(x, out, walk, head_dim, m, s);
+    // Halves move as 16-bit patterns; the element type does not matter.
+    return sph::launch_move<sph::f16, sph::f16, sph::M_TRANSPOSE>(x, out, walk, head_dim, m, s);
+}
+
+extern "C" int sph_kv_append(const void* src, int src_dtype, void* cache, int cache_dtype, int64_t n_kv, int64_t seq,
+                             int64_t head_dim, int64_t max_seq, int64_t pos, void* stream) {
+    if (n_kv < 0 || seq < 0 || head_dim < 0 || max_seq < 0 || pos < 0) return SPH_EINVAL;
+    if (!sph::is_float_dtype(src_dtype) || !sph::is_float_dtype(cache_dtype)) return SPH_EINVAL;
+    if (pos > max_seq || seq > max_seq - pos) return SPH_ERANGE;
+    const uint64_t rows = (uint64_t)n_kv * (uint64_t)seq;
+    if (rows == 0 || head_dim == 0) return SPH_OK;
+    if (src == nullptr || cache == nullptr) return SPH_EINVAL;
+    if (seq > UINT32_MAX || max_seq > UINT32_MAX) return SPH_EINVAL;
+    const sph::RowMap m{(uint32_t)seq, (uint32_t)max_seq, (uint64_t)pos};
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    return sph::with_float_type(src_dtype, [&](auto ts) -> int {
+        using TS = decltype(ts);
+        return sph::with_float_type(cache_dtype, [&](auto td) -> int {
+            using TD = decltype(td);
+            return sph::launch_move<TS, TD, sph::M_KV>(src, cache, rows, head_dim, m, s);
+        });
+    });
+}

@@ -246,3 +246,30 @@ def embed(table: torch.Tensor, table_dtype: int, vocab: int, hidden: int, ids: t
     check(lib().sph_embed(table.data_ptr(), table_dtype, vocab, hidden, ids.data_ptr(), n, out.data_ptr(),
                           None if flag is None else flag.data_ptr(), _stream(ids)), "embed")
     return out
+
+
+def transpose_heads(x: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """[outer, inner, head_dim] -> [inner, outer, head_dim] (resident.rs:420-458), bit for bit."""
+    _dev(x, "x")
+    if x.dim() != 3:
+        raise ValueError("x must be [outer, inner, head_dim]")
+    outer, inner, hd = x.shape
+    out = _out(out, (inner, outer, hd), x.dtype, x.device)
+    if out.data_ptr() == x.data_ptr() and x.numel():
+        raise ValueError("out must not alias x")
+    check(lib().sph_transpose_heads(x.data_ptr(), out.data_ptr(), dtype_code(x.dtype), outer, inner, hd, _stream(x)),
+          "transpose_heads")
+    return out
+
+
+def kv_append(src: torch.Tensor, cache: torch.Tensor, pos: int) -> None:
+    """Write src [n_kv, seq, head_dim] into cache [n_kv, max_seq, head_dim] at
+    positions pos..pos+seq, converted to the cache's dtype (resident.rs:645-711)."""
+    _dev(src, "src")
+    _dev(cache, "cache")
+    if src.dim() != 3 or cache.dim() != 3 or src.shape[0] != cache.shape[0] or src.shape[2] != cache.shape[2]:
+        raise ValueError("src must be [n_kv, seq, head_dim] and cache [n_kv, max_seq, head_dim]")
+    n_kv, seq, hd = src.shape
+    max_seq = cache.shape[1]
+    check(lib().sph_kv_append(src.data_ptr(), dtype_code(src.dtype), cache.data_ptr(), dtype_code(cache.dtype),
+                              n_kv, seq, hd, max_seq, int(pos), _stream(src)), "kv_append")

@@ -45,7 +45,7 @@ def test_library_loads_and_binding_covers_header(built_lib):
     L = _lib.lib()
     assert set(_lib.SIGNATURES) == declared_symbols()
     assert L.sph_abi_version() == 1
-    assert L.sph_status_string(_lib.ERANGE) == b"token id out of vocab range"
+    assert L.sph_status_string(_lib.ERANGE).startswith(b"index out of range")
     assert L.sph_status_string(12345) == b"unknown status"
 
 

@@ -1,0 +1,126 @@
+"""GPU parity: the device-resident decode helpers against the oracle.
+
+Reference: crates/sapient-backends/wgpu/src/resident.rs:420-458 (transpose_heads)
+and :645-711 (kv_append), with their tests tests/resident.rs:339-415 and :956-982.
+
+Both are moves: bit-exact. Same-type moves keep every bit pattern (NaN payloads
+included); f32 → f16 / bf16 cache writes round to nearest-even, bit-exact
+against the oracle's narrowing.
+"""
+import numpy as np
+import pytest
+import torch
+
+from helpers import assert_bits16_equal, assert_bits_equal, to_np, widen
+from refvec import WgpuLcg
+
+import sapient_amd.ops as ops
+
+pytestmark = pytest.mark.gpu
+DTYPES = [torch.float32, torch.float16, torch.bfloat16]
+IDS = lambda d: str(d).split(".")[-1]
+CODE = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 30}
+
+
+def _gen(shape, seed, dev, dtype=torch.float32):
+    g = torch.Generator(device=dev).manual_seed(seed)
+    return torch.randn(shape, generator=g, device=dev).to(dtype)
+
+
+def _same(got: torch.Tensor, want: np.ndarray, what: str):
+    if got.dtype == torch.float32:
+        assert_bits_equal(to_np(got), want, what)
+    else:
+        assert_bits16_equal(to_np(got), want, what)
+
+
+def test_transpose_heads_matches_wgpu_test(dev, orc):
+    """tests/resident.rs:956-982: [7, 5, 16] → [5, 7, 16] and back is the identity."""
+    x = WgpuLcg().take(7 * 5 * 16).reshape(7, 5, 16)
+    print("case transpose wgpu-vectors", flush=True)
+    t = ops.transpose_heads(torch.from_numpy(x).to(dev))
+    assert_bits_equal(to_np(t), orc.transpose_heads(x, 7, 5, 16), "forward")
+    back = ops.transpose_heads(t)
+    assert_bits_equal(to_np(back), x, "round trip")
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=IDS)
+@pytest.mark.parametrize("outer,inner,hd", [(8192, 32, 128), (1, 32, 128), (512, 14, 64), (7, 5, 16), (3, 4, 6),
+                                            (5, 3, 9), (1, 1, 1), (33, 8, 80)])
+def test_transpose_heads_shapes(dev, orc, dtype, outer, inner, hd):
+    print(f"case transpose {dtype} {outer}x{inner}x{hd}", flush=True)
+    x = _gen((outer, inner, hd), outer * 31 + hd, dev, dtype)
+    got = ops.transpose_heads(x)
+    _same(got, orc.transpose_heads(to_np(x), outer, inner, hd), f"transpose {dtype}")
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=IDS)
+def test_transpose_heads_keeps_every_half_pattern(dev, orc, dtype):
+    """All 65536 16-bit patterns (NaN payloads and signalling NaNs included) move unchanged."""
+    bits = torch.arange(0, 65536, dtype=torch.int32).to(torch.int16).view(dtype).reshape(64, 8, 128).to(dev)
+    got = ops.transpose_heads(bits)
+    assert np.array_equal(to_np(got), np.transpose(to_np(bits), (1, 0, 2)))
+
+
+def test_transpose_heads_unaligned_views_take_scalar_path(dev, orc):
+    base = _gen((4 * 6 * 32 + 1,), 5, dev)
+    x = base[1:].view(4, 6, 32)
+    out = torch.empty(4 * 6 * 32 + 1, device=dev)[1:].view(6, 4, 32)
+    ops.transpose_heads(x, out=out)
+    assert_bits_equal(to_np(out), orc.transpose_heads(to_np(x), 4, 6, 32), "unaligned")
+
+
+@pytest.mark.parametrize("cdtype", DTYPES, ids=IDS)
+def test_kv_append_matches_wgpu_test_sequence(dev, orc, cdtype):
+    """tests/resident.rs:339-415: n_kv 2, head_dim 64, max_seq 16; a 3-token prefill append
+    then three single-token appends; the cache equals the oracle's bit for bit and positions
+    past the last append are untouched."""
+    n_kv, hd, max_seq, steps = 2, 64, 16, 6
+    nxt = WgpuLcg()
+    sentinel = 0x7E7E if cdtype != torch.float32 else 0x7E7E7E7E
+    cache = torch.full((n_kv, max_seq, hd), sentinel, dtype=torch.int32 if cdtype == torch.float32 else torch.int16,
+                       device=dev).view(cdtype)
+    ref = to_np(cache).copy()
+    chunk = nxt.take(n_kv * 3 * hd).reshape(n_kv, 3, hd)
+    print(f"case kv_append sequence {cdtype}", flush=True)
+    ops.kv_append(torch.from_numpy(chunk).to(dev), cache, 0)
+    orc.kv_append(chunk, ref, CODE[cdtype], n_kv, 3, hd, max_seq, 0)
+    for t in range(3, steps):
+        knew = nxt.take(n_kv * hd).reshape(n_kv, 1, hd)
+        ops.kv_append(torch.from_numpy(knew).to(dev), cache, t)
+        orc.kv_append(knew, ref, CODE[cdtype], n_kv, 1, hd, max_seq, t)
+    _same(cache, ref, f"kv cache {cdtype}")
+
+
+@pytest.mark.parametrize("sdtype", DTYPES, ids=IDS)
+@pytest.mark.parametrize("cdtype", DTYPES, ids=IDS)
+@pytest.mark.parametrize("n_kv,seq,hd,max_seq,pos", [(8, 8192, 128, 8192, 0), (8, 1, 128, 8192, 8191),
+                                                     (2, 5, 64, 40, 17), (3, 4, 6, 10, 6), (1, 1, 1, 1, 0)])
+def test_kv_append_shapes(dev, orc, sdtype, cdtype, n_kv, seq, hd, max_seq, pos):
+    if seq == 8192 and sdtype != torch.float32 and cdtype != torch.float16:
+        pytest.skip("the large prefill runs f32 sources and every cache type, and half sources into f16")
+    print(f"case kv_append {sdtype}->{cdtype} {n_kv}x{seq}x{hd} max {max_seq} pos {pos}", flush=True)
+    src = _gen((n_kv, seq, hd), seq + hd, dev, sdtype)
+    cache = _gen((n_kv, max_seq, hd), 99, dev, cdtype)
+    ref = to_np(cache).copy()
+    ops.kv_append(src, cache, pos)
+    orc.kv_append(widen(src, orc), ref, CODE[cdtype], n_kv, seq, hd, max_seq, pos)
+    _same(cache, ref, f"kv_append {sdtype}->{cdtype}")
+
+
+def test_kv_append_rejects_out_of_range(dev):
+    from sapient_amd._lib import EINVAL, ERANGE, SapientHipError, lib
+    cache = torch.zeros(2, 8, 16, device=dev)
+    before = cache.clone()
+    with pytest.raises(SapientHipError):
+        ops.kv_append(torch.ones(2, 3, 16, device=dev), cache, 6)
+    assert torch.equal(cache, before)
+    L = lib()
+    s = torch.cuda.current_stream().cuda_stream
+    p = cache.data_ptr()
+    assert L.sph_kv_append(p, 0, p, 0, 2, 3, 16, 8, 6, s) == ERANGE
+    assert L.sph_kv_append(p, 0, p, 0, 2, 1, 16, 8, 8, s) == ERANGE
+    assert L.sph_kv_append(p, 0, p, 0, 2, 1, 16, 8, -1, s) == EINVAL
+    assert L.sph_kv_append(p, 8, p, 0, 2, 1, 16, 8, 0, s) == EINVAL       # src dtype
+    assert L.sph_transpose_heads(p, p, 0, 2, 8, 16, s) == EINVAL            # out aliases x
+    assert L.sph_transpose_heads(p, None, 0, 2, 8, 16, s) == EINVAL

@@ -495,3 +495,44 @@ def test_row_bytes_match_dtype_byte_count():
     assert oracle.row_bytes(oracle.Q6_K, 4096) == 3360
     assert oracle.row_bytes(oracle.F16, 10) == 20
     assert oracle.row_bytes(oracle.Q8_0, 48) == 0   # not a whole number of blocks
+
+
+def test_transpose_heads_is_the_axis_permutation():
+    """wgpu tests/resident.rs:956-982 (7 x 5 x 16, lcg): out[h][s][c] = x[s][h][c] and the round
+    trip is the identity; numpy's axis permutation is the independent statement; half tensors
+    move as raw 16-bit patterns (NaN payloads kept)."""
+    x = WgpuLcg().take(7 * 5 * 16).reshape(7, 5, 16)
+    t = oracle.transpose_heads(x, 7, 5, 16)
+    assert np.array_equal(_bits(t), _bits(np.transpose(x, (1, 0, 2))))
+    assert np.array_equal(_bits(oracle.transpose_heads(t, 5, 7, 16)), _bits(x))
+    h = np.arange(3 * 4 * 6, dtype=np.uint16).reshape(3, 4, 6) | np.uint16(0x7C01)  # f16 NaN patterns
+    assert np.array_equal(oracle.transpose_heads(h, 3, 4, 6), np.transpose(h, (1, 0, 2)))
+
+
+@pytest.mark.parametrize("cache_dtype", [0, 1, 30])
+def test_kv_append_is_a_slice_assignment(cache_dtype):
+    """wgpu tests/resident.rs:339-415: a 3-token prefill then single-token decode appends into a
+    [2, 16, 64] cache; the cache equals numpy slice assignment of the RNE-rounded values
+    (f16 via numpy's float16, bf16 via torch) and nothing else is written; pos + seq > max_seq
+    is an error."""
+    n_kv, hd, max_seq, steps = 2, 64, 16, 6
+    nxt = WgpuLcg()
+    dt = np.float32 if cache_dtype == 0 else np.uint16
+    cache = np.zeros((n_kv, max_seq, hd), dt)
+    want = np.zeros((n_kv, max_seq, hd), np.float32)
+    chunk = nxt.take(n_kv * 3 * hd).reshape(n_kv, 3, hd)
+    oracle.kv_append(chunk, cache, cache_dtype, n_kv, 3, hd, max_seq, 0)
+    want[:, 0:3] = chunk
+    for t in range(3, steps):
+        knew = nxt.take(n_kv * hd).reshape(n_kv, 1, hd)
+        oracle.kv_append(knew, cache, cache_dtype, n_kv, 1, hd, max_seq, t)
+        want[:, t:t + 1] = knew
+    if cache_dtype == 0:
+        assert np.array_equal(_bits(cache), _bits(want))
+    elif cache_dtype == 1:
+        assert np.array_equal(cache, want.astype(np.float16).view(np.uint16))
+    else:
+        assert np.array_equal(cache, torch.from_numpy(want).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16))
+    assert (cache[:, steps:] == 0).all()
+    with pytest.raises(oracle.OracleError):
+        oracle.kv_append(np.zeros((n_kv, 2, hd), np.float32), cache, cache_dtype, n_kv, 2, hd, max_seq, 15)
