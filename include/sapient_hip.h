@@ -148,6 +148,26 @@ int sph_rope(void* q, int64_t n_q_heads, void* k, int64_t n_k_heads, int dtype, 
              const int32_t* positions, int64_t batch, int64_t seq, int64_t head_dim,
              int64_t rotary_dim, float base, float pos_scale, void* stream);
 
+/* Decode-step fusion of RoPE and the KV-cache append: q [n_q_heads, seq,
+ * head_dim] is rotated in place; k and v [n_kv_heads, seq, head_dim] are read
+ * (not modified), and for each token s the rotated k row and the v row are
+ * written to kcache / vcache [n_kv_heads, max_seq, head_dim] at row
+ * positions[s], converted to cache_dtype (nearest-even for half caches).
+ * Results equal sph_rope (batch 1, rotary_dim = head_dim) on q and k followed
+ * by sph_kv_append of k and v at pos = positions[0] when positions are
+ * consecutive — the sequence of WgpuForwardEngine::forward_token
+ * (crates/sapient-models/src/forward/wgpu_engine.rs:413-440, resident.rs:467
+ * then :645-711) — in one launch. Positions are read on the device, so a HIP
+ * graph capturing this call replays correctly as positions change. A position
+ * outside [0, max_seq) writes nothing to the caches and stores 1 to
+ * `bad_pos_flag` (device int32, optional). dtype ∈ {F32, F16, BF16} for q, k,
+ * v; cache_dtype ∈ {F32, F16, BF16}; head_dim even, ≤ 512, and such that the
+ * rows allow 16-byte-or-narrower vector access (any multiple of 8 does). */
+int sph_rope_kv_append(void* q, int64_t n_q_heads, const void* k, const void* v, int64_t n_kv_heads, int dtype,
+                       int layout, const int32_t* positions, int64_t seq, int64_t head_dim, float base,
+                       float pos_scale, void* kcache, void* vcache, int cache_dtype, int64_t max_seq,
+                       int32_t* bad_pos_flag, void* stream);
+
 /* Token-embedding gather with on-the-fly row dequantization into f32:
  * out[t, :] = dequant(table[ids[t], :]). The table is the raw GGUF tensor
  * data, rows of byte_count(hidden) bytes, consumed verbatim (no repacking).

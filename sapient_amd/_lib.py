@@ -34,6 +34,8 @@ SIGNATURES = {
     "sph_add_bias": (_i32, [_vp, _vp, _i32, _vp, _i32, _i64, _i64, _vp]),
     "sph_rope": (_i32, [_vp, _i64, _vp, _i64, _i32, _i32, _vp, _i64, _i64, _i64, _i64, _f, _f, _vp]),
     "sph_embed": (_i32, [_vp, _i32, _i64, _i64, _vp, _i64, _vp, _vp, _vp]),
+    "sph_rope_kv_append": (_i32, [_vp, _i64, _vp, _vp, _i64, _i32, _i32, _vp, _i64, _i64, _f, _f, _vp, _vp, _i32,
+                                  _i64, _vp, _vp]),
     "sph_transpose_heads": (_i32, [_vp, _vp, _i32, _i64, _i64, _i64, _vp]),
     "sph_kv_append": (_i32, [_vp, _i32, _vp, _i32, _i64, _i64, _i64, _i64, _i64, _vp]),
 }

@@ -21,7 +21,16 @@
 //    add/subtract (-ffp-contract=off), exactly as the reference.
 //  - grid.x covers tokens, grid.y splits the heads into groups (512-1024
 //    blocks in all) so that short sequences still put waves on every CU.
+//  - The decode-step variant (sph_rope_kv_append) fuses the RoPE of q and k
+//    with the KV-cache append of k and v (resident.rs:467 then :645-711): the
+//    same threads that rotate a k row write it, and the matching v row, into
+//    the caches at the position read from device memory, converted to the
+//    cache type. One launch instead of three, and since no host-side position
+//    is baked into its arguments, a captured HIP graph replays it token after
+//    token.
 #include <math.h>
+
+#include <type_traits>
 
 #include "sph_common.h"
 
@@ -102,6 +111,116 @@ __global__ __launch_bounds__(kThreads) void rope_kernel(T* q, int nq, T* k, int 
     }
 }
 
+// Fused decode step: heads [0, nq) are q rows rotated in place; heads
+// [nq, nq + nkv) rotate the k row and write it, plus the v row, to cache row
+// (h, positions[s]). batch = 1 and rotary_dim = head_dim, so a thread's P
+// pairs and the pairs of its lane neighbours cover every channel of the row.
+template <typename T, typename TC, int P, bool INTERLEAVED>
+__global__ __launch_bounds__(kThreads) void rope_kv_kernel(T* q, int nq, const T* __restrict__ k,
+                                                           const T* __restrict__ v, int nkv,
+                                                           const int32_t* __restrict__ pos, int64_t seq, int head_dim,
+                                                           int half, int lanes_per_tok, int toks_per_block,
+                                                           int heads_per_group, float pos_scale, TC* kc, TC* vc,
+                                                           int64_t max_seq, int32_t* bad_pos_flag, DenTable den) {
+    const int tib = threadIdx.x / lanes_per_tok;
+    const int lit = threadIdx.x - tib * lanes_per_tok;
+    if (tib >= toks_per_block) return;
+    const int64_t s = (int64_t)blockIdx.x * toks_per_block + tib;
+    if (s >= seq) return;
+    const int i0 = lit * P;
+    const int32_t ps = pos[s];
+    const float p = (float)ps / pos_scale;
+    float cs[P], sn[P];
+#pragma unroll
+    for (int j = 0; j < P; ++j) {
+        const float freq = p / den.v[i0 + j];
+        double sd, cd;
+        sincos((double)freq, &sd, &cd);
+        sn[j] = (float)sd;
+        cs[j] = (float)cd;
+    }
+    const bool pos_ok = ps >= 0 && (int64_t)ps < max_seq;
+    if (!pos_ok && bad_pos_flag != nullptr && lit == 0 && blockIdx.y == 0) *bad_pos_flag = 1;
+
+    // Element offsets of this thread's two runs of P elements within a row.
+    const int a0 = INTERLEAVED ? 2 * i0 : i0;
+    const int a1 = INTERLEAVED ? 2 * i0 + P : i0 + half;
+    const int h_begin = blockIdx.y * heads_per_group;
+    int h_end = h_begin + heads_per_group;
+    if (h_end > nq + nkv) h_end = nq + nkv;
+    for (int hh = h_begin; hh < h_end; ++hh) {
+        const bool is_q = hh < nq;
+        const T* src = is_q ? q + ((size_t)hh * (size_t)seq + (size_t)s) * (size_t)head_dim
+                            : k + ((size_t)(hh - nq) * (size_t)seq + (size_t)s) * (size_t)head_dim;
+        if (!is_q && !pos_ok) continue;
+        float x0[P], x1[P];
+        if constexpr (!INTERLEAVED) {
+            load_f32<T, P, true>(src + a0, x0);
+            load_f32<T, P, true>(src + a1, x1);
+        } else {
+            float x[2 * P];
+            load_f32<T, 2 * P, true>(src + a0, x);
+#pragma unroll
+            for (int j = 0; j < P; ++j) {
+                x0[j] = x[2 * j];
+                x1[j] = x[2 * j + 1];
+            }
+        }
+        float o0[P], o1[P];
+#pragma unroll
+        for (int j = 0; j < P; ++j) {
+            o0[j] = x0[j] * cs[j] - x1[j] * sn[j];
+            o1[j] = x1[j] * cs[j] + x0[j] * sn[j];
+        }
+        auto put = [&](auto* row, const float (&u0)[P], const float (&u1)[P]) {
+            using TR = typename std::remove_pointer<decltype(row)>::type;
+            if constexpr (!INTERLEAVED) {
+                store_f32<TR, P, true>(row + a0, u0);
+                store_f32<TR, P, true>(row + a1, u1);
+            } else {
+                float o[2 * P];
+#pragma unroll
+                for (int j = 0; j < P; ++j) {
+                    o[2 * j] = u0[j];
+                    o[2 * j + 1] = u1[j];
+                }
+                store_f32<TR, 2 * P, true>(row + a0, o);
+            }
+        };
+        if (is_q) {
+            put(q + ((size_t)hh * (size_t)seq + (size_t)s) * (size_t)head_dim, o0, o1);
+        } else {
+            const size_t crow = ((size_t)(hh - nq) * (size_t)max_seq + (size_t)ps) * (size_t)head_dim;
+            // The unfused sequence stores rotated k in the activation type
+            // before converting it to the cache type: round through T first.
+            if constexpr (!std::is_same<T, float>::value) {
+#pragma unroll
+                for (int j = 0; j < P; ++j) {
+                    o0[j] = widen(narrow<T>(o0[j]));
+                    o1[j] = widen(narrow<T>(o1[j]));
+                }
+            }
+            put(kc + crow, o0, o1);
+            // v: the same channels, moved unrotated.
+            const T* vrow = v + ((size_t)(hh - nq) * (size_t)seq + (size_t)s) * (size_t)head_dim;
+            float v0[P], v1[P];
+            if constexpr (!INTERLEAVED) {
+                load_f32<T, P, true>(vrow + a0, v0);
+                load_f32<T, P, true>(vrow + a1, v1);
+            } else {
+                float x[2 * P];
+                load_f32<T, 2 * P, true>(vrow + a0, x);
+#pragma unroll
+                for (int j = 0; j < P; ++j) {
+                    v0[j] = x[2 * j];
+                    v1[j] = x[2 * j + 1];
+                }
+            }
+            put(vc + crow, v0, v1);
+        }
+    }
+}
+
 template <typename T, int P, bool IL>
 int launch_rope_p(T* q, int nq, T* k, int nk, const int32_t* pos, int64_t ntok, int64_t seq, int head_dim,
                   int half, float pos_scale, const DenTable& den, hipStream_t stream) {
@@ -127,6 +246,75 @@ int launch_rope_p(T* q, int nq, T* k, int nk, const int32_t* pos, int64_t ntok, 
     return launch_status();
 }
 
+// Denominators powf(base, 2i / rotary_dim) from the host libm, the call the reference makes.
+inline void fill_dens(DenTable& den, int half, int rotary_dim, float base) {
+    for (int i = 0; i < kMaxHalf; ++i)
+        den.v[i] = i < half ? powf(base, 2.0f * (float)i / (float)rotary_dim) : 1.0f;
+}
+
+template <typename T, typename TC, int P, bool IL>
+int launch_rope_kv_p(T* q, int nq, const T* k, const T* v, int nkv, const int32_t* pos, int64_t seq, int head_dim,
+                     float pos_scale, TC* kc, TC* vc, int64_t max_seq, int32_t* flag, const DenTable& den,
+                     hipStream_t stream) {
+    const int half = head_dim / 2;
+    const int lanes_per_tok = half / P;
+    const int toks_per_block = kThreads / lanes_per_tok;
+    const int64_t blocks_x = (seq + toks_per_block - 1) / toks_per_block;
+    const int heads = nq + nkv;
+    const int target = sizeof(T) == 4 ? 512 : 1024;
+    int groups = (int)((target + blocks_x - 1) / blocks_x);
+    if (groups > heads) groups = heads;
+    if (groups < 1) groups = 1;
+    const int heads_per_group = (heads + groups - 1) / groups;
+    groups = (heads + heads_per_group - 1) / heads_per_group;
+    if (blocks_x > INT32_MAX) return SPH_EINVAL;
+    const dim3 grid((unsigned)blocks_x, (unsigned)groups);
+    rope_kv_kernel<T, TC, P, IL><<<grid, kThreads, 0, stream>>>(q, nq, k, v, nkv, pos, seq, head_dim, half,
+                                                                lanes_per_tok, toks_per_block, heads_per_group,
+                                                                pos_scale, kc, vc, max_seq, flag, den);
+    return launch_status();
+}
+
+// P: pairs per thread, the widest whose accesses of q/k/v (type T) and of the
+// caches (type TC) stay within 16 bytes and aligned.
+template <typename T, typename TC>
+int launch_rope_kv(void* qv, int nq, const void* kv, const void* vv, int nkv, int layout, const int32_t* pos,
+                   int64_t seq, int head_dim, float base, float pos_scale, void* kcv, void* vcv, int64_t max_seq,
+                   int32_t* flag, hipStream_t stream) {
+    T* q = static_cast<T*>(qv);
+    const T* k = static_cast<const T*>(kv);
+    const T* v = static_cast<const T*>(vv);
+    TC* kc = static_cast<TC*>(kcv);
+    TC* vc = static_cast<TC*>(vcv);
+    const int half = head_dim / 2;
+    DenTable den;
+    fill_dens(den, half, head_dim, base);
+    const bool il = layout == SPH_ROPE_INTERLEAVED;
+    auto ok = [&](int P) {
+        const int run = il ? 2 * P : P;  // contiguous elements per access
+        if (half % P != 0 || head_dim % run != 0) return false;
+        if (run * sizeof(T) > 16 || run * sizeof(TC) > 16) return false;
+        if ((run * sizeof(T)) % 4 != 0 || (run * sizeof(TC)) % 4 != 0) return false;
+        const size_t at = run * sizeof(T) < 16 ? run * sizeof(T) : 16;
+        const size_t ac = run * sizeof(TC) < 16 ? run * sizeof(TC) : 16;
+        return aligned(q, at) && aligned(k, at) && aligned(v, at) && aligned(kc, ac) && aligned(vc, ac);
+    };
+    constexpr int V = vec16<T>::n < vec16<TC>::n ? vec16<T>::n : vec16<TC>::n;
+    if (!il) {
+        if (ok(V)) return launch_rope_kv_p<T, TC, V, false>(q, nq, k, v, nkv, pos, seq, head_dim, pos_scale, kc, vc, max_seq, flag, den, stream);
+        if (ok(V / 2)) return launch_rope_kv_p<T, TC, V / 2, false>(q, nq, k, v, nkv, pos, seq, head_dim, pos_scale, kc, vc, max_seq, flag, den, stream);
+        if constexpr (V / 4 >= 2) {
+            if (ok(V / 4)) return launch_rope_kv_p<T, TC, V / 4, false>(q, nq, k, v, nkv, pos, seq, head_dim, pos_scale, kc, vc, max_seq, flag, den, stream);
+        }
+    } else {
+        if (ok(V / 2)) return launch_rope_kv_p<T, TC, V / 2, true>(q, nq, k, v, nkv, pos, seq, head_dim, pos_scale, kc, vc, max_seq, flag, den, stream);
+        if constexpr (V / 4 >= 1) {
+            if (ok(V / 4)) return launch_rope_kv_p<T, TC, V / 4, true>(q, nq, k, v, nkv, pos, seq, head_dim, pos_scale, kc, vc, max_seq, flag, den, stream);
+        }
+    }
+    return SPH_EINVAL;  // head_dim or alignment the vector paths do not cover
+}
+
 template <typename T>
 int launch_rope(void* qv, int nq, void* kv, int nk, int layout, const int32_t* pos, int64_t batch, int64_t seq,
                 int head_dim, int rotary_dim, float base, float pos_scale, hipStream_t stream) {
@@ -135,8 +323,7 @@ int launch_rope(void* qv, int nq, void* kv, int nk, int layout, const int32_t* p
     const int half = rotary_dim / 2;
     // The reference's denominators: base.powf(2.0 * i as f32 / rotary_dim as f32), host libm.
     DenTable den;
-    for (int i = 0; i < kMaxHalf; ++i)
-        den.v[i] = i < half ? powf(base, 2.0f * (float)i / (float)rotary_dim) : 1.0f;
+    fill_dens(den, half, rotary_dim, base);
     const int64_t ntok = batch * seq;
     auto ok = [&](int P, int elems_per_access) {
         const size_t bytes = (size_t)elems_per_access * sizeof(T);
@@ -183,5 +370,29 @@ extern "C" int sph_rope(void* q, int64_t n_q_heads, void* k, int64_t n_k_heads, 
         using T = decltype(t);
         return sph::launch_rope<T>(q, (int)n_q_heads, k, (int)n_k_heads, layout, positions, batch, seq, (int)head_dim,
                                    (int)rotary_dim, base, pos_scale, s);
+    });
+}
+
+extern "C" int sph_rope_kv_append(void* q, int64_t n_q_heads, const void* k, const void* v, int64_t n_kv_heads,
+                                  int dtype, int layout, const int32_t* positions, int64_t seq, int64_t head_dim,
+                                  float base, float pos_scale, void* kcache, void* vcache, int cache_dtype,
+                                  int64_t max_seq, int32_t* bad_pos_flag, void* stream) {
+    if (layout != SPH_ROPE_NEOX && layout != SPH_ROPE_INTERLEAVED) return SPH_EINVAL;
+    if (!sph::is_float_dtype(dtype) || !sph::is_float_dtype(cache_dtype)) return SPH_EINVAL;
+    if (n_q_heads < 0 || n_kv_heads < 0 || seq < 0 || max_seq < 0) return SPH_EINVAL;
+    if (head_dim <= 0 || head_dim % 2 != 0 || head_dim / 2 > sph::kMaxHalf) return SPH_EINVAL;
+    if (n_q_heads + n_kv_heads > INT32_MAX) return SPH_EINVAL;
+    if (seq == 0 || n_q_heads + n_kv_heads == 0) return SPH_OK;
+    if (positions == nullptr || (n_q_heads > 0 && q == nullptr)) return SPH_EINVAL;
+    if (n_kv_heads > 0 && (k == nullptr || v == nullptr || kcache == nullptr || vcache == nullptr)) return SPH_EINVAL;
+    if (!(pos_scale == pos_scale) || pos_scale == 0.0f) return SPH_EINVAL;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    return sph::with_float_type(dtype, [&](auto t) -> int {
+        using T = decltype(t);
+        return sph::with_float_type(cache_dtype, [&](auto tc) -> int {
+            using TC = decltype(tc);
+            return sph::launch_rope_kv<T, TC>(q, (int)n_q_heads, k, v, (int)n_kv_heads, layout, positions, seq,
+                                             (int)head_dim, base, pos_scale, kcache, vcache, max_seq, bad_pos_flag, s);
+        });
     });
 }

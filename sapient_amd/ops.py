@@ -273,3 +273,33 @@ def kv_append(src: torch.Tensor, cache: torch.Tensor, pos: int) -> None:
     max_seq = cache.shape[1]
     check(lib().sph_kv_append(src.data_ptr(), dtype_code(src.dtype), cache.data_ptr(), dtype_code(cache.dtype),
                               n_kv, seq, hd, max_seq, int(pos), _stream(src)), "kv_append")
+
+
+def rope_kv_append(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, positions: torch.Tensor, base: float,
+                   kcache: torch.Tensor, vcache: torch.Tensor, pos_scale: float = 1.0, interleaved: bool = False,
+                   bad_pos_flag: Optional[torch.Tensor] = None) -> None:
+    """Fused decode step: RoPE on q in place; rotated k and v written to the caches at rows
+    positions[s] (wgpu_engine.rs:413-440). q [Hq, S, D], k/v [Hkv, S, D], caches [Hkv, max_seq, D]."""
+    for t, n in ((q, "q"), (k, "k"), (v, "v"), (kcache, "kcache"), (vcache, "vcache"), (positions, "positions")):
+        _dev(t, n)
+    if q.dim() != 3 or k.dim() != 3 or k.shape != v.shape or q.shape[1:] != k.shape[1:]:
+        raise ValueError("q must be [Hq, S, D] and k, v [Hkv, S, D]")
+    if k.dtype != q.dtype or v.dtype != q.dtype:
+        raise ValueError("q, k and v must share dtype")
+    Hq, S, D = q.shape
+    Hkv = k.shape[0]
+    if kcache.shape != vcache.shape or kcache.dim() != 3 or kcache.shape[0] != Hkv or kcache.shape[2] != D \
+            or kcache.dtype != vcache.dtype:
+        raise ValueError("caches must be [Hkv, max_seq, D] of one dtype")
+    if positions.dtype != torch.int32 or positions.numel() != S:
+        raise ValueError("positions must be int32 with seq entries")
+    flag = None
+    if bad_pos_flag is not None:
+        flag = _dev(bad_pos_flag, "bad_pos_flag")
+        if flag.dtype != torch.int32 or flag.numel() < 1:
+            raise ValueError("bad_pos_flag must be an int32 device tensor")
+    layout = _lib.ROPE_INTERLEAVED if interleaved else _lib.ROPE_NEOX
+    check(lib().sph_rope_kv_append(q.data_ptr(), Hq, k.data_ptr(), v.data_ptr(), Hkv, dtype_code(q.dtype), layout,
+                                   positions.data_ptr(), S, D, float(base), float(pos_scale), kcache.data_ptr(),
+                                   vcache.data_ptr(), dtype_code(kcache.dtype), kcache.shape[1],
+                                   None if flag is None else flag.data_ptr(), _stream(q)), "rope_kv_append")

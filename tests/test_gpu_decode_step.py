@@ -1,0 +1,124 @@
+"""GPU parity: the fused decode step (RoPE on q and k + KV-cache append of k and v).
+
+Reference sequence: WgpuForwardEngine::forward_token / forward_chunk
+(crates/sapient-models/src/forward/wgpu_engine.rs:413-440, :561-589) — rope on q
+and k (resident.rs:467), then kv_append of k and v (resident.rs:645-711).
+
+Bar: bit-exact against the unfused sequence of this library's own kernels
+(sph_rope in place, then sph_kv_append of k and v), whose parity with the oracle
+the RoPE and layout tests establish; and q / the caches against the oracle at
+the RoPE tolerance (≤ 1e-5 of the pair's norm for f32).
+"""
+import numpy as np
+import pytest
+import torch
+
+from helpers import to_np, widen
+from refvec import WgpuLcg
+
+import sapient_amd.ops as ops
+
+pytestmark = pytest.mark.gpu
+DTYPES = [torch.float32, torch.float16, torch.bfloat16]
+IDS = lambda d: str(d).split(".")[-1]
+
+
+def _gen(shape, seed, dev, dtype):
+    g = torch.Generator(device=dev).manual_seed(seed)
+    return torch.randn(shape, generator=g, device=dev).to(dtype)
+
+
+def _unfused(q, k, v, positions, base, kcache, vcache, interleaved):
+    """sph_rope on copies of q and k ([1, H, S, D] views), then one kv_append per token at positions[s]."""
+    q2, k2 = q.clone(), k.clone()
+    ops.rope_(q2.unsqueeze(0), k2.unsqueeze(0), positions, base, interleaved=interleaved)
+    for s, p in enumerate(positions.cpu().tolist()):
+        ops.kv_append(k2[:, s:s + 1].contiguous(), kcache, p)
+        ops.kv_append(v[:, s:s + 1].contiguous(), vcache, p)
+    return q2
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=IDS)
+@pytest.mark.parametrize("cdtype", DTYPES, ids=IDS)
+@pytest.mark.parametrize("interleaved", [False, True], ids=["neox", "interleaved"])
+@pytest.mark.parametrize("Hq,Hkv,S,D,max_seq,pos0", [(14, 2, 1, 64, 64, 37), (32, 8, 512, 128, 1024, 100),
+                                                     (32, 32, 3, 80, 16, 13), (4, 2, 5, 8, 12, 0)])
+def test_fused_equals_unfused(dev, dtype, cdtype, interleaved, Hq, Hkv, S, D, max_seq, pos0):
+    print(f"case rope_kv {dtype} cache {cdtype} {'il' if interleaved else 'neox'} {Hq}+{Hkv}x{S}x{D} pos {pos0}",
+          flush=True)
+    q = _gen((Hq, S, D), 1, dev, dtype)
+    k = _gen((Hkv, S, D), 2, dev, dtype)
+    v = _gen((Hkv, S, D), 3, dev, dtype)
+    positions = torch.arange(pos0, pos0 + S, dtype=torch.int32, device=dev)
+    kc = _gen((Hkv, max_seq, D), 4, dev, cdtype)
+    vc = _gen((Hkv, max_seq, D), 5, dev, cdtype)
+    kc2, vc2 = kc.clone(), vc.clone()
+    k_before = k.clone()
+    q_ref = _unfused(q, k, v, positions, 5e5, kc2, vc2, interleaved)
+    ops.rope_kv_append(q, k, v, positions, 5e5, kc, vc, interleaved=interleaved)
+    assert np.array_equal(to_np(q), to_np(q_ref)), "q"
+    assert np.array_equal(to_np(kc), to_np(kc2)), "k cache"
+    assert np.array_equal(to_np(vc), to_np(vc2)), "v cache"
+    assert torch.equal(k, k_before), "k is read-only"
+
+
+def test_fused_matches_oracle_and_scatters_by_position(dev, orc):
+    """Non-consecutive positions (a shuffled chunk): each token's rows land at its own cache
+    row; q and the k cache agree with the oracle's apply_rope at the RoPE tolerance; v is copied."""
+    Hq, Hkv, S, D, max_seq = 8, 2, 6, 64, 32
+    nxt = WgpuLcg()
+    q = nxt.take(Hq * S * D).reshape(Hq, S, D)
+    k = nxt.take(Hkv * S * D).reshape(Hkv, S, D)
+    v = nxt.take(Hkv * S * D).reshape(Hkv, S, D)
+    pos = np.array([9, 3, 30, 0, 17, 4], np.int32)
+    tq, tk, tv = (torch.from_numpy(a).to(dev) for a in (q, k, v))
+    kc = torch.zeros(Hkv, max_seq, D, device=dev)
+    vc = torch.zeros(Hkv, max_seq, D, device=dev)
+    ops.rope_kv_append(tq, tk, tv, torch.from_numpy(pos).to(dev), 1e4, kc, vc)
+    want_q = orc.apply_rope(q[None], pos, 1e4)[0]
+    want_k = orc.apply_rope(k[None], pos, 1e4)[0]
+    pair = lambda x: np.sqrt(np.concatenate([x[..., :D // 2] ** 2 + x[..., D // 2:] ** 2] * 2, axis=-1))
+    assert (np.abs(to_np(tq) - want_q) <= 1e-5 * pair(q) + 1e-30).all()
+    got_k, got_v = to_np(kc), to_np(vc)
+    for s, p in enumerate(pos):
+        assert (np.abs(got_k[:, p] - want_k[:, s]) <= 1e-5 * pair(k[:, s]) + 1e-30).all()
+        assert np.array_equal(got_v[:, p], v[:, s])
+    untouched = np.setdiff1d(np.arange(max_seq), pos)
+    assert (got_k[:, untouched] == 0).all() and (got_v[:, untouched] == 0).all()
+
+
+def test_bad_position_writes_nothing_and_raises_flag(dev):
+    Hq, Hkv, S, D, max_seq = 4, 2, 3, 64, 8
+    q = _gen((Hq, S, D), 7, dev, torch.float32)
+    k = _gen((Hkv, S, D), 8, dev, torch.float32)
+    v = _gen((Hkv, S, D), 9, dev, torch.float32)
+    kc = torch.zeros(Hkv, max_seq, D, device=dev)
+    vc = torch.zeros(Hkv, max_seq, D, device=dev)
+    flag = torch.zeros(1, dtype=torch.int32, device=dev)
+    positions = torch.tensor([2, 8, -1], dtype=torch.int32, device=dev)
+    q_ref = q.clone()
+    ops.rope_(q_ref.unsqueeze(0), None, positions, 1e4)
+    ops.rope_kv_append(q, k, v, positions, 1e4, kc, vc, bad_pos_flag=flag)
+    assert flag.item() == 1
+    assert torch.equal(q, q_ref)  # q rotates at every position
+    nz = (kc.abs().sum(dim=(0, 2)) > 0).cpu().tolist()
+    assert nz == [False, False, True, False, False, False, False, False]
+    assert (vc.abs().sum(dim=(0, 2)) > 0).cpu().tolist() == nz
+
+
+def test_rejects_bad_arguments(dev):
+    from sapient_amd._lib import EINVAL, lib
+    L = lib()
+    t = torch.zeros(2, 1, 64, device=dev)
+    p = torch.zeros(1, dtype=torch.int32, device=dev)
+    s = torch.cuda.current_stream().cuda_stream
+    d = t.data_ptr()
+    args = lambda **kw: dict(dict(q=d, hq=2, k=d, v=d, hkv=2, dt=0, lay=0, pos=p.data_ptr(), seq=1, hd=64, base=1e4,
+                                  ps=1.0, kc=d, vc=d, cdt=0, ms=1, flag=None, s=s), **kw)
+    call = lambda a: L.sph_rope_kv_append(*a.values())
+    assert call(args(hd=63)) == EINVAL                  # odd head_dim
+    assert call(args(lay=2)) == EINVAL                  # layout
+    assert call(args(cdt=8)) == EINVAL                  # cache dtype
+    assert call(args(kc=None)) == EINVAL                # missing cache
+    assert call(args(ps=0.0)) == EINVAL                 # pos_scale
+    assert call(args(hd=6)) == EINVAL                   # 3 pairs: no vector width divides them
