@@ -114,6 +114,52 @@ def headline(torch, ops, dev, args):
     return rows, dim, alg_bytes, per, wall
 
 
+def engine_rows(torch, dev, table, vocab):
+    import time
+    import sapient_amd._lib as L
+    from sapient_amd.engine import Engine
+    f32 = torch.float32
+    H, layers_n = 896, 24
+    cfg = L.EngineConfig(H, 14, 2, 64, 4864, layers_n, 4096, 512, 1e-6, 1e6, L.ROPE_NEOX, L.F16, L.F32)
+    layers = [dict(input_ln=gen(torch, (H,), 200 + l, dev, f32, 0.1, 1.0), post_ln=gen(torch, (H,), 300 + l, dev, f32, 0.1, 1.0),
+                   bq=gen(torch, (896,), 400 + l, dev, f32, 0.1), bk=gen(torch, (128,), 500 + l, dev, f32, 0.1),
+                   bv=gen(torch, (128,), 600 + l, dev, f32, 0.1), bo=None) for l in range(layers_n)]
+    eng = Engine(cfg, table, L.Q8_0, vocab, layers, gen(torch, (H,), 700, dev, f32, 0.1, 1.0))
+    rows = []
+    for graph in (False, True):
+        eng.reset()
+        eng.use_graph(graph)
+        for t in range(8):
+            eng.forward_token(t)
+        torch.cuda.synchronize()
+        n = 256
+        t0 = time.perf_counter()
+        for t in range(n):
+            eng.forward_token((t * 7919) % vocab)
+        torch.cuda.synchronize()
+        us = (time.perf_counter() - t0) / n * 1e6
+        rows.append({"op": "engine decode token" + (" (graph)" if graph else " (eager)"),
+                     "shape": "qwen2.5-0.5b 24 layers, op-set part", "dtype": "f32 act, f16 kv",
+                     "us": round(us, 2), "tokens/s": round(1e6 / us, 1), "latency_bound": True,
+                     "kernels_per_token": 1 + layers_n * 4 + 1})
+    eng.reset()
+    eng.use_graph(False)
+    toks = [(t * 104729) % vocab for t in range(512)]
+    eng.forward_chunk(toks)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(4):
+        eng.reset()
+        eng.forward_chunk(toks)
+    torch.cuda.synchronize()
+    us = (time.perf_counter() - t0) / 4 * 1e6
+    rows.append({"op": "engine prefill chunk", "shape": "qwen2.5-0.5b 24 layers, 512 tokens, op-set part",
+                 "dtype": "f32 act, f16 kv", "us": round(us, 2), "tokens/s": round(512e6 / us, 1),
+                 "latency_bound": True})
+    eng.close()
+    return rows
+
+
 def op_table(torch, ops, dev, only=None):
     """Per-op GB/s at each configuration shape (median of 20 launches after 3 warm-ups)."""
     import sapient_amd._lib as L
@@ -238,6 +284,11 @@ def op_table(torch, ops, dev, only=None):
         run(f"embed_q8_0 qwen T={T1}", f"{vocab_q}x{hid_q} -> {T1} ids", "q8_0->f32", T1 * (952 + 4 + hid_q * 4),
             T1, "rows", lambda T1=T1: [torch.empty(T1, hid_q, device=dev) for _ in range(2)],
             lambda o, ids=ids: ops.embed(tq, L.Q8_0, vocab_q, hid_q, ids, out=o), latency_bound=True)
+    # Device-resident decode engine at Qwen2.5-0.5B shape (24 layers, 896 hidden, 14 + 2 heads x 64,
+    # 4864 intermediate, f16 KV cache, Q8_0 embedding): this library's part of a token
+    # (projections / attention skipped), launched eagerly and replayed from a HIP graph.
+    if not only or "engine" in only:
+        res.extend(engine_rows(torch, dev, tq, vocab_q))
     return res
 
 

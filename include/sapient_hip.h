@@ -162,11 +162,17 @@ int sph_rope(void* q, int64_t n_q_heads, void* k, int64_t n_k_heads, int dtype, 
  * outside [0, max_seq) writes nothing to the caches and stores 1 to
  * `bad_pos_flag` (device int32, optional). dtype ∈ {F32, F16, BF16} for q, k,
  * v; cache_dtype ∈ {F32, F16, BF16}; head_dim even, ≤ 512, and such that the
- * rows allow 16-byte-or-narrower vector access (any multiple of 8 does). */
+ * rows allow 16-byte-or-narrower vector access (any multiple of 8 does).
+ * Optional biases bq [n_q_heads · head_dim], bk and bv [n_kv_heads · head_dim]
+ * (bias_dtype ∈ {F32, F16, BF16}; NULL = none) are added first, as
+ * sph_add_bias on q, k, v would (the projections' bias step,
+ * wgpu_engine.rs:398-409): the sum is rounded to `dtype` before RoPE / the
+ * cache conversion, so the result equals that unfused sequence bit for bit. */
 int sph_rope_kv_append(void* q, int64_t n_q_heads, const void* k, const void* v, int64_t n_kv_heads, int dtype,
                        int layout, const int32_t* positions, int64_t seq, int64_t head_dim, float base,
                        float pos_scale, void* kcache, void* vcache, int cache_dtype, int64_t max_seq,
-                       int32_t* bad_pos_flag, void* stream);
+                       const void* bq, const void* bk, const void* bv, int bias_dtype, int32_t* bad_pos_flag,
+                       void* stream);
 
 /* Token-embedding gather with on-the-fly row dequantization into f32:
  * out[t, :] = dequant(table[ids[t], :]). The table is the raw GGUF tensor

@@ -115,13 +115,14 @@ __global__ __launch_bounds__(kThreads) void rope_kernel(T* q, int nq, T* k, int 
 // [nq, nq + nkv) rotate the k row and write it, plus the v row, to cache row
 // (h, positions[s]). batch = 1 and rotary_dim = head_dim, so a thread's P
 // pairs and the pairs of its lane neighbours cover every channel of the row.
-template <typename T, typename TC, int P, bool INTERLEAVED>
+template <typename T, typename TC, typename TB, int P, bool INTERLEAVED>
 __global__ __launch_bounds__(kThreads) void rope_kv_kernel(T* q, int nq, const T* __restrict__ k,
                                                            const T* __restrict__ v, int nkv,
                                                            const int32_t* __restrict__ pos, int64_t seq, int head_dim,
                                                            int half, int lanes_per_tok, int toks_per_block,
                                                            int heads_per_group, float pos_scale, TC* kc, TC* vc,
-                                                           int64_t max_seq, int32_t* bad_pos_flag, DenTable den) {
+                                                           int64_t max_seq, int32_t* bad_pos_flag, const TB* bq,
+                                                           const TB* bk, const TB* bv, DenTable den) {
     const int tib = threadIdx.x / lanes_per_tok;
     const int lit = threadIdx.x - tib * lanes_per_tok;
     if (tib >= toks_per_block) return;
@@ -153,19 +154,46 @@ __global__ __launch_bounds__(kThreads) void rope_kv_kernel(T* q, int nq, const T
         const T* src = is_q ? q + ((size_t)hh * (size_t)seq + (size_t)s) * (size_t)head_dim
                             : k + ((size_t)(hh - nq) * (size_t)seq + (size_t)s) * (size_t)head_dim;
         if (!is_q && !pos_ok) continue;
-        float x0[P], x1[P];
-        if constexpr (!INTERLEAVED) {
-            load_f32<T, P, true>(src + a0, x0);
-            load_f32<T, P, true>(src + a1, x1);
-        } else {
-            float x[2 * P];
-            load_f32<T, 2 * P, true>(src + a0, x);
+        // Row values with the bias of their channels added (y + b in f32, then
+        // stored in the activation type before RoPE reads it: round through T).
+        auto load_row = [&](const T* row, const TB* bias, float (&u0)[P], float (&u1)[P]) {
+            if constexpr (!INTERLEAVED) {
+                load_f32<T, P, true>(row + a0, u0);
+                load_f32<T, P, true>(row + a1, u1);
+            } else {
+                float x[2 * P];
+                load_f32<T, 2 * P, true>(row + a0, x);
 #pragma unroll
-            for (int j = 0; j < P; ++j) {
-                x0[j] = x[2 * j];
-                x1[j] = x[2 * j + 1];
+                for (int j = 0; j < P; ++j) {
+                    u0[j] = x[2 * j];
+                    u1[j] = x[2 * j + 1];
+                }
             }
-        }
+            if (bias != nullptr) {
+                float b0[P], b1[P];
+                if constexpr (!INTERLEAVED) {
+                    load_f32<TB, P>(bias + a0, b0);
+                    load_f32<TB, P>(bias + a1, b1);
+                } else {
+                    float b[2 * P];
+                    load_f32<TB, 2 * P>(bias + a0, b);
+#pragma unroll
+                    for (int j = 0; j < P; ++j) {
+                        b0[j] = b[2 * j];
+                        b1[j] = b[2 * j + 1];
+                    }
+                }
+#pragma unroll
+                for (int j = 0; j < P; ++j) {
+                    u0[j] = widen(narrow<T>(u0[j] + b0[j]));
+                    u1[j] = widen(narrow<T>(u1[j] + b1[j]));
+                }
+            }
+        };
+        const TB* bias = is_q ? (bq ? bq + (size_t)hh * head_dim : nullptr)
+                              : (bk ? bk + (size_t)(hh - nq) * head_dim : nullptr);
+        float x0[P], x1[P];
+        load_row(src, bias, x0, x1);
         float o0[P], o1[P];
 #pragma unroll
         for (int j = 0; j < P; ++j) {
@@ -204,18 +232,7 @@ __global__ __launch_bounds__(kThreads) void rope_kv_kernel(T* q, int nq, const T
             // v: the same channels, moved unrotated.
             const T* vrow = v + ((size_t)(hh - nq) * (size_t)seq + (size_t)s) * (size_t)head_dim;
             float v0[P], v1[P];
-            if constexpr (!INTERLEAVED) {
-                load_f32<T, P, true>(vrow + a0, v0);
-                load_f32<T, P, true>(vrow + a1, v1);
-            } else {
-                float x[2 * P];
-                load_f32<T, 2 * P, true>(vrow + a0, x);
-#pragma unroll
-                for (int j = 0; j < P; ++j) {
-                    v0[j] = x[2 * j];
-                    v1[j] = x[2 * j + 1];
-                }
-            }
+            load_row(vrow, bv ? bv + (size_t)(hh - nq) * head_dim : nullptr, v0, v1);
             put(vc + crow, v0, v1);
         }
     }
@@ -252,10 +269,10 @@ inline void fill_dens(DenTable& den, int half, int rotary_dim, float base) {
         den.v[i] = i < half ? powf(base, 2.0f * (float)i / (float)rotary_dim) : 1.0f;
 }
 
-template <typename T, typename TC, int P, bool IL>
+template <typename T, typename TC, typename TB, int P, bool IL>
 int launch_rope_kv_p(T* q, int nq, const T* k, const T* v, int nkv, const int32_t* pos, int64_t seq, int head_dim,
-                     float pos_scale, TC* kc, TC* vc, int64_t max_seq, int32_t* flag, const DenTable& den,
-                     hipStream_t stream) {
+                     float pos_scale, TC* kc, TC* vc, int64_t max_seq, int32_t* flag, const TB* bq, const TB* bk,
+                     const TB* bv, const DenTable& den, hipStream_t stream) {
     const int half = head_dim / 2;
     const int lanes_per_tok = half / P;
     const int toks_per_block = kThreads / lanes_per_tok;
@@ -269,18 +286,21 @@ int launch_rope_kv_p(T* q, int nq, const T* k, const T* v, int nkv, const int32_
     groups = (heads + heads_per_group - 1) / heads_per_group;
     if (blocks_x > INT32_MAX) return SPH_EINVAL;
     const dim3 grid((unsigned)blocks_x, (unsigned)groups);
-    rope_kv_kernel<T, TC, P, IL><<<grid, kThreads, 0, stream>>>(q, nq, k, v, nkv, pos, seq, head_dim, half,
-                                                                lanes_per_tok, toks_per_block, heads_per_group,
-                                                                pos_scale, kc, vc, max_seq, flag, den);
+    rope_kv_kernel<T, TC, TB, P, IL><<<grid, kThreads, 0, stream>>>(q, nq, k, v, nkv, pos, seq, head_dim, half,
+                                                                    lanes_per_tok, toks_per_block, heads_per_group,
+                                                                    pos_scale, kc, vc, max_seq, flag, bq, bk, bv, den);
     return launch_status();
 }
 
 // P: pairs per thread, the widest whose accesses of q/k/v (type T) and of the
 // caches (type TC) stay within 16 bytes and aligned.
-template <typename T, typename TC>
+template <typename T, typename TC, typename TB>
 int launch_rope_kv(void* qv, int nq, const void* kv, const void* vv, int nkv, int layout, const int32_t* pos,
                    int64_t seq, int head_dim, float base, float pos_scale, void* kcv, void* vcv, int64_t max_seq,
-                   int32_t* flag, hipStream_t stream) {
+                   int32_t* flag, const void* bqv, const void* bkv, const void* bvv, hipStream_t stream) {
+    const TB* bq = static_cast<const TB*>(bqv);
+    const TB* bk = static_cast<const TB*>(bkv);
+    const TB* bv = static_cast<const TB*>(bvv);
     T* q = static_cast<T*>(qv);
     const T* k = static_cast<const T*>(kv);
     const T* v = static_cast<const T*>(vv);
@@ -297,19 +317,21 @@ int launch_rope_kv(void* qv, int nq, const void* kv, const void* vv, int nkv, in
         if ((run * sizeof(T)) % 4 != 0 || (run * sizeof(TC)) % 4 != 0) return false;
         const size_t at = run * sizeof(T) < 16 ? run * sizeof(T) : 16;
         const size_t ac = run * sizeof(TC) < 16 ? run * sizeof(TC) : 16;
-        return aligned(q, at) && aligned(k, at) && aligned(v, at) && aligned(kc, ac) && aligned(vc, ac);
+        const size_t ab = run * sizeof(TB) < 16 ? run * sizeof(TB) : 16;  // bias runs may span two 16-byte loads
+        return aligned(q, at) && aligned(k, at) && aligned(v, at) && aligned(kc, ac) && aligned(vc, ac) &&
+               aligned(bq, ab) && aligned(bk, ab) && aligned(bv, ab);
     };
     constexpr int V = vec16<T>::n < vec16<TC>::n ? vec16<T>::n : vec16<TC>::n;
     if (!il) {
-        if (ok(V)) return launch_rope_kv_p<T, TC, V, false>(q, nq, k, v, nkv, pos, seq, head_dim, pos_scale, kc, vc, max_seq, flag, den, stream);
-        if (ok(V / 2)) return launch_rope_kv_p<T, TC, V / 2, false>(q, nq, k, v, nkv, pos, seq, head_dim, pos_scale, kc, vc, max_seq, flag, den, stream);
+        if (ok(V)) return launch_rope_kv_p<T, TC, TB, V, false>(q, nq, k, v, nkv, pos, seq, head_dim, pos_scale, kc, vc, max_seq, flag, bq, bk, bv, den, stream);
+        if (ok(V / 2)) return launch_rope_kv_p<T, TC, TB, V / 2, false>(q, nq, k, v, nkv, pos, seq, head_dim, pos_scale, kc, vc, max_seq, flag, bq, bk, bv, den, stream);
         if constexpr (V / 4 >= 2) {
-            if (ok(V / 4)) return launch_rope_kv_p<T, TC, V / 4, false>(q, nq, k, v, nkv, pos, seq, head_dim, pos_scale, kc, vc, max_seq, flag, den, stream);
+            if (ok(V / 4)) return launch_rope_kv_p<T, TC, TB, V / 4, false>(q, nq, k, v, nkv, pos, seq, head_dim, pos_scale, kc, vc, max_seq, flag, bq, bk, bv, den, stream);
         }
     } else {
-        if (ok(V / 2)) return launch_rope_kv_p<T, TC, V / 2, true>(q, nq, k, v, nkv, pos, seq, head_dim, pos_scale, kc, vc, max_seq, flag, den, stream);
+        if (ok(V / 2)) return launch_rope_kv_p<T, TC, TB, V / 2, true>(q, nq, k, v, nkv, pos, seq, head_dim, pos_scale, kc, vc, max_seq, flag, bq, bk, bv, den, stream);
         if constexpr (V / 4 >= 1) {
-            if (ok(V / 4)) return launch_rope_kv_p<T, TC, V / 4, true>(q, nq, k, v, nkv, pos, seq, head_dim, pos_scale, kc, vc, max_seq, flag, den, stream);
+            if (ok(V / 4)) return launch_rope_kv_p<T, TC, TB, V / 4, true>(q, nq, k, v, nkv, pos, seq, head_dim, pos_scale, kc, vc, max_seq, flag, bq, bk, bv, den, stream);
         }
     }
     return SPH_EINVAL;  // head_dim or alignment the vector paths do not cover
@@ -376,9 +398,12 @@ extern "C" int sph_rope(void* q, int64_t n_q_heads, void* k, int64_t n_k_heads, 
 extern "C" int sph_rope_kv_append(void* q, int64_t n_q_heads, const void* k, const void* v, int64_t n_kv_heads,
                                   int dtype, int layout, const int32_t* positions, int64_t seq, int64_t head_dim,
                                   float base, float pos_scale, void* kcache, void* vcache, int cache_dtype,
-                                  int64_t max_seq, int32_t* bad_pos_flag, void* stream) {
+                                  int64_t max_seq, const void* bq, const void* bk, const void* bv, int bias_dtype,
+                                  int32_t* bad_pos_flag, void* stream) {
     if (layout != SPH_ROPE_NEOX && layout != SPH_ROPE_INTERLEAVED) return SPH_EINVAL;
     if (!sph::is_float_dtype(dtype) || !sph::is_float_dtype(cache_dtype)) return SPH_EINVAL;
+    if ((bq || bk || bv) && !sph::is_float_dtype(bias_dtype)) return SPH_EINVAL;
+    if (!(bq || bk || bv)) bias_dtype = SPH_F32;
     if (n_q_heads < 0 || n_kv_heads < 0 || seq < 0 || max_seq < 0) return SPH_EINVAL;
     if (head_dim <= 0 || head_dim % 2 != 0 || head_dim / 2 > sph::kMaxHalf) return SPH_EINVAL;
     if (n_q_heads + n_kv_heads > INT32_MAX) return SPH_EINVAL;
@@ -391,8 +416,12 @@ extern "C" int sph_rope_kv_append(void* q, int64_t n_q_heads, const void* k, con
         using T = decltype(t);
         return sph::with_float_type(cache_dtype, [&](auto tc) -> int {
             using TC = decltype(tc);
-            return sph::launch_rope_kv<T, TC>(q, (int)n_q_heads, k, v, (int)n_kv_heads, layout, positions, seq,
-                                             (int)head_dim, base, pos_scale, kcache, vcache, max_seq, bad_pos_flag, s);
+            return sph::with_float_type(bias_dtype, [&](auto tb) -> int {
+                using TB = decltype(tb);
+                return sph::launch_rope_kv<T, TC, TB>(q, (int)n_q_heads, k, v, (int)n_kv_heads, layout, positions,
+                                                     seq, (int)head_dim, base, pos_scale, kcache, vcache, max_seq,
+                                                     bad_pos_flag, bq, bk, bv, s);
+            });
         });
     });
 }

@@ -277,9 +277,11 @@ def kv_append(src: torch.Tensor, cache: torch.Tensor, pos: int) -> None:
 
 def rope_kv_append(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, positions: torch.Tensor, base: float,
                    kcache: torch.Tensor, vcache: torch.Tensor, pos_scale: float = 1.0, interleaved: bool = False,
-                   bad_pos_flag: Optional[torch.Tensor] = None) -> None:
-    """Fused decode step: RoPE on q in place; rotated k and v written to the caches at rows
-    positions[s] (wgpu_engine.rs:413-440). q [Hq, S, D], k/v [Hkv, S, D], caches [Hkv, max_seq, D]."""
+                   bad_pos_flag: Optional[torch.Tensor] = None, bq: Optional[torch.Tensor] = None,
+                   bk: Optional[torch.Tensor] = None, bv: Optional[torch.Tensor] = None) -> None:
+    """Fused decode step: optional q/k/v biases, RoPE on q in place; rotated k and v written to
+    the caches at rows positions[s] (wgpu_engine.rs:398-440). q [Hq, S, D], k/v [Hkv, S, D],
+    caches [Hkv, max_seq, D], biases [Hq·D] / [Hkv·D] of one dtype."""
     for t, n in ((q, "q"), (k, "k"), (v, "v"), (kcache, "kcache"), (vcache, "vcache"), (positions, "positions")):
         _dev(t, n)
     if q.dim() != 3 or k.dim() != 3 or k.shape != v.shape or q.shape[1:] != k.shape[1:]:
@@ -298,8 +300,14 @@ def rope_kv_append(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, positions:
         flag = _dev(bad_pos_flag, "bad_pos_flag")
         if flag.dtype != torch.int32 or flag.numel() < 1:
             raise ValueError("bad_pos_flag must be an int32 device tensor")
+    biases = [_vec(bq, Hq * D, "bq"), _vec(bk, Hkv * D, "bk"), _vec(bv, Hkv * D, "bv")]
+    bdt = {b.dtype for b in biases if b is not None}
+    if len(bdt) > 1:
+        raise ValueError("biases must share dtype")
+    bias_code = dtype_code(bdt.pop()) if bdt else 0
     layout = _lib.ROPE_INTERLEAVED if interleaved else _lib.ROPE_NEOX
     check(lib().sph_rope_kv_append(q.data_ptr(), Hq, k.data_ptr(), v.data_ptr(), Hkv, dtype_code(q.dtype), layout,
                                    positions.data_ptr(), S, D, float(base), float(pos_scale), kcache.data_ptr(),
                                    vcache.data_ptr(), dtype_code(kcache.dtype), kcache.shape[1],
+                                   *[None if b is None else b.data_ptr() for b in biases], bias_code,
                                    None if flag is None else flag.data_ptr(), _stream(q)), "rope_kv_append")

@@ -114,7 +114,8 @@ def test_rejects_bad_arguments(dev):
     s = torch.cuda.current_stream().cuda_stream
     d = t.data_ptr()
     args = lambda **kw: dict(dict(q=d, hq=2, k=d, v=d, hkv=2, dt=0, lay=0, pos=p.data_ptr(), seq=1, hd=64, base=1e4,
-                                  ps=1.0, kc=d, vc=d, cdt=0, ms=1, flag=None, s=s), **kw)
+                                  ps=1.0, kc=d, vc=d, cdt=0, ms=1, bq=None, bk=None, bv=None, bdt=0, flag=None,
+                                  s=s), **kw)
     call = lambda a: L.sph_rope_kv_append(*a.values())
     assert call(args(hd=63)) == EINVAL                  # odd head_dim
     assert call(args(lay=2)) == EINVAL                  # layout
@@ -122,3 +123,43 @@ def test_rejects_bad_arguments(dev):
     assert call(args(kc=None)) == EINVAL                # missing cache
     assert call(args(ps=0.0)) == EINVAL                 # pos_scale
     assert call(args(hd=6)) == EINVAL                   # 3 pairs: no vector width divides them
+    assert call(args(bq=d, bdt=8)) == EINVAL            # bias dtype
+
+
+@pytest.mark.parametrize("dtype,cdtype,bdtype", [(torch.float32, torch.float16, torch.float16),
+                                                 (torch.float32, torch.float32, torch.float32),
+                                                 (torch.float16, torch.float16, torch.float32),
+                                                 (torch.bfloat16, torch.float32, torch.bfloat16),
+                                                 (torch.float16, torch.bfloat16, torch.bfloat16)], ids=str)
+@pytest.mark.parametrize("interleaved", [False, True], ids=["neox", "interleaved"])
+@pytest.mark.parametrize("Hq,Hkv,S,D", [(14, 2, 1, 64), (32, 8, 37, 128), (4, 2, 5, 8)])
+def test_fused_biases_equal_add_bias_then_rope_then_append(dev, dtype, cdtype, bdtype, interleaved, Hq, Hkv, S, D):
+    """The projections' bias step (wgpu_engine.rs:398-409, sph_add_bias on token-major q/k/v), the
+    token-major → heads-major transpose, RoPE and the appends, against the fused call on the
+    transposed, bias-free tensors: bit for bit."""
+    print(f"case rope_kv bias {dtype} cache {cdtype} bias {bdtype} {'il' if interleaved else 'neox'} "
+          f"{Hq}+{Hkv}x{S}x{D}", flush=True)
+    max_seq, pos0 = 64, 11
+    q_tok = _gen((S, Hq, D), 11, dev, dtype)
+    k_tok = _gen((S, Hkv, D), 12, dev, dtype)
+    v_tok = _gen((S, Hkv, D), 13, dev, dtype)
+    bq = _gen((Hq * D,), 14, dev, bdtype)
+    bk = _gen((Hkv * D,), 15, dev, bdtype)
+    bv = _gen((Hkv * D,), 16, dev, bdtype)
+    positions = torch.arange(pos0, pos0 + S, dtype=torch.int32, device=dev)
+    kc = torch.zeros(Hkv, max_seq, D, device=dev, dtype=cdtype)
+    vc = torch.zeros(Hkv, max_seq, D, device=dev, dtype=cdtype)
+    kc2, vc2 = kc.clone(), vc.clone()
+    # unfused: bias in token-major layout, then transpose, RoPE, appends
+    qb = ops.add_bias(q_tok.reshape(S, Hq * D), bq).view(S, Hq, D)
+    kb = ops.add_bias(k_tok.reshape(S, Hkv * D), bk).view(S, Hkv, D)
+    vb = ops.add_bias(v_tok.reshape(S, Hkv * D), bv).view(S, Hkv, D)
+    q_ref = _unfused(ops.transpose_heads(qb), ops.transpose_heads(kb), ops.transpose_heads(vb), positions, 1e6,
+                     kc2, vc2, interleaved)
+    # fused
+    q = ops.transpose_heads(q_tok)
+    ops.rope_kv_append(q, ops.transpose_heads(k_tok), ops.transpose_heads(v_tok), positions, 1e6, kc, vc,
+                       interleaved=interleaved, bq=bq, bk=bk, bv=bv)
+    assert np.array_equal(to_np(q), to_np(q_ref)), "q"
+    assert np.array_equal(to_np(kc), to_np(kc2)), "k cache"
+    assert np.array_equal(to_np(vc), to_np(vc2)), "v cache"

@@ -1,0 +1,192 @@
+"""GPU tests of the device-resident decode engine (include/sapient_hip_engine.h).
+
+Reference sequence: WgpuForwardEngine::forward_token / forward_chunk
+(crates/sapient-models/src/forward/wgpu_engine.rs:362-615). Projections and
+attention are outside the library, so the tests plug in exactly reproducible
+stand-ins, enqueued with torch on the engine's stream:
+  projection  out[r, j] = 0.5 · in[r, j mod n_in]   (exact in f32)
+  attention   out = q (the rotated queries, heads-major)
+and check, in order:
+  1. graph replay = eager launches, bit for bit, at every decode step (the
+     graph is replayed for several tokens, eager work and synchronizations in
+     between);
+  2. the engine's hidden states and KV caches against the oracle's
+     restatement of the reference sequence: RMSNorm and SwiGLU compound over
+     the layers, so the bound is 1e-4 of the largest |value| (hidden) and
+     one f16 ulp plus that bound (caches);
+  3. the engine's refusals (full cache, id ≥ vocab, oversized chunk).
+"""
+import numpy as np
+import pytest
+import torch
+
+from helpers import to_np, widen
+
+import sapient_amd._lib as L
+from sapient_amd.engine import Engine
+
+pytestmark = pytest.mark.gpu
+
+H, NQ, NKV, HD, INTER, LAYERS, MAX_SEQ, MAX_CHUNK, VOCAB = 256, 8, 2, 32, 512, 3, 64, 16, 100
+EPS, THETA = 1e-6, 1e4
+PROMPT = [5, 17, 99, 0, 42, 42, 7]
+DECODE = [3, 64, 11, 98, 1]
+
+
+def _gen(shape, seed, dev, mean=0.0, std=1.0, dtype=torch.float32):
+    g = torch.Generator(device=dev).manual_seed(seed)
+    return (torch.randn(shape, generator=g, device=dev) * std + mean).to(dtype)
+
+
+def _n_out(which):
+    return {L.PROJ_Q: NQ * HD, L.PROJ_K: NKV * HD, L.PROJ_V: NKV * HD, L.PROJ_O: H, L.PROJ_GATE: INTER,
+            L.PROJ_UP: INTER, L.PROJ_DOWN: H}[which]
+
+
+def _n_in(which):
+    return {L.PROJ_O: NQ * HD, L.PROJ_DOWN: INTER}.get(which, H)
+
+
+def _view(ptr, n):
+    from sapient_amd.engine import _DevArray
+    return torch.as_tensor(_DevArray(ptr, (n,), "<f4"), device="cuda")
+
+
+def project(layer, which, in_ptr, out_ptr, rows, stream):
+    n_in, n_out = _n_in(which), _n_out(which)
+    src = _view(in_ptr, rows * n_in).view(rows, n_in)
+    dst = _view(out_ptr, rows * n_out).view(rows, n_out)
+    with torch.cuda.stream(torch.cuda.ExternalStream(stream)):
+        for j0 in range(0, n_out, n_in):
+            w = min(n_in, n_out - j0)
+            dst[:, j0:j0 + w].copy_(src[:, :w])
+        dst.mul_(0.5)
+    return 0
+
+
+def attend(layer, q_ptr, kc, vc, kv_dtype, pos_ptr, n_tok, max_seq, out_ptr, stream):
+    n = NQ * n_tok * HD
+    with torch.cuda.stream(torch.cuda.ExternalStream(stream)):
+        _view(out_ptr, n).copy_(_view(q_ptr, n))
+    return 0
+
+
+@pytest.fixture(scope="module")
+def model(dev):
+    table = _gen((VOCAB, H), 1, dev)
+    layers = [dict(input_ln=_gen((H,), 10 + l, dev, 1.0, 0.1), post_ln=_gen((H,), 20 + l, dev, 1.0, 0.1),
+                   bq=_gen((NQ * HD,), 30 + l, dev, 0.0, 0.1, torch.float16),
+                   bk=_gen((NKV * HD,), 40 + l, dev, 0.0, 0.1, torch.float16),
+                   bv=_gen((NKV * HD,), 50 + l, dev, 0.0, 0.1, torch.float16), bo=None) for l in range(LAYERS)]
+    final = _gen((H,), 60, dev, 1.0, 0.1)
+    return table, layers, final
+
+
+def _engine(model, kv_dtype=L.F16):
+    table, layers, final = model
+    cfg = L.EngineConfig(H, NQ, NKV, HD, INTER, LAYERS, MAX_SEQ, MAX_CHUNK, EPS, THETA, L.ROPE_NEOX, kv_dtype, L.F16)
+    return Engine(cfg, table, L.F32, VOCAB, layers, final, project, attend)
+
+
+def _run(eng, graph):
+    eng.use_graph(graph)
+    outs = [eng.forward_chunk(PROMPT).clone()]
+    torch.cuda.synchronize()
+    for t in DECODE:
+        outs.append(eng.forward_token(t).clone())
+        torch.cuda.synchronize()
+    return [to_np(o) for o in outs]
+
+
+def test_graph_replay_equals_eager(dev, model):
+    eager = _engine(model)
+    e_out = _run(eager, False)
+    graph = _engine(model)
+    g_out = _run(graph, True)
+    print("case engine graph vs eager", flush=True)
+    for i, (a, b) in enumerate(zip(e_out, g_out)):
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), f"step {i}"
+    for l in range(LAYERS):
+        for w in "kv":
+            assert torch.equal(eager.cache(l, w), graph.cache(l, w)), f"layer {l} {w} cache"
+    assert eager.position == graph.position == len(PROMPT) + len(DECODE)
+    eager.close()
+    graph.close()
+
+
+def _oracle_step(orc, model_np, ids, pos0, caches):
+    """One forward call of the reference sequence (wgpu_engine.rs:362-615) with the stand-ins."""
+    table, layers, final = model_np
+    T = len(ids)
+    pos = np.arange(pos0, pos0 + T)
+    proj = lambda x, n_out: 0.5 * np.tile(x, (1, -(-n_out // x.shape[1])))[:, :n_out]
+    x = orc.embed_tokens(table.reshape(-1).view(np.uint8), L.F32, VOCAB, H, np.array(ids, np.uint32))
+    x = x.reshape(T, H)
+    down = None
+    for l, Lw in enumerate(layers):
+        if l > 0:
+            x = orc.add(x, down)
+        h = orc.rms_norm(x, Lw["input_ln"], EPS)
+        q = orc.add_bias_last_dim(proj(h, NQ * HD).astype(np.float32), Lw["bq"])
+        k = orc.add_bias_last_dim(proj(h, NKV * HD).astype(np.float32), Lw["bk"])
+        v = orc.add_bias_last_dim(proj(h, NKV * HD).astype(np.float32), Lw["bv"])
+        qh = q.reshape(T, NQ, HD).transpose(1, 0, 2)[None]
+        kh = k.reshape(T, NKV, HD).transpose(1, 0, 2)[None]
+        vh = v.reshape(T, NKV, HD).transpose(1, 0, 2)
+        qr = orc.apply_rope(np.ascontiguousarray(qh), pos, THETA)[0]
+        kr = orc.apply_rope(np.ascontiguousarray(kh), pos, THETA)[0]
+        orc.kv_append(kr, caches[l][0], L.F16, NKV, T, HD, MAX_SEQ, pos0)
+        orc.kv_append(np.ascontiguousarray(vh), caches[l][1], L.F16, NKV, T, HD, MAX_SEQ, pos0)
+        attn = qr.transpose(1, 0, 2).reshape(T, NQ * HD)
+        o = proj(attn, H).astype(np.float32)
+        x = orc.add(x, o)
+        h2 = orc.rms_norm(x, Lw["post_ln"], EPS)
+        act = orc.swiglu(proj(h2, INTER).astype(np.float32), proj(h2, INTER).astype(np.float32))
+        down = proj(act, H).astype(np.float32)
+    last = orc.add(x[-1:], down[-1:])
+    return orc.rms_norm(last, final, EPS)[0]
+
+
+def test_engine_matches_oracle_sequence(dev, orc, model):
+    table, layers, final = model
+    model_np = (to_np(table), [{k: (None if v is None else widen(v, orc)) for k, v in Lw.items()} for Lw in layers],
+                to_np(final))
+    eng = _engine(model)
+    got = _run(eng, True)
+    caches = [(np.zeros((NKV, MAX_SEQ, HD), np.uint16), np.zeros((NKV, MAX_SEQ, HD), np.uint16))
+              for _ in range(LAYERS)]
+    want = [_oracle_step(orc, model_np, PROMPT, 0, caches)]
+    for i, t in enumerate(DECODE):
+        want.append(_oracle_step(orc, model_np, [t], len(PROMPT) + i, caches))
+    print("case engine vs oracle", flush=True)
+    for i, (g, w) in enumerate(zip(got, want)):
+        assert np.abs(g - w).max() <= 1e-4 * np.abs(w).max(), f"step {i}: {np.abs(g - w).max()}"
+    used = len(PROMPT) + len(DECODE)
+    for l in range(LAYERS):
+        for j, which in enumerate("kv"):
+            g = widen(eng.cache(l, which), orc).reshape(NKV, MAX_SEQ, HD)
+            w = orc.f16_bits_to_f32(caches[l][j])
+            scale = np.abs(w[:, :used]).max()
+            assert np.all(np.abs(g[:, :used] - w[:, :used]) <= 2.0 ** -10 * np.abs(w[:, :used]) + 1e-4 * scale), \
+                f"layer {l} {which} cache"
+            assert (g[:, used:] == 0).all()
+    eng.close()
+
+
+def test_engine_refusals(dev, model):
+    from sapient_amd._lib import SapientHipError
+    eng = _engine(model)
+    with pytest.raises(SapientHipError, match="index out of range"):
+        eng.forward_token(VOCAB)
+    with pytest.raises(SapientHipError, match="invalid"):
+        eng.forward_chunk(list(range(MAX_CHUNK + 1)))
+    for _ in range(MAX_SEQ // MAX_CHUNK):
+        eng.forward_chunk([1] * MAX_CHUNK)
+    assert eng.position == MAX_SEQ
+    with pytest.raises(SapientHipError, match="index out of range"):
+        eng.forward_token(1)
+    eng.reset()
+    assert eng.position == 0
+    eng.forward_token(2)
+    torch.cuda.synchronize()
+    eng.close()
