@@ -156,7 +156,7 @@ int sph_rope(void* q, int64_t n_q_heads, void* k, int64_t n_k_heads, int dtype, 
  * Results equal sph_rope (batch 1, rotary_dim = head_dim) on q and k followed
  * by sph_kv_append of k and v at pos = positions[0] when positions are
  * consecutive — the sequence of WgpuForwardEngine::forward_token
- * (crates/sapient-models/src/forward/wgpu_engine.rs:413-440, resident.rs:467
+ * (crates/sapient-models/src/forward/wgpu_engine.rs:408-432, resident.rs:467
  * then :645-711) — in one launch. Positions are read on the device, so a HIP
  * graph capturing this call replays correctly as positions change. A position
  * outside [0, max_seq) writes nothing to the caches and stores 1 to
@@ -166,7 +166,7 @@ int sph_rope(void* q, int64_t n_q_heads, void* k, int64_t n_k_heads, int dtype, 
  * Optional biases bq [n_q_heads · head_dim], bk and bv [n_kv_heads · head_dim]
  * (bias_dtype ∈ {F32, F16, BF16}; NULL = none) are added first, as
  * sph_add_bias on q, k, v would (the projections' bias step,
- * wgpu_engine.rs:398-409): the sum is rounded to `dtype` before RoPE / the
+ * wgpu_engine.rs:397-407): the sum is rounded to `dtype` before RoPE / the
  * cache conversion, so the result equals that unfused sequence bit for bit. */
 int sph_rope_kv_append(void* q, int64_t n_q_heads, const void* k, const void* v, int64_t n_kv_heads, int dtype,
                        int layout, const int32_t* positions, int64_t seq, int64_t head_dim, float base,

@@ -3,7 +3,7 @@
  * sapient_hip.h, for callers that keep a model's activations on one MI355X.
  *
  * It is the HIP counterpart of sapient's WgpuForwardEngine
- * (crates/sapient-models/src/forward/wgpu_engine.rs:362-615): the same per-layer
+ * (crates/sapient-models/src/forward/wgpu_engine.rs:362-629): the same per-layer
  * sequence for a Llama-family decoder — embed → per layer {RMSNorm → Q/K/V
  * projections (+bias) → RoPE → KV-cache append → attention → O projection
  * (+bias) → residual add → RMSNorm → gate/up projections → SwiGLU → down

@@ -1,6 +1,6 @@
 // hip_forward_engine.cpp — the device-resident decode engine of
 // sapient_hip_engine.h: sapient's WgpuForwardEngine sequence
-// (crates/sapient-models/src/forward/wgpu_engine.rs:362-615) on one HIP stream,
+// (crates/sapient-models/src/forward/wgpu_engine.rs:362-629) on one HIP stream,
 // built from the op set's C ABI.
 //
 // Differences from the reference's op-by-op sequence, each result-preserving:
@@ -11,7 +11,7 @@
 //    channel, so adding them after the token-major → heads-major transpose of
 //    a chunk gives the same sums);
 //  - forward_chunk adds the last layer's residual and normalises only the last
-//    row, the one the reference slices out before its final norm (:608-611).
+//    row, the one the reference slices out before its final norm (:623-627).
 // Decode steps can be captured into a HIP graph once and replayed: every
 // per-token value (token id, position) lives in device memory, refreshed by an
 // H2D copy from pinned staging before each launch.

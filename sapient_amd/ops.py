@@ -280,7 +280,7 @@ def rope_kv_append(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, positions:
                    bad_pos_flag: Optional[torch.Tensor] = None, bq: Optional[torch.Tensor] = None,
                    bk: Optional[torch.Tensor] = None, bv: Optional[torch.Tensor] = None) -> None:
     """Fused decode step: optional q/k/v biases, RoPE on q in place; rotated k and v written to
-    the caches at rows positions[s] (wgpu_engine.rs:398-440). q [Hq, S, D], k/v [Hkv, S, D],
+    the caches at rows positions[s] (wgpu_engine.rs:397-432). q [Hq, S, D], k/v [Hkv, S, D],
     caches [Hkv, max_seq, D], biases [Hq·D] / [Hkv·D] of one dtype."""
     for t, n in ((q, "q"), (k, "k"), (v, "v"), (kcache, "kcache"), (vcache, "vcache"), (positions, "positions")):
         _dev(t, n)

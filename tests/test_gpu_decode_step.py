@@ -1,7 +1,7 @@
 """GPU parity: the fused decode step (RoPE on q and k + KV-cache append of k and v).
 
 Reference sequence: WgpuForwardEngine::forward_token / forward_chunk
-(crates/sapient-models/src/forward/wgpu_engine.rs:413-440, :561-589) — rope on q
+(crates/sapient-models/src/forward/wgpu_engine.rs:397-432, :527-573) — rope on q
 and k (resident.rs:467), then kv_append of k and v (resident.rs:645-711).
 
 Bar: bit-exact against the unfused sequence of this library's own kernels
@@ -134,7 +134,7 @@ def test_rejects_bad_arguments(dev):
 @pytest.mark.parametrize("interleaved", [False, True], ids=["neox", "interleaved"])
 @pytest.mark.parametrize("Hq,Hkv,S,D", [(14, 2, 1, 64), (32, 8, 37, 128), (4, 2, 5, 8)])
 def test_fused_biases_equal_add_bias_then_rope_then_append(dev, dtype, cdtype, bdtype, interleaved, Hq, Hkv, S, D):
-    """The projections' bias step (wgpu_engine.rs:398-409, sph_add_bias on token-major q/k/v), the
+    """The projections' bias step (wgpu_engine.rs:397-407, :527-538, sph_add_bias on token-major q/k/v), the
     token-major → heads-major transpose, RoPE and the appends, against the fused call on the
     transposed, bias-free tensors: bit for bit."""
     print(f"case rope_kv bias {dtype} cache {cdtype} bias {bdtype} {'il' if interleaved else 'neox'} "

@@ -1,7 +1,7 @@
 """GPU tests of the device-resident decode engine (include/sapient_hip_engine.h).
 
 Reference sequence: WgpuForwardEngine::forward_token / forward_chunk
-(crates/sapient-models/src/forward/wgpu_engine.rs:362-615). Projections and
+(crates/sapient-models/src/forward/wgpu_engine.rs:362-629). Projections and
 attention are outside the library, so the tests plug in exactly reproducible
 stand-ins, enqueued with torch on the engine's stream:
   projection  out[r, j] = 0.5 · in[r, j mod n_in]   (exact in f32)
@@ -115,7 +115,7 @@ def test_graph_replay_equals_eager(dev, model):
 
 
 def _oracle_step(orc, model_np, ids, pos0, caches):
-    """One forward call of the reference sequence (wgpu_engine.rs:362-615) with the stand-ins."""
+    """One forward call of the reference sequence (wgpu_engine.rs:362-629) with the stand-ins."""
     table, layers, final = model_np
     T = len(ids)
     pos = np.arange(pos0, pos0 + T)
