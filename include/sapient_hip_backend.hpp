@@ -51,6 +51,8 @@ class Tensor {
     DType dtype() const { return dtype_; }
     size_t numel() const;
     const std::vector<uint8_t>& bytes() const { return bytes_; }
+    // The same bytes under another shape of equal numel (Tensor::reshape).
+    Tensor reshaped(std::vector<size_t> shape) const;
     // The values of an F32 tensor (as_f32_slice); throws for other dtypes.
     std::vector<float> as_f32() const;
 
@@ -76,9 +78,13 @@ class HipLlmBackend {
 
     // LlmBackend::rms_norm (backend.rs:72 → layernorm.rs:75-106): f32 output.
     Tensor rms_norm(const Tensor& x, const Tensor& weight, float eps);
+    // kernels::layernorm::rms_norm with the kernel's optional weight (graph path).
+    Tensor rms_norm(const Tensor& x, const Tensor* weight, float eps);
     // LlmBackend::layer_norm (backend.rs:73-79 → layernorm.rs:17-69, last axis):
     // `bias` may be null; f32 output.
     Tensor layer_norm(const Tensor& x, const Tensor& weight, const Tensor* bias, float eps);
+    // kernels::layernorm::layer_norm over the axes from `axis` on; weight and bias optional.
+    Tensor layer_norm(const Tensor& x, const Tensor* weight, const Tensor* bias, int64_t axis, float eps);
     // common::add_bias_last_dim (common.rs:556-569), the bias step of
     // LlmBackend::linear_3d_bias (backend.rs:64-70): y F32, bias [y.last_dim].
     Tensor add_bias_last_dim(const Tensor& y, const Tensor& bias);
@@ -130,6 +136,34 @@ class HipLlmBackend {
 
     void* stream_ = nullptr;
     std::mutex mu_;
+};
+
+// Graph-side ops the HIP backend executes: the ExecutionBackend's supports_op
+// set of the path (crates/sapient-backends/cpu/src/backend.rs:168-196 lists
+// the CPU's); every other op stays on the CPU backend.
+enum class OpKind { Add, Mul, Silu, Gelu, RmsNorm, LayerNorm, RotaryEmbedding, Embedding };
+
+// The attributes these ops carry in OpType (epsilon, axis, base).
+struct OpAttrs {
+    float epsilon = 1e-5f;
+    int64_t axis = -1;
+    float base = 10000.0f;
+};
+
+// The per-node part of ExecutionBackend::execute for the path: one arm of
+// CpuBackend::dispatch (cpu/src/backend.rs:239-487) per OpKind, with its input
+// order (nullptr for an absent optional input) and output shapes. Walking the
+// graph stays with the caller's executor. Differences from the CPU arms: an
+// embedding id >= vocab is an error here (the CPU arm indexes out of bounds).
+class HipExecutionBackend {
+ public:
+    explicit HipExecutionBackend(HipLlmBackend& llm) : llm_(llm) {}
+    const char* name() const { return "hip"; }
+    static bool supports_op(OpKind op);
+    std::vector<Tensor> dispatch(OpKind op, const OpAttrs& attrs, const std::vector<const Tensor*>& inputs);
+
+ private:
+    HipLlmBackend& llm_;
 };
 
 }  // namespace sapient_hip

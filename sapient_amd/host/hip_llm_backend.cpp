@@ -91,6 +91,13 @@ Tensor Tensor::from_quant_bytes(std::vector<uint8_t> bytes, std::vector<size_t> 
     return Tensor(std::move(shape), dt, std::move(bytes));
 }
 
+Tensor Tensor::reshaped(std::vector<size_t> shape) const {
+    size_t n = 1;
+    for (size_t d : shape) n *= d;
+    if (n != numel()) throw Error("cannot reshape " + shape_str(shape_) + " to " + shape_str(shape));
+    return Tensor(std::move(shape), dtype_, bytes_);
+}
+
 std::vector<float> Tensor::as_f32() const {
     if (dtype_ != DType::F32) throw Error(std::string("type mismatch: expected f32, got ") + dtype_name(dtype_));
     std::vector<float> v(numel());
@@ -186,7 +193,10 @@ Tensor HipLlmBackend::f32_input(const Tensor& t) const {
     return Tensor::from_f32(v, t.shape());
 }
 
-Tensor HipLlmBackend::rms_norm(const Tensor& x, const Tensor& weight_t, float eps) {
+Tensor HipLlmBackend::rms_norm(const Tensor& x, const Tensor& weight_t, float eps) { return rms_norm(x, &weight_t, eps); }
+
+// layernorm::rms_norm (layernorm.rs:75-106): last axis, weight optional.
+Tensor HipLlmBackend::rms_norm(const Tensor& x, const Tensor* weight_t, float eps) {
     std::lock_guard<std::mutex> lock(mu_);
     const auto& s = x.shape();
     const size_t dim = s.empty() ? 1 : s.back();
@@ -194,13 +204,17 @@ Tensor HipLlmBackend::rms_norm(const Tensor& x, const Tensor& weight_t, float ep
     if (x.dtype() != DType::F32 && x.dtype() != DType::F16 && x.dtype() != DType::BF16)
         throw Error(std::string("type mismatch: expected a float tensor, got ") + dtype_name(x.dtype()));
     // The device kernel takes an f32 weight or one of x's type (widened exactly on the host otherwise).
-    const Tensor wt = (weight_t.dtype() == DType::F32 || weight_t.dtype() == x.dtype()) ? weight_t : f32_input(weight_t);
-    if (wt.numel() != dim) throw Error("shape mismatch: weight " + shape_str(wt.shape()) + " for rows of " + std::to_string(dim));
+    Tensor wt;
+    if (weight_t) {
+        wt = (weight_t->dtype() == DType::F32 || weight_t->dtype() == x.dtype()) ? *weight_t : f32_input(*weight_t);
+        if (wt.numel() != dim)
+            throw Error("shape mismatch: weight " + shape_str(wt.shape()) + " for rows of " + std::to_string(dim));
+    }
     DeviceBuf xd = upload(x.bytes().data(), x.bytes().size());
-    DeviceBuf wd = upload(wt.bytes().data(), wt.bytes().size());
+    DeviceBuf wd = weight_t ? upload(wt.bytes().data(), wt.bytes().size()) : DeviceBuf{};
     DeviceBuf od = alloc(x.numel() * 4);
-    const int st = sph_rms_norm(xd.ptr, (int)x.dtype(), wd.ptr, (int)wt.dtype(), od.ptr, SPH_F32, (int64_t)rows,
-                                (int64_t)dim, eps, stream_);
+    const int st = sph_rms_norm(xd.ptr, (int)x.dtype(), wd.ptr, weight_t ? (int)wt.dtype() : SPH_F32, od.ptr, SPH_F32,
+                                (int64_t)rows, (int64_t)dim, eps, stream_);
     std::vector<float> out(x.numel());
     if (st == SPH_OK) download(od, out.data(), out.size() * 4);
     release(xd);
@@ -289,19 +303,31 @@ Tensor HipLlmBackend::silu(const Tensor& x) { return unary_f32(x, "silu"); }
 Tensor HipLlmBackend::gelu(const Tensor& x) { return unary_f32(x, "gelu"); }
 Tensor HipLlmBackend::gelu_erf(const Tensor& x) { return unary_f32(x, "gelu_erf"); }
 
-// layernorm::layer_norm (layernorm.rs:17-69) over the last axis: x, weight and
-// bias are widened to f32 (to_f32_cow) and the output is f32.
-Tensor HipLlmBackend::layer_norm(const Tensor& x0, const Tensor& weight0, const Tensor* bias0, float eps) {
-    const Tensor x = f32_input(x0), w = f32_input(weight0);
+Tensor HipLlmBackend::layer_norm(const Tensor& x, const Tensor& weight, const Tensor* bias, float eps) {
+    return layer_norm(x, &weight, bias, -1, eps);
+}
+
+// layernorm::layer_norm (layernorm.rs:17-69): normalises over the axes from
+// `axis` on (negative counts from the end); x, weight and bias are widened to
+// f32 (to_f32_cow) and the output is f32. Weight and bias are optional.
+Tensor HipLlmBackend::layer_norm(const Tensor& x0, const Tensor* weight0, const Tensor* bias0, int64_t axis,
+                                 float eps) {
+    const Tensor x = f32_input(x0);
+    const Tensor w = weight0 ? f32_input(*weight0) : Tensor();
     const Tensor b = bias0 ? f32_input(*bias0) : Tensor();
     const auto& s = x.shape();
-    const size_t dim = s.empty() ? 1 : s.back();
+    const int64_t nd = (int64_t)s.size();
+    const int64_t ax = axis < 0 ? nd + axis : axis;
+    if (ax < 0 || ax > nd) throw Error("axis " + std::to_string(axis) + " out of range for " + shape_str(s));
+    size_t dim = 1;
+    for (int64_t i = ax; i < nd; ++i) dim *= s[i];
     const size_t rows = dim ? x.numel() / dim : 0;
-    if (w.numel() != dim) throw Error("shape mismatch: weight " + shape_str(w.shape()) + " for rows of " + std::to_string(dim));
+    if (weight0 && w.numel() != dim)
+        throw Error("shape mismatch: weight " + shape_str(w.shape()) + " for rows of " + std::to_string(dim));
     if (bias0 && b.numel() != dim) throw Error("shape mismatch: bias " + shape_str(b.shape()) + " for rows of " + std::to_string(dim));
     std::lock_guard<std::mutex> lock(mu_);
     DeviceBuf xd = upload(x.bytes().data(), x.bytes().size());
-    DeviceBuf wd = upload(w.bytes().data(), w.bytes().size());
+    DeviceBuf wd = weight0 ? upload(w.bytes().data(), w.bytes().size()) : DeviceBuf{};
     DeviceBuf bd = bias0 ? upload(b.bytes().data(), b.bytes().size()) : DeviceBuf{};
     DeviceBuf od = alloc(x.numel() * 4);
     const int st = sph_layer_norm(xd.ptr, SPH_F32, wd.ptr, bd.ptr, SPH_F32, od.ptr, SPH_F32, (int64_t)rows,
@@ -428,6 +454,59 @@ Tensor HipLlmBackend::embed_tokens(const Tensor& w, const std::vector<uint32_t>&
     if (st == SPH_EINVAL) throw Error(std::string("unsupported embedding dtype ") + dtype_name(w.dtype()));
     check(st, "embed_tokens");
     return Tensor::from_f32(out, {1, ids.size(), hidden});
+}
+
+// ── graph-side dispatch ─────────────────────────────────────────────────────
+
+bool HipExecutionBackend::supports_op(OpKind) { return true; }  // every kind of OpKind runs here
+
+std::vector<Tensor> HipExecutionBackend::dispatch(OpKind op, const OpAttrs& attrs,
+                                                  const std::vector<const Tensor*>& in) {
+    auto need = [&](size_t i, const char* what) -> const Tensor& {
+        if (i >= in.size() || in[i] == nullptr) throw Error(std::string(what));
+        return *in[i];
+    };
+    auto opt = [&](size_t i) -> const Tensor* { return i < in.size() ? in[i] : nullptr; };
+    switch (op) {
+    case OpKind::Add: return {llm_.add(need(0, "Add: missing a"), need(1, "Add: missing b"))};
+    case OpKind::Mul: return {llm_.mul(need(0, "Mul: missing a"), need(1, "Mul: missing b"))};
+    case OpKind::Silu: return {llm_.silu(need(0, "Silu: missing input"))};
+    case OpKind::Gelu: return {llm_.gelu(need(0, "Gelu: missing input"))};
+    case OpKind::RmsNorm: return {llm_.rms_norm(need(0, "RmsNorm: missing input"), opt(1), attrs.epsilon)};
+    case OpKind::LayerNorm:
+        return {llm_.layer_norm(need(0, "LayerNorm: missing input"), opt(1), opt(2), attrs.axis, attrs.epsilon)};
+    case OpKind::RotaryEmbedding: {
+        // positions 0 .. seq_len - 1, seq_len = dims[2] (cpu/src/backend.rs:480-487)
+        const Tensor& x = need(0, "RoPE: missing input");
+        const size_t seq = x.shape().size() > 2 ? x.shape()[2] : 1;
+        std::vector<size_t> pos(seq);
+        for (size_t i = 0; i < seq; ++i) pos[i] = i;
+        return {llm_.apply_rope_positions(x, pos, attrs.base)};
+    }
+    case OpKind::Embedding: {
+        // weight [vocab, hidden] at inputs[0], ids at inputs[1]: F32 values cast to u32
+        // (Rust `as`: saturating, NaN → 0) or raw little-endian u32 (cpu/src/backend.rs:381-411)
+        const Tensor& w = need(0, "Embedding: missing weight");
+        const Tensor& ids_t = need(1, "Embedding: missing input_ids");
+        std::vector<uint32_t> ids;
+        if (ids_t.dtype() == DType::F32) {
+            for (float v : ids_t.as_f32())
+                ids.push_back(!(v > 0.0f) ? 0u : (v >= 4294967295.0f ? 0xFFFFFFFFu : (uint32_t)v));
+        } else {
+            const auto& b = ids_t.bytes();
+            for (size_t i = 0; i + 4 <= b.size(); i += 4)
+                ids.push_back((uint32_t)b[i] | ((uint32_t)b[i + 1] << 8) | ((uint32_t)b[i + 2] << 16) |
+                              ((uint32_t)b[i + 3] << 24));
+        }
+        const auto& d = ids_t.shape();
+        const size_t batch = d.size() >= 2 ? d[0] : 1;
+        const size_t seq = d.size() >= 2 ? d[1] : ids.size();
+        Tensor out = llm_.embed_tokens(w, ids);
+        if (batch * seq != ids.size()) throw Error("Embedding: ids shape " + shape_str(d) + " is not [batch, seq]");
+        return {out.reshaped({batch, seq, w.shape()[1]})};
+    }
+    }
+    throw Error("unsupported op");
 }
 
 }  // namespace sapient_hip

@@ -1,7 +1,8 @@
 // GPU tests of the C++ LlmBackend mirror (include/sapient_hip_backend.hpp),
 // written after the reference's own unit tests so they read the same way:
 //   layernorm.rs:113-149, elementwise.rs:176-232, rope.rs:155-206,
-//   common.rs:556-569 and :669-718, and the trait's validation errors (rope.rs:19-35,
+//   common.rs:556-569 and :669-718, the graph-side dispatch arms of
+//   crates/sapient-backends/cpu/src/backend.rs:239-487, and the trait's validation errors (rope.rs:19-35,
 //   elementwise.rs:15-21, common.rs:171-173).
 // Prints "test <name> ... ok|FAILED: <why>" per test; exits 1 if any failed.
 #include <cmath>
@@ -146,6 +147,65 @@ static void add_bias_last_dim_broadcasts(HipLlmBackend& bk) {  // common.rs:556-
     ASSERT(h == std::vector<float>({1.5f, 1.0f, 5.0f, 4.5f, 4.0f, 8.0f}), "f16 bias");
     const std::string e = expect_error([&] { bk.add_bias_last_dim(y, Tensor::from_f32({1.0f, 2.0f}, {2})); });
     ASSERT(e.find("bias length 2 does not match last dim 3") != std::string::npos, "length error");
+}
+
+// ── graph-side dispatch (cpu/src/backend.rs:239-487) ──────────────────────────
+static void graph_rms_norm_optional_weight(HipLlmBackend& bk) {  // :313-320 with inputs.get(1) = None
+    sapient_hip::HipExecutionBackend ex(bk);
+    const Tensor x = Tensor::from_f32({3.0f, 4.0f}, {1, 2});
+    sapient_hip::OpAttrs a;
+    a.epsilon = 0.0f;
+    const std::vector<float> d = ex.dispatch(sapient_hip::OpKind::RmsNorm, a, {&x}).at(0).as_f32();
+    ASSERT(std::fabs(d[0] - 3.0f / std::sqrt(12.5f)) < 1e-5f && std::fabs(d[1] - 4.0f / std::sqrt(12.5f)) < 1e-5f,
+           "unit-weight rms_norm");
+}
+
+static void graph_layer_norm_axis(HipLlmBackend& bk) {  // :302-312, axis = 1 on [2, 2, 2]
+    sapient_hip::HipExecutionBackend ex(bk);
+    const std::vector<float> v = {1, 2, 3, 4, 10, 20, 30, 40};
+    const Tensor x = Tensor::from_f32(v, {2, 2, 2});
+    sapient_hip::OpAttrs a;
+    a.axis = 1;
+    a.epsilon = 1e-5f;
+    const std::vector<float> d = ex.dispatch(sapient_hip::OpKind::LayerNorm, a, {&x}).at(0).as_f32();
+    for (int r = 0; r < 2; ++r) {  // each outer row normalises 4 values
+        double m = 0, var = 0;
+        for (int i = 0; i < 4; ++i) m += v[r * 4 + i] / 4.0;
+        for (int i = 0; i < 4; ++i) var += (v[r * 4 + i] - m) * (v[r * 4 + i] - m) / 4.0;
+        for (int i = 0; i < 4; ++i)
+            ASSERT(std::fabs(d[r * 4 + i] - (v[r * 4 + i] - m) / std::sqrt(var + 1e-5)) < 1e-5, "layer_norm axis 1");
+    }
+}
+
+static void graph_embedding_ids_and_shape(HipLlmBackend& bk) {  // :381-411
+    sapient_hip::HipExecutionBackend ex(bk);
+    std::vector<float> table(5 * 4);
+    for (size_t i = 0; i < table.size(); ++i) table[i] = (float)i;
+    const Tensor w = Tensor::from_f32(table, {5, 4});
+    const Tensor ids_f = Tensor::from_f32({4.0f, 0.0f, 2.0f}, {1, 3});  // F32 ids, cast as Rust `as u32`
+    const Tensor out = ex.dispatch(sapient_hip::OpKind::Embedding, {}, {&w, &ids_f}).at(0);
+    ASSERT(out.shape() == std::vector<size_t>({1, 3, 4}), "output [batch, seq, hidden]");
+    const std::vector<float> o = out.as_f32();
+    for (int c = 0; c < 4; ++c)
+        ASSERT(o[c] == 16.0f + c && o[4 + c] == (float)c && o[8 + c] == 8.0f + c, "gathered rows");
+    const std::string e = expect_error([&] {
+        const Tensor bad = Tensor::from_f32({5.0f}, {1, 1});
+        ex.dispatch(sapient_hip::OpKind::Embedding, {}, {&w, &bad});
+    });
+    ASSERT(e.find("out of vocab range") != std::string::npos, "id >= vocab");
+}
+
+static void graph_rope_positions_from_seq(HipLlmBackend& bk) {  // :480-487: positions 0 .. dims[2]
+    sapient_hip::HipExecutionBackend ex(bk);
+    std::vector<float> data;
+    for (int i = 0; i < 2 * 3 * 8; ++i) data.push_back(0.05f * (float)i - 1.0f);
+    const Tensor x = Tensor::from_f32(data, {1, 2, 3, 8});
+    sapient_hip::OpAttrs a;
+    a.base = 10000.0f;
+    const std::vector<float> g = ex.dispatch(sapient_hip::OpKind::RotaryEmbedding, a, {&x}).at(0).as_f32();
+    const std::vector<float> w = bk.apply_rope_positions(x, {0, 1, 2}, 10000.0f).as_f32();
+    ASSERT(g == w, "graph RoPE == apply_rope_positions(0..S)");
+    ASSERT(sapient_hip::HipExecutionBackend::supports_op(sapient_hip::OpKind::RotaryEmbedding), "supports_op");
 }
 
 static void test_add(HipLlmBackend& bk) {  // elementwise.rs:184-194
@@ -305,6 +365,10 @@ int main() {
         {"layernorm_zero_mean_unit_var", layernorm_zero_mean_unit_var},
         {"test_gelu_erf", test_gelu_erf},
         {"add_bias_last_dim_broadcasts", add_bias_last_dim_broadcasts},
+        {"graph_rms_norm_optional_weight", graph_rms_norm_optional_weight},
+        {"graph_layer_norm_axis", graph_layer_norm_axis},
+        {"graph_embedding_ids_and_shape", graph_embedding_ids_and_shape},
+        {"graph_rope_positions_from_seq", graph_rope_positions_from_seq},
         {"test_add", test_add},
         {"test_scalar_broadcast", test_scalar_broadcast},
         {"test_gelu", test_gelu},
