@@ -205,6 +205,10 @@ def op_table(torch, ops, dev, only=None):
         lambda: [(gen(torch, (8192, 14336), 70 + i, dev, f16, 2.0), gen(torch, (8192, 14336), 80 + i, dev, f16, 2.0),
                   torch.empty(8192, 14336, device=dev, dtype=f16)) for i in range(2)],
         lambda s: ops.swiglu(s[0], s[1], out=s[2]))
+    run("swiglu", "8192x14336", "f32", 3 * n * 4, 8192, "rows",
+        lambda: [(gen(torch, (8192, 14336), 75 + i, dev, f32, 2.0), gen(torch, (8192, 14336), 85 + i, dev, f32, 2.0),
+                  torch.empty(8192, 14336, device=dev, dtype=f32)) for i in range(2)],
+        lambda s: ops.swiglu(s[0], s[1], out=s[2]))
     ops.init(dev)
     n = 8192 * 10240
     run("gelu_tanh", "8192x10240", "f16", 2 * n * 2, 8192, "rows",

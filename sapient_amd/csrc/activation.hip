@@ -72,18 +72,24 @@ __device__ __forceinline__ float silu_f(float g) {
     return g * __builtin_amdgcn_rcpf(1.0f + e);
 }
 
-template <int OP>
+// T: the storage type. f32 SiLU / SwiGLU evaluate the reference's expression
+// exactly (glibc's expf restated, IEEE division): bit-exact, and within the
+// bandwidth budget of 8-12 bytes per element.
+template <int OP, typename T>
 __device__ __forceinline__ float apply_op(float a, float b, const uint64_t* exp_tab) {
+    constexpr bool kExact = sizeof(T) == 4;
     if constexpr (OP == OP_ADD) return a + b;
     if constexpr (OP == OP_MUL) return a * b;
-    if constexpr (OP == OP_SILU) return silu_f(a);
-    if constexpr (OP == OP_SWIGLU) return silu_f(a) * b;
+    if constexpr (OP == OP_SILU) return kExact ? silu_ref_order(a, exp_tab) : silu_f(a);
+    if constexpr (OP == OP_SWIGLU) return (kExact ? silu_ref_order(a, exp_tab) : silu_f(a)) * b;
     if constexpr (OP == OP_GELU) return gelu_tanh_ref_order(a);
     if constexpr (OP == OP_GELU_ERF) return gelu_erf_ref_order(a, exp_tab);
     return 0.0f;
 }
 
-template <int OP> constexpr bool needs_exp_table() { return OP == OP_GELU_ERF; }
+template <int OP, typename T> constexpr bool needs_exp_table() {
+    return OP == OP_GELU_ERF || (sizeof(T) == 4 && (OP == OP_SILU || OP == OP_SWIGLU));
+}
 
 // Copy the 2^(i/32) table into LDS (block-wide; call before any use).
 __device__ __forceinline__ void stage_exp_table(uint64_t* tab) {
@@ -100,8 +106,8 @@ template <int OP> constexpr bool binary_op() { return OP == OP_ADD || OP == OP_M
 template <typename T, int OP, int BC>
 __global__ __launch_bounds__(kThreads) void ew_vec(const T* a, const T* b, T* out, int64_t nvec) {
     constexpr int E = vec16<T>::n;
-    __shared__ uint64_t exp_tab[needs_exp_table<OP>() ? 32 : 1];
-    if constexpr (needs_exp_table<OP>()) stage_exp_table(exp_tab);
+    __shared__ uint64_t exp_tab[needs_exp_table<OP, T>() ? 32 : 1];
+    if constexpr (needs_exp_table<OP, T>()) stage_exp_table(exp_tab);
     float sa = 0.0f, sb = 0.0f;
     if constexpr (BC == B_SCALAR_A) sa = widen(a[0]);
     if constexpr (BC == B_SCALAR_B) sb = widen(b[0]);
@@ -125,7 +131,7 @@ __global__ __launch_bounds__(kThreads) void ew_vec(const T* a, const T* b, T* ou
                 for (int e = 0; e < E; ++e) {
                     const float x = BC == B_SCALAR_A ? sa : va[u][e];
                     const float y = BC == B_SCALAR_B ? sb : vb[u][e];
-                    o[e] = apply_op<OP>(x, y, exp_tab);
+                    o[e] = apply_op<OP, T>(x, y, exp_tab);
                 }
                 store_f32<T, E, true>(out + i * E, o);
             }
@@ -137,13 +143,13 @@ __global__ __launch_bounds__(kThreads) void ew_vec(const T* a, const T* b, T* ou
 template <typename T, int OP, int BC>
 __global__ __launch_bounds__(kThreads) void ew_scalar(const T* a, const T* b, T* out, int64_t begin,
                                                       int64_t end) {
-    __shared__ uint64_t exp_tab[needs_exp_table<OP>() ? 32 : 1];
-    if constexpr (needs_exp_table<OP>()) stage_exp_table(exp_tab);
+    __shared__ uint64_t exp_tab[needs_exp_table<OP, T>() ? 32 : 1];
+    if constexpr (needs_exp_table<OP, T>()) stage_exp_table(exp_tab);
     const int64_t stride = (int64_t)gridDim.x * kThreads;
     for (int64_t i = begin + (int64_t)blockIdx.x * kThreads + threadIdx.x; i < end; i += stride) {
         const float x = widen(a[BC == B_SCALAR_A ? 0 : i]);
         const float y = binary_op<OP>() ? widen(b[BC == B_SCALAR_B ? 0 : i]) : 0.0f;
-        out[i] = narrow<T>(apply_op<OP>(x, y, exp_tab));
+        out[i] = narrow<T>(apply_op<OP, T>(x, y, exp_tab));
     }
 }
 

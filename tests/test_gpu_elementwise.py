@@ -8,7 +8,7 @@ crates/sapient-models/src/forward/common.rs:556-569.
 
 Tolerances:
   add / mul          bit-exact (one IEEE operation, same rounding)
-  SiLU / SwiGLU f32  ≤ 1e-5 relative (hardware exp2 / reciprocal vs glibc expf)
+  SiLU / SwiGLU f32  bit-exact: the kernel evaluates glibc's own expf algorithm
   SiLU / SwiGLU half ≤ 1 ulp of the output format vs the f32 oracle rounded
   GELU (every dtype) bit-exact: the kernel evaluates glibc's own tanhf algorithm
   erf-GELU (every dtype) bit-exact: glibc's own expf algorithm
@@ -96,16 +96,37 @@ def test_silu_swiglu(dev, orc, dtype, n):
     print(f"case silu/swiglu {dtype} n={n}", flush=True)
     g, u = _gen((n,), 6, dev, 2.0, dtype), _gen((n,), 7, dev, 2.0, dtype)
     g32, u32 = widen(g, orc), widen(u, orc)
-    _check(ops.silu(g), orc.silu(g32), orc, 1e-5, f"silu {dtype}")
-    _check(ops.swiglu(g, u), orc.swiglu(g32, u32), orc, 1e-5, f"swiglu {dtype}")
+    if dtype == torch.float32:
+        assert_bits_equal(to_np(ops.silu(g)), orc.silu(g32), "silu f32")
+        assert_bits_equal(to_np(ops.swiglu(g, u)), orc.swiglu(g32, u32), "swiglu f32")
+    else:
+        _check(ops.silu(g), orc.silu(g32), orc, 1e-5, f"silu {dtype}")
+        _check(ops.swiglu(g, u), orc.swiglu(g32, u32), orc, 1e-5, f"swiglu {dtype}")
 
 
 def test_silu_special_values(dev, orc):
     x = torch.from_numpy(SPECIALS).to(dev)
-    got = to_np(ops.silu(x))
-    want = orc.silu(SPECIALS)
-    assert max_rel(got, want, floor=1e-37) <= 1e-5, list(zip(SPECIALS, got, want))
-    assert np.array_equal(np.signbit(got[want == 0]), np.signbit(want[want == 0]))
+    assert_bits_equal(to_np(ops.silu(x)), orc.silu(SPECIALS), "silu specials")
+
+
+def test_silu_f32_bit_exact_wide_range(dev, orc):
+    """f32 SiLU over ~N(0, 30) and a log-uniform magnitude sweep (−104 .. 104, subnormal results
+    included): the reference's bits."""
+    g = torch.Generator(device=dev).manual_seed(17)
+    mags = torch.exp(torch.rand(1 << 20, generator=g, device=dev) * 9.3 - 4.6)
+    signs = torch.where(torch.rand(1 << 20, generator=g, device=dev) < 0.5, -1.0, 1.0)
+    x = torch.cat([_gen((1 << 20,), 18, dev, 30.0), mags * signs])
+    assert_bits_equal(to_np(ops.silu(x)), orc.silu(to_np(x)), "silu f32 wide")
+
+
+def test_swiglu_f32_full(dev, orc):
+    """SwiGLU on [8192, 14336] f32, inputs ~N(0, 2): bit-exact."""
+    shape = (8192, 14336)
+    print("case swiglu full f32", flush=True)
+    g, u = _gen(shape, 53, dev, 2.0), _gen(shape, 54, dev, 2.0)
+    out = ops.swiglu(g, u)
+    torch.cuda.synchronize()
+    assert_bits_equal(to_np(out), orc.swiglu(to_np(g), to_np(u)), "swiglu full f32")
 
 
 def test_swiglu_llama3_8b_full(dev, orc):
