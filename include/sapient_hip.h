@@ -100,12 +100,15 @@ int sph_add(const void* a, int64_t na, const void* b, int64_t nb, void* out, int
 int sph_mul(const void* a, int64_t na, const void* b, int64_t nb, void* out, int dtype, void* stream);
 
 /* SiLU: x / (1 + exp(-x)). Replaces LlmBackend::silu (backend.rs:80)
- * → elementwise::silu (crates/sapient-backends/cpu/src/kernels/elementwise.rs:141-143). */
+ * → elementwise::silu (crates/sapient-backends/cpu/src/kernels/elementwise.rs:141-143).
+ * Bit-exact with the reference on glibc in every dtype (half outputs: the
+ * reference's f32 result rounded once): exp is evaluated by glibc's own expf
+ * algorithm wherever it can change the result. */
 int sph_silu(const void* x, void* out, int dtype, int64_t n, void* stream);
 
 /* SwiGLU: silu(gate) * up, fused. Replaces LlmBackend::silu then ::mul
  * (llama.rs:531-532) and the wgpu analog WgpuContext::swiglu (resident.rs:409).
- * `out` may alias `gate` or `up`. */
+ * Bit-exact like sph_silu. `out` may alias `gate` or `up`. */
 int sph_swiglu(const void* gate, const void* up, void* out, int dtype, int64_t n, void* stream);
 
 /* GELU, tanh approximation: 0.5 x (1 + tanh(0.79788456 (x + 0.044715 x^3))).

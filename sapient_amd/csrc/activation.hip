@@ -15,12 +15,14 @@
 // is sized so each thread makes about one trip (up to 64K blocks) — measured
 // on MI355X, a near-flat grid streams faster than a grid-stride loop over few
 // blocks (SwiGLU f16: 125 → 114 µs).
-//  - SiLU evaluates exp(-v) with the hardware exp2 on a split-precision
-//    argument and 1/(1+e) with the hardware reciprocal: ≤ ~4 f32 ulp from the
-//    reference, no cancellation anywhere, ~12 VALU ops per element. Inputs
-//    below -80 (where 1/(1+e) would be subnormal) take the IEEE expf / divide
-//    path, which also reproduces the reference's -0 once expf(-v) overflows;
-//    inputs above 64 return v, exactly as the reference does.
+//  - SiLU / SwiGLU return the reference's bits. f32 evaluates the reference's
+//    expression (glibc's expf restated, see glibc_expf.h, then the IEEE
+//    division) on every element: ~45 VALU ops, within the budget of 8-12
+//    bytes per element. Half types (4-6 bytes per element) would be
+//    VALU-bound that way, so they evaluate a fast SiLU (hardware exp2 /
+//    reciprocal, ≤ 5 ulp — measured over every f32 input it serves) and run
+//    the exact expression only where that error could change the rounding to
+//    the half type (silu_certified).
 //  - GELU: the reference's 1 + tanh(z) cancels for z < -3, so its result there
 //    is glibc's rounding of tanh; only glibc's own algorithm reproduces it (see
 //    glibc_tanhf.h). For f16 / bf16 inputs the op is a function of 16 bits, so
@@ -38,6 +40,7 @@
 //  - Bias add: a block owns a tile of up to 256 16-byte column vectors over
 //    two rows; each thread loads its bias vector once and adds it to both.
 #include <mutex>
+#include <type_traits>
 
 #include "glibc_expf.h"
 #include "glibc_tanhf.h"
@@ -56,10 +59,10 @@ enum Op { OP_ADD = 0, OP_MUL = 1, OP_SILU = 2, OP_SWIGLU = 3, OP_GELU = 4, OP_GE
 __constant__ Exp2fTable kExp2f = exp2f_table();
 enum Bcast { B_NONE = 0, B_SCALAR_B = 1, B_SCALAR_A = 2 };
 
+// Fast SiLU for g >= -80: exp(-g) from the hardware exp2 on a split-precision
+// argument, 1 / (1 + e) from the hardware reciprocal, ~12 VALU ops. Above 64,
+// exp(-g) < 2^-92, so 1 + e rounds to 1 and the reference returns g itself.
 __device__ __forceinline__ float silu_f(float g) {
-    // Below -80 (and NaN): IEEE path. Above 64: exp(-g) < 2^-92, so 1 + e
-    // rounds to 1 and the reference returns g itself (also for +inf).
-    if (!(g >= -80.0f)) return g / (1.0f + expf(-g));
     if (g > 64.0f) return g;
     const float kL2eHi = 1.44269502162933349609375f;  // f32(log2 e)
     const float kL2eLo = 1.925963033500011e-08f;      // log2 e - kL2eHi
@@ -72,23 +75,75 @@ __device__ __forceinline__ float silu_f(float g) {
     return g * __builtin_amdgcn_rcpf(1.0f + e);
 }
 
-// T: the storage type. f32 SiLU / SwiGLU evaluate the reference's expression
-// exactly (glibc's expf restated, IEEE division): bit-exact, and within the
-// bandwidth budget of 8-12 bytes per element.
+// True when every f32 within 16 ulp of p rounds to the same T: p is far enough
+// from the midpoint between two T values (a window around a midpoint never
+// reaches a binade edge, so bit units are ulps). f16: the 13 bits below its
+// mantissa, for |p| in [2^-14, 2^16) (normal f16 results and their overflow to
+// inf); bf16: the 16 bits below its mantissa, anywhere in the finite range.
+template <typename T>
+__device__ __forceinline__ bool rounding_is_clear(float p) {
+    const uint32_t b = __builtin_bit_cast(uint32_t, p);
+    const uint32_t e = (b >> 23) & 0xFFu;
+    if constexpr (std::is_same<T, f16>::value) {
+        if (e < 113u || e > 142u) return false;
+        const int low = (int)(b & 0x1FFFu) - 0x1000;
+        return low > 16 || low < -16;
+    } else {
+        if (e == 0xFFu || e < 2u) return false;
+        const int low = (int)(b & 0xFFFFu) - 0x8000;
+        return low > 16 || low < -16;
+    }
+}
+
+// SiLU (times u for SwiGLU) whose rounding to the half type T equals the
+// reference's: the fast silu_f is certified where it decides the result. Over
+// every f32 g in [-80, 64] silu_f lies within 5 ulp of the exact
+// silu_ref_order (measured on MI355X over all 2^31 such inputs). In ulps of
+// the product that is < 10 ulp (ulp(s)·|u| < 2 ulp(s·u)), and the roundings
+// RN(s·u), RN(s'·u) add one more, so the exact result lies within 11 ulp of the
+// fast p. When every f32 within 16 ulp of p rounds to the same T value,
+// rounding being monotonic, so does the exact result. Otherwise (about 0.4 %
+// of elements), outside the measured domain, for non-finite values and for
+// results outside the ranges rounding_is_clear covers, the exact expression
+// runs inline: it touches only registers and the LDS copy of the 2^(i/32)
+// table, so its rare divergent executions cost ~1 % (measured: fast-only
+// 112 µs, certified 113 µs on f16 SwiGLU [8192, 14336]; a table load from
+// global memory in the same branch stalls the wave on its stream traffic,
+// 136 µs).
+template <typename T, bool MUL>
+__device__ __forceinline__ float silu_certified(float g, float u, const uint64_t* exp_tab) {
+    const float s = silu_f(g);
+    const float p = MUL ? s * u : s;
+    if (g >= -80.0f && rounding_is_clear<T>(p)) return p;
+    const float x = silu_ref_order(g, exp_tab);
+    return MUL ? x * u : x;
+}
+
+// T: the storage type. SiLU / SwiGLU give the reference's bits: f32 evaluates
+// the reference's expression exactly (glibc's expf restated, IEEE division —
+// within the bandwidth budget of 8-12 bytes per element); half types take the
+// certified fast path (4-6 bytes per element leave no room for the exact
+// expression on every element: f16 SwiGLU 149 µs instead of 113).
 template <int OP, typename T>
 __device__ __forceinline__ float apply_op(float a, float b, const uint64_t* exp_tab) {
     constexpr bool kExact = sizeof(T) == 4;
     if constexpr (OP == OP_ADD) return a + b;
     if constexpr (OP == OP_MUL) return a * b;
-    if constexpr (OP == OP_SILU) return kExact ? silu_ref_order(a, exp_tab) : silu_f(a);
-    if constexpr (OP == OP_SWIGLU) return (kExact ? silu_ref_order(a, exp_tab) : silu_f(a)) * b;
+    if constexpr (OP == OP_SILU) {
+        if constexpr (kExact) return silu_ref_order(a, exp_tab);
+        else return silu_certified<T, false>(a, 0.0f, exp_tab);
+    }
+    if constexpr (OP == OP_SWIGLU) {
+        if constexpr (kExact) return silu_ref_order(a, exp_tab) * b;
+        else return silu_certified<T, true>(a, b, exp_tab);
+    }
     if constexpr (OP == OP_GELU) return gelu_tanh_ref_order(a);
     if constexpr (OP == OP_GELU_ERF) return gelu_erf_ref_order(a, exp_tab);
     return 0.0f;
 }
 
 template <int OP, typename T> constexpr bool needs_exp_table() {
-    return OP == OP_GELU_ERF || (sizeof(T) == 4 && (OP == OP_SILU || OP == OP_SWIGLU));
+    return OP == OP_GELU_ERF || OP == OP_SILU || OP == OP_SWIGLU;
 }
 
 // Copy the 2^(i/32) table into LDS (block-wide; call before any use).

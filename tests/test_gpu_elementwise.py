@@ -8,8 +8,10 @@ crates/sapient-models/src/forward/common.rs:556-569.
 
 Tolerances:
   add / mul          bit-exact (one IEEE operation, same rounding)
-  SiLU / SwiGLU f32  bit-exact: the kernel evaluates glibc's own expf algorithm
-  SiLU / SwiGLU half ≤ 1 ulp of the output format vs the f32 oracle rounded
+  SiLU / SwiGLU      bit-exact in every dtype: f32 evaluates glibc's own expf
+                     algorithm; half types a certified fast path with that
+                     expression as the fallback (exhaustive over the gate's
+                     16-bit patterns)
   GELU (every dtype) bit-exact: the kernel evaluates glibc's own tanhf algorithm
   erf-GELU (every dtype) bit-exact: glibc's own expf algorithm
   bias add           bit-exact (one IEEE add)
@@ -96,12 +98,35 @@ def test_silu_swiglu(dev, orc, dtype, n):
     print(f"case silu/swiglu {dtype} n={n}", flush=True)
     g, u = _gen((n,), 6, dev, 2.0, dtype), _gen((n,), 7, dev, 2.0, dtype)
     g32, u32 = widen(g, orc), widen(u, orc)
-    if dtype == torch.float32:
-        assert_bits_equal(to_np(ops.silu(g)), orc.silu(g32), "silu f32")
-        assert_bits_equal(to_np(ops.swiglu(g, u)), orc.swiglu(g32, u32), "swiglu f32")
+    _exact(ops.silu(g), orc.silu(g32), orc, f"silu {dtype}")
+    _exact(ops.swiglu(g, u), orc.swiglu(g32, u32), orc, f"swiglu {dtype}")
+
+
+def _exact(out: torch.Tensor, ref32: np.ndarray, orc, what: str):
+    """Bit-exact against the oracle (half types: its f32 result rounded to nearest-even); NaN
+    matches NaN."""
+    if out.dtype == torch.float32:
+        assert_bits_equal(to_np(out), ref32, what)
     else:
-        _check(ops.silu(g), orc.silu(g32), orc, 1e-5, f"silu {dtype}")
-        _check(ops.swiglu(g, u), orc.swiglu(g32, u32), orc, 1e-5, f"swiglu {dtype}")
+        got, want = to_np(out).reshape(-1), narrow_bits(ref32, out.dtype, orc).reshape(-1)
+        nan = np.isnan(ref32.reshape(-1))
+        assert_bits16_equal(got[~nan], want[~nan], what)
+        assert (ulp_diff16(got[nan], want[nan], out.dtype) == 0).all(), what + " NaN"
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=IDS)
+def test_silu_swiglu_half_exhaustive_bit_exact(dev, orc, dtype):
+    """Every 16-bit gate pattern: SiLU, and SwiGLU with up = 1, −3.7, ~N(0, 2), ~N(0, 300) and
+    ±tiny — the reference's f32 result rounded once to the half type, bit for bit."""
+    g = torch.arange(0, 65536, dtype=torch.int32).to(torch.int16).view(dtype).to(dev)
+    g32 = widen(g, orc)
+    print(f"case silu/swiglu exhaustive {dtype}", flush=True)
+    _exact(ops.silu(g), orc.silu(g32), orc, f"silu {dtype}")
+    ups = [torch.ones(65536, device=dev), torch.full((65536,), -3.7, device=dev),
+           _gen((65536,), 31, dev, 2.0), _gen((65536,), 32, dev, 300.0), _gen((65536,), 33, dev, 1e-30)]
+    for i, u in enumerate(ups):
+        u = u.to(dtype)
+        _exact(ops.swiglu(g, u), orc.swiglu(g32, widen(u, orc)), orc, f"swiglu {dtype} up #{i}")
 
 
 def test_silu_special_values(dev, orc):
@@ -129,15 +154,15 @@ def test_swiglu_f32_full(dev, orc):
     assert_bits_equal(to_np(out), orc.swiglu(to_np(g), to_np(u)), "swiglu full f32")
 
 
-def test_swiglu_llama3_8b_full(dev, orc):
-    """SwiGLU on [8192, 14336] f16, inputs ~N(0, 2): ≤ 1 f16 ulp everywhere."""
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=IDS)
+def test_swiglu_llama3_8b_full(dev, orc, dtype):
+    """SwiGLU on [8192, 14336] in half types, inputs ~N(0, 2): bit-exact everywhere."""
     shape = (8192, 14336)
-    print("case swiglu full f16", flush=True)
-    g, u = _gen(shape, 51, dev, 2.0, torch.float16), _gen(shape, 52, dev, 2.0, torch.float16)
+    print(f"case swiglu full {dtype}", flush=True)
+    g, u = _gen(shape, 51, dev, 2.0, dtype), _gen(shape, 52, dev, 2.0, dtype)
     out = ops.swiglu(g, u)
     torch.cuda.synchronize()
-    want = orc.swiglu(widen(g, orc), widen(u, orc))
-    assert_ulp16(to_np(out), narrow_bits(want, torch.float16, orc), torch.float16, 1, "swiglu full f16")
+    _exact(out, orc.swiglu(widen(g, orc), widen(u, orc)), orc, f"swiglu full {dtype}")
 
 
 def test_swiglu_in_place(dev, orc):
