@@ -7,7 +7,8 @@
 // with the reference's argument meaning, validation and error messages. It is
 // what a Rust `HipLlmBackend` wrapper does over FFI, written in C++ because the
 // reference is compiled code. There is no CPU fallback: a failed HIP call
-// raises sapient_hip::Error.
+// raises sapient_hip::Error (the debug switches below route an op elsewhere
+// only when the caller asks for it).
 #pragma once
 
 #include <cstddef>
@@ -64,51 +65,106 @@ class Tensor {
     std::vector<uint8_t> bytes_;
 };
 
-class HipLlmBackend {
+// The op surface of the LlmBackend trait on this path
+// (crates/sapient-models/src/forward/backend.rs:57-115) plus the fused
+// extensions, which default to compositions of the trait's own ops as the
+// Rust default methods do. HipLlmBackend implements it; a caller may hand
+// HipLlmBackend another implementation (its CPU backend) for the debug
+// switches below.
+class LlmBackend {
+ public:
+    virtual ~LlmBackend() = default;
+    virtual const char* name() const = 0;
+
+    // LlmBackend::rms_norm (backend.rs:72 → layernorm.rs:75-106): f32 output.
+    virtual Tensor rms_norm(const Tensor& x, const Tensor& weight, float eps) = 0;
+    // LlmBackend::layer_norm (backend.rs:73-79 → layernorm.rs:17-69, last axis):
+    // `bias` may be null; f32 output.
+    virtual Tensor layer_norm(const Tensor& x, const Tensor& weight, const Tensor* bias, float eps) = 0;
+    // common::add_bias_last_dim (common.rs:556-569), the bias step of
+    // LlmBackend::linear_3d_bias (backend.rs:64-70): y F32, bias [y.last_dim].
+    virtual Tensor add_bias_last_dim(const Tensor& y, const Tensor& bias) = 0;
+    // LlmBackend::silu / gelu (elementwise.rs:141-143, :120-127): F32 input only.
+    virtual Tensor silu(const Tensor& x) = 0;
+    virtual Tensor gelu(const Tensor& x) = 0;
+    // elementwise::gelu_erf (elementwise.rs:135-138): F32 input only.
+    virtual Tensor gelu_erf(const Tensor& x) = 0;
+    // LlmBackend::add / mul (elementwise.rs:27-69): same length or a length-1 side.
+    virtual Tensor add(const Tensor& a, const Tensor& b) = 0;
+    virtual Tensor mul(const Tensor& a, const Tensor& b) = 0;
+    // LlmBackend::apply_rope_positions (rope.rs:18-62): x [B, H, S, D].
+    virtual Tensor apply_rope_positions(const Tensor& x, const std::vector<size_t>& positions, float base) = 0;
+    // LlmBackend::apply_rope_partial (rope.rs:71-78, :83-136).
+    virtual Tensor apply_rope_partial(const Tensor& x, const std::vector<size_t>& positions, float base,
+                                      size_t rotary_dim) = 0;
+    // RoPE on adjacent pairs (x[2i], x[2i+1]) — the layout of GGUF's unpermuted
+    // q/k rows (gguf_weights.rs:113-115).
+    virtual Tensor apply_rope_interleaved(const Tensor& x, const std::vector<size_t>& positions, float base) = 0;
+    // common::embed_tokens (common.rs:164-179): weight [vocab, hidden] →
+    // [1, ids.size(), hidden] f32; an id >= vocab is an error.
+    virtual Tensor embed_tokens(const Tensor& weight, const std::vector<uint32_t>& ids) = 0;
+
+    // Fused extensions: (rms_norm(residual + x), residual + x) and silu(gate) · up.
+    virtual std::pair<Tensor, Tensor> add_rms_norm(const Tensor& x, const Tensor& residual, const Tensor& weight,
+                                                   float eps) {
+        Tensor r = add(residual, x);
+        Tensor y = rms_norm(r, weight, eps);
+        return {std::move(y), std::move(r)};
+    }
+    virtual Tensor swiglu(const Tensor& gate, const Tensor& up) { return mul(silu(gate), up); }
+};
+
+// Debug switches, read from the environment when a HipLlmBackend is built —
+// the HIP counterparts of SAPIENT_MLX_DISABLE / SAPIENT_MLX_VERIFY
+// (backend.rs:191-216):
+//   SAPIENT_HIP_DISABLE=rms_norm,rope,…  routes the listed ops ("all": every op)
+//     to the backend given to the constructor, so a wrong-numbers kernel can be
+//     found per op without rebuilding. Op names: rms_norm, layer_norm, add_bias,
+//     silu, gelu, gelu_erf, add, mul, rope (all three RoPE methods),
+//     add_rms_norm, swiglu, embed. With no backend given, a disabled op raises
+//     Error; nothing falls back silently.
+//   SAPIENT_HIP_VERIFY=1  runs the given backend beside the first 64 HIP calls
+//     and prints "[hip-verify] <op> #<n> max_abs_diff=… cpu_rms=…" to stderr;
+//     the HIP result is returned.
+// Unlike the Metal backend, a failed HIP call is never retried on the CPU.
+class HipLlmBackend final : public LlmBackend {
  public:
     // Binds the current HIP device and creates one stream (default priority).
-    HipLlmBackend();
-    ~HipLlmBackend();
+    // `cpu`, if given, must outlive this backend; only the debug switches use it.
+    explicit HipLlmBackend(LlmBackend* cpu = nullptr);
+    ~HipLlmBackend() override;
     HipLlmBackend(const HipLlmBackend&) = delete;
     HipLlmBackend& operator=(const HipLlmBackend&) = delete;
 
     // A gfx950 device is present and the library answers.
     static bool is_available();
-    const char* name() const { return "hip"; }
+    const char* name() const override { return "hip"; }
 
-    // LlmBackend::rms_norm (backend.rs:72 → layernorm.rs:75-106): f32 output.
-    Tensor rms_norm(const Tensor& x, const Tensor& weight, float eps);
+    Tensor rms_norm(const Tensor& x, const Tensor& weight, float eps) override;
     // kernels::layernorm::rms_norm with the kernel's optional weight (graph path).
     Tensor rms_norm(const Tensor& x, const Tensor* weight, float eps);
-    // LlmBackend::layer_norm (backend.rs:73-79 → layernorm.rs:17-69, last axis):
-    // `bias` may be null; f32 output.
-    Tensor layer_norm(const Tensor& x, const Tensor& weight, const Tensor* bias, float eps);
+    Tensor layer_norm(const Tensor& x, const Tensor& weight, const Tensor* bias, float eps) override;
     // kernels::layernorm::layer_norm over the axes from `axis` on; weight and bias optional.
     Tensor layer_norm(const Tensor& x, const Tensor* weight, const Tensor* bias, int64_t axis, float eps);
-    // common::add_bias_last_dim (common.rs:556-569), the bias step of
-    // LlmBackend::linear_3d_bias (backend.rs:64-70): y F32, bias [y.last_dim].
-    Tensor add_bias_last_dim(const Tensor& y, const Tensor& bias);
-    // LlmBackend::silu / gelu (elementwise.rs:141-143, :120-127): F32 input only.
-    Tensor silu(const Tensor& x);
-    Tensor gelu(const Tensor& x);
-    // elementwise::gelu_erf (elementwise.rs:135-138): F32 input only.
-    Tensor gelu_erf(const Tensor& x);
-    // LlmBackend::add / mul (elementwise.rs:27-69): same length or a length-1 side.
-    Tensor add(const Tensor& a, const Tensor& b);
-    Tensor mul(const Tensor& a, const Tensor& b);
-    // LlmBackend::apply_rope_positions (rope.rs:18-62): x [B, H, S, D].
-    Tensor apply_rope_positions(const Tensor& x, const std::vector<size_t>& positions, float base);
-    // LlmBackend::apply_rope_partial (rope.rs:71-78, :83-136).
-    Tensor apply_rope_partial(const Tensor& x, const std::vector<size_t>& positions, float base, size_t rotary_dim);
+    Tensor add_bias_last_dim(const Tensor& y, const Tensor& bias) override;
+    Tensor silu(const Tensor& x) override;
+    Tensor gelu(const Tensor& x) override;
+    Tensor gelu_erf(const Tensor& x) override;
+    Tensor add(const Tensor& a, const Tensor& b) override;
+    Tensor mul(const Tensor& a, const Tensor& b) override;
+    Tensor apply_rope_positions(const Tensor& x, const std::vector<size_t>& positions, float base) override;
+    Tensor apply_rope_partial(const Tensor& x, const std::vector<size_t>& positions, float base,
+                              size_t rotary_dim) override;
+    Tensor apply_rope_interleaved(const Tensor& x, const std::vector<size_t>& positions, float base) override;
+    Tensor embed_tokens(const Tensor& weight, const std::vector<uint32_t>& ids) override;
+    // One fused kernel each (sph_add_rms_norm, sph_swiglu).
+    std::pair<Tensor, Tensor> add_rms_norm(const Tensor& x, const Tensor& residual, const Tensor& weight,
+                                           float eps) override;
+    Tensor swiglu(const Tensor& gate, const Tensor& up) override;
 
-    // Fused / layout extensions (default trait methods composing the above).
-    std::pair<Tensor, Tensor> add_rms_norm(const Tensor& x, const Tensor& residual, const Tensor& weight, float eps);
-    Tensor swiglu(const Tensor& gate, const Tensor& up);
-    Tensor apply_rope_interleaved(const Tensor& x, const std::vector<size_t>& positions, float base);
-
-    // common::embed_tokens (common.rs:164-179): weight [vocab, hidden] →
-    // [1, ids.size(), hidden] f32; an id >= vocab is an error.
-    Tensor embed_tokens(const Tensor& weight, const std::vector<uint32_t>& ids);
+    // The switches as read at construction.
+    bool disabled(const char* op) const;
+    bool verifying() const { return verify_; }
 
  private:
     // A device allocation owned by one call; freed on scope exit (also when a
@@ -133,9 +189,26 @@ class HipLlmBackend {
     Tensor rope(const Tensor& x, const std::vector<size_t>& positions, float base, size_t rotary_dim, int layout,
                 bool partial);
     void check(int status, const char* op) const;
+    // The debug switches around one trait op: `hip` computes on the device,
+    // `ref` on the given backend.
+    template <typename R, typename Hip, typename Ref>
+    R routed(const char* op, Hip&& hip, Ref&& ref);
+    void report(const char* op, int n, const Tensor& hip, const Tensor& ref);
+    void report(const char* op, int n, const std::pair<Tensor, Tensor>& hip, const std::pair<Tensor, Tensor>& ref);
+    // The device paths of the fused, bias and embedding ops.
+    std::pair<Tensor, Tensor> fused_add_rms_norm(const Tensor& x, const Tensor& residual, const Tensor& weight,
+                                                 float eps);
+    Tensor fused_swiglu(const Tensor& gate, const Tensor& up);
+    Tensor bias_last_dim(const Tensor& y, const Tensor& bias);
+    Tensor gather_rows(const Tensor& weight, const std::vector<uint32_t>& ids);
 
     void* stream_ = nullptr;
     std::mutex mu_;
+    LlmBackend* cpu_ = nullptr;
+    std::vector<std::string> disabled_;
+    bool verify_ = false;
+    int verified_ = 0;  // calls cross-checked so far (under verify_mu_)
+    std::mutex verify_mu_;
 };
 
 // Graph-side ops the HIP backend executes: the ExecutionBackend's supports_op

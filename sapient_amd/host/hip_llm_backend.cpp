@@ -13,6 +13,10 @@
 
 #include <hip/hip_runtime.h>
 
+#include <cctype>
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <string>
 
@@ -120,11 +124,90 @@ bool HipLlmBackend::is_available() {
     return std::strncmp(prop.gcnArchName, "gfx950", 6) == 0 && sph_abi_version() == SPH_ABI_VERSION;
 }
 
-HipLlmBackend::HipLlmBackend() {
+// SAPIENT_HIP_DISABLE: comma-separated, trimmed, lower-cased, empties dropped
+// (the parsing of mlx_disabled, backend.rs:194-207).
+static std::vector<std::string> disable_list() {
+    std::vector<std::string> out;
+    const char* v = std::getenv("SAPIENT_HIP_DISABLE");
+    if (!v) return out;
+    std::string item;
+    auto flush = [&] {
+        size_t b = 0, e = item.size();
+        while (b < e && std::isspace((unsigned char)item[b])) ++b;
+        while (e > b && std::isspace((unsigned char)item[e - 1])) --e;
+        std::string t = item.substr(b, e - b);
+        for (char& c : t) c = (char)std::tolower((unsigned char)c);
+        if (!t.empty()) out.push_back(t);
+        item.clear();
+    };
+    for (const char* p = v; *p; ++p) {
+        if (*p == ',') flush();
+        else item += *p;
+    }
+    flush();
+    return out;
+}
+
+HipLlmBackend::HipLlmBackend(LlmBackend* cpu) : cpu_(cpu) {
     if (!is_available()) throw Error("hip: no gfx950 device available");
     hipStream_t s = nullptr;
     hip_ok(hipStreamCreate(&s), "stream create");  // default priority
     stream_ = s;
+    disabled_ = disable_list();
+    const char* v = std::getenv("SAPIENT_HIP_VERIFY");
+    verify_ = v != nullptr && std::strcmp(v, "1") == 0;
+    if (verify_ && cpu_ == nullptr) std::fprintf(stderr, "[hip-verify] no CPU backend given; nothing is cross-checked\n");
+}
+
+bool HipLlmBackend::disabled(const char* op) const {
+    for (const std::string& s : disabled_)
+        if (s == op || s == "all") return true;
+    return false;
+}
+
+template <typename R, typename Hip, typename Ref>
+R HipLlmBackend::routed(const char* op, Hip&& hip, Ref&& ref) {
+    if (disabled(op)) {
+        if (cpu_ == nullptr)
+            throw Error(std::string("hip backend: ") + op + ": disabled by SAPIENT_HIP_DISABLE and no CPU backend was given");
+        return ref(*cpu_);
+    }
+    R out = hip();
+    if (verify_ && cpu_ != nullptr) {
+        int n;
+        {
+            std::lock_guard<std::mutex> lock(verify_mu_);
+            n = verified_ < 64 ? verified_++ : -1;
+        }
+        if (n >= 0) report(op, n, out, ref(*cpu_));
+    }
+    return out;
+}
+
+// Largest |hip - ref| (NaN against a number counts as infinite) and ref's RMS.
+void HipLlmBackend::report(const char* op, int n, const Tensor& hip, const Tensor& ref) {
+    if (hip.shape() != ref.shape()) {
+        std::fprintf(stderr, "[hip-verify] %s #%d shape %s vs cpu %s\n", op, n, shape_str(hip.shape()).c_str(),
+                     shape_str(ref.shape()).c_str());
+        return;
+    }
+    const std::vector<float> a = f32_input(hip).as_f32(), b = f32_input(ref).as_f32();
+    double max_abs = 0.0, norm = 0.0;
+    for (size_t i = 0; i < a.size(); ++i) {
+        const bool na = std::isnan(a[i]), nb = std::isnan(b[i]);
+        const double d = (na || nb) ? (na && nb ? 0.0 : INFINITY) : std::fabs((double)a[i] - (double)b[i]);
+        if (d > max_abs) max_abs = d;
+        norm += (double)b[i] * (double)b[i];
+    }
+    const double rms = b.empty() ? 0.0 : std::sqrt(norm / (double)b.size());
+    std::fprintf(stderr, "[hip-verify] %s #%d shape=%s max_abs_diff=%.6g cpu_rms=%.6g\n", op, n,
+                 shape_str(hip.shape()).c_str(), max_abs, rms);
+}
+
+void HipLlmBackend::report(const char* op, int n, const std::pair<Tensor, Tensor>& hip,
+                           const std::pair<Tensor, Tensor>& ref) {
+    report(op, n, hip.first, ref.first);
+    report(op, n, hip.second, ref.second);
 }
 
 HipLlmBackend::~HipLlmBackend() {
@@ -193,7 +276,10 @@ Tensor HipLlmBackend::f32_input(const Tensor& t) const {
     return Tensor::from_f32(v, t.shape());
 }
 
-Tensor HipLlmBackend::rms_norm(const Tensor& x, const Tensor& weight_t, float eps) { return rms_norm(x, &weight_t, eps); }
+Tensor HipLlmBackend::rms_norm(const Tensor& x, const Tensor& weight_t, float eps) {
+    return routed<Tensor>("rms_norm", [&] { return rms_norm(x, &weight_t, eps); },
+                          [&](LlmBackend& c) { return c.rms_norm(x, weight_t, eps); });
+}
 
 // layernorm::rms_norm (layernorm.rs:75-106): last axis, weight optional.
 Tensor HipLlmBackend::rms_norm(const Tensor& x, const Tensor* weight_t, float eps) {
@@ -226,6 +312,12 @@ Tensor HipLlmBackend::rms_norm(const Tensor& x, const Tensor* weight_t, float ep
 
 std::pair<Tensor, Tensor> HipLlmBackend::add_rms_norm(const Tensor& x, const Tensor& residual, const Tensor& weight_t,
                                                       float eps) {
+    return routed<std::pair<Tensor, Tensor>>("add_rms_norm", [&] { return fused_add_rms_norm(x, residual, weight_t, eps); },
+                                             [&](LlmBackend& c) { return c.add_rms_norm(x, residual, weight_t, eps); });
+}
+
+std::pair<Tensor, Tensor> HipLlmBackend::fused_add_rms_norm(const Tensor& x, const Tensor& residual,
+                                                            const Tensor& weight_t, float eps) {
     const Tensor xf = f32_input(x), rf = f32_input(residual);
     if (xf.shape() != rf.shape())
         throw Error("shape mismatch: " + shape_str(xf.shape()) + " vs " + shape_str(rf.shape()));
@@ -277,8 +369,12 @@ Tensor HipLlmBackend::binary(const Tensor& a0, const Tensor& b0, bool mul) {
     return Tensor::from_f32(out, shape);
 }
 
-Tensor HipLlmBackend::add(const Tensor& a, const Tensor& b) { return binary(a, b, false); }
-Tensor HipLlmBackend::mul(const Tensor& a, const Tensor& b) { return binary(a, b, true); }
+Tensor HipLlmBackend::add(const Tensor& a, const Tensor& b) {
+    return routed<Tensor>("add", [&] { return binary(a, b, false); }, [&](LlmBackend& c) { return c.add(a, b); });
+}
+Tensor HipLlmBackend::mul(const Tensor& a, const Tensor& b) {
+    return routed<Tensor>("mul", [&] { return binary(a, b, true); }, [&](LlmBackend& c) { return c.mul(a, b); });
+}
 
 // unary_f32 (elementwise.rs:15-24): only F32 input is accepted.
 Tensor HipLlmBackend::unary_f32(const Tensor& x, const char* op) {
@@ -299,12 +395,20 @@ Tensor HipLlmBackend::unary_f32(const Tensor& x, const char* op) {
     return Tensor::from_f32(out, x.shape());
 }
 
-Tensor HipLlmBackend::silu(const Tensor& x) { return unary_f32(x, "silu"); }
-Tensor HipLlmBackend::gelu(const Tensor& x) { return unary_f32(x, "gelu"); }
-Tensor HipLlmBackend::gelu_erf(const Tensor& x) { return unary_f32(x, "gelu_erf"); }
+Tensor HipLlmBackend::silu(const Tensor& x) {
+    return routed<Tensor>("silu", [&] { return unary_f32(x, "silu"); }, [&](LlmBackend& c) { return c.silu(x); });
+}
+Tensor HipLlmBackend::gelu(const Tensor& x) {
+    return routed<Tensor>("gelu", [&] { return unary_f32(x, "gelu"); }, [&](LlmBackend& c) { return c.gelu(x); });
+}
+Tensor HipLlmBackend::gelu_erf(const Tensor& x) {
+    return routed<Tensor>("gelu_erf", [&] { return unary_f32(x, "gelu_erf"); },
+                          [&](LlmBackend& c) { return c.gelu_erf(x); });
+}
 
 Tensor HipLlmBackend::layer_norm(const Tensor& x, const Tensor& weight, const Tensor* bias, float eps) {
-    return layer_norm(x, &weight, bias, -1, eps);
+    return routed<Tensor>("layer_norm", [&] { return layer_norm(x, &weight, bias, -1, eps); },
+                          [&](LlmBackend& c) { return c.layer_norm(x, weight, bias, eps); });
 }
 
 // layernorm::layer_norm (layernorm.rs:17-69): normalises over the axes from
@@ -345,6 +449,11 @@ Tensor HipLlmBackend::layer_norm(const Tensor& x0, const Tensor* weight0, const 
 // common::add_bias_last_dim (common.rs:556-569): y is F32, the bias any float
 // type of length equal to y's last dimension.
 Tensor HipLlmBackend::add_bias_last_dim(const Tensor& y, const Tensor& bias0) {
+    return routed<Tensor>("add_bias", [&] { return bias_last_dim(y, bias0); },
+                          [&](LlmBackend& c) { return c.add_bias_last_dim(y, bias0); });
+}
+
+Tensor HipLlmBackend::bias_last_dim(const Tensor& y, const Tensor& bias0) {
     if (y.shape().empty()) throw Error("empty tensor");
     if (y.dtype() != DType::F32) throw Error(std::string("type mismatch: expected f32, got ") + dtype_name(y.dtype()));
     const size_t n = y.shape().back();
@@ -367,6 +476,11 @@ Tensor HipLlmBackend::add_bias_last_dim(const Tensor& y, const Tensor& bias0) {
 }
 
 Tensor HipLlmBackend::swiglu(const Tensor& gate, const Tensor& up) {
+    return routed<Tensor>("swiglu", [&] { return fused_swiglu(gate, up); },
+                          [&](LlmBackend& c) { return c.swiglu(gate, up); });
+}
+
+Tensor HipLlmBackend::fused_swiglu(const Tensor& gate, const Tensor& up) {
     if (gate.dtype() != DType::F32 || up.dtype() != DType::F32)
         throw Error(std::string("type mismatch: expected f32, got ") + dtype_name(gate.dtype() != DType::F32 ? gate.dtype() : up.dtype()));
     if (gate.numel() != up.numel())
@@ -419,21 +533,29 @@ Tensor HipLlmBackend::rope(const Tensor& x0, const std::vector<size_t>& position
 
 Tensor HipLlmBackend::apply_rope_positions(const Tensor& x, const std::vector<size_t>& positions, float base) {
     const size_t head_dim = x.shape().size() == 4 ? x.shape()[3] : 0;
-    return rope(x, positions, base, head_dim, SPH_ROPE_NEOX, false);
+    return routed<Tensor>("rope", [&] { return rope(x, positions, base, head_dim, SPH_ROPE_NEOX, false); },
+                          [&](LlmBackend& c) { return c.apply_rope_positions(x, positions, base); });
 }
 
 Tensor HipLlmBackend::apply_rope_partial(const Tensor& x, const std::vector<size_t>& positions, float base,
                                          size_t rotary_dim) {
-    return rope(x, positions, base, rotary_dim, SPH_ROPE_NEOX, true);
+    return routed<Tensor>("rope", [&] { return rope(x, positions, base, rotary_dim, SPH_ROPE_NEOX, true); },
+                          [&](LlmBackend& c) { return c.apply_rope_partial(x, positions, base, rotary_dim); });
 }
 
 Tensor HipLlmBackend::apply_rope_interleaved(const Tensor& x, const std::vector<size_t>& positions, float base) {
     const size_t head_dim = x.shape().size() == 4 ? x.shape()[3] : 0;
-    return rope(x, positions, base, head_dim, SPH_ROPE_INTERLEAVED, false);
+    return routed<Tensor>("rope", [&] { return rope(x, positions, base, head_dim, SPH_ROPE_INTERLEAVED, false); },
+                          [&](LlmBackend& c) { return c.apply_rope_interleaved(x, positions, base); });
 }
 
 // common.rs:164-217: every id is checked against vocab before any row is read.
 Tensor HipLlmBackend::embed_tokens(const Tensor& w, const std::vector<uint32_t>& ids) {
+    return routed<Tensor>("embed", [&] { return gather_rows(w, ids); },
+                          [&](LlmBackend& c) { return c.embed_tokens(w, ids); });
+}
+
+Tensor HipLlmBackend::gather_rows(const Tensor& w, const std::vector<uint32_t>& ids) {
     const auto& d = w.shape();
     if (d.size() != 2) throw Error("embedding table must be [vocab, hidden], got " + shape_str(d));
     const size_t vocab = d[0], hidden = d[1];

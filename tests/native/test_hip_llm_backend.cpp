@@ -2,11 +2,12 @@
 // written after the reference's own unit tests so they read the same way:
 //   layernorm.rs:113-149, elementwise.rs:176-232, rope.rs:155-206,
 //   common.rs:556-569 and :669-718, the graph-side dispatch arms of
-//   crates/sapient-backends/cpu/src/backend.rs:239-487, and the trait's validation errors (rope.rs:19-35,
-//   elementwise.rs:15-21, common.rs:171-173).
+//   crates/sapient-backends/cpu/src/backend.rs:239-487, the trait's validation errors (rope.rs:19-35,
+//   elementwise.rs:15-21, common.rs:171-173), and the debug switches of backend.rs:191-216.
 // Prints "test <name> ... ok|FAILED: <why>" per test; exits 1 if any failed.
 #include <cmath>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <functional>
 #include <string>
@@ -348,6 +349,92 @@ static void embed_row_gather_matches_full_dequant(HipLlmBackend& bk) {  // commo
     ASSERT(e.find("token id 17 out of vocab range") != std::string::npos, "OOR error");
 }
 
+// ── debug switches (SAPIENT_HIP_DISABLE / SAPIENT_HIP_VERIFY, after backend.rs:191-216) ──
+// A stand-in for the caller's CPU backend: records each call and answers 7.0.
+struct RecordingBackend : sapient_hip::LlmBackend {
+    std::vector<std::string> calls;
+    Tensor sevens(const Tensor& like) { return Tensor::from_f32(std::vector<float>(like.numel(), 7.0f), like.shape()); }
+    Tensor hit(const char* op, const Tensor& like) {
+        calls.push_back(op);
+        return sevens(like);
+    }
+    const char* name() const override { return "recording"; }
+    Tensor rms_norm(const Tensor& x, const Tensor&, float) override { return hit("rms_norm", x); }
+    Tensor layer_norm(const Tensor& x, const Tensor&, const Tensor*, float) override { return hit("layer_norm", x); }
+    Tensor add_bias_last_dim(const Tensor& y, const Tensor&) override { return hit("add_bias_last_dim", y); }
+    Tensor silu(const Tensor& x) override { return hit("silu", x); }
+    Tensor gelu(const Tensor& x) override { return hit("gelu", x); }
+    Tensor gelu_erf(const Tensor& x) override { return hit("gelu_erf", x); }
+    Tensor add(const Tensor& a, const Tensor&) override { return hit("add", a); }
+    Tensor mul(const Tensor& a, const Tensor&) override { return hit("mul", a); }
+    Tensor apply_rope_positions(const Tensor& x, const std::vector<size_t>&, float) override { return hit("rope", x); }
+    Tensor apply_rope_partial(const Tensor& x, const std::vector<size_t>&, float, size_t) override {
+        return hit("rope_partial", x);
+    }
+    Tensor apply_rope_interleaved(const Tensor& x, const std::vector<size_t>&, float) override {
+        return hit("rope_interleaved", x);
+    }
+    Tensor embed_tokens(const Tensor& w, const std::vector<uint32_t>& ids) override {
+        calls.push_back("embed_tokens");
+        return Tensor::from_f32(std::vector<float>(ids.size() * w.shape()[1], 7.0f), {1, ids.size(), w.shape()[1]});
+    }
+};
+
+// Sets an environment variable for one scope.
+struct EnvVar {
+    const char* name;
+    EnvVar(const char* n, const char* v) : name(n) { setenv(n, v, 1); }
+    ~EnvVar() { unsetenv(name); }
+};
+
+static bool all_sevens(const Tensor& t) {
+    for (float v : t.as_f32())
+        if (v != 7.0f) return false;
+    return true;
+}
+
+static void disable_routes_listed_ops(HipLlmBackend&) {
+    EnvVar env("SAPIENT_HIP_DISABLE", " RMS_norm, swiglu ,,rope");
+    RecordingBackend cpu;
+    HipLlmBackend bk(&cpu);
+    ASSERT(bk.disabled("rms_norm") && bk.disabled("swiglu") && bk.disabled("rope") && !bk.disabled("silu"),
+           "list parsed trimmed and lower-cased");
+    const Tensor x = Tensor::from_f32({0.0f, 1.0f, -2.0f, 3.0f}, {1, 4});
+    const Tensor w = Tensor::from_f32({1.0f, 1.0f, 1.0f, 1.0f}, {4});
+    ASSERT(all_sevens(bk.rms_norm(x, w, 1e-5f)), "rms_norm answered by the given backend");
+    ASSERT(cpu.calls == std::vector<std::string>({"rms_norm"}), "one rms_norm call");
+    // swiglu goes to the given backend's default composition: mul(silu(gate), up).
+    ASSERT(all_sevens(bk.swiglu(x, x)), "swiglu answered by the given backend");
+    ASSERT(cpu.calls == std::vector<std::string>({"rms_norm", "silu", "mul"}), "swiglu via silu then mul");
+    const Tensor q = Tensor::from_f32(std::vector<float>(8, 1.0f), {1, 1, 2, 4});
+    ASSERT(all_sevens(bk.apply_rope_partial(q, {0, 1}, 1e4f, 2)), "every RoPE method is 'rope'");
+    // Ops not listed stay on the device.
+    const std::vector<float> s = bk.silu(x).as_f32();
+    ASSERT(s[0] == 0.0f && s[1] > 0.73f && s[1] < 0.74f, "silu on the device");
+    ASSERT(cpu.calls.size() == 4, "silu did not reach the given backend");
+}
+
+static void disable_without_backend_raises(HipLlmBackend&) {
+    EnvVar env("SAPIENT_HIP_DISABLE", "all");
+    HipLlmBackend bk;
+    const Tensor a = Tensor::from_f32({1.0f, 2.0f}, {2});
+    const std::string e = expect_error([&] { bk.add(a, a); });
+    ASSERT(e.find("add: disabled by SAPIENT_HIP_DISABLE") != std::string::npos, "names op and switch: " + e);
+}
+
+static void verify_returns_the_device_result(HipLlmBackend&) {
+    EnvVar env("SAPIENT_HIP_VERIFY", "1");
+    RecordingBackend cpu;
+    HipLlmBackend bk(&cpu);
+    ASSERT(bk.verifying(), "switch read");
+    const Tensor a = Tensor::from_f32({1.0f, 2.0f, 3.0f}, {3});
+    const std::vector<float> sum = bk.add(a, a).as_f32();
+    ASSERT(sum == std::vector<float>({2.0f, 4.0f, 6.0f}), "device result returned");
+    ASSERT(cpu.calls == std::vector<std::string>({"add"}), "the given backend ran beside it");
+    for (int i = 0; i < 70; ++i) (void)bk.mul(a, a);
+    ASSERT(cpu.calls.size() == 64, "only the first 64 calls are cross-checked");
+}
+
 static void quant_bytes_are_validated(HipLlmBackend&) {  // tensor.rs:143-169
     ASSERT(expect_error([] { Tensor::from_quant_bytes(std::vector<uint8_t>(33), {32}, DType::Q8_0); })
                .find("shape mismatch") != std::string::npos, "byte count");
@@ -383,6 +470,9 @@ int main() {
         {"add_rms_norm_is_add_then_rms_norm", add_rms_norm_is_add_then_rms_norm},
         {"embed_row_gather_matches_full_dequant", embed_row_gather_matches_full_dequant},
         {"quant_bytes_are_validated", quant_bytes_are_validated},
+        {"disable_routes_listed_ops", disable_routes_listed_ops},
+        {"disable_without_backend_raises", disable_without_backend_raises},
+        {"verify_returns_the_device_result", verify_returns_the_device_result},
     };
     int failed = 0;
     for (const auto& [name, fn] : tests) {

@@ -23,3 +23,6 @@ def test_cpp_llm_backend_mirror():
     print(res.stdout)
     assert res.returncode == 0, res.stdout + res.stderr
     assert res.stdout.strip().endswith("0 failed")
+    # SAPIENT_HIP_VERIFY=1 reports each cross-checked call: the device's 2·a against the stand-in's 7s.
+    assert "[hip-verify] add #0 shape=[3] max_abs_diff=5 cpu_rms=7" in res.stderr, res.stderr
+    assert "[hip-verify] mul #63 " in res.stderr and "#64" not in res.stderr
