@@ -144,7 +144,8 @@ int sph_add_bias(const void* y, const void* bias, int bias_dtype, void* out, int
  * rope::apply_rope_partial_scaled (rope.rs:83-136), and WgpuContext::rope
  * (resident.rs:467). layout = SPH_ROPE_INTERLEAVED rotates (2i, 2i+1) pairs
  * instead (the layout the reference reaches by permuting GGUF q/k rows,
- * crates/sapient-models/src/gguf_weights.rs:111-115).
+ * crates/sapient-models/src/gguf_weights.rs:111-115). Bit-exact with the
+ * reference on glibc: powf from the host libm, sinf/cosf by glibc's algorithm.
  * `k` may be NULL (n_k_heads ignored). positions: device int32[seq], >= 0.
  * dtype ∈ {F32, F16, BF16}; head_dim even; rotary_dim even, 2..min(head_dim, 512). */
 int sph_rope(void* q, int64_t n_q_heads, void* k, int64_t n_k_heads, int dtype, int layout,

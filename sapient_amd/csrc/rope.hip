@@ -15,10 +15,11 @@
 //    element is read once and written once).
 //  - Parity: the d/2 denominators powf(base, 2i/d) come from the host's libm
 //    (the call the reference makes, passed in as kernel arguments); the
-//    division by them is IEEE f32 in-kernel; sin and cos are evaluated in f64
-//    and rounded once to f32 (correctly rounded except in vanishingly rare
-//    double-rounding cases); the rotation rounds each product before the
-//    add/subtract (-ffp-contract=off), exactly as the reference.
+//    division by them is IEEE f32 in-kernel; sin and cos are glibc's sinf and
+//    cosf restated (glibc_sincosf.h, bit-exact with the host libm over every
+//    f32 input); the rotation rounds each product before the add/subtract
+//    (-ffp-contract=off), exactly as the reference. The result is therefore
+//    the reference's, bit for bit.
 //  - grid.x covers tokens, grid.y splits the heads into groups (512-1024
 //    blocks in all) so that short sequences still put waves on every CU.
 //  - The decode-step variant (sph_rope_kv_append) fuses the RoPE of q and k
@@ -32,6 +33,7 @@
 
 #include <type_traits>
 
+#include "glibc_sincosf.h"
 #include "sph_common.h"
 
 namespace sph {
@@ -44,11 +46,25 @@ struct DenTable {
     float v[kMaxHalf];
 };
 
+__constant__ InvPio4Table kInvPio4 = inv_pio4_table();
+
+// The large-argument reduction indexes the 4/pi table per lane; staged in LDS
+// the lookups stay off the vector-memory queue the row stream keeps full
+// (measured: ~1.5 µs of 58 at the Llama-3-8B shape). Every thread of the block
+// must call this before any returns.
+__device__ __forceinline__ const uint32_t* stage_inv_pio4(uint32_t (&tab)[24]) {
+    if (threadIdx.x < 24) tab[threadIdx.x] = kInvPio4.w[threadIdx.x];
+    __syncthreads();
+    return tab;
+}
+
 template <typename T, int P, bool INTERLEAVED>
 __global__ __launch_bounds__(kThreads) void rope_kernel(T* q, int nq, T* k, int nk, const int32_t* __restrict__ pos,
                                                         int64_t ntok, int64_t seq, int head_dim, int half,
                                                         int lanes_per_tok, int toks_per_block, int heads_per_group,
                                                         float pos_scale, DenTable den) {
+    __shared__ uint32_t inv_pio4[24];
+    const uint32_t* tab = stage_inv_pio4(inv_pio4);
     const int tib = threadIdx.x / lanes_per_tok;
     const int lit = threadIdx.x - tib * lanes_per_tok;
     if (tib >= toks_per_block) return;
@@ -63,10 +79,7 @@ __global__ __launch_bounds__(kThreads) void rope_kernel(T* q, int nq, T* k, int 
 #pragma unroll
     for (int j = 0; j < P; ++j) {
         const float freq = p / den.v[i0 + j];
-        double sd, cd;
-        sincos((double)freq, &sd, &cd);
-        sn[j] = (float)sd;
-        cs[j] = (float)cd;
+        glibc_sincosf_tab(freq, tab, &sn[j], &cs[j]);
     }
 
     const int h_begin = blockIdx.y * heads_per_group;
@@ -123,6 +136,8 @@ __global__ __launch_bounds__(kThreads) void rope_kv_kernel(T* q, int nq, const T
                                                            int heads_per_group, float pos_scale, TC* kc, TC* vc,
                                                            int64_t max_seq, int32_t* bad_pos_flag, const TB* bq,
                                                            const TB* bk, const TB* bv, DenTable den) {
+    __shared__ uint32_t inv_pio4[24];
+    const uint32_t* tab = stage_inv_pio4(inv_pio4);
     const int tib = threadIdx.x / lanes_per_tok;
     const int lit = threadIdx.x - tib * lanes_per_tok;
     if (tib >= toks_per_block) return;
@@ -135,10 +150,7 @@ __global__ __launch_bounds__(kThreads) void rope_kv_kernel(T* q, int nq, const T
 #pragma unroll
     for (int j = 0; j < P; ++j) {
         const float freq = p / den.v[i0 + j];
-        double sd, cd;
-        sincos((double)freq, &sd, &cd);
-        sn[j] = (float)sd;
-        cs[j] = (float)cd;
+        glibc_sincosf_tab(freq, tab, &sn[j], &cs[j]);
     }
     const bool pos_ok = ps >= 0 && (int64_t)ps < max_seq;
     if (!pos_ok && bad_pos_flag != nullptr && lit == 0 && blockIdx.y == 0) *bad_pos_flag = 1;
@@ -238,6 +250,18 @@ __global__ __launch_bounds__(kThreads) void rope_kv_kernel(T* q, int nq, const T
     }
 }
 
+// Blocks to aim for in total (head groups × token blocks). Each head group
+// recomputes its sin/cos, so fewer, longer-running groups stream faster, down
+// to the point where too few waves are left in flight. Measured optimum at the
+// Llama-3-8B shape on MI355X (32 + 8 heads × 8192 tokens × 128):
+//   f32 NEOX 58.4 µs at 512 (60.8 at 1024), interleaved 58.9 at 512;
+//   f16 NEOX 34.3 µs at 512 (35.8 at 1024), interleaved 34.3 at 1536
+//   (35.4 at 1024, 41.1 at 512, where one group holds all 40 heads).
+template <typename T, bool IL>
+constexpr int rope_grid_target() {
+    return sizeof(T) == 4 ? 512 : (IL ? 1536 : 512);
+}
+
 template <typename T, int P, bool IL>
 int launch_rope_p(T* q, int nq, T* k, int nk, const int32_t* pos, int64_t ntok, int64_t seq, int head_dim,
                   int half, float pos_scale, const DenTable& den, hipStream_t stream) {
@@ -245,12 +269,7 @@ int launch_rope_p(T* q, int nq, T* k, int nk, const int32_t* pos, int64_t ntok, 
     const int toks_per_block = kThreads / lanes_per_tok;
     const int64_t blocks_x = (ntok + toks_per_block - 1) / toks_per_block;
     const int heads = nq + nk;
-    // Aim for ~512 blocks (f32) or ~1024 (half types) in total: each head
-    // group recomputes its sin/cos, so fewer, longer-running groups stream
-    // faster, but half types move half the bytes per thread and need the extra
-    // waves (Llama-3-8B shape on MI355X: f32 NEOX 58.5 µs at 512 vs 59.7 at
-    // 1024; f16 interleaved 41.5 µs at 512 vs 33.8 at 1024).
-    const int target = sizeof(T) == 4 ? 512 : 1024;
+    const int target = rope_grid_target<T, IL>();
     int groups = (int)((target + blocks_x - 1) / blocks_x);
     if (groups > heads) groups = heads;
     if (groups < 1) groups = 1;
@@ -278,7 +297,7 @@ int launch_rope_kv_p(T* q, int nq, const T* k, const T* v, int nkv, const int32_
     const int toks_per_block = kThreads / lanes_per_tok;
     const int64_t blocks_x = (seq + toks_per_block - 1) / toks_per_block;
     const int heads = nq + nkv;
-    const int target = sizeof(T) == 4 ? 512 : 1024;
+    const int target = rope_grid_target<T, IL>();
     int groups = (int)((target + blocks_x - 1) / blocks_x);
     if (groups > heads) groups = heads;
     if (groups < 1) groups = 1;

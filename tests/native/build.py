@@ -2,8 +2,8 @@
 
 - test_hip_llm_backend: GPU tests of the C++ LlmBackend mirror, linked against the
   in-tree libsapient_hip.so (rpath relative to the binary, so the tree can move);
-- check_glibc_tanhf, check_glibc_expf: the host-side exhaustive checks of
-  glibc_tanhf.h and glibc_expf.h.
+- check_glibc_tanhf, check_glibc_expf, check_glibc_sincosf: the host-side
+  exhaustive checks of glibc_tanhf.h, glibc_expf.h and glibc_sincosf.h.
 """
 import shutil
 import subprocess
@@ -20,7 +20,7 @@ def build() -> None:
     subprocess.run([gxx, "-std=c++17", "-O1", "-Wall", f"-I{ROOT / 'include'}", str(HERE / "test_hip_llm_backend.cpp"),
                     "-o", str(OUT / "test_hip_llm_backend"), f"-L{ROOT / 'sapient_amd'}", "-lsapient_hip",
                     "-Wl,-rpath,$ORIGIN/../../../sapient_amd", "-Wl,-rpath,/opt/rocm/lib"], check=True)
-    for check in ("check_glibc_tanhf", "check_glibc_expf"):
+    for check in ("check_glibc_tanhf", "check_glibc_expf", "check_glibc_sincosf"):
         subprocess.run([gxx, "-O2", "-std=c++17", "-ffp-contract=off", "-fno-fast-math", "-D__HIP_PLATFORM_AMD__",
                         "-I/opt/rocm/include", f"-I{ROOT / 'sapient_amd' / 'csrc'}", f"-I{ROOT / 'include'}",
                         str(HERE / f"{check}.cpp"), "-o", str(OUT / check), "-lpthread", "-lm"], check=True)

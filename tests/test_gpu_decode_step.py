@@ -6,8 +6,8 @@ and k (resident.rs:467), then kv_append of k and v (resident.rs:645-711).
 
 Bar: bit-exact against the unfused sequence of this library's own kernels
 (sph_rope in place, then sph_kv_append of k and v), whose parity with the oracle
-the RoPE and layout tests establish; and q / the caches against the oracle at
-the RoPE tolerance (≤ 1e-5 of the pair's norm for f32).
+the RoPE and layout tests establish; and q / the caches bit-exact against the
+oracle.
 """
 import numpy as np
 import pytest
@@ -64,7 +64,7 @@ def test_fused_equals_unfused(dev, dtype, cdtype, interleaved, Hq, Hkv, S, D, ma
 
 def test_fused_matches_oracle_and_scatters_by_position(dev, orc):
     """Non-consecutive positions (a shuffled chunk): each token's rows land at its own cache
-    row; q and the k cache agree with the oracle's apply_rope at the RoPE tolerance; v is copied."""
+    row; q and the k cache equal the oracle's apply_rope bit for bit; v is copied."""
     Hq, Hkv, S, D, max_seq = 8, 2, 6, 64, 32
     nxt = WgpuLcg()
     q = nxt.take(Hq * S * D).reshape(Hq, S, D)
@@ -77,11 +77,11 @@ def test_fused_matches_oracle_and_scatters_by_position(dev, orc):
     ops.rope_kv_append(tq, tk, tv, torch.from_numpy(pos).to(dev), 1e4, kc, vc)
     want_q = orc.apply_rope(q[None], pos, 1e4)[0]
     want_k = orc.apply_rope(k[None], pos, 1e4)[0]
-    pair = lambda x: np.sqrt(np.concatenate([x[..., :D // 2] ** 2 + x[..., D // 2:] ** 2] * 2, axis=-1))
-    assert (np.abs(to_np(tq) - want_q) <= 1e-5 * pair(q) + 1e-30).all()
+    bits = lambda a: np.ascontiguousarray(a, np.float32).view(np.uint32)
+    assert np.array_equal(bits(to_np(tq)), bits(want_q))
     got_k, got_v = to_np(kc), to_np(vc)
     for s, p in enumerate(pos):
-        assert (np.abs(got_k[:, p] - want_k[:, s]) <= 1e-5 * pair(k[:, s]) + 1e-30).all()
+        assert np.array_equal(bits(got_k[:, p]), bits(want_k[:, s]))
         assert np.array_equal(got_v[:, p], v[:, s])
     untouched = np.setdiff1d(np.arange(max_seq), pos)
     assert (got_k[:, untouched] == 0).all() and (got_v[:, untouched] == 0).all()
