@@ -178,6 +178,21 @@ int sph_rope_kv_append(void* q, int64_t n_q_heads, const void* k, const void* v,
                        const void* bq, const void* bk, const void* bv, int bias_dtype, int32_t* bad_pos_flag,
                        void* stream);
 
+/* sph_rope_kv_append for a chunk straight from the projections: q, k and v
+ * are read token-major, [seq, n_q_heads | n_kv_heads, head_dim] (not
+ * modified), and the rotated q is written heads-major to q_out [n_q_heads,
+ * seq, head_dim], the layout attention reads. Replaces the chunk sequence of
+ * WgpuForwardEngine::forward_chunk (wgpu_engine.rs:525-573): bias adds,
+ * transpose_heads of q, k and v (resident.rs:420-458), rope of q and k, and
+ * kv_append of k and v. Results equal sph_transpose_heads of q, k, v followed
+ * by sph_rope_kv_append, bit for bit. q_out must not overlap q (SPH_EINVAL);
+ * every other rule is sph_rope_kv_append's. */
+int sph_rope_kv_append_tokens(const void* q, void* q_out, int64_t n_q_heads, const void* k, const void* v,
+                              int64_t n_kv_heads, int dtype, int layout, const int32_t* positions, int64_t seq,
+                              int64_t head_dim, float base, float pos_scale, void* kcache, void* vcache,
+                              int cache_dtype, int64_t max_seq, const void* bq, const void* bk, const void* bv,
+                              int bias_dtype, int32_t* bad_pos_flag, void* stream);
+
 /* Token-embedding gather with on-the-fly row dequantization into f32:
  * out[t, :] = dequant(table[ids[t], :]). The table is the raw GGUF tensor
  * data, rows of byte_count(hidden) bytes, consumed verbatim (no repacking).

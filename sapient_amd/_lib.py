@@ -60,6 +60,8 @@ SIGNATURES = {
     "sph_embed": (_i32, [_vp, _i32, _i64, _i64, _vp, _i64, _vp, _vp, _vp]),
     "sph_rope_kv_append": (_i32, [_vp, _i64, _vp, _vp, _i64, _i32, _i32, _vp, _i64, _i64, _f, _f, _vp, _vp, _i32,
                                   _i64, _vp, _vp, _vp, _i32, _vp, _vp]),
+    "sph_rope_kv_append_tokens": (_i32, [_vp, _vp, _i64, _vp, _vp, _i64, _i32, _i32, _vp, _i64, _i64, _f, _f, _vp,
+                                         _vp, _i32, _i64, _vp, _vp, _vp, _i32, _vp, _vp]),
     "sph_transpose_heads": (_i32, [_vp, _vp, _i32, _i64, _i64, _i64, _vp]),
     "sph_kv_append": (_i32, [_vp, _i32, _vp, _i32, _i64, _i64, _i64, _i64, _i64, _vp]),
     # sapient_hip_engine.h

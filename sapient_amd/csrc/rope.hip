@@ -124,12 +124,14 @@ __global__ __launch_bounds__(kThreads) void rope_kernel(T* q, int nq, T* k, int 
     }
 }
 
-// Fused decode step: heads [0, nq) are q rows rotated in place; heads
-// [nq, nq + nkv) rotate the k row and write it, plus the v row, to cache row
-// (h, positions[s]). batch = 1 and rotary_dim = head_dim, so a thread's P
-// pairs and the pairs of its lane neighbours cover every channel of the row.
-template <typename T, typename TC, typename TB, int P, bool INTERLEAVED>
-__global__ __launch_bounds__(kThreads) void rope_kv_kernel(T* q, int nq, const T* __restrict__ k,
+// Fused decode step: heads [0, nq) are q rows, rotated and written to qo
+// heads-major; heads [nq, nq + nkv) rotate the k row and write it, plus the v
+// row, to cache row (h, positions[s]). batch = 1 and rotary_dim = head_dim, so
+// a thread's P pairs and the pairs of its lane neighbours cover every channel
+// of the row. TM: q, k and v are read token-major [seq, heads, head_dim] (the
+// projections' layout) instead of heads-major; without TM, qo == q (in place).
+template <typename T, typename TC, typename TB, int P, bool INTERLEAVED, bool TM>
+__global__ __launch_bounds__(kThreads) void rope_kv_kernel(const T* q, T* qo, int nq, const T* __restrict__ k,
                                                            const T* __restrict__ v, int nkv,
                                                            const int32_t* __restrict__ pos, int64_t seq, int head_dim,
                                                            int half, int lanes_per_tok, int toks_per_block,
@@ -163,8 +165,12 @@ __global__ __launch_bounds__(kThreads) void rope_kv_kernel(T* q, int nq, const T
     if (h_end > nq + nkv) h_end = nq + nkv;
     for (int hh = h_begin; hh < h_end; ++hh) {
         const bool is_q = hh < nq;
-        const T* src = is_q ? q + ((size_t)hh * (size_t)seq + (size_t)s) * (size_t)head_dim
-                            : k + ((size_t)(hh - nq) * (size_t)seq + (size_t)s) * (size_t)head_dim;
+        // Row (head h, token s) of a [heads, seq, hd] (or, TM, [seq, heads, hd]) tensor.
+        auto row_of = [&](const T* base, int heads, int h) {
+            return base + (TM ? (size_t)s * (size_t)heads + (size_t)h : (size_t)h * (size_t)seq + (size_t)s) *
+                              (size_t)head_dim;
+        };
+        const T* src = is_q ? row_of(q, nq, hh) : row_of(k, nkv, hh - nq);
         if (!is_q && !pos_ok) continue;
         // Row values with the bias of their channels added (y + b in f32, then
         // stored in the activation type before RoPE reads it: round through T).
@@ -228,7 +234,7 @@ __global__ __launch_bounds__(kThreads) void rope_kv_kernel(T* q, int nq, const T
             }
         };
         if (is_q) {
-            put(q + ((size_t)hh * (size_t)seq + (size_t)s) * (size_t)head_dim, o0, o1);
+            put(qo + ((size_t)hh * (size_t)seq + (size_t)s) * (size_t)head_dim, o0, o1);
         } else {
             const size_t crow = ((size_t)(hh - nq) * (size_t)max_seq + (size_t)ps) * (size_t)head_dim;
             // The unfused sequence stores rotated k in the activation type
@@ -242,7 +248,7 @@ __global__ __launch_bounds__(kThreads) void rope_kv_kernel(T* q, int nq, const T
             }
             put(kc + crow, o0, o1);
             // v: the same channels, moved unrotated.
-            const T* vrow = v + ((size_t)(hh - nq) * (size_t)seq + (size_t)s) * (size_t)head_dim;
+            const T* vrow = row_of(v, nkv, hh - nq);
             float v0[P], v1[P];
             load_row(vrow, bv ? bv + (size_t)(hh - nq) * head_dim : nullptr, v0, v1);
             put(vc + crow, v0, v1);
@@ -288,8 +294,8 @@ inline void fill_dens(DenTable& den, int half, int rotary_dim, float base) {
         den.v[i] = i < half ? powf(base, 2.0f * (float)i / (float)rotary_dim) : 1.0f;
 }
 
-template <typename T, typename TC, typename TB, int P, bool IL>
-int launch_rope_kv_p(T* q, int nq, const T* k, const T* v, int nkv, const int32_t* pos, int64_t seq, int head_dim,
+template <typename T, typename TC, typename TB, int P, bool IL, bool TM>
+int launch_rope_kv_p(const T* q, T* qo, int nq, const T* k, const T* v, int nkv, const int32_t* pos, int64_t seq, int head_dim,
                      float pos_scale, TC* kc, TC* vc, int64_t max_seq, int32_t* flag, const TB* bq, const TB* bk,
                      const TB* bv, const DenTable& den, hipStream_t stream) {
     const int half = head_dim / 2;
@@ -305,22 +311,24 @@ int launch_rope_kv_p(T* q, int nq, const T* k, const T* v, int nkv, const int32_
     groups = (heads + heads_per_group - 1) / heads_per_group;
     if (blocks_x > INT32_MAX) return SPH_EINVAL;
     const dim3 grid((unsigned)blocks_x, (unsigned)groups);
-    rope_kv_kernel<T, TC, TB, P, IL><<<grid, kThreads, 0, stream>>>(q, nq, k, v, nkv, pos, seq, head_dim, half,
-                                                                    lanes_per_tok, toks_per_block, heads_per_group,
-                                                                    pos_scale, kc, vc, max_seq, flag, bq, bk, bv, den);
+    rope_kv_kernel<T, TC, TB, P, IL, TM><<<grid, kThreads, 0, stream>>>(q, qo, nq, k, v, nkv, pos, seq, head_dim, half,
+                                                                        lanes_per_tok, toks_per_block, heads_per_group,
+                                                                        pos_scale, kc, vc, max_seq, flag, bq, bk, bv, den);
     return launch_status();
 }
 
 // P: pairs per thread, the widest whose accesses of q/k/v (type T) and of the
 // caches (type TC) stay within 16 bytes and aligned.
-template <typename T, typename TC, typename TB>
-int launch_rope_kv(void* qv, int nq, const void* kv, const void* vv, int nkv, int layout, const int32_t* pos,
-                   int64_t seq, int head_dim, float base, float pos_scale, void* kcv, void* vcv, int64_t max_seq,
-                   int32_t* flag, const void* bqv, const void* bkv, const void* bvv, hipStream_t stream) {
+template <typename T, typename TC, typename TB, bool TM>
+int launch_rope_kv(const void* qv, void* qov, int nq, const void* kv, const void* vv, int nkv, int layout,
+                   const int32_t* pos, int64_t seq, int head_dim, float base, float pos_scale, void* kcv, void* vcv,
+                   int64_t max_seq, int32_t* flag, const void* bqv, const void* bkv, const void* bvv,
+                   hipStream_t stream) {
     const TB* bq = static_cast<const TB*>(bqv);
     const TB* bk = static_cast<const TB*>(bkv);
     const TB* bv = static_cast<const TB*>(bvv);
-    T* q = static_cast<T*>(qv);
+    const T* q = static_cast<const T*>(qv);
+    T* qo = static_cast<T*>(qov);
     const T* k = static_cast<const T*>(kv);
     const T* v = static_cast<const T*>(vv);
     TC* kc = static_cast<TC*>(kcv);
@@ -337,20 +345,20 @@ int launch_rope_kv(void* qv, int nq, const void* kv, const void* vv, int nkv, in
         const size_t at = run * sizeof(T) < 16 ? run * sizeof(T) : 16;
         const size_t ac = run * sizeof(TC) < 16 ? run * sizeof(TC) : 16;
         const size_t ab = run * sizeof(TB) < 16 ? run * sizeof(TB) : 16;  // bias runs may span two 16-byte loads
-        return aligned(q, at) && aligned(k, at) && aligned(v, at) && aligned(kc, ac) && aligned(vc, ac) &&
-               aligned(bq, ab) && aligned(bk, ab) && aligned(bv, ab);
+        return aligned(q, at) && aligned(qo, at) && aligned(k, at) && aligned(v, at) && aligned(kc, ac) &&
+               aligned(vc, ac) && aligned(bq, ab) && aligned(bk, ab) && aligned(bv, ab);
     };
     constexpr int V = vec16<T>::n < vec16<TC>::n ? vec16<T>::n : vec16<TC>::n;
     if (!il) {
-        if (ok(V)) return launch_rope_kv_p<T, TC, TB, V, false>(q, nq, k, v, nkv, pos, seq, head_dim, pos_scale, kc, vc, max_seq, flag, bq, bk, bv, den, stream);
-        if (ok(V / 2)) return launch_rope_kv_p<T, TC, TB, V / 2, false>(q, nq, k, v, nkv, pos, seq, head_dim, pos_scale, kc, vc, max_seq, flag, bq, bk, bv, den, stream);
+        if (ok(V)) return launch_rope_kv_p<T, TC, TB, V, false, TM>(q, qo, nq, k, v, nkv, pos, seq, head_dim, pos_scale, kc, vc, max_seq, flag, bq, bk, bv, den, stream);
+        if (ok(V / 2)) return launch_rope_kv_p<T, TC, TB, V / 2, false, TM>(q, qo, nq, k, v, nkv, pos, seq, head_dim, pos_scale, kc, vc, max_seq, flag, bq, bk, bv, den, stream);
         if constexpr (V / 4 >= 2) {
-            if (ok(V / 4)) return launch_rope_kv_p<T, TC, TB, V / 4, false>(q, nq, k, v, nkv, pos, seq, head_dim, pos_scale, kc, vc, max_seq, flag, bq, bk, bv, den, stream);
+            if (ok(V / 4)) return launch_rope_kv_p<T, TC, TB, V / 4, false, TM>(q, qo, nq, k, v, nkv, pos, seq, head_dim, pos_scale, kc, vc, max_seq, flag, bq, bk, bv, den, stream);
         }
     } else {
-        if (ok(V / 2)) return launch_rope_kv_p<T, TC, TB, V / 2, true>(q, nq, k, v, nkv, pos, seq, head_dim, pos_scale, kc, vc, max_seq, flag, bq, bk, bv, den, stream);
+        if (ok(V / 2)) return launch_rope_kv_p<T, TC, TB, V / 2, true, TM>(q, qo, nq, k, v, nkv, pos, seq, head_dim, pos_scale, kc, vc, max_seq, flag, bq, bk, bv, den, stream);
         if constexpr (V / 4 >= 1) {
-            if (ok(V / 4)) return launch_rope_kv_p<T, TC, TB, V / 4, true>(q, nq, k, v, nkv, pos, seq, head_dim, pos_scale, kc, vc, max_seq, flag, bq, bk, bv, den, stream);
+            if (ok(V / 4)) return launch_rope_kv_p<T, TC, TB, V / 4, true, TM>(q, qo, nq, k, v, nkv, pos, seq, head_dim, pos_scale, kc, vc, max_seq, flag, bq, bk, bv, den, stream);
         }
     }
     return SPH_EINVAL;  // head_dim or alignment the vector paths do not cover
@@ -414,33 +422,66 @@ extern "C" int sph_rope(void* q, int64_t n_q_heads, void* k, int64_t n_k_heads, 
     });
 }
 
+namespace sph {
+namespace {
+
+// Validation and dispatch shared by the two fused entry points.
+template <bool TM>
+int rope_kv_entry(const void* q, void* q_out, int64_t n_q_heads, const void* k, const void* v, int64_t n_kv_heads,
+                  int dtype, int layout, const int32_t* positions, int64_t seq, int64_t head_dim, float base,
+                  float pos_scale, void* kcache, void* vcache, int cache_dtype, int64_t max_seq, const void* bq,
+                  const void* bk, const void* bv, int bias_dtype, int32_t* bad_pos_flag, void* stream) {
+    if (layout != SPH_ROPE_NEOX && layout != SPH_ROPE_INTERLEAVED) return SPH_EINVAL;
+    if (!is_float_dtype(dtype) || !is_float_dtype(cache_dtype)) return SPH_EINVAL;
+    if ((bq || bk || bv) && !is_float_dtype(bias_dtype)) return SPH_EINVAL;
+    if (!(bq || bk || bv)) bias_dtype = SPH_F32;
+    if (n_q_heads < 0 || n_kv_heads < 0 || seq < 0 || max_seq < 0) return SPH_EINVAL;
+    if (head_dim <= 0 || head_dim % 2 != 0 || head_dim / 2 > kMaxHalf) return SPH_EINVAL;
+    if (n_q_heads + n_kv_heads > INT32_MAX) return SPH_EINVAL;
+    if (seq == 0 || n_q_heads + n_kv_heads == 0) return SPH_OK;
+    if (positions == nullptr || (n_q_heads > 0 && (q == nullptr || q_out == nullptr))) return SPH_EINVAL;
+    if (n_kv_heads > 0 && (k == nullptr || v == nullptr || kcache == nullptr || vcache == nullptr)) return SPH_EINVAL;
+    if (!(pos_scale == pos_scale) || pos_scale == 0.0f) return SPH_EINVAL;
+    if (TM && n_q_heads > 0) {  // q_out is written while q is still being read: they must not overlap
+        const uintptr_t bytes = (uintptr_t)n_q_heads * (uintptr_t)seq * (uintptr_t)head_dim * dtype_size(dtype);
+        const uintptr_t a = (uintptr_t)q, b = (uintptr_t)q_out;
+        if (a < b + bytes && b < a + bytes) return SPH_EINVAL;
+    }
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    return with_float_type(dtype, [&](auto t) -> int {
+        using T = decltype(t);
+        return with_float_type(cache_dtype, [&](auto tc) -> int {
+            using TC = decltype(tc);
+            return with_float_type(bias_dtype, [&](auto tb) -> int {
+                using TB = decltype(tb);
+                return launch_rope_kv<T, TC, TB, TM>(q, q_out, (int)n_q_heads, k, v, (int)n_kv_heads, layout,
+                                                     positions, seq, (int)head_dim, base, pos_scale, kcache, vcache,
+                                                     max_seq, bad_pos_flag, bq, bk, bv, s);
+            });
+        });
+    });
+}
+
+}  // namespace
+}  // namespace sph
+
 extern "C" int sph_rope_kv_append(void* q, int64_t n_q_heads, const void* k, const void* v, int64_t n_kv_heads,
                                   int dtype, int layout, const int32_t* positions, int64_t seq, int64_t head_dim,
                                   float base, float pos_scale, void* kcache, void* vcache, int cache_dtype,
                                   int64_t max_seq, const void* bq, const void* bk, const void* bv, int bias_dtype,
                                   int32_t* bad_pos_flag, void* stream) {
-    if (layout != SPH_ROPE_NEOX && layout != SPH_ROPE_INTERLEAVED) return SPH_EINVAL;
-    if (!sph::is_float_dtype(dtype) || !sph::is_float_dtype(cache_dtype)) return SPH_EINVAL;
-    if ((bq || bk || bv) && !sph::is_float_dtype(bias_dtype)) return SPH_EINVAL;
-    if (!(bq || bk || bv)) bias_dtype = SPH_F32;
-    if (n_q_heads < 0 || n_kv_heads < 0 || seq < 0 || max_seq < 0) return SPH_EINVAL;
-    if (head_dim <= 0 || head_dim % 2 != 0 || head_dim / 2 > sph::kMaxHalf) return SPH_EINVAL;
-    if (n_q_heads + n_kv_heads > INT32_MAX) return SPH_EINVAL;
-    if (seq == 0 || n_q_heads + n_kv_heads == 0) return SPH_OK;
-    if (positions == nullptr || (n_q_heads > 0 && q == nullptr)) return SPH_EINVAL;
-    if (n_kv_heads > 0 && (k == nullptr || v == nullptr || kcache == nullptr || vcache == nullptr)) return SPH_EINVAL;
-    if (!(pos_scale == pos_scale) || pos_scale == 0.0f) return SPH_EINVAL;
-    hipStream_t s = static_cast<hipStream_t>(stream);
-    return sph::with_float_type(dtype, [&](auto t) -> int {
-        using T = decltype(t);
-        return sph::with_float_type(cache_dtype, [&](auto tc) -> int {
-            using TC = decltype(tc);
-            return sph::with_float_type(bias_dtype, [&](auto tb) -> int {
-                using TB = decltype(tb);
-                return sph::launch_rope_kv<T, TC, TB>(q, (int)n_q_heads, k, v, (int)n_kv_heads, layout, positions,
-                                                     seq, (int)head_dim, base, pos_scale, kcache, vcache, max_seq,
-                                                     bad_pos_flag, bq, bk, bv, s);
-            });
-        });
-    });
+    return sph::rope_kv_entry<false>(q, q, n_q_heads, k, v, n_kv_heads, dtype, layout, positions, seq, head_dim, base,
+                                     pos_scale, kcache, vcache, cache_dtype, max_seq, bq, bk, bv, bias_dtype,
+                                     bad_pos_flag, stream);
+}
+
+extern "C" int sph_rope_kv_append_tokens(const void* q, void* q_out, int64_t n_q_heads, const void* k, const void* v,
+                                         int64_t n_kv_heads, int dtype, int layout, const int32_t* positions,
+                                         int64_t seq, int64_t head_dim, float base, float pos_scale, void* kcache,
+                                         void* vcache, int cache_dtype, int64_t max_seq, const void* bq,
+                                         const void* bk, const void* bv, int bias_dtype, int32_t* bad_pos_flag,
+                                         void* stream) {
+    return sph::rope_kv_entry<true>(q, q_out, n_q_heads, k, v, n_kv_heads, dtype, layout, positions, seq, head_dim,
+                                    base, pos_scale, kcache, vcache, cache_dtype, max_seq, bq, bk, bv, bias_dtype,
+                                    bad_pos_flag, stream);
 }

@@ -7,9 +7,9 @@
 //  - `x = add(x, o); h = rms_norm(x)` pairs run as one sph_add_rms_norm
 //    (IEEE addition commutes, so o + x is x + o bit for bit);
 //  - `add_bias(q|k|v); rope(q); rope(k); kv_append(k); kv_append(v)` runs as
-//    one sph_rope_kv_append, bit-exact with that sequence (biases are per
-//    channel, so adding them after the token-major → heads-major transpose of
-//    a chunk gives the same sums);
+//    one sph_rope_kv_append, bit-exact with that sequence; for a chunk the
+//    three transpose_heads before it fold into the same launch
+//    (sph_rope_kv_append_tokens reads the projections' token-major rows);
 //  - forward_chunk adds the last layer's residual and normalises only the last
 //    row, the one the reference slices out before its final norm (:623-627).
 // Decode steps can be captured into a HIP graph once and replayed: every
@@ -37,9 +37,9 @@ struct sph_engine {
 
     hipStream_t stream = nullptr;
     std::vector<std::pair<void*, size_t>> device_allocs;
-    float *x = nullptr, *h = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *qt = nullptr, *kt = nullptr,
-          *vt = nullptr, *attn = nullptr, *attn_sm = nullptr, *o = nullptr, *gate = nullptr, *up = nullptr,
-          *act = nullptr, *down = nullptr, *out = nullptr;
+    float *x = nullptr, *h = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *qt = nullptr, *attn = nullptr,
+          *attn_sm = nullptr, *o = nullptr, *gate = nullptr, *up = nullptr, *act = nullptr, *down = nullptr,
+          *out = nullptr;
     uint32_t* ids = nullptr;
     int32_t* positions = nullptr;
     int32_t* flags = nullptr;  // [0] bad token id, [1] bad cache position (both checked on the host first)
@@ -116,20 +116,21 @@ int body(sph_engine* e, int64_t T) {
         SPH_TRY(proj(e, l, SPH_PROJ_Q, e->h, e->q, T));
         SPH_TRY(proj(e, l, SPH_PROJ_K, e->h, e->k, T));
         SPH_TRY(proj(e, l, SPH_PROJ_V, e->h, e->v, T));
-        // token-major [T, heads, hd] → heads-major [heads, T, hd]; one token: the same memory
-        float *qh = e->q, *kh = e->k, *vh = e->v;
-        if (T > 1) {
-            SPH_TRY(sph_transpose_heads(e->q, e->qt, SPH_F32, T, c.n_heads, c.head_dim, s));
-            SPH_TRY(sph_transpose_heads(e->k, e->kt, SPH_F32, T, c.n_kv_heads, c.head_dim, s));
-            SPH_TRY(sph_transpose_heads(e->v, e->vt, SPH_F32, T, c.n_kv_heads, c.head_dim, s));
+        // q/k/v biases, RoPE and the cache append in one launch. One token: token-major
+        // [1, heads, hd] is heads-major already, q is rotated in place. A chunk: q, k, v
+        // are read token-major and q is written heads-major to qt, the transposes fused.
+        float* qh = e->q;
+        if (T == 1) {
+            SPH_TRY(sph_rope_kv_append(e->q, c.n_heads, e->k, e->v, c.n_kv_heads, SPH_F32, c.rope_layout,
+                                       e->positions, T, c.head_dim, c.rope_theta, 1.0f, e->kcache[l], e->vcache[l],
+                                       c.kv_dtype, c.max_seq, L.bq, L.bk, L.bv, c.bias_dtype, e->flags + 1, s));
+        } else {
             qh = e->qt;
-            kh = e->kt;
-            vh = e->vt;
+            SPH_TRY(sph_rope_kv_append_tokens(e->q, e->qt, c.n_heads, e->k, e->v, c.n_kv_heads, SPH_F32,
+                                              c.rope_layout, e->positions, T, c.head_dim, c.rope_theta, 1.0f,
+                                              e->kcache[l], e->vcache[l], c.kv_dtype, c.max_seq, L.bq, L.bk, L.bv,
+                                              c.bias_dtype, e->flags + 1, s));
         }
-        // q/k/v biases, RoPE and the cache append in one launch
-        SPH_TRY(sph_rope_kv_append(qh, c.n_heads, kh, vh, c.n_kv_heads, SPH_F32, c.rope_layout, e->positions, T,
-                                   c.head_dim, c.rope_theta, 1.0f, e->kcache[l], e->vcache[l], c.kv_dtype,
-                                   c.max_seq, L.bq, L.bk, L.bv, c.bias_dtype, e->flags + 1, s));
         if (e->attend)
             SPH_TRY(callback_status(e->attend(e->user, l, qh, e->kcache[l], e->vcache[l], c.kv_dtype, e->positions, T,
                                               c.max_seq, e->attn, s)));
@@ -226,7 +227,7 @@ extern "C" int sph_engine_create(const sph_engine_config* cfg, const void* embed
               hipHostMalloc((void**)&e->staged_pos, T * 4, hipHostMallocDefault) == hipSuccess &&
               dalloc(e, &e->x, T * c.hidden * 4) && dalloc(e, &e->h, T * c.hidden * 4) && dalloc(e, &e->q, T * qd * 4) &&
               dalloc(e, &e->k, T * kd * 4) && dalloc(e, &e->v, T * kd * 4) && dalloc(e, &e->qt, T * qd * 4) &&
-              dalloc(e, &e->kt, T * kd * 4) && dalloc(e, &e->vt, T * kd * 4) && dalloc(e, &e->attn, T * qd * 4) &&
+              dalloc(e, &e->attn, T * qd * 4) &&
               dalloc(e, &e->attn_sm, T * qd * 4) && dalloc(e, &e->o, T * c.hidden * 4) &&
               dalloc(e, &e->gate, T * c.intermediate * 4) && dalloc(e, &e->up, T * c.intermediate * 4) &&
               dalloc(e, &e->act, T * c.intermediate * 4) && dalloc(e, &e->down, T * c.hidden * 4) &&

@@ -275,21 +275,10 @@ def kv_append(src: torch.Tensor, cache: torch.Tensor, pos: int) -> None:
                               n_kv, seq, hd, max_seq, int(pos), _stream(src)), "kv_append")
 
 
-def rope_kv_append(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, positions: torch.Tensor, base: float,
-                   kcache: torch.Tensor, vcache: torch.Tensor, pos_scale: float = 1.0, interleaved: bool = False,
-                   bad_pos_flag: Optional[torch.Tensor] = None, bq: Optional[torch.Tensor] = None,
-                   bk: Optional[torch.Tensor] = None, bv: Optional[torch.Tensor] = None) -> None:
-    """Fused decode step: optional q/k/v biases, RoPE on q in place; rotated k and v written to
-    the caches at rows positions[s] (wgpu_engine.rs:397-432). q [Hq, S, D], k/v [Hkv, S, D],
-    caches [Hkv, max_seq, D], biases [Hq·D] / [Hkv·D] of one dtype."""
-    for t, n in ((q, "q"), (k, "k"), (v, "v"), (kcache, "kcache"), (vcache, "vcache"), (positions, "positions")):
+def _rope_kv_args(Hq, Hkv, S, D, positions, kcache, vcache, bad_pos_flag, bq, bk, bv):
+    """Checks shared by the fused decode steps; returns (flag, biases, bias dtype code)."""
+    for t, n in ((kcache, "kcache"), (vcache, "vcache"), (positions, "positions")):
         _dev(t, n)
-    if q.dim() != 3 or k.dim() != 3 or k.shape != v.shape or q.shape[1:] != k.shape[1:]:
-        raise ValueError("q must be [Hq, S, D] and k, v [Hkv, S, D]")
-    if k.dtype != q.dtype or v.dtype != q.dtype:
-        raise ValueError("q, k and v must share dtype")
-    Hq, S, D = q.shape
-    Hkv = k.shape[0]
     if kcache.shape != vcache.shape or kcache.dim() != 3 or kcache.shape[0] != Hkv or kcache.shape[2] != D \
             or kcache.dtype != vcache.dtype:
         raise ValueError("caches must be [Hkv, max_seq, D] of one dtype")
@@ -305,9 +294,55 @@ def rope_kv_append(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, positions:
     if len(bdt) > 1:
         raise ValueError("biases must share dtype")
     bias_code = dtype_code(bdt.pop()) if bdt else 0
+    return flag, [None if b is None else b.data_ptr() for b in biases], bias_code
+
+
+def rope_kv_append(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, positions: torch.Tensor, base: float,
+                   kcache: torch.Tensor, vcache: torch.Tensor, pos_scale: float = 1.0, interleaved: bool = False,
+                   bad_pos_flag: Optional[torch.Tensor] = None, bq: Optional[torch.Tensor] = None,
+                   bk: Optional[torch.Tensor] = None, bv: Optional[torch.Tensor] = None) -> None:
+    """Fused decode step: optional q/k/v biases, RoPE on q in place; rotated k and v written to
+    the caches at rows positions[s] (wgpu_engine.rs:397-432). q [Hq, S, D], k/v [Hkv, S, D],
+    caches [Hkv, max_seq, D], biases [Hq·D] / [Hkv·D] of one dtype."""
+    for t, n in ((q, "q"), (k, "k"), (v, "v")):
+        _dev(t, n)
+    if q.dim() != 3 or k.dim() != 3 or k.shape != v.shape or q.shape[1:] != k.shape[1:]:
+        raise ValueError("q must be [Hq, S, D] and k, v [Hkv, S, D]")
+    if k.dtype != q.dtype or v.dtype != q.dtype:
+        raise ValueError("q, k and v must share dtype")
+    Hq, S, D = q.shape
+    Hkv = k.shape[0]
+    flag, biases, bias_code = _rope_kv_args(Hq, Hkv, S, D, positions, kcache, vcache, bad_pos_flag, bq, bk, bv)
     layout = _lib.ROPE_INTERLEAVED if interleaved else _lib.ROPE_NEOX
     check(lib().sph_rope_kv_append(q.data_ptr(), Hq, k.data_ptr(), v.data_ptr(), Hkv, dtype_code(q.dtype), layout,
                                    positions.data_ptr(), S, D, float(base), float(pos_scale), kcache.data_ptr(),
-                                   vcache.data_ptr(), dtype_code(kcache.dtype), kcache.shape[1],
-                                   *[None if b is None else b.data_ptr() for b in biases], bias_code,
+                                   vcache.data_ptr(), dtype_code(kcache.dtype), kcache.shape[1], *biases, bias_code,
                                    None if flag is None else flag.data_ptr(), _stream(q)), "rope_kv_append")
+
+
+def rope_kv_append_tokens(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, positions: torch.Tensor, base: float,
+                          kcache: torch.Tensor, vcache: torch.Tensor, pos_scale: float = 1.0,
+                          interleaved: bool = False, bad_pos_flag: Optional[torch.Tensor] = None,
+                          bq: Optional[torch.Tensor] = None, bk: Optional[torch.Tensor] = None,
+                          bv: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """The fused step on a chunk in the projections' layout: q [S, Hq, D], k/v [S, Hkv, D] token-major
+    (read only); returns the rotated q heads-major [Hq, S, D] (wgpu_engine.rs:525-573 without the
+    transposes); k and v rows go to the caches as in rope_kv_append."""
+    for t, n in ((q, "q"), (k, "k"), (v, "v")):
+        _dev(t, n)
+    if q.dim() != 3 or k.dim() != 3 or k.shape != v.shape or q.shape[0] != k.shape[0] or q.shape[2] != k.shape[2]:
+        raise ValueError("q must be [S, Hq, D] and k, v [S, Hkv, D]")
+    if k.dtype != q.dtype or v.dtype != q.dtype:
+        raise ValueError("q, k and v must share dtype")
+    S, Hq, D = q.shape
+    Hkv = k.shape[1]
+    flag, biases, bias_code = _rope_kv_args(Hq, Hkv, S, D, positions, kcache, vcache, bad_pos_flag, bq, bk, bv)
+    q_out = _out(out, (Hq, S, D), q.dtype, q.device)
+    layout = _lib.ROPE_INTERLEAVED if interleaved else _lib.ROPE_NEOX
+    check(lib().sph_rope_kv_append_tokens(q.data_ptr(), q_out.data_ptr(), Hq, k.data_ptr(), v.data_ptr(), Hkv,
+                                          dtype_code(q.dtype), layout, positions.data_ptr(), S, D, float(base),
+                                          float(pos_scale), kcache.data_ptr(), vcache.data_ptr(),
+                                          dtype_code(kcache.dtype), kcache.shape[1], *biases, bias_code,
+                                          None if flag is None else flag.data_ptr(), _stream(q)),
+          "rope_kv_append_tokens")
+    return q_out

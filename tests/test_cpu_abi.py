@@ -66,3 +66,8 @@ def test_argument_validation_needs_no_device(built_lib):
     assert L.sph_embed(None, 8, 10, 48, None, 1, None, None, None) == E                 # 48 % 32
     assert L.sph_embed(None, 12, 10, 512, None, 0, None, None, None) == _lib.OK         # no ids
     assert L.sph_embed(None, 2, 10, 512, None, 1, None, None, None) == E                # Q4_0 unsupported
+    tok = lambda q, qo, seq: L.sph_rope_kv_append_tokens(q, qo, 2, 64, 64, 1, 0, 0, 64, seq, 64, 1e4, 1.0, 64, 64, 0,
+                                                         16, None, None, None, 0, None, None)
+    assert tok(4096, 4096, 3) == E                                                     # q_out overlaps q
+    assert tok(4096, None, 3) == E                                                     # no q_out
+    assert tok(4096, 4096, 0) == _lib.OK                                               # empty chunk

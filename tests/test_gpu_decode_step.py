@@ -163,3 +163,73 @@ def test_fused_biases_equal_add_bias_then_rope_then_append(dev, dtype, cdtype, b
     assert np.array_equal(to_np(q), to_np(q_ref)), "q"
     assert np.array_equal(to_np(kc), to_np(kc2)), "k cache"
     assert np.array_equal(to_np(vc), to_np(vc2)), "v cache"
+
+
+@pytest.mark.parametrize("dtype,cdtype,bdtype", [(torch.float32, torch.float16, None),
+                                                 (torch.float32, torch.float32, torch.float32),
+                                                 (torch.float32, torch.bfloat16, torch.float16),
+                                                 (torch.float16, torch.float16, torch.float32),
+                                                 (torch.bfloat16, torch.float32, torch.bfloat16)], ids=str)
+@pytest.mark.parametrize("interleaved", [False, True], ids=["neox", "interleaved"])
+@pytest.mark.parametrize("Hq,Hkv,S,D,pos0", [(14, 2, 512, 64, 0), (32, 8, 37, 128, 100), (4, 2, 5, 8, 3),
+                                             (14, 2, 1, 64, 40)])
+def test_token_major_variant_equals_transpose_then_fused(dev, dtype, cdtype, bdtype, interleaved, Hq, Hkv, S, D,
+                                                         pos0):
+    """sph_rope_kv_append_tokens on the projections' token-major q/k/v (the chunk step of
+    wgpu_engine.rs:525-573 with its transposes folded in) against sph_transpose_heads of q, k, v and then
+    sph_rope_kv_append: q_out, both caches and the flag bit for bit; the inputs are left unchanged."""
+    print(f"case rope_kv tokens {dtype} cache {cdtype} bias {bdtype} {'il' if interleaved else 'neox'} "
+          f"{Hq}+{Hkv}x{S}x{D} pos {pos0}", flush=True)
+    max_seq = pos0 + S + 3
+    q_tok = _gen((S, Hq, D), 21, dev, dtype)
+    k_tok = _gen((S, Hkv, D), 22, dev, dtype)
+    v_tok = _gen((S, Hkv, D), 23, dev, dtype)
+    before = [t.clone() for t in (q_tok, k_tok, v_tok)]
+    b = {} if bdtype is None else dict(bq=_gen((Hq * D,), 24, dev, bdtype), bk=_gen((Hkv * D,), 25, dev, bdtype),
+                                       bv=_gen((Hkv * D,), 26, dev, bdtype))
+    positions = torch.arange(pos0, pos0 + S, dtype=torch.int32, device=dev)
+    kc = _gen((Hkv, max_seq, D), 27, dev, cdtype)
+    vc = _gen((Hkv, max_seq, D), 28, dev, cdtype)
+    kc2, vc2 = kc.clone(), vc.clone()
+    f1 = torch.zeros(1, dtype=torch.int32, device=dev)
+    f2 = torch.zeros(1, dtype=torch.int32, device=dev)
+    q_ref = ops.transpose_heads(q_tok)
+    ops.rope_kv_append(q_ref, ops.transpose_heads(k_tok), ops.transpose_heads(v_tok), positions, 1e6, kc2, vc2,
+                       interleaved=interleaved, bad_pos_flag=f2, **b)
+    q_out = ops.rope_kv_append_tokens(q_tok, k_tok, v_tok, positions, 1e6, kc, vc, interleaved=interleaved,
+                                      bad_pos_flag=f1, **b)
+    assert q_out.shape == (Hq, S, D)
+    assert np.array_equal(to_np(q_out), to_np(q_ref)), "q"
+    assert np.array_equal(to_np(kc), to_np(kc2)), "k cache"
+    assert np.array_equal(to_np(vc), to_np(vc2)), "v cache"
+    assert f1.item() == f2.item() == 0
+    for t, t0, n in zip((q_tok, k_tok, v_tok), before, "qkv"):
+        assert torch.equal(t, t0), f"{n} is read-only"
+
+
+def test_token_major_variant_rejects_overlap_and_flags_bad_positions(dev):
+    from sapient_amd._lib import EINVAL, lib
+    S, Hq, Hkv, D, max_seq = 3, 4, 2, 64, 8
+    q = _gen((S, Hq, D), 31, dev, torch.float32)
+    k = _gen((S, Hkv, D), 32, dev, torch.float32)
+    v = _gen((S, Hkv, D), 33, dev, torch.float32)
+    kc = torch.zeros(Hkv, max_seq, D, device=dev)
+    vc = torch.zeros(Hkv, max_seq, D, device=dev)
+    pos = torch.tensor([2, 8, -1], dtype=torch.int32, device=dev)
+    s = torch.cuda.current_stream().cuda_stream
+    call = lambda qo: lib().sph_rope_kv_append_tokens(q.data_ptr(), qo, Hq, k.data_ptr(), v.data_ptr(), Hkv, 0, 0,
+                                                      pos.data_ptr(), S, D, 1e4, 1.0, kc.data_ptr(), vc.data_ptr(),
+                                                      0, max_seq, None, None, None, 0, None, s)
+    assert call(q.data_ptr()) == EINVAL                 # q_out == q
+    assert call(q.data_ptr() + 4 * D) == EINVAL         # partial overlap
+    assert call(None) == EINVAL                         # no q_out
+    flag = torch.zeros(1, dtype=torch.int32, device=dev)
+    q_out = ops.rope_kv_append_tokens(q, k, v, pos, 1e4, kc, vc, bad_pos_flag=flag)
+    torch.cuda.synchronize()
+    assert flag.item() == 1
+    q_ref = ops.transpose_heads(q)
+    ops.rope_(q_ref.unsqueeze(0), None, pos, 1e4)
+    assert torch.equal(q_out, q_ref)  # q rotates at every position
+    nz = (kc.abs().sum(dim=(0, 2)) > 0).cpu().tolist()
+    assert nz == [False, False, True, False, False, False, False, False]
+    assert (vc.abs().sum(dim=(0, 2)) > 0).cpu().tolist() == nz
