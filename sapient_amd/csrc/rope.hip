@@ -139,14 +139,85 @@ __global__ __launch_bounds__(kThreads) void rope_kv_kernel(const T* q, T* qo, in
                                                            int64_t max_seq, int32_t* bad_pos_flag, const TB* bq,
                                                            const TB* bk, const TB* bv, DenTable den) {
     __shared__ uint32_t inv_pio4[24];
-    const uint32_t* tab = stage_inv_pio4(inv_pio4);
     const int tib = threadIdx.x / lanes_per_tok;
     const int lit = threadIdx.x - tib * lanes_per_tok;
-    if (tib >= toks_per_block) return;
     const int64_t s = (int64_t)blockIdx.x * toks_per_block + tib;
-    if (s >= seq) return;
+    const bool active = tib < toks_per_block && s < seq;
     const int i0 = lit * P;
-    const int32_t ps = pos[s];
+    // Element offsets of this thread's two runs of P elements within a row.
+    const int a0 = INTERLEAVED ? 2 * i0 : i0;
+    const int a1 = INTERLEAVED ? 2 * i0 + P : i0 + half;
+    const int h_begin = blockIdx.y * heads_per_group;
+    int h_end = h_begin + heads_per_group;
+    if (h_end > nq + nkv) h_end = nq + nkv;
+
+    // Row (head h, token s) of a [heads, seq, hd] (or, TM, [seq, heads, hd]) tensor.
+    auto row_of = [&](const T* base, int heads, int h) {
+        return base + (TM ? (size_t)s * (size_t)heads + (size_t)h : (size_t)h * (size_t)seq + (size_t)s) *
+                          (size_t)head_dim;
+    };
+    // Row values with the bias of their channels added (y + b in f32, then
+    // stored in the activation type before RoPE reads it: round through T).
+    auto load_row = [&](const T* row, const TB* bias, float (&u0)[P], float (&u1)[P]) {
+        if constexpr (!INTERLEAVED) {
+            load_f32<T, P, true>(row + a0, u0);
+            load_f32<T, P, true>(row + a1, u1);
+        } else {
+            float x[2 * P];
+            load_f32<T, 2 * P, true>(row + a0, x);
+#pragma unroll
+            for (int j = 0; j < P; ++j) {
+                u0[j] = x[2 * j];
+                u1[j] = x[2 * j + 1];
+            }
+        }
+        if (bias != nullptr) {
+            float b0[P], b1[P];
+            if constexpr (!INTERLEAVED) {
+                load_f32<TB, P>(bias + a0, b0);
+                load_f32<TB, P>(bias + a1, b1);
+            } else {
+                float b[2 * P];
+                load_f32<TB, 2 * P>(bias + a0, b);
+#pragma unroll
+                for (int j = 0; j < P; ++j) {
+                    b0[j] = b[2 * j];
+                    b1[j] = b[2 * j + 1];
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < P; ++j) {
+                u0[j] = widen(narrow<T>(u0[j] + b0[j]));
+                u1[j] = widen(narrow<T>(u1[j] + b1[j]));
+            }
+        }
+    };
+
+    // The position and the first head's rows need neither the angle nor the
+    // table: they are issued before the table is staged, so the block waits
+    // on memory once instead of three times (what a one-token decode step
+    // costs is mostly these latencies).
+    int32_t ps = 0;
+    float x0[P], x1[P], v0[P], v1[P];
+    // A head's input rows: q (heads < nq), or k and v. (A macro: a lambda taking
+    // these arrays by reference left them in scratch memory for P = 1.)
+#define SPH_LOAD_HEAD(hh)                                                                         \
+    do {                                                                                          \
+        if ((hh) < nq) {                                                                          \
+            load_row(row_of(q, nq, (hh)), bq ? bq + (size_t)(hh) * head_dim : nullptr, x0, x1);   \
+        } else {                                                                                  \
+            const int h_ = (hh) - nq;                                                             \
+            load_row(row_of(k, nkv, h_), bk ? bk + (size_t)h_ * head_dim : nullptr, x0, x1);      \
+            load_row(row_of(v, nkv, h_), bv ? bv + (size_t)h_ * head_dim : nullptr, v0, v1);      \
+        }                                                                                         \
+    } while (0)
+    if (active) {
+        ps = pos[s];
+        if (h_begin < h_end) SPH_LOAD_HEAD(h_begin);
+    }
+    const uint32_t* tab = stage_inv_pio4(inv_pio4);
+    if (!active) return;
+
     const float p = (float)ps / pos_scale;
     float cs[P], sn[P];
 #pragma unroll
@@ -157,82 +228,31 @@ __global__ __launch_bounds__(kThreads) void rope_kv_kernel(const T* q, T* qo, in
     const bool pos_ok = ps >= 0 && (int64_t)ps < max_seq;
     if (!pos_ok && bad_pos_flag != nullptr && lit == 0 && blockIdx.y == 0) *bad_pos_flag = 1;
 
-    // Element offsets of this thread's two runs of P elements within a row.
-    const int a0 = INTERLEAVED ? 2 * i0 : i0;
-    const int a1 = INTERLEAVED ? 2 * i0 + P : i0 + half;
-    const int h_begin = blockIdx.y * heads_per_group;
-    int h_end = h_begin + heads_per_group;
-    if (h_end > nq + nkv) h_end = nq + nkv;
+    auto put = [&](auto* row, const float (&u0)[P], const float (&u1)[P]) {
+        using TR = typename std::remove_pointer<decltype(row)>::type;
+        if constexpr (!INTERLEAVED) {
+            store_f32<TR, P, true>(row + a0, u0);
+            store_f32<TR, P, true>(row + a1, u1);
+        } else {
+            float o[2 * P];
+#pragma unroll
+            for (int j = 0; j < P; ++j) {
+                o[2 * j] = u0[j];
+                o[2 * j + 1] = u1[j];
+            }
+            store_f32<TR, 2 * P, true>(row + a0, o);
+        }
+    };
     for (int hh = h_begin; hh < h_end; ++hh) {
         const bool is_q = hh < nq;
-        // Row (head h, token s) of a [heads, seq, hd] (or, TM, [seq, heads, hd]) tensor.
-        auto row_of = [&](const T* base, int heads, int h) {
-            return base + (TM ? (size_t)s * (size_t)heads + (size_t)h : (size_t)h * (size_t)seq + (size_t)s) *
-                              (size_t)head_dim;
-        };
-        const T* src = is_q ? row_of(q, nq, hh) : row_of(k, nkv, hh - nq);
+        if (hh != h_begin) SPH_LOAD_HEAD(hh);
         if (!is_q && !pos_ok) continue;
-        // Row values with the bias of their channels added (y + b in f32, then
-        // stored in the activation type before RoPE reads it: round through T).
-        auto load_row = [&](const T* row, const TB* bias, float (&u0)[P], float (&u1)[P]) {
-            if constexpr (!INTERLEAVED) {
-                load_f32<T, P, true>(row + a0, u0);
-                load_f32<T, P, true>(row + a1, u1);
-            } else {
-                float x[2 * P];
-                load_f32<T, 2 * P, true>(row + a0, x);
-#pragma unroll
-                for (int j = 0; j < P; ++j) {
-                    u0[j] = x[2 * j];
-                    u1[j] = x[2 * j + 1];
-                }
-            }
-            if (bias != nullptr) {
-                float b0[P], b1[P];
-                if constexpr (!INTERLEAVED) {
-                    load_f32<TB, P>(bias + a0, b0);
-                    load_f32<TB, P>(bias + a1, b1);
-                } else {
-                    float b[2 * P];
-                    load_f32<TB, 2 * P>(bias + a0, b);
-#pragma unroll
-                    for (int j = 0; j < P; ++j) {
-                        b0[j] = b[2 * j];
-                        b1[j] = b[2 * j + 1];
-                    }
-                }
-#pragma unroll
-                for (int j = 0; j < P; ++j) {
-                    u0[j] = widen(narrow<T>(u0[j] + b0[j]));
-                    u1[j] = widen(narrow<T>(u1[j] + b1[j]));
-                }
-            }
-        };
-        const TB* bias = is_q ? (bq ? bq + (size_t)hh * head_dim : nullptr)
-                              : (bk ? bk + (size_t)(hh - nq) * head_dim : nullptr);
-        float x0[P], x1[P];
-        load_row(src, bias, x0, x1);
         float o0[P], o1[P];
 #pragma unroll
         for (int j = 0; j < P; ++j) {
             o0[j] = x0[j] * cs[j] - x1[j] * sn[j];
             o1[j] = x1[j] * cs[j] + x0[j] * sn[j];
         }
-        auto put = [&](auto* row, const float (&u0)[P], const float (&u1)[P]) {
-            using TR = typename std::remove_pointer<decltype(row)>::type;
-            if constexpr (!INTERLEAVED) {
-                store_f32<TR, P, true>(row + a0, u0);
-                store_f32<TR, P, true>(row + a1, u1);
-            } else {
-                float o[2 * P];
-#pragma unroll
-                for (int j = 0; j < P; ++j) {
-                    o[2 * j] = u0[j];
-                    o[2 * j + 1] = u1[j];
-                }
-                store_f32<TR, 2 * P, true>(row + a0, o);
-            }
-        };
         if (is_q) {
             put(qo + ((size_t)hh * (size_t)seq + (size_t)s) * (size_t)head_dim, o0, o1);
         } else {
@@ -247,13 +267,10 @@ __global__ __launch_bounds__(kThreads) void rope_kv_kernel(const T* q, T* qo, in
                 }
             }
             put(kc + crow, o0, o1);
-            // v: the same channels, moved unrotated.
-            const T* vrow = row_of(v, nkv, hh - nq);
-            float v0[P], v1[P];
-            load_row(vrow, bv ? bv + (size_t)(hh - nq) * head_dim : nullptr, v0, v1);
-            put(vc + crow, v0, v1);
+            put(vc + crow, v0, v1);  // v: the same channels, moved unrotated
         }
     }
+#undef SPH_LOAD_HEAD
 }
 
 // Blocks to aim for in total (head groups × token blocks). Each head group
