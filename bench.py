@@ -261,6 +261,22 @@ def op_table(torch, ops, dev, only=None):
             lambda: [torch.empty(n_ids, hidden, device=dev) for _ in range(2)],
             lambda o, ids=ids: ops.embed(table, L.Q4_K, vocab, hidden, ids, out=o))
     del table
+    # The other GGUF table formats at the same shape and uniform ids (f1 and the data formats around C5)
+    ids = torch.from_numpy(rng.integers(0, vocab, n_ids).astype(np.int32)).to(dev)
+    for dt, name, block, nbytes, d_off in ((L.Q8_0, "q8_0", 32, 34, 0), (L.Q4_0, "q4_0", 32, 18, 0),
+                                           (L.Q5_K, "q5_k", 256, 176, 0), (L.Q6_K, "q6_k", 256, 210, 208)):
+        nb = vocab * hidden // block
+        table = torch.randint(0, 256, (nb, nbytes), generator=g, device=dev, dtype=torch.int32).to(torch.uint8)
+        nd = 2 if dt == L.Q5_K else 1  # d (and dmin) as f16 in [0.0005, 0.02)
+        dd = (torch.rand((nb, nd), generator=g, device=dev) * (0.02 - 0.0005) + 0.0005).to(f16)
+        table[:, d_off:d_off + 2 * nd] = dd.view(torch.uint8).view(nb, 2 * nd)
+        table = table.reshape(-1)
+        row_bytes = hidden // block * nbytes
+        run(f"embed_{name} uniform", f"{vocab}x{hidden} -> {n_ids} ids", f"{name}->f32",
+            n_ids * (row_bytes + 4 + hidden * 4), n_ids, "rows",
+            lambda: [torch.empty(n_ids, hidden, device=dev) for _ in range(2)],
+            lambda o, table=table, dt=dt: ops.embed(table, dt, vocab, hidden, ids, out=o))
+        del table
     # C1: Qwen2.5-0.5B layer ops (latency-bound, reported only)
     H = 896
     for T1 in (1, 512):

@@ -42,8 +42,10 @@ extern "C" {
  * (crates/sapient-io/src/gguf.rs:90-104), so a caller can pass them through. */
 #define SPH_F32 0
 #define SPH_F16 1
+#define SPH_Q4_0 2
 #define SPH_Q8_0 8
 #define SPH_Q4_K 12
+#define SPH_Q5_K 13
 #define SPH_Q6_K 14
 #define SPH_BF16 30
 
@@ -198,8 +200,10 @@ int sph_rope_kv_append_tokens(const void* q, void* q_out, int64_t n_q_heads, con
  * data, rows of byte_count(hidden) bytes, consumed verbatim (no repacking).
  * Replaces common::embed_tokens (crates/sapient-models/src/forward/common.rs:164-217)
  * and WgpuContext::embed / embed_q8_0 / embed_q4_k (resident.rs:714,
- * quant.rs:445, quant.rs:273). table_dtype ∈ {F32, F16, BF16, Q8_0, Q4_K, Q6_K};
- * hidden a multiple of the block width (32 for Q8_0, 256 for K-quants).
+ * quant.rs:445, quant.rs:273). table_dtype ∈ {F32, F16, BF16, Q4_0, Q8_0, Q4_K,
+ * Q5_K, Q6_K} — every type gather_row_f32 accepts (common.rs:186-214; the
+ * row-interleaved R4 repacks are refused there too);
+ * hidden a multiple of the block width (32 for Q4_0 / Q8_0, 256 for K-quants).
  * ids: device uint32[n_ids]. An id >= vocab never reads the table: its
  * output row is zero-filled and, if `bad_id_flag` (device int32) is not NULL,
  * 1 is stored there. Callers holding the ids on the host validate them first,

@@ -24,7 +24,10 @@
 namespace sapient_hip {
 
 // Tensor dtypes of the op set (values are GGUF type ids, as in sapient_hip.h).
-enum class DType : int { F32 = SPH_F32, F16 = SPH_F16, BF16 = SPH_BF16, Q8_0 = SPH_Q8_0, Q4_K = SPH_Q4_K, Q6_K = SPH_Q6_K };
+enum class DType : int {
+    F32 = SPH_F32, F16 = SPH_F16, BF16 = SPH_BF16, Q4_0 = SPH_Q4_0, Q8_0 = SPH_Q8_0, Q4_K = SPH_Q4_K, Q5_K = SPH_Q5_K,
+    Q6_K = SPH_Q6_K
+};
 
 const char* dtype_name(DType dt);
 bool is_quantized(DType dt);

@@ -18,7 +18,7 @@ HERE = Path(__file__).resolve().parent
 LIB_PATH = HERE / "liboracle.so"
 
 # GGUF tensor type ids (crates/sapient-io/src/gguf.rs:90-104)
-F32, F16, Q8_0, Q4_K, Q6_K, BF16 = 0, 1, 8, 12, 14, 30
+F32, F16, Q4_0, Q8_0, Q4_K, Q5_K, Q6_K, BF16 = 0, 1, 2, 8, 12, 13, 14, 30
 OK, EINVAL, ERANGE = 0, -1, -3
 
 _lib = None
@@ -56,8 +56,10 @@ def lib() -> C.CDLL:
             "sor_apply_rope_partial_scaled": (C.c_int, [vp, vp, sz, sz, sz, sz, vp, sz, fl, sz, fl]),
             "sor_apply_rope_interleaved": (C.c_int, [vp, vp, sz, sz, sz, sz, vp, sz, fl, sz, fl]),
             "sor_unpermute_qk_rows": (C.c_int, [vp, vp, sz, sz, sz]),
+            "sor_dequant_q4_0": (None, [vp, sz, vp]),
             "sor_dequant_q8_0": (None, [vp, sz, vp]),
             "sor_dequant_q4_k": (None, [vp, sz, vp]),
+            "sor_dequant_q5_k": (None, [vp, sz, vp]),
             "sor_dequant_q6_k": (None, [vp, sz, vp]),
             "sor_row_bytes": (sz, [C.c_int, sz]),
             "sor_embed_tokens": (C.c_int, [vp, C.c_int, sz, sz, vp, sz, vp]),
@@ -251,11 +253,11 @@ def row_bytes(dtype: int, hidden: int) -> int:
 
 
 def dequant(blocks: np.ndarray, dtype: int, numel: int) -> np.ndarray:
-    """Tensor::to_f32_vec for a quantized tensor of `numel` elements (tensor.rs:378-398,468-476)."""
+    """Tensor::to_f32_vec for a quantized tensor of `numel` elements (tensor.rs:362-398, 421-476)."""
     b = np.ascontiguousarray(blocks, dtype=np.uint8)
     out = np.empty(numel, np.float32)
-    fn = {Q8_0: (lib().sor_dequant_q8_0, 32), Q4_K: (lib().sor_dequant_q4_k, 256),
-          Q6_K: (lib().sor_dequant_q6_k, 256)}[dtype]
+    fn = {Q4_0: (lib().sor_dequant_q4_0, 32), Q8_0: (lib().sor_dequant_q8_0, 32), Q4_K: (lib().sor_dequant_q4_k, 256),
+          Q5_K: (lib().sor_dequant_q5_k, 256), Q6_K: (lib().sor_dequant_q6_k, 256)}[dtype]
     fn[0](_p(b), numel // fn[1], _p(out))
     return out
 

@@ -27,7 +27,7 @@
 #define SOR_ERANGE (-3)
 
 /* Table dtypes for the embedding gather: GGUF type ids (crates/sapient-io/src/gguf.rs:90-104). */
-enum { SOR_F32 = 0, SOR_F16 = 1, SOR_Q8_0 = 8, SOR_Q4_K = 12, SOR_Q6_K = 14, SOR_BF16 = 30 };
+enum { SOR_F32 = 0, SOR_F16 = 1, SOR_Q4_0 = 2, SOR_Q8_0 = 8, SOR_Q4_K = 12, SOR_Q5_K = 13, SOR_Q6_K = 14, SOR_BF16 = 30 };
 
 static inline uint32_t f2u(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
 static inline float u2f(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
@@ -345,12 +345,30 @@ int sor_unpermute_qk_rows(const uint8_t* src, uint8_t* dst, size_t n_head, size_
 /* ─────────────────────── a7: GGUF block dequantization ───────────────────────
  * Block constants: crates/sapient-core/src/dtype.rs:57-69; byte_count :136-145. */
 #define QK 32
+#define Q4_0_BYTES 18
 #define Q8_0_BYTES 34
 #define QK_K 256
 #define Q4_K_BYTES 144
+#define Q5_K_BYTES 176
 #define Q6_K_BYTES 210
 
 static inline float le_f16(const uint8_t* p) { return sor_f16_to_f32((uint16_t)(p[0] | (p[1] << 8))); }
+
+/* tensor.rs:362-376: byte j of the 16 after d holds element j (low nibble)
+ * and element j + 16 (high nibble), each minus 8, times d. */
+void sor_dequant_q4_0(const uint8_t* bytes, size_t nblocks, float* out) {
+    for (size_t b = 0; b < nblocks; b++) {
+        const uint8_t* blk = bytes + b * Q4_0_BYTES;
+        float d = le_f16(blk);
+        for (size_t j = 0; j < QK / 2; j++) {
+            uint8_t byte = blk[2 + j];
+            int32_t lo = (int32_t)(byte & 0x0f) - 8;
+            int32_t hi = (int32_t)(byte >> 4) - 8;
+            out[b * QK + j] = (float)lo * d;
+            out[b * QK + j + QK / 2] = (float)hi * d;
+        }
+    }
+}
 
 /* tensor.rs:378-389: out[32b + j] = (block[2 + j] as i8) as f32 * d. */
 void sor_dequant_q8_0(const uint8_t* bytes, size_t nblocks, float* out) {
@@ -398,6 +416,48 @@ void sor_dequant_q4_k(const uint8_t* bytes, size_t nblocks, float* out) {
     }
 }
 
+/* tensor.rs:421-467: as Q4_K, plus a fifth bit per element from qh[l] —
+ * bit-plane u1 = 1 << 2k for the low nibbles of 64-element chunk k, u2 =
+ * 2 << 2k for the high nibbles (the per-element reading the reference
+ * adopted; crates/sapient-io/src/gguf.rs:391-434 still reads one qh byte per
+ * chunk, but that copy is not on the embedding path, which keeps Q5_K tables
+ * as blocks, gguf.rs:160-169, :658-661). */
+void sor_dequant_q5_k(const uint8_t* bytes, size_t nblocks, float* out) {
+    for (size_t b = 0; b < nblocks; b++) {
+        const uint8_t* blk = bytes + b * Q5_K_BYTES;
+        float d = le_f16(blk), dmin = le_f16(blk + 2);
+        const uint8_t* scales = blk + 4;
+        const uint8_t* qh = blk + 16;
+        const uint8_t* ql = blk + 48;
+        float* o = out + b * QK_K;
+        size_t out_idx = 0, ql_off = 0, is = 0;
+        uint8_t u1 = 1, u2 = 2;
+        for (int k = 0; k < QK_K / 64; k++) {
+            uint8_t sc1, m1, sc2, m2;
+            scale_min_k4(is, scales, &sc1, &m1);
+            float d1 = d * (float)sc1, m1v = dmin * (float)m1;
+            scale_min_k4(is + 1, scales, &sc2, &m2);
+            float d2 = d * (float)sc2, m2v = dmin * (float)m2;
+            for (size_t l = 0; l < 32; l++) {
+                float hi = (qh[l] & u1) ? 16.0f : 0.0f;
+                o[out_idx + l] = d1 * ((float)(ql[ql_off + l] & 0x0F) + hi) - m1v;
+                float hi2 = (qh[l] & u2) ? 16.0f : 0.0f;
+                o[out_idx + l + 32] = d2 * ((float)(ql[ql_off + l] >> 4) + hi2) - m2v;
+            }
+            out_idx += 64;
+            ql_off += 32;
+            is += 2;
+            if (is % 8 == 0) {
+                u1 = 1;
+                u2 = 2;
+            } else {
+                u1 = (uint8_t)(u1 << 2);
+                u2 = (uint8_t)(u2 << 2);
+            }
+        }
+    }
+}
+
 /* tensor.rs:468-476 → dequant_q6_k_block :534-565 (next-row dtype). */
 void sor_dequant_q6_k(const uint8_t* bytes, size_t nblocks, float* out) {
     for (size_t b = 0; b < nblocks; b++) {
@@ -435,8 +495,10 @@ size_t sor_row_bytes(int dtype, size_t hidden) {
     case SOR_F32: return hidden * 4;
     case SOR_F16:
     case SOR_BF16: return hidden * 2;
+    case SOR_Q4_0: return hidden % QK ? 0 : hidden / QK * Q4_0_BYTES;
     case SOR_Q8_0: return hidden % QK ? 0 : hidden / QK * Q8_0_BYTES;
     case SOR_Q4_K: return hidden % QK_K ? 0 : hidden / QK_K * Q4_K_BYTES;
+    case SOR_Q5_K: return hidden % QK_K ? 0 : hidden / QK_K * Q5_K_BYTES;
     case SOR_Q6_K: return hidden % QK_K ? 0 : hidden / QK_K * Q6_K_BYTES;
     default: return 0;
     }
@@ -462,8 +524,10 @@ int sor_embed_tokens(const uint8_t* table, int dtype, size_t vocab, size_t hidde
         case SOR_BF16:
             for (size_t i = 0; i < hidden; i++) dst[i] = sor_bf16_to_f32((uint16_t)(row[2 * i] | (row[2 * i + 1] << 8)));
             break;
+        case SOR_Q4_0: sor_dequant_q4_0(row, hidden / QK, dst); break;
         case SOR_Q8_0: sor_dequant_q8_0(row, hidden / QK, dst); break;
         case SOR_Q4_K: sor_dequant_q4_k(row, hidden / QK_K, dst); break;
+        case SOR_Q5_K: sor_dequant_q5_k(row, hidden / QK_K, dst); break;
         case SOR_Q6_K: sor_dequant_q6_k(row, hidden / QK_K, dst); break;
         }
     }

@@ -2,16 +2,21 @@
 //
 // Reference: common::embed_tokens → gather_row_f32
 // (crates/sapient-models/src/forward/common.rs:164-217) and the dequant arms of
-// Tensor::to_f32_vec (crates/sapient-core/src/tensor.rs:378-398, Q4_K
-// :504-527 with get_scale_min_k4 :567-576, Q6_K :534-565):
+// Tensor::to_f32_vec (crates/sapient-core/src/tensor.rs:362-398, Q4_K
+// :504-527 with get_scale_min_k4 :567-576, Q5_K :421-467, Q6_K :534-565):
+//   Q4_0 (18-byte block of 32): y = f32(q − 8) · f32(d), q the low nibbles of
+//        bytes 0..15 for elements 0..15 and their high nibbles for 16..31
 //   Q8_0 (34-byte block of 32): y = f32(i8 q) · f32(d)
 //   Q4_K (144-byte block of 256): y = (d·sc)·q − dmin·m, 6-bit (sc, m) unpacked per
 //        32-element sub-block, low nibbles then high nibbles per 64 elements
+//   Q5_K (176-byte block of 256): as Q4_K with q + 16·h, h one bit per element
+//        from the 32-byte qh plane (bit 2c of qh[l] for the low-nibble half of
+//        64-element chunk c, bit 2c + 1 for the high-nibble half)
 //   Q6_K (210-byte block of 256): y = (d·sc)·(q − 32)
-// Every product above is exact in f32 (≤ 21 significant bits) except Q6_K's
-// last one, which is rounded in the reference's order; Q4_K's single rounding
-// is the final subtraction, which one FMA performs identically (d·sc·q is
-// exact). The gather is therefore bit-exact.
+// Every product above is exact in f32 (≤ 22 significant bits) except Q6_K's
+// last one, which is rounded in the reference's order; the K-quants' single
+// rounding is the final subtraction, which one FMA performs identically
+// (d·sc·q is exact). The gather is therefore bit-exact.
 //
 // Design (write-dominated: 16 KiB of f32 out per 2.3 KiB Q4_K row in):
 //  - One wave64 per token, 16 tokens per 1024-thread block; each lane produces
@@ -23,8 +28,10 @@
 //    12 scale bytes; wave-uniform, so a scalar load) and the dword of nibbles
 //    it needs, and unpacks its (sc, m) pair in registers. A row's loads are
 //    all issued before the first is consumed (16 super-blocks per batch).
-//  - Q8_0 / Q6_K blocks are 2-byte aligned only (34 / 210 bytes), so lanes read
-//    them in 16-bit pieces.
+//  - Q4_0 / Q8_0 / Q6_K blocks are 2-byte aligned only (18 / 34 / 210 bytes),
+//    so lanes read them in 16-bit pieces; Q5_K blocks (176 bytes) stay
+//    16-byte aligned, so a lane reads its header, nibble dword and high-bit
+//    dword whole.
 //  - An id >= vocab zero-fills its row and raises `bad_id_flag`; the table is
 //    never read out of bounds.
 #include "sph_common.h"
@@ -85,6 +92,59 @@ __device__ __forceinline__ void dequant4<SPH_Q8_0>(const uint8_t* __restrict__ r
 }
 
 template <>
+__device__ __forceinline__ void dequant4<SPH_Q4_0>(const uint8_t* __restrict__ row, int e4, float (&o)[4]) {
+    const int blk = e4 >> 3;            // 8 groups of 4 per 32-element block
+    const int j = (e4 & 7) * 4;         // first element of the group
+    const uint8_t* b = row + blk * 18;
+    const float d = f16_at(b);
+    const uint16_t* q = reinterpret_cast<const uint16_t*>(b + 2 + (j & 15));  // 2-byte aligned
+    const uint32_t w = (uint32_t)q[0] | ((uint32_t)q[1] << 16);
+    const int sh = j >= 16 ? 4 : 0;     // elements 16..31 are the high nibbles
+#pragma unroll
+    for (int c = 0; c < 4; ++c) o[c] = (float)((int)((w >> (8 * c + sh)) & 0xF) - 8) * d;
+}
+
+// 6-bit (sc, m) of sub-block sb (0..7) from the 12 scale bytes of a K-quant
+// header whose dwords 1..3 are s0, s1, s2 (get_scale_min_k4, tensor.rs:567-576).
+__device__ __forceinline__ void scale_min_k4(uint32_t s0, uint32_t s1, uint32_t s2, int sb, uint32_t& sc,
+                                             uint32_t& m) {
+    const int sh = 8 * (sb & 3);
+    const uint32_t A = (s0 >> sh) & 0xFF;  // scales[sb & 3]
+    const uint32_t B = (s1 >> sh) & 0xFF;  // scales[(sb & 3) + 4]
+    const uint32_t C = (s2 >> sh) & 0xFF;  // scales[(sb & 3) + 8]
+    if (sb < 4) {
+        sc = A & 63;
+        m = B & 63;
+    } else {
+        sc = (C & 0x0F) | ((A >> 6) << 4);
+        m = (C >> 4) | ((B >> 6) << 4);
+    }
+}
+
+template <>
+__device__ __forceinline__ void dequant4<SPH_Q5_K>(const uint8_t* __restrict__ row, int e4, float (&o)[4]) {
+    const int blk = e4 >> 6;            // 64 groups of 4 per 256-element super-block
+    const int e = (e4 & 63) * 4;        // element within the super-block
+    const int c = e >> 6;               // 64-element chunk 0..3
+    const int hi = (e >> 5) & 1;        // 0: low nibbles, 1: high nibbles of the chunk's 32 bytes
+    const int l = e & 31;               // 4 consecutive l
+    const uint8_t* b = row + blk * 176;  // 16-byte aligned
+    const u32x4 hdr = *reinterpret_cast<const u32x4*>(b);
+    const uint32_t qh = *reinterpret_cast<const uint32_t*>(b + 16 + l);
+    const uint32_t ql = *reinterpret_cast<const uint32_t*>(b + 48 + 32 * c + l);
+    uint32_t sc, m;
+    scale_min_k4(hdr.y, hdr.z, hdr.w, 2 * c + hi, sc, m);
+    const float d1 = widen(f16{(uint16_t)hdr.x}) * (float)sc;
+    const float m1 = widen(f16{(uint16_t)(hdr.x >> 16)}) * (float)m;
+    const int plane = 2 * c + hi;       // the qh bit of this half-chunk
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const uint32_t q = ((ql >> (8 * k + 4 * hi)) & 0xF) | (((qh >> (8 * k + plane)) & 1u) << 4);
+        o[k] = __builtin_fmaf(d1, (float)q, -m1);
+    }
+}
+
+template <>
 __device__ __forceinline__ void dequant4<SPH_Q6_K>(const uint8_t* __restrict__ row, int e4, float (&o)[4]) {
     const int blk = e4 >> 6;            // 64 groups of 4 per 256-element super-block
     const int e = (e4 & 63) * 4;        // element within the super-block
@@ -115,18 +175,8 @@ __device__ __forceinline__ void dequant_q4k_lane(const u32x4 hdr, uint32_t qw, i
     const int sb = lane >> 3;            // 32-element sub-block 0..7
     const float d = widen(f16{(uint16_t)hdr.x});
     const float dmin = widen(f16{(uint16_t)(hdr.x >> 16)});
-    const int k = sb & 3, sh = 8 * k;
-    const uint32_t A = (hdr.y >> sh) & 0xFF;  // scales[k]
-    const uint32_t B = (hdr.z >> sh) & 0xFF;  // scales[k + 4]
-    const uint32_t C = (hdr.w >> sh) & 0xFF;  // scales[k + 8]
     uint32_t sc, m;
-    if (sb < 4) {
-        sc = A & 63;
-        m = B & 63;
-    } else {
-        sc = (C & 0x0F) | ((A >> 6) << 4);
-        m = (C >> 4) | ((B >> 6) << 4);
-    }
+    scale_min_k4(hdr.y, hdr.z, hdr.w, sb, sc, m);
     const float d1 = d * (float)sc;
     const float m1 = dmin * (float)m;
     const uint32_t nib = (sb & 1) ? (qw >> 4) & 0x0F0F0F0Fu : qw & 0x0F0F0F0Fu;
@@ -217,8 +267,10 @@ extern "C" int sph_embed(const void* table, int table_dtype, int64_t vocab, int6
     case SPH_F32: row_bytes = hidden * 4; if (hidden % 4) return SPH_EINVAL; break;
     case SPH_F16:
     case SPH_BF16: row_bytes = hidden * 2; align = 8; if (hidden % 4) return SPH_EINVAL; break;
+    case SPH_Q4_0: if (hidden % 32) return SPH_EINVAL; row_bytes = hidden / 32 * 18; align = 2; break;
     case SPH_Q8_0: if (hidden % 32) return SPH_EINVAL; row_bytes = hidden / 32 * 34; align = 2; break;
     case SPH_Q4_K: if (hidden % 256) return SPH_EINVAL; row_bytes = hidden / 256 * 144; break;
+    case SPH_Q5_K: if (hidden % 256) return SPH_EINVAL; row_bytes = hidden / 256 * 176; break;
     case SPH_Q6_K: if (hidden % 256) return SPH_EINVAL; row_bytes = hidden / 256 * 210; align = 2; break;
     default: return SPH_EINVAL;
     }
@@ -230,8 +282,10 @@ extern "C" int sph_embed(const void* table, int table_dtype, int64_t vocab, int6
     case SPH_F32: return launch_embed<SPH_F32>(table, vocab, hidden, row_bytes, ids, n_ids, out, bad_id_flag, s);
     case SPH_F16: return launch_embed<SPH_F16>(table, vocab, hidden, row_bytes, ids, n_ids, out, bad_id_flag, s);
     case SPH_BF16: return launch_embed<SPH_BF16>(table, vocab, hidden, row_bytes, ids, n_ids, out, bad_id_flag, s);
+    case SPH_Q4_0: return launch_embed<SPH_Q4_0>(table, vocab, hidden, row_bytes, ids, n_ids, out, bad_id_flag, s);
     case SPH_Q8_0: return launch_embed<SPH_Q8_0>(table, vocab, hidden, row_bytes, ids, n_ids, out, bad_id_flag, s);
     case SPH_Q4_K: return launch_embed<SPH_Q4_K>(table, vocab, hidden, row_bytes, ids, n_ids, out, bad_id_flag, s);
+    case SPH_Q5_K: return launch_embed<SPH_Q5_K>(table, vocab, hidden, row_bytes, ids, n_ids, out, bad_id_flag, s);
     case SPH_Q6_K: return launch_embed<SPH_Q6_K>(table, vocab, hidden, row_bytes, ids, n_ids, out, bad_id_flag, s);
     }
     return SPH_EINVAL;

@@ -27,22 +27,28 @@ const char* dtype_name(DType dt) {
     case DType::F32: return "f32";
     case DType::F16: return "f16";
     case DType::BF16: return "bf16";
+    case DType::Q4_0: return "q4_0";
     case DType::Q8_0: return "q8_0";
     case DType::Q4_K: return "q4_k";
+    case DType::Q5_K: return "q5_k";
     case DType::Q6_K: return "q6_k";
     }
     return "?";
 }
 
-bool is_quantized(DType dt) { return dt == DType::Q8_0 || dt == DType::Q4_K || dt == DType::Q6_K; }
+bool is_quantized(DType dt) {
+    return dt == DType::Q4_0 || dt == DType::Q8_0 || dt == DType::Q4_K || dt == DType::Q5_K || dt == DType::Q6_K;
+}
 
 size_t byte_count(DType dt, size_t numel) {
     switch (dt) {
     case DType::F32: return numel * 4;
     case DType::F16:
     case DType::BF16: return numel * 2;
+    case DType::Q4_0: return numel / 32 * 18;
     case DType::Q8_0: return numel / 32 * 34;
     case DType::Q4_K: return numel / 256 * 144;
+    case DType::Q5_K: return numel / 256 * 176;
     case DType::Q6_K: return numel / 256 * 210;
     }
     return 0;
@@ -88,7 +94,7 @@ Tensor Tensor::from_bf16_bytes(std::vector<uint8_t> bytes, std::vector<size_t> s
 
 Tensor Tensor::from_quant_bytes(std::vector<uint8_t> bytes, std::vector<size_t> shape, DType dt) {
     if (!is_quantized(dt))
-        throw Error(std::string("type mismatch: expected a quantized dtype (Q8_0, Q4_K, Q6_K), got ") + dtype_name(dt));
+        throw Error(std::string("type mismatch: expected a quantized dtype (Q4_0, Q8_0, Q4_K, Q5_K, Q6_K), got ") + dtype_name(dt));
     const size_t expected = byte_count(dt, product(shape));
     if (bytes.size() != expected)
         throw Error("shape mismatch: expected " + std::to_string(expected) + " bytes, got " + std::to_string(bytes.size()));

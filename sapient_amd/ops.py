@@ -218,8 +218,8 @@ def rope_(q: torch.Tensor, k: Optional[torch.Tensor], positions: torch.Tensor, b
 
 # Bytes per row as (bytes per block, elements per block) of each table type
 # (crates/sapient-core/src/dtype.rs:136-145).
-_ROW_BYTES = {_lib.F32: (4, 1), _lib.F16: (2, 1), _lib.BF16: (2, 1), _lib.Q8_0: (34, 32), _lib.Q4_K: (144, 256),
-              _lib.Q6_K: (210, 256)}
+_ROW_BYTES = {_lib.F32: (4, 1), _lib.F16: (2, 1), _lib.BF16: (2, 1), _lib.Q4_0: (18, 32), _lib.Q8_0: (34, 32),
+              _lib.Q4_K: (144, 256), _lib.Q5_K: (176, 256), _lib.Q6_K: (210, 256)}
 
 
 def embed(table: torch.Tensor, table_dtype: int, vocab: int, hidden: int, ids: torch.Tensor,

@@ -65,7 +65,9 @@ def test_argument_validation_needs_no_device(built_lib):
     assert L.sph_rope(None, 1, None, 0, 0, 5, None, 1, 1, 8, 8, 1e4, 1.0, None) == E    # layout
     assert L.sph_embed(None, 8, 10, 48, None, 1, None, None, None) == E                 # 48 % 32
     assert L.sph_embed(None, 12, 10, 512, None, 0, None, None, None) == _lib.OK         # no ids
-    assert L.sph_embed(None, 2, 10, 512, None, 1, None, None, None) == E                # Q4_0 unsupported
+    assert L.sph_embed(None, 3, 10, 512, None, 1, None, None, None) == E                # Q4_1: not a table type
+    assert L.sph_embed(None, 2, 10, 48, None, 1, None, None, None) == E                 # Q4_0: 48 % 32
+    assert L.sph_embed(None, 13, 10, 512, None, 0, None, None, None) == _lib.OK         # Q5_K, no ids
     tok = lambda q, qo, seq: L.sph_rope_kv_append_tokens(q, qo, 2, 64, 64, 1, 0, 0, 64, seq, 64, 1e4, 1.0, 64, 64, 0,
                                                          16, None, None, None, 0, None, None)
     assert tok(4096, 4096, 3) == E                                                     # q_out overlaps q

@@ -1,9 +1,9 @@
 """GPU parity: token-embedding gather with GGUF row dequantization — bit-exact.
 
 Reference: crates/sapient-models/src/forward/common.rs:164-217 (embed_tokens /
-gather_row_f32), crates/sapient-core/src/tensor.rs:378-398, :504-527, :534-576
-(Q8_0 / Q4_K / Q6_K dequant). Every dequantized value must equal the oracle's
-bits (NaN table entries: NaN-ness only).
+gather_row_f32), crates/sapient-core/src/tensor.rs:362-398, :421-467, :504-527,
+:534-576 (Q4_0 / Q8_0 / Q4_K / Q5_K / Q6_K dequant). Every dequantized value
+must equal the oracle's bits (NaN table entries: NaN-ness only).
 """
 import numpy as np
 import pytest
@@ -14,7 +14,7 @@ from refvec import (WgpuLcg, f16_bits, gather_test_values, quantize_q8_0_blocks,
                     random_q6_k_blocks)
 
 import sapient_amd.ops as ops
-from sapient_amd._lib import BF16, F16, F32, Q4_K, Q6_K, Q8_0
+from sapient_amd._lib import BF16, F16, F32, Q4_0, Q4_K, Q5_K, Q6_K, Q8_0
 
 pytestmark = pytest.mark.gpu
 
@@ -107,6 +107,83 @@ def test_embed_q4_k_both_scale_branches_and_subnormal_scales(dev, orc):
     assert_bits_equal(got, orc.embed_tokens(blocks, Q4_K, vocab, dim, ids), "q4_k hand-built")
 
 
+def _k_quant_headers(blocks: np.ndarray, dvals: np.ndarray) -> None:
+    """d and dmin cycling through subnormal, tiny, one, large and negative f16 values; scale bytes that
+    hit both get_scale_min_k4 branches with every high-bit combination."""
+    nb = blocks.shape[0]
+    for b in range(nb):
+        blocks[b, 0:2] = np.array([dvals[b % len(dvals)]], np.uint16).view(np.uint8)
+        blocks[b, 2:4] = np.array([dvals[(b + 3) % len(dvals)]], np.uint16).view(np.uint8)
+        blocks[b, 4:16] = (np.arange(12) * 21 + b * 7) % 256
+
+
+def test_embed_q5_k_bit_planes_scale_branches_and_reference_kat(dev, orc):
+    """Q5_K (tensor.rs:421-467): random nibbles and high-bit planes under hand-built headers; the reference's
+    KAT block (tensor.rs:800-830); and one qh bit at a time, which must move exactly one element."""
+    rng = np.random.default_rng(6)
+    nb = 64
+    blocks = rng.integers(0, 256, (nb, 176), dtype=np.uint8)
+    _k_quant_headers(blocks, np.array([0x0001, 0x03FF, 0x0400, 0x3C00, 0x7BFF, 0x1234, 0x8400], np.uint16))
+    vocab, dim = nb // 4, 1024
+    ids = list(range(vocab))[::-1]
+    print("case embed q5_k hand-built", flush=True)
+    got = _gather(dev, blocks, Q5_K, vocab, dim, ids)
+    assert_bits_equal(got, orc.embed_tokens(blocks, Q5_K, vocab, dim, ids), "q5_k hand-built")
+    # 256 one-bit blocks: block 8l + p sets bit p of qh[l] (d = 1, sc = 1, m = 0)
+    planes = np.zeros((256, 176), np.uint8)
+    planes[:, 0:2] = np.array([np.float16(1.0)]).view(np.uint8)
+    planes[:, 4:8], planes[:, 12:16] = 1, 1
+    for l in range(32):
+        for p in range(8):
+            planes[8 * l + p, 16 + l] = 1 << p
+    got = _gather(dev, planes, Q5_K, 256, 256, list(range(256)))
+    want = np.zeros((256, 256), np.float32)
+    for l in range(32):
+        for p in range(8):
+            want[8 * l + p, 64 * (p // 2) + 32 * (p % 2) + l] = 16.0
+    assert_bits_equal(got, want, "q5_k bit planes")
+    kat = np.zeros(176, np.uint8)
+    kat[0:2] = np.array([np.float16(1.0)]).view(np.uint8)
+    kat[4:8], kat[12:16], kat[16 + 5], kat[16 + 0], kat[48 + 3] = 1, 1, 0b1, 0b100, 0x02
+    y = _gather(dev, kat, Q5_K, 1, 256, [0]).reshape(-1)
+    assert y[3] == 2.0 and y[5] == 16.0 and y[64] == 16.0 and np.count_nonzero(y) == 3
+
+
+def test_embed_q4_0_every_byte_at_every_position(dev, orc):
+    """Q4_0 (tensor.rs:362-376, the ggml split nibble order): all 256 byte values at each of the 16 byte
+    positions under six scales (subnormal, one, negative, largest)."""
+    blocks = []
+    for dv in np.array([0x0001, 0x03FF, 0x3C00, 0xBC00, 0x7BFF, 0x2E66], np.uint16):
+        for j in range(16):
+            b = np.zeros((256, 18), np.uint8)
+            b[:, 0:2] = np.array([dv], np.uint16).view(np.uint8)
+            b[:, 2:] = np.random.default_rng(int(dv) + j).integers(0, 256, (256, 16), dtype=np.uint8)
+            b[:, 2 + j] = np.arange(256, dtype=np.uint32).astype(np.uint8)
+            blocks.append(b)
+    blocks = np.concatenate(blocks)                       # 24576 blocks: vocab 3072 x hidden 256
+    vocab, hidden = blocks.shape[0] * 32 // 256, 256
+    ids = np.random.default_rng(7).permutation(vocab)
+    print("case embed q4_0 every byte", flush=True)
+    got = _gather(dev, blocks, Q4_0, vocab, hidden, ids)
+    assert_bits_equal(got, orc.embed_tokens(blocks, Q4_0, vocab, hidden, ids), "q4_0")
+
+
+@pytest.mark.parametrize("dt,block,nbytes", [(Q4_0, 32, 18), (Q5_K, 256, 176)], ids=["q4_0", "q5_k"])
+def test_embed_new_formats_model_shape(dev, orc, dt, block, nbytes):
+    """A Llama-3.2-1B-shaped table (vocab 128256 x 2048) with 8192 uniform ids — the whole gather bit-exact."""
+    vocab, hidden, n = 128256, 2048, 8192
+    rng = np.random.default_rng(8)
+    nb = vocab * hidden // block
+    table = rng.integers(0, 256, (nb, nbytes), dtype=np.uint8)
+    hdr = 4 if dt == Q5_K else 2
+    table[:, 0:hdr] = np.frombuffer(rng.uniform(0.0005, 0.02, nb * hdr // 2).astype(np.float16).tobytes(),
+                                    np.uint8).reshape(nb, hdr)
+    ids = rng.integers(0, vocab, n).astype(np.uint32)
+    print(f"case embed {dt} {vocab}x{hidden} {n} ids", flush=True)
+    got = _gather(dev, table, dt, vocab, hidden, ids)
+    assert_bits_equal(got, orc.embed_tokens(table, dt, vocab, hidden, ids), f"{dt} model shape")
+
+
 def test_embed_q8_0_every_quant_value(dev, orc):
     """All 256 int8 quants under f16 scales incl. subnormal / max / negative."""
     scales = np.array([0x0001, 0x0200, 0x3C00, 0xBC00, 0x7BFF, 0x2E66, 0x1000, 0x8001], np.uint16)
@@ -191,5 +268,7 @@ def test_embed_rejects_bad_arguments(dev):
     s = torch.cuda.current_stream().cuda_stream
     assert L.sph_embed(t.data_ptr(), Q8_0, 1, 48, ids.data_ptr(), 2, out.data_ptr(), None, s) == EINVAL  # 48 % 32
     assert L.sph_embed(t.data_ptr(), Q4_K, 1, 300, ids.data_ptr(), 2, out.data_ptr(), None, s) == EINVAL  # % 256
-    assert L.sph_embed(t.data_ptr(), 2, 1, 256, ids.data_ptr(), 2, out.data_ptr(), None, s) == EINVAL    # Q4_0
+    assert L.sph_embed(t.data_ptr(), 3, 1, 256, ids.data_ptr(), 2, out.data_ptr(), None, s) == EINVAL    # Q4_1
+    assert L.sph_embed(t.data_ptr(), Q4_0, 1, 48, ids.data_ptr(), 2, out.data_ptr(), None, s) == EINVAL  # 48 % 32
+    assert L.sph_embed(t.data_ptr() + 2, Q5_K, 1, 256, ids.data_ptr(), 2, out.data_ptr(), None, s) == EINVAL
     assert L.sph_embed(t.data_ptr() + 1, Q4_K, 1, 256, ids.data_ptr(), 2, out.data_ptr(), None, s) == EINVAL

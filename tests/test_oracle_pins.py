@@ -472,15 +472,104 @@ def test_q6_k_matches_reference_test_generator_and_kat():
     assert np.array_equal(y, np.repeat(np.arange(16, dtype=np.float32), 16)) and y.sum() == 1920.0
 
 
+def test_q4_0_split_nibble_layout_and_exact_values():
+    """tensor.rs:362-376 / gguf.rs:259-283 (the ggml split order): byte j of a block holds element j in its
+    low nibble and element j + 16 in its high nibble, each q − 8, times d — exact in f32. Every byte value
+    at every position under scales that include subnormal, negative and large d."""
+    dvals = np.array([0x0001, 0x03FF, 0x3C00, 0xBC00, 0x7BFF, 0x2E66], np.uint16)
+    for dv in dvals:
+        d = float(np.array([dv], np.uint16).view(np.float16)[0])
+        for j in range(16):
+            blocks = np.zeros((256, 18), np.uint8)
+            blocks[:, 0:2] = np.array([dv], np.uint16).view(np.uint8)
+            blocks[:, 2:] = 0x88                              # every other element decodes to 0
+            blocks[:, 2 + j] = np.arange(256, dtype=np.uint32).astype(np.uint8)
+            y = oracle.dequant(blocks, oracle.Q4_0, 256 * 32).reshape(256, 32).astype(np.float64)
+            v = np.arange(256)
+            want = np.zeros((256, 32))
+            want[:, j] = ((v & 0xF) - 8) * d
+            want[:, j + 16] = ((v >> 4) - 8) * d
+            assert np.array_equal(y, want), (hex(int(dv)), j)
+
+
+def test_q5_k_reference_kat():
+    """tensor.rs:800-830: d = 1, dmin = 0, sc = 1, m = 0 everywhere; qh[5] bit 0 and qh[0] bit 2 set, ql[3] = 2
+    → element 3 is 2, elements 5 and 64 are 16 (the per-element high bit), every other element 0."""
+    blk = np.zeros(176, np.uint8)
+    blk[0:2] = np.array([np.float16(1.0)]).view(np.uint8)
+    blk[2:4] = np.array([np.float16(0.0)]).view(np.uint8)
+    blk[4:8] = 1
+    blk[12:16] = 1
+    blk[16 + 5] = 0b0000_0001
+    blk[16 + 0] = 0b0000_0100
+    blk[48 + 3] = 0x02
+    y = oracle.dequant(blk, oracle.Q5_K, 256)
+    want = np.zeros(256, np.float32)
+    want[3], want[5], want[64] = 2.0, 16.0, 16.0
+    assert np.array_equal(y, want)
+
+
+def _q5k_f64(blocks: np.ndarray) -> np.ndarray:
+    """The Q5_K values in float64: d·sc·(q + 16·h) and dmin·m are exact there, so rounding their difference once
+    to f32 gives the reference's f32 result (whose products are exact and whose subtraction rounds once).
+    Element 64c + 32·half + l: q = nibble `half` of ql[32c + l], h = bit 2c + half of qh[l], (sc, m) of
+    sub-block 2c + half."""
+    b = blocks.reshape(-1, 176)
+    d = b[:, 0:2].copy().view(np.float16).astype(np.float64)[:, 0]
+    dm = b[:, 2:4].copy().view(np.float16).astype(np.float64)[:, 0]
+    s = b[:, 4:16].astype(np.int64)
+    sc = np.concatenate([s[:, 0:4] & 63, (s[:, 8:12] & 0xF) | ((s[:, 0:4] >> 6) << 4)], axis=1)
+    mn = np.concatenate([s[:, 4:8] & 63, (s[:, 8:12] >> 4) | ((s[:, 4:8] >> 6) << 4)], axis=1)
+    qh = b[:, 16:48].astype(np.int64)
+    ql = b[:, 48:176].astype(np.int64).reshape(-1, 4, 32)
+    out = np.empty((b.shape[0], 4, 2, 32))
+    for c in range(4):
+        for half in range(2):
+            q = (ql[:, c] >> (4 * half)) & 0xF
+            h = (qh >> (2 * c + half)) & 1
+            sb = 2 * c + half
+            out[:, c, half] = (d * sc[:, sb])[:, None] * (q + 16 * h) - (dm * mn[:, sb])[:, None]
+    return out.reshape(-1).astype(np.float32)
+
+
+def test_q5_k_exact_against_float64_and_every_bit_plane():
+    rng = np.random.default_rng(13)
+    blocks = rng.integers(0, 256, (300, 176), dtype=np.uint8)
+    dvals = np.array([0x0001, 0x03FF, 0x0400, 0x3C00, 0x7BFF, 0x1234, 0x8400], np.uint16)
+    blocks[:, 0:2] = dvals[np.arange(300) % 7].view(np.uint8).reshape(300, 2)
+    blocks[:, 2:4] = dvals[(np.arange(300) + 3) % 7].view(np.uint8).reshape(300, 2)
+    got = oracle.dequant(blocks, oracle.Q5_K, 300 * 256)
+    assert np.array_equal(_bits(got), _bits(_q5k_f64(blocks)))
+    # one qh bit at a time: bit p of qh[l] adds 16·d·sc to element 64·(p // 2) + 32·(p % 2) + l only
+    base = np.zeros(176, np.uint8)
+    base[0:2] = np.array([np.float16(1.0)]).view(np.uint8)
+    base[4:8], base[12:16] = 1, 1                             # sc = 1, m = 0 for all eight sub-blocks
+    for l in range(32):
+        for p in range(8):
+            blk = base.copy()
+            blk[16 + l] = 1 << p
+            y = oracle.dequant(blk, oracle.Q5_K, 256)
+            assert np.flatnonzero(y).tolist() == [64 * (p // 2) + 32 * (p % 2) + l] and y.max() == 16.0
+
+
 def test_embed_row_gather_matches_full_dequant():
     """common.rs:678-718: vocab 17 x 256, seed 0xABCD, ids [0, 7, 16, 3]; OOR id errors."""
     vocab, hidden = 17, 256
     data = gather_test_values(vocab, hidden)
     q8 = oracle.quantize_q8_0(data)
     ids = [0, 7, 16, 3]
+    rng = np.random.default_rng(0xABCD)
+    q4_0 = rng.integers(0, 256, (vocab * hidden // 32, 18), dtype=np.uint8)
+    q4_0[:, 0:2] = np.frombuffer(rng.uniform(-0.05, 0.05, len(q4_0)).astype(np.float16).tobytes(),
+                                 np.uint8).reshape(-1, 2)
+    q5_k = rng.integers(0, 256, (vocab * hidden // 256, 176), dtype=np.uint8)
+    q5_k[:, 0:4] = np.frombuffer(rng.uniform(0.001, 0.05, 2 * len(q5_k)).astype(np.float16).tobytes(),
+                                 np.uint8).reshape(-1, 4)
     for dt, table, full in ((oracle.F32, data, data.reshape(-1)),
                             (oracle.F16, f16_bits(data), f16_bits(data).view(np.float16).astype(np.float32)),
-                            (oracle.Q8_0, q8, oracle.dequant(q8, oracle.Q8_0, vocab * hidden))):
+                            (oracle.Q8_0, q8, oracle.dequant(q8, oracle.Q8_0, vocab * hidden)),
+                            (oracle.Q4_0, q4_0, oracle.dequant(q4_0, oracle.Q4_0, vocab * hidden)),
+                            (oracle.Q5_K, q5_k, oracle.dequant(q5_k, oracle.Q5_K, vocab * hidden))):
         got = oracle.embed_tokens(table, dt, vocab, hidden, ids)
         assert np.array_equal(_bits(got), _bits(full.reshape(vocab, hidden)[ids]))
     with pytest.raises(oracle.OracleError) as e:
@@ -493,6 +582,8 @@ def test_row_bytes_match_dtype_byte_count():
     assert oracle.row_bytes(oracle.Q8_0, 896) == 952
     assert oracle.row_bytes(oracle.Q4_K, 4096) == 2304
     assert oracle.row_bytes(oracle.Q6_K, 4096) == 3360
+    assert oracle.row_bytes(oracle.Q4_0, 896) == 504
+    assert oracle.row_bytes(oracle.Q5_K, 4096) == 2816
     assert oracle.row_bytes(oracle.F16, 10) == 20
     assert oracle.row_bytes(oracle.Q8_0, 48) == 0   # not a whole number of blocks
 
