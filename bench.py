@@ -39,6 +39,7 @@ def parse():
     p.add_argument("--no-ops", action="store_true", help="skip the per-op table")
     p.add_argument("--only", default=None, help="comma list of op names for the per-op table")
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU-baseline time budget")
+    p.add_argument("--op-cpu-seconds", type=float, default=0.3, help="CPU time budget per op-table row")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--profile-run", action="store_true",
                    help="launch only the headline kernel (warmup + steps) and a calibration copy: for rocprofv3")
@@ -160,23 +161,40 @@ def engine_rows(torch, dev, table, vocab):
     return rows
 
 
-def op_table(torch, ops, dev, only=None):
-    """Per-op GB/s at each configuration shape (median of 20 launches after 3 warm-ups)."""
+def op_table(torch, ops, dev, only=None, cpu_budget=0.0):
+    """Per-op GB/s at each configuration shape (median of 20 launches after 3 warm-ups), and beside it
+    the oracle — the reference's algorithm restated in C, one thread — on a sample of the same shape's
+    rows (or tokens, ids), `cpu_budget` seconds each, reported in the same units."""
     import sapient_amd._lib as L
     f32, f16, bf16 = torch.float32, torch.float16, torch.bfloat16
     res = []
+    orc = None
+    if cpu_budget > 0:
+        import oracle as orc
+    crng = np.random.default_rng(1)
 
-    def run(name, shape_desc, dtype_s, alg_bytes, units, unit_name, make_sets, fn, latency_bound=False):
+    def nrm(*shape, scale=1.0, mean=0.0):
+        return crng.standard_normal(shape, dtype=np.float32) * np.float32(scale) + np.float32(mean)
+
+    def run(name, shape_desc, dtype_s, alg_bytes, units, unit_name, make_sets, fn, latency_bound=False, cpu=None):
+        """cpu: a factory returning (oracle call, units it covers) for the CPU column."""
         if only and name.split()[0] not in only:
             return
         sets = make_sets()
         per, _ = time_launches(torch, fn, sets, 3, 20)
         ms = median(per)
         gbs = alg_bytes / (ms * 1e-3) / 1e9
-        res.append({"op": name, "shape": shape_desc, "dtype": dtype_s, "us": round(ms * 1e3, 2),
-                    "GB/s": round(gbs, 1), "pct_peak": round(100 * gbs / PEAK_GBS, 1),
-                    f"{unit_name}/s": round(units / (ms * 1e-3), 1), "alg_bytes": alg_bytes,
-                    "latency_bound": latency_bound})
+        row = {"op": name, "shape": shape_desc, "dtype": dtype_s, "us": round(ms * 1e3, 2),
+               "GB/s": round(gbs, 1), "pct_peak": round(100 * gbs / PEAK_GBS, 1),
+               f"{unit_name}/s": round(units / (ms * 1e-3), 1), "alg_bytes": alg_bytes,
+               "latency_bound": latency_bound}
+        if cpu is not None and orc is not None:
+            call, sample = cpu()
+            sec, _ = cpu_time(call, cpu_budget)
+            row[f"cpu_{unit_name}/s"] = round(sample / sec, 1)
+            row["cpu_sample"] = sample
+            row["gpu_vs_cpu"] = round((units / (ms * 1e-3)) / (sample / sec), 1)
+        res.append(row)
         del sets
         torch.cuda.empty_cache()
 
@@ -187,7 +205,9 @@ def op_table(torch, ops, dev, only=None):
         run("add_rms_norm", f"{rows}x{dim}", tag + " (f32 w)", 4 * rows * dim * 2 + dim * 4, rows, "rows",
             lambda dt=dt: [(gen(torch, (rows, dim), 30 + i, dev, dt), gen(torch, (rows, dim), 40 + i, dev, dt),
                             torch.empty(rows, dim, device=dev, dtype=dt)) for i in range(3)],
-            lambda s, w=w: ops.add_rms_norm(s[0], s[1], w, 1e-5, out=s[2]))
+            lambda s, w=w: ops.add_rms_norm(s[0], s[1], w, 1e-5, out=s[2]),
+            cpu=lambda: (lambda x=nrm(256, dim), r=nrm(256, dim), w=nrm(dim, scale=0.1, mean=1.0):
+                         orc.add_rms_norm(x, r, w, 1e-5), 256))
     # C3: RoPE, Q 32 + K 8 heads, T 8192, head_dim 128, in place
     T, D = 8192, 128
     for dt, tag in ((f32, "f32"), (f16, "f16")):
@@ -198,23 +218,28 @@ def op_table(torch, ops, dev, only=None):
                 T, "tokens",
                 lambda dt=dt: [(gen(torch, (1, 32, T, D), 50 + i, dev, dt), gen(torch, (1, 8, T, D), 60 + i, dev, dt))
                                for i in range(4 if dt == f16 else 2)],
-                lambda s, il=il, pos=pos: ops.rope_(s[0], s[1], pos, 5e5, interleaved=il))
+                lambda s, il=il, pos=pos: ops.rope_(s[0], s[1], pos, 5e5, interleaved=il),
+                cpu=lambda il=il: (lambda x=nrm(1, 40, 32, D), p=np.arange(4000, 4032):
+                                   orc.apply_rope_partial_scaled(x, p, 5e5, D, 1.0, il), 32))
     # C4: SwiGLU [8192, 14336] f16, GELU-tanh [8192, 10240] f16
     n = 8192 * 14336
     run("swiglu", "8192x14336", "f16", 3 * n * 2, 8192, "rows",
         lambda: [(gen(torch, (8192, 14336), 70 + i, dev, f16, 2.0), gen(torch, (8192, 14336), 80 + i, dev, f16, 2.0),
                   torch.empty(8192, 14336, device=dev, dtype=f16)) for i in range(2)],
-        lambda s: ops.swiglu(s[0], s[1], out=s[2]))
+        lambda s: ops.swiglu(s[0], s[1], out=s[2]),
+        cpu=lambda: (lambda g=nrm(64, 14336, scale=2.0), u=nrm(64, 14336, scale=2.0): orc.swiglu(g, u), 64))
     run("swiglu", "8192x14336", "f32", 3 * n * 4, 8192, "rows",
         lambda: [(gen(torch, (8192, 14336), 75 + i, dev, f32, 2.0), gen(torch, (8192, 14336), 85 + i, dev, f32, 2.0),
                   torch.empty(8192, 14336, device=dev, dtype=f32)) for i in range(2)],
-        lambda s: ops.swiglu(s[0], s[1], out=s[2]))
+        lambda s: ops.swiglu(s[0], s[1], out=s[2]),
+        cpu=lambda: (lambda g=nrm(64, 14336, scale=2.0), u=nrm(64, 14336, scale=2.0): orc.swiglu(g, u), 64))
     ops.init(dev)
     n = 8192 * 10240
     run("gelu_tanh", "8192x10240", "f16", 2 * n * 2, 8192, "rows",
         lambda: [(gen(torch, (8192, 10240), 90 + i, dev, f16, 2.0), torch.empty(8192, 10240, device=dev, dtype=f16))
                  for i in range(3)],
-        lambda s: ops.gelu_tanh(s[0], out=s[1]))
+        lambda s: ops.gelu_tanh(s[0], out=s[1]),
+        cpu=lambda: (lambda x=nrm(64, 10240, scale=2.0): orc.gelu(x), 64))
     # LayerNorm (+ bias), erf-GELU and the bias add: the encoder-family norm / activation path
     rows, dim = 16384, 4096
     wl, bl = gen(torch, (dim,), 4, dev, f32, 0.1, 1.0), gen(torch, (dim,), 5, dev, f32, 0.1)
@@ -222,27 +247,46 @@ def op_table(torch, ops, dev, only=None):
         run("layer_norm", f"{rows}x{dim}", tag, 2 * rows * dim * es + 2 * dim * 4, rows, "rows",
             lambda dt=dt: [(gen(torch, (rows, dim), 150 + i, dev, dt, 2.0, 0.5), torch.empty(rows, dim, device=dev, dtype=dt))
                            for i in range(3)],
-            lambda s: ops.layer_norm(s[0], wl, bl, 1e-5, out=s[1]))
+            lambda s: ops.layer_norm(s[0], wl, bl, 1e-5, out=s[1]),
+            cpu=lambda: (lambda x=nrm(256, dim, scale=2.0, mean=0.5), w=nrm(dim, scale=0.1, mean=1.0),
+                         b=nrm(dim, scale=0.1): orc.layer_norm(x, w, b, 1e-5), 256))
     run("add_bias", f"{rows}x{dim}", "f32", 2 * rows * dim * 4 + dim * 4, rows, "rows",
         lambda: [(gen(torch, (rows, dim), 160 + i, dev, f32), torch.empty(rows, dim, device=dev)) for i in range(3)],
-        lambda s: ops.add_bias(s[0], bl, out=s[1]))
+        lambda s: ops.add_bias(s[0], bl, out=s[1]),
+        cpu=lambda: (lambda y=nrm(256, dim), b=nrm(dim, scale=0.1): orc.add_bias_last_dim(y, b), 256))
     n = 12000 * 5120
     for dt, tag, es in ((f32, "f32", 4), (f16, "f16", 2)):
         run("gelu_erf", "12000x5120", tag, 2 * n * es, 12000, "rows",
             lambda dt=dt: [(gen(torch, (12000, 5120), 170 + i, dev, dt, 2.0), torch.empty(12000, 5120, device=dev, dtype=dt))
                            for i in range(3)],
-            lambda s: ops.gelu_erf(s[0], out=s[1]))
+            lambda s: ops.gelu_erf(s[0], out=s[1]),
+            cpu=lambda: (lambda x=nrm(64, 5120, scale=2.0): orc.gelu_erf(x), 64))
     # Decode-chain helpers: head transpose of a Llama-3-8B prefill Q, KV-cache append of its K
     T, H, D = 8192, 32, 128
     for dt, tag, es in ((f32, "f32", 4), (f16, "f16", 2)):
         run("transpose_heads", f"{T}x{H}x{D}", tag, 2 * T * H * D * es, T, "tokens",
             lambda dt=dt: [(gen(torch, (T, H, D), 180 + i, dev, dt), torch.empty(H, T, D, device=dev, dtype=dt))
                            for i in range(3)],
-            lambda s: ops.transpose_heads(s[0], out=s[1]))
+            lambda s: ops.transpose_heads(s[0], out=s[1]),
+            cpu=lambda es=es: (lambda x=(nrm(64, H, D) if es == 4 else crng.integers(0, 65536, (64, H, D), dtype=np.uint16)):
+                               orc.transpose_heads(x, 64, H, D), 64))
     run("kv_append", f"8x{T}x{D} -> cache 8x{T}x{D}", "f32->f16", 8 * T * D * (4 + 2), T, "tokens",
         lambda: [(gen(torch, (8, T, D), 190 + i, dev, f32), torch.empty(8, T, D, device=dev, dtype=f16))
                  for i in range(3)],
-        lambda s: ops.kv_append(s[0], s[1], 0))
+        lambda s: ops.kv_append(s[0], s[1], 0),
+        cpu=lambda: (lambda x=nrm(8, 64, D), c=np.zeros((8, T, D), np.uint16):
+                     orc.kv_append(x, c, L.F16, 8, 64, D, T, 0), 64))
+
+    def cpu_gather(dt, block, nbytes, d_off, nd, hidden, n):
+        """The oracle's gather of n ids from a 2048-row table of the same format (cost per row does not
+        depend on vocab)."""
+        vocab_c = 2048
+        nb_c = vocab_c * hidden // block
+        t = crng.integers(0, 256, (nb_c, nbytes), dtype=np.uint8)
+        if nd:
+            t[:, d_off:d_off + 2 * nd] = crng.uniform(0.0005, 0.02, (nb_c, nd)).astype(np.float16).view(np.uint8)
+        ids_c = crng.integers(0, vocab_c, n).astype(np.uint32)
+        return (lambda: orc.embed_tokens(t, dt, vocab_c, hidden, ids_c)), n
     # C5: Q4_K embedding gather, 128256 x 4096 table, 65536 ids (uniform, Zipf 1.1)
     vocab, hidden, n_ids = 128256, 4096, 65536
     nb = vocab * hidden // 256
@@ -259,7 +303,8 @@ def op_table(torch, ops, dev, only=None):
         run(f"embed_q4_k {dist}", f"{vocab}x{hidden} -> {n_ids} ids", "q4_k->f32",
             n_ids * (2304 + 4 + hidden * 4), n_ids, "rows",
             lambda: [torch.empty(n_ids, hidden, device=dev) for _ in range(2)],
-            lambda o, ids=ids: ops.embed(table, L.Q4_K, vocab, hidden, ids, out=o))
+            lambda o, ids=ids: ops.embed(table, L.Q4_K, vocab, hidden, ids, out=o),
+            cpu=lambda: cpu_gather(L.Q4_K, 256, 144, 0, 2, hidden, 1024))
     del table
     # The other GGUF table formats at the same shape and uniform ids (f1 and the data formats around C5)
     ids = torch.from_numpy(rng.integers(0, vocab, n_ids).astype(np.int32)).to(dev)
@@ -275,7 +320,9 @@ def op_table(torch, ops, dev, only=None):
         run(f"embed_{name} uniform", f"{vocab}x{hidden} -> {n_ids} ids", f"{name}->f32",
             n_ids * (row_bytes + 4 + hidden * 4), n_ids, "rows",
             lambda: [torch.empty(n_ids, hidden, device=dev) for _ in range(2)],
-            lambda o, table=table, dt=dt: ops.embed(table, dt, vocab, hidden, ids, out=o))
+            lambda o, table=table, dt=dt: ops.embed(table, dt, vocab, hidden, ids, out=o),
+            cpu=lambda dt=dt, block=block, nbytes=nbytes, d_off=d_off, nd=nd:
+                cpu_gather(dt, block, nbytes, d_off, nd, hidden, 1024))
         del table
     # C1: Qwen2.5-0.5B layer ops (latency-bound, reported only)
     H = 896
@@ -283,16 +330,19 @@ def op_table(torch, ops, dev, only=None):
         w = gen(torch, (H,), 3, dev, f32, 0.1, 1.0)
         run(f"rms_norm qwen T={T1}", f"{T1}x{H}", "f32", T1 * H * 8 + H * 4, T1, "rows",
             lambda T1=T1: [(gen(torch, (T1, H), 100 + i, dev, f32), torch.empty(T1, H, device=dev)) for i in range(2)],
-            lambda s, w=w: ops.rms_norm(s[0], w, 1e-6, out=s[1]), latency_bound=True)
+            lambda s, w=w: ops.rms_norm(s[0], w, 1e-6, out=s[1]), latency_bound=True,
+            cpu=lambda T1=T1: (lambda x=nrm(T1, H), w=nrm(H, scale=0.1, mean=1.0): orc.rms_norm(x, w, 1e-6), T1))
         pos = torch.arange(T1, dtype=torch.int32, device=dev)
         run(f"rope_neox qwen T={T1}", f"q14+k2 x {T1} x 64", "f32", 2 * 16 * T1 * 64 * 4, T1, "tokens",
             lambda T1=T1: [(gen(torch, (1, 14, T1, 64), 110 + i, dev, f32), gen(torch, (1, 2, T1, 64), 120 + i, dev, f32))
                            for i in range(2)],
-            lambda s, pos=pos: ops.rope_(s[0], s[1], pos, 1e6), latency_bound=True)
+            lambda s, pos=pos: ops.rope_(s[0], s[1], pos, 1e6), latency_bound=True,
+            cpu=lambda T1=T1: (lambda q=nrm(1, 16, T1, 64), p=np.arange(T1): orc.apply_rope(q, p, 1e6), T1))
         run(f"swiglu qwen T={T1}", f"{T1}x4864", "f32", 3 * T1 * 4864 * 4, T1, "rows",
             lambda T1=T1: [(gen(torch, (T1, 4864), 130 + i, dev, f32), gen(torch, (T1, 4864), 140 + i, dev, f32),
                             torch.empty(T1, 4864, device=dev)) for i in range(2)],
-            lambda s: ops.swiglu(s[0], s[1], out=s[2]), latency_bound=True)
+            lambda s: ops.swiglu(s[0], s[1], out=s[2]), latency_bound=True,
+            cpu=lambda T1=T1: (lambda g=nrm(T1, 4864), u=nrm(T1, 4864): orc.swiglu(g, u), T1))
     vocab_q, hid_q = 151936, 896
     nbq = vocab_q * hid_q // 32
     tq = torch.randint(-127, 128, (nbq, 34), generator=g, device=dev, dtype=torch.int32).to(torch.int8).view(torch.uint8)
@@ -303,7 +353,8 @@ def op_table(torch, ops, dev, only=None):
         ids = torch.from_numpy(rng.integers(0, vocab_q, T1).astype(np.int32)).to(dev)
         run(f"embed_q8_0 qwen T={T1}", f"{vocab_q}x{hid_q} -> {T1} ids", "q8_0->f32", T1 * (952 + 4 + hid_q * 4),
             T1, "rows", lambda T1=T1: [torch.empty(T1, hid_q, device=dev) for _ in range(2)],
-            lambda o, ids=ids: ops.embed(tq, L.Q8_0, vocab_q, hid_q, ids, out=o), latency_bound=True)
+            lambda o, ids=ids: ops.embed(tq, L.Q8_0, vocab_q, hid_q, ids, out=o), latency_bound=True,
+            cpu=lambda T1=T1: cpu_gather(L.Q8_0, 32, 34, 0, 1, hid_q, T1))
     # Device-resident decode engine at Qwen2.5-0.5B shape (24 layers, 896 hidden, 14 + 2 heads x 64,
     # 4864 intermediate, f16 KV cache, Q8_0 embedding): this library's part of a token
     # (projections / attention skipped), launched eagerly and replayed from a HIP graph.
@@ -385,7 +436,11 @@ def main():
     }
     if not args.no_ops:
         only = set(args.only.split(",")) if args.only else None
-        line["ops"] = op_table(torch, ops, dev, only)
+        line["ops"] = op_table(torch, ops, dev, only, 0.0 if args.no_cpu else args.op_cpu_seconds)
+        if not args.no_cpu:
+            line["ops_cpu"] = ("cpu_*/s: the oracle (the reference's algorithm restated in C, f32, one thread) on "
+                               "cpu_sample rows / tokens / ids of each shape, timed on this host; gpu_vs_cpu = the "
+                               "ratio of the two rates")
     print(json.dumps(line), flush=True)
 
 
