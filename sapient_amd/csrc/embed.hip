@@ -29,9 +29,10 @@
 //    it needs, and unpacks its (sc, m) pair in registers. A row's loads are
 //    all issued before the first is consumed (16 super-blocks per batch).
 //  - Q4_0 / Q8_0 / Q6_K blocks are 2-byte aligned only (18 / 34 / 210 bytes),
-//    so lanes read them in 16-bit pieces; Q5_K blocks (176 bytes) stay
-//    16-byte aligned, so a lane reads its header, nibble dword and high-bit
-//    dword whole.
+//    so lanes read them in 16-bit pieces — except Q8_0, whose rows are staged
+//    through LDS with wide loads first (embed_q8_0_staged); Q5_K blocks (176
+//    bytes) stay 16-byte aligned, so a lane reads its header, nibble dword and
+//    high-bit dword whole.
 //  - An id >= vocab zero-fills its row and raises `bad_id_flag`; the table is
 //    never read out of bounds.
 #include "sph_common.h"
@@ -239,6 +240,82 @@ __global__ __launch_bounds__(kThreads) void embed_rows(const uint8_t* __restrict
     }
 }
 
+// Q8_0 rows staged through LDS: 34-byte blocks leave every block 2-byte
+// aligned, so reading them in place costs three 2-byte loads per 4 outputs.
+// A wave instead copies a chunk of its row (up to 128 blocks, 4352 bytes) into
+// LDS with W-byte loads — W the widest power of two dividing both the row
+// length and the table's alignment — and dequantizes from there. Every wave of
+// a block runs the same number of chunk steps (hidden is uniform), so the
+// block barriers are reached by all, tokens past n_ids included.
+constexpr int kQ8ChunkBlocks = 128;
+constexpr int kQ8ChunkBytes = kQ8ChunkBlocks * 34;  // a multiple of 16
+
+template <int W> struct StageWord;
+template <> struct StageWord<16> { using type = u32x4; };
+template <> struct StageWord<8> { using type = u32x2; };
+template <> struct StageWord<4> { using type = uint32_t; };
+
+template <int W>
+__global__ __launch_bounds__(kThreads) void embed_q8_0_staged(const uint8_t* __restrict__ table, int64_t vocab,
+                                                              int hidden, int64_t row_bytes,
+                                                              const uint32_t* __restrict__ ids, int64_t n_ids,
+                                                              float* __restrict__ out, int32_t* bad_id_flag) {
+    using Word = typename StageWord<W>::type;
+    __shared__ __align__(16) uint8_t stage[kTokPerBlock][kQ8ChunkBytes];
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wv = threadIdx.x / kWave;
+    const int64_t t = (int64_t)blockIdx.x * kTokPerBlock + wv;
+    const bool active = t < n_ids;
+    const uint32_t id = active ? __builtin_amdgcn_readfirstlane(ids[t]) : 0u;
+    const bool valid = active && (int64_t)id < vocab;
+    float* dst = out + (size_t)(active ? t : 0) * (size_t)hidden;
+    if (active && !valid) {
+        for (int e4 = lane; e4 < hidden / 4; e4 += kWave) store4(dst + 4 * e4, 0.f, 0.f, 0.f, 0.f);
+        if (lane == 0 && bad_id_flag != nullptr) *bad_id_flag = 1;
+    }
+    const uint8_t* row = table + (size_t)(valid ? id : 0u) * (size_t)row_bytes;
+    uint8_t* buf = stage[wv];
+    const int nblk = hidden / 32;
+    for (int c0 = 0; c0 < nblk; c0 += kQ8ChunkBlocks) {
+        const int nb = nblk - c0 < kQ8ChunkBlocks ? nblk - c0 : kQ8ChunkBlocks;
+        const int bytes = nb * 34;  // a multiple of W: so are row_bytes and kQ8ChunkBytes
+        if (valid) {
+            const uint8_t* src = row + (size_t)c0 * 34;
+            for (int o = lane * W; o < bytes; o += kWave * W)
+                *reinterpret_cast<Word*>(buf + o) = *reinterpret_cast<const Word*>(src + o);
+        }
+        __syncthreads();
+        if (valid) {
+            for (int e4 = lane; e4 < nb * 8; e4 += kWave) {
+                const uint8_t* b = buf + (e4 >> 3) * 34;
+                const int j = (e4 & 7) * 4;
+                const float d = widen(f16{*reinterpret_cast<const uint16_t*>(b)});
+                const uint32_t lo = *reinterpret_cast<const uint16_t*>(b + 2 + j);
+                const uint32_t hi = *reinterpret_cast<const uint16_t*>(b + 4 + j);
+                store4(dst + 32 * c0 + 4 * e4, (float)(int8_t)(lo & 0xFF) * d, (float)(int8_t)(lo >> 8) * d,
+                       (float)(int8_t)(hi & 0xFF) * d, (float)(int8_t)(hi >> 8) * d);
+            }
+        }
+        __syncthreads();
+    }
+}
+
+template <int W>
+int launch_q8_0_staged(const void* table, int64_t vocab, int64_t hidden, int64_t row_bytes, const uint32_t* ids,
+                       int64_t n_ids, float* out, int32_t* flag, hipStream_t stream) {
+    constexpr int64_t kChunk = int64_t(1) << 24;  // tokens per launch
+    for (int64_t t0 = 0; t0 < n_ids; t0 += kChunk) {
+        const int64_t nt = n_ids - t0 < kChunk ? n_ids - t0 : kChunk;
+        const dim3 grid((unsigned)((nt + kTokPerBlock - 1) / kTokPerBlock));
+        embed_q8_0_staged<W><<<grid, kThreads, 0, stream>>>(static_cast<const uint8_t*>(table), vocab, (int)hidden,
+                                                            row_bytes, ids + t0, nt, out + (size_t)t0 * (size_t)hidden,
+                                                            flag);
+        const int st = launch_status();
+        if (st != SPH_OK) return st;
+    }
+    return SPH_OK;
+}
+
 template <int DT>
 int launch_embed(const void* table, int64_t vocab, int64_t hidden, int64_t row_bytes, const uint32_t* ids,
                  int64_t n_ids, float* out, int32_t* flag, hipStream_t stream) {
@@ -283,7 +360,15 @@ extern "C" int sph_embed(const void* table, int table_dtype, int64_t vocab, int6
     case SPH_F16: return launch_embed<SPH_F16>(table, vocab, hidden, row_bytes, ids, n_ids, out, bad_id_flag, s);
     case SPH_BF16: return launch_embed<SPH_BF16>(table, vocab, hidden, row_bytes, ids, n_ids, out, bad_id_flag, s);
     case SPH_Q4_0: return launch_embed<SPH_Q4_0>(table, vocab, hidden, row_bytes, ids, n_ids, out, bad_id_flag, s);
-    case SPH_Q8_0: return launch_embed<SPH_Q8_0>(table, vocab, hidden, row_bytes, ids, n_ids, out, bad_id_flag, s);
+    case SPH_Q8_0:
+        // Staged through LDS with the widest aligned loads the row layout allows.
+        if (row_bytes % 16 == 0 && aligned(table, 16))
+            return launch_q8_0_staged<16>(table, vocab, hidden, row_bytes, ids, n_ids, out, bad_id_flag, s);
+        if (row_bytes % 8 == 0 && aligned(table, 8))
+            return launch_q8_0_staged<8>(table, vocab, hidden, row_bytes, ids, n_ids, out, bad_id_flag, s);
+        if (row_bytes % 4 == 0 && aligned(table, 4))
+            return launch_q8_0_staged<4>(table, vocab, hidden, row_bytes, ids, n_ids, out, bad_id_flag, s);
+        return launch_embed<SPH_Q8_0>(table, vocab, hidden, row_bytes, ids, n_ids, out, bad_id_flag, s);
     case SPH_Q4_K: return launch_embed<SPH_Q4_K>(table, vocab, hidden, row_bytes, ids, n_ids, out, bad_id_flag, s);
     case SPH_Q5_K: return launch_embed<SPH_Q5_K>(table, vocab, hidden, row_bytes, ids, n_ids, out, bad_id_flag, s);
     case SPH_Q6_K: return launch_embed<SPH_Q6_K>(table, vocab, hidden, row_bytes, ids, n_ids, out, bad_id_flag, s);

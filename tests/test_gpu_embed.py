@@ -272,3 +272,28 @@ def test_embed_rejects_bad_arguments(dev):
     assert L.sph_embed(t.data_ptr(), Q4_0, 1, 48, ids.data_ptr(), 2, out.data_ptr(), None, s) == EINVAL  # 48 % 32
     assert L.sph_embed(t.data_ptr() + 2, Q5_K, 1, 256, ids.data_ptr(), 2, out.data_ptr(), None, s) == EINVAL
     assert L.sph_embed(t.data_ptr() + 1, Q4_K, 1, 256, ids.data_ptr(), 2, out.data_ptr(), None, s) == EINVAL
+
+
+@pytest.mark.parametrize("hidden", [96, 320, 896, 4096, 8448])
+@pytest.mark.parametrize("offset", [0, 2, 4, 8])
+def test_embed_q8_0_every_staging_width(dev, orc, hidden, offset):
+    """Q8_0 rows are staged through LDS with 16-, 8- or 4-byte loads, whichever divides both the row
+    length and the table address, and read in place otherwise: widths 96 (102-byte rows: in place),
+    320 (4-byte), 896 (8-byte), 4096 (16-byte), 8448 (16-byte, three chunks), each with the table
+    shifted by 0, 2, 4 and 8 bytes, and one out-of-range id (zero row, flag raised)."""
+    vocab = 64
+    rng = np.random.default_rng(hidden + offset)
+    nb = vocab * hidden // 32
+    blocks = rng.integers(0, 256, (nb, 34), dtype=np.uint8)
+    blocks[:, 0:2] = np.frombuffer(rng.uniform(-0.05, 0.05, nb).astype(np.float16).tobytes(), np.uint8).reshape(nb, 2)
+    raw = torch.zeros(nb * 34 + 16, dtype=torch.uint8, device=dev)
+    table = raw[offset:offset + nb * 34]
+    table.copy_(torch.from_numpy(blocks.reshape(-1)).to(dev))
+    ids = np.array(list(rng.permutation(vocab)[:40]) + [vocab + 5, 0, vocab - 1], np.uint32)
+    flag = torch.zeros(1, dtype=torch.int32, device=dev)
+    print(f"case embed q8_0 staging hidden {hidden} offset {offset}", flush=True)
+    out = to_np(ops.embed(table, Q8_0, vocab, hidden, _ids(ids, dev), bad_id_flag=flag))
+    ok = ids < vocab
+    assert flag.item() == 1
+    assert (out[~ok] == 0).all()
+    assert_bits_equal(out[ok], orc.embed_tokens(blocks, Q8_0, vocab, hidden, ids[ok]), f"q8_0 {hidden} +{offset}")
