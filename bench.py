@@ -181,7 +181,8 @@ def engine_rows(torch, dev, table, vocab):
 
 
 def op_table(torch, ops, dev, only=None, cpu_budget=0.0):
-    """Per-op GB/s at each configuration shape (median of 20 launches after 3 warm-ups), and beside it
+    """Per-op GB/s at each configuration shape (20 back-to-back launches after 3 warm-ups between one
+    event pair; latency-bound rows: the median of 20 individually bracketed launches), and beside it
     the oracle — the reference's algorithm restated in C, one thread — on a sample of the same shape's
     rows (or tokens, ids), `cpu_budget` seconds each, reported in the same units."""
     import sapient_amd._lib as L
@@ -200,8 +201,11 @@ def op_table(torch, ops, dev, only=None, cpu_budget=0.0):
         if only and name.split()[0] not in only:
             return
         sets = make_sets()
-        per, _ = time_launches(torch, fn, sets, 3, 20)
-        ms = median(per)
+        if latency_bound:  # one call's latency: the median of 20 event-bracketed launches
+            per, _ = time_launches(torch, fn, sets, 3, 20)
+            ms = median(per)
+        else:  # throughput: 20 back-to-back launches between one event pair
+            ms = time_region(torch, fn, sets, 3, 20)[0] / 20
         gbs = alg_bytes / (ms * 1e-3) / 1e9
         row = {"op": name, "shape": shape_desc, "dtype": dtype_s, "us": round(ms * 1e3, 2),
                "GB/s": round(gbs, 1), "pct_peak": round(100 * gbs / PEAK_GBS, 1),
