@@ -224,8 +224,13 @@ int sph_transpose_heads(const void* x, void* out, int dtype, int64_t outer, int6
  * positions pos .. pos+seq-1 of cache [n_kv, max_seq, head_dim], converted to
  * the cache's type (f32 → f16 / bf16 rounds to nearest-even). seq = 1 is a
  * decode step, seq > 1 a batched prefill. Replaces WgpuContext::kv_append
- * (resident.rs:645-711). src_dtype, cache_dtype ∈ {F32, F16, BF16};
- * pos + seq > max_seq returns SPH_ERANGE without writing. */
+ * (resident.rs:645-711). src_dtype ∈ {F32, F16, BF16}; cache_dtype ∈ {F32,
+ * F16, BF16, Q8_0}. A Q8_0 cache is the reference's quantized KV cache
+ * (update_kv_cache_q8, crates/sapient-models/src/forward/common.rs:449-508):
+ * rows of head_dim / 32 blocks of 34 bytes (f16 scale, 32 × i8), each block
+ * quantized on append as quantize_f32_to_q8_0_block does (common.rs:336-348),
+ * bit for bit; head_dim a multiple of 32, src 16-byte and cache 2-byte
+ * aligned. pos + seq > max_seq returns SPH_ERANGE without writing. */
 int sph_kv_append(const void* src, int src_dtype, void* cache, int cache_dtype, int64_t n_kv, int64_t seq,
                   int64_t head_dim, int64_t max_seq, int64_t pos, void* stream);
 

@@ -295,11 +295,12 @@ def transpose_heads(x, outer: int, inner: int, head_dim: int) -> np.ndarray:
 def kv_append(src, cache: np.ndarray, cache_dtype: int, n_kv: int, seq: int, head_dim: int, max_seq: int,
               pos: int) -> None:
     """resident.rs:645-711, in place on `cache` ([n_kv, max_seq, hd]; float32, or
-    uint16 bits for F16 / BF16)."""
+    uint16 bits for F16 / BF16; for Q8_0 uint8 [n_kv, max_seq, hd / 32 · 34], common.rs:449-508)."""
     src = _f32(src)
-    if src.size != n_kv * seq * head_dim or cache.size != n_kv * max_seq * head_dim or not cache.flags.c_contiguous:
+    row = head_dim // 32 * 34 if cache_dtype == Q8_0 else head_dim
+    if src.size != n_kv * seq * head_dim or cache.size != n_kv * max_seq * row or not cache.flags.c_contiguous:
         raise ValueError("src / cache sizes do not match the layout")
-    want = np.float32 if cache_dtype == 0 else np.uint16
+    want = {F32: np.float32, Q8_0: np.uint8}.get(cache_dtype, np.uint16)
     if cache.dtype != want:
         raise ValueError("cache dtype does not match cache_dtype")
     st = lib().sor_kv_append(_p(src), _p(cache), cache_dtype, n_kv, seq, head_dim, max_seq, pos)

@@ -579,6 +579,20 @@ void sor_transpose_heads(const void* x, void* out, size_t esize, size_t outer, s
 int sor_kv_append(const float* src, void* cache, int cache_dtype, size_t n_kv, size_t seq, size_t hd,
                   size_t max_seq, size_t pos) {
     if (pos + seq > max_seq) return SOR_ERANGE;
+    if (cache_dtype == SOR_Q8_0) {
+        /* The quantized KV cache of common.rs:449-508 (update_kv_cache_q8):
+         * each new row is quantized block by block with
+         * quantize_f32_to_q8_0_block (common.rs:336-348), the same steps as
+         * quant.rs:223-235 restated in sor_quantize_q8_0; rows of a head sit at
+         * (h · max_seq + position) · (hd / 32) · 34 bytes. */
+        if (hd % QK != 0) return SOR_EINVAL;
+        const size_t bpr = hd / QK;
+        for (size_t h = 0; h < n_kv; h++)
+            for (size_t s = 0; s < seq; s++)
+                sor_quantize_q8_0(src + (h * seq + s) * hd, bpr,
+                                  (uint8_t*)cache + (h * max_seq + pos + s) * bpr * Q8_0_BYTES);
+        return SOR_OK;
+    }
     if (cache_dtype != SOR_F32 && cache_dtype != SOR_F16 && cache_dtype != SOR_BF16) return SOR_EINVAL;
     for (size_t h = 0; h < n_kv; h++)
         for (size_t s = 0; s < seq; s++)

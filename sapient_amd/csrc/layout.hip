@@ -134,6 +134,45 @@ int launch_move(const void* src, void* dst, uint64_t rows, uint64_t hd, RowMap m
     return SPH_OK;
 }
 
+// Q8_0 cache: one thread per 32-element block of a (head, token) row, the
+// quantizer of the reference's quantized KV cache
+// (crates/sapient-models/src/forward/common.rs:336-348, the same steps as
+// quant.rs:223-235): amax over the block (NaN skipped, as f32::max folds),
+// scale = amax / 127 in f32, d = f16(scale), q = clamp(round(v · 1/scale),
+// ±127) with round half away from zero and NaN → 0 (the `as i8` cast), and 0
+// throughout for an all-zero block. Row layout: head_dim / 32 blocks of
+// 34 bytes (f16 d, 32 × i8), rows of a head at positions 0 .. max_seq - 1.
+template <typename TS>
+__global__ __launch_bounds__(kThreads) void kv_append_q8_0(const TS* __restrict__ src, uint8_t* __restrict__ cache,
+                                                           uint64_t blocks, uint32_t bpr, uint32_t seq,
+                                                           uint32_t max_seq, uint64_t pos) {
+    const uint64_t k = (uint64_t)blockIdx.x * kThreads + threadIdx.x;
+    if (k >= blocks) return;
+    const uint64_t row = k / bpr;                // source row h · seq + s
+    const uint32_t blk = (uint32_t)(k - row * bpr);
+    const uint64_t h = row / seq, s = row - h * seq;
+    float v[32];
+    load_f32<TS, 32>(src + row * (uint64_t)bpr * 32 + (uint64_t)blk * 32, v);
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(v[i]));
+    const float scale = amax / 127.0f;
+    const float inv = scale > 0.0f ? 1.0f / scale : 0.0f;
+    uint8_t* out = cache + ((h * max_seq + pos + s) * (uint64_t)bpr + blk) * 34;  // 2-byte aligned
+    uint16_t* o16 = reinterpret_cast<uint16_t*>(out);
+    o16[0] = narrow<f16>(scale).bits;
+#pragma unroll
+    for (int i = 0; i < 32; i += 2) {
+        int8_t q[2];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const float r = roundf(v[i + j] * inv);  // half away from zero
+            q[j] = r != r ? (int8_t)0 : (int8_t)fminf(fmaxf(r, -127.0f), 127.0f);
+        }
+        o16[1 + i / 2] = (uint16_t)((uint8_t)q[0] | ((uint16_t)(uint8_t)q[1] << 8));
+    }
+}
+
 }  // namespace
 }  // namespace sph
 
@@ -157,14 +196,32 @@ extern "C" int sph_transpose_heads(const void* x, void* out, int dtype, int64_t 
 extern "C" int sph_kv_append(const void* src, int src_dtype, void* cache, int cache_dtype, int64_t n_kv, int64_t seq,
                              int64_t head_dim, int64_t max_seq, int64_t pos, void* stream) {
     if (n_kv < 0 || seq < 0 || head_dim < 0 || max_seq < 0 || pos < 0) return SPH_EINVAL;
-    if (!sph::is_float_dtype(src_dtype) || !sph::is_float_dtype(cache_dtype)) return SPH_EINVAL;
+    const bool q8 = cache_dtype == SPH_Q8_0;
+    if (!sph::is_float_dtype(src_dtype) || !(q8 || sph::is_float_dtype(cache_dtype))) return SPH_EINVAL;
+    if (q8 && head_dim % 32 != 0) return SPH_EINVAL;
     if (pos > max_seq || seq > max_seq - pos) return SPH_ERANGE;
     const uint64_t rows = (uint64_t)n_kv * (uint64_t)seq;
     if (rows == 0 || head_dim == 0) return SPH_OK;
     if (src == nullptr || cache == nullptr) return SPH_EINVAL;
     if (seq > UINT32_MAX || max_seq > UINT32_MAX) return SPH_EINVAL;
-    const sph::RowMap m{(uint32_t)seq, (uint32_t)max_seq, (uint64_t)pos};
     hipStream_t s = static_cast<hipStream_t>(stream);
+    if (q8) {
+        if (!sph::aligned(cache, 2) || !sph::aligned(src, 16) || head_dim / 32 > UINT32_MAX) return SPH_EINVAL;
+        const uint64_t bpr = (uint64_t)head_dim / 32;
+        const uint64_t blocks = rows * bpr;
+        return sph::with_float_type(src_dtype, [&](auto ts) -> int {
+            using TS = decltype(ts);
+            const uint64_t nblk = (blocks + sph::kThreads - 1) / sph::kThreads;
+            if (nblk > INT32_MAX) return SPH_EINVAL;
+            const dim3 grid((unsigned)nblk);
+            sph::kv_append_q8_0<TS><<<grid, sph::kThreads, 0, s>>>(static_cast<const TS*>(src),
+                                                                    static_cast<uint8_t*>(cache), blocks,
+                                                                    (uint32_t)bpr, (uint32_t)seq, (uint32_t)max_seq,
+                                                                    (uint64_t)pos);
+            return sph::launch_status();
+        });
+    }
+    const sph::RowMap m{(uint32_t)seq, (uint32_t)max_seq, (uint64_t)pos};
     return sph::with_float_type(src_dtype, [&](auto ts) -> int {
         using TS = decltype(ts);
         return sph::with_float_type(cache_dtype, [&](auto td) -> int {

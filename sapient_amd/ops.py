@@ -264,14 +264,20 @@ def transpose_heads(x: torch.Tensor, out: Optional[torch.Tensor] = None) -> torc
 
 def kv_append(src: torch.Tensor, cache: torch.Tensor, pos: int) -> None:
     """Write src [n_kv, seq, head_dim] into cache [n_kv, max_seq, head_dim] at
-    positions pos..pos+seq, converted to the cache's dtype (resident.rs:645-711)."""
+    positions pos..pos+seq, converted to the cache's dtype (resident.rs:645-711).
+    A uint8 cache [n_kv, max_seq, head_dim / 32 * 34] is a Q8_0 cache, quantized
+    on append (common.rs:336-348, :449-508)."""
     _dev(src, "src")
     _dev(cache, "cache")
-    if src.dim() != 3 or cache.dim() != 3 or src.shape[0] != cache.shape[0] or src.shape[2] != cache.shape[2]:
-        raise ValueError("src must be [n_kv, seq, head_dim] and cache [n_kv, max_seq, head_dim]")
+    q8 = cache.dtype == torch.uint8
+    if src.dim() != 3 or cache.dim() != 3 or src.shape[0] != cache.shape[0]:
+        raise ValueError("src must be [n_kv, seq, head_dim] and cache [n_kv, max_seq, row]")
     n_kv, seq, hd = src.shape
+    if cache.shape[2] != (hd // 32 * 34 if q8 else hd) or (q8 and hd % 32):
+        raise ValueError("cache rows must hold head_dim elements (Q8_0: head_dim / 32 blocks of 34 bytes)")
     max_seq = cache.shape[1]
-    check(lib().sph_kv_append(src.data_ptr(), dtype_code(src.dtype), cache.data_ptr(), dtype_code(cache.dtype),
+    cdt = _lib.Q8_0 if q8 else dtype_code(cache.dtype)
+    check(lib().sph_kv_append(src.data_ptr(), dtype_code(src.dtype), cache.data_ptr(), cdt,
                               n_kv, seq, hd, max_seq, int(pos), _stream(src)), "kv_append")
 
 

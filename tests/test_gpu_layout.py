@@ -92,13 +92,17 @@ def test_kv_append_matches_wgpu_test_sequence(dev, orc, cdtype):
     _same(cache, ref, f"kv cache {cdtype}")
 
 
-@pytest.mark.parametrize("sdtype", DTYPES, ids=IDS)
-@pytest.mark.parametrize("cdtype", DTYPES, ids=IDS)
-@pytest.mark.parametrize("n_kv,seq,hd,max_seq,pos", [(8, 8192, 128, 8192, 0), (8, 1, 128, 8192, 8191),
-                                                     (2, 5, 64, 40, 17), (3, 4, 6, 10, 6), (1, 1, 1, 1, 0)])
+# Every (source, cache) dtype pair at the small shapes; the large prefill runs f32 sources into every
+# cache type and half sources into f16.
+_KV_CASES = [pytest.param(sd, cd, *shape, id=f"{IDS(sd)}-{IDS(cd)}-{'x'.join(map(str, shape))}")
+             for sd in DTYPES for cd in DTYPES
+             for shape in [(8, 8192, 128, 8192, 0), (8, 1, 128, 8192, 8191), (2, 5, 64, 40, 17), (3, 4, 6, 10, 6),
+                           (1, 1, 1, 1, 0)]
+             if not (shape[1] == 8192 and sd != torch.float32 and cd != torch.float16)]
+
+
+@pytest.mark.parametrize("sdtype,cdtype,n_kv,seq,hd,max_seq,pos", _KV_CASES)
 def test_kv_append_shapes(dev, orc, sdtype, cdtype, n_kv, seq, hd, max_seq, pos):
-    if seq == 8192 and sdtype != torch.float32 and cdtype != torch.float16:
-        pytest.skip("the large prefill runs f32 sources and every cache type, and half sources into f16")
     print(f"case kv_append {sdtype}->{cdtype} {n_kv}x{seq}x{hd} max {max_seq} pos {pos}", flush=True)
     src = _gen((n_kv, seq, hd), seq + hd, dev, sdtype)
     cache = _gen((n_kv, max_seq, hd), 99, dev, cdtype)
@@ -124,3 +128,41 @@ def test_kv_append_rejects_out_of_range(dev):
     assert L.sph_kv_append(p, 8, p, 0, 2, 1, 16, 8, 0, s) == EINVAL       # src dtype
     assert L.sph_transpose_heads(p, p, 0, 2, 8, 16, s) == EINVAL            # out aliases x
     assert L.sph_transpose_heads(p, None, 0, 2, 8, 16, s) == EINVAL
+
+
+@pytest.mark.parametrize("sdtype", [torch.float32, torch.float16, torch.bfloat16], ids=lambda d: str(d).split(".")[-1])
+@pytest.mark.parametrize("n_kv,seq,hd,max_seq,pos", [(2, 1, 64, 16, 5), (8, 37, 128, 64, 20), (4, 512, 64, 600, 0)])
+def test_kv_append_q8_0_cache(dev, orc, sdtype, n_kv, seq, hd, max_seq, pos):
+    """The quantized KV cache (update_kv_cache_q8, common.rs:449-508): new rows quantized block by block on
+    append, bit-exact with the oracle's quantizer; rows outside pos .. pos + seq untouched. The source mixes
+    ordinary values with all-zero blocks, huge and tiny magnitudes, ties of v / scale at .5, and NaN / inf."""
+    g = torch.Generator(device=dev).manual_seed(n_kv * 1000 + seq)
+    src = torch.randn(n_kv, seq, hd, generator=g, device=dev) * 3
+    flat = src.view(-1, 32)
+    nb = flat.shape[0]
+    flat[0::7] = 0.0                                                     # all-zero blocks
+    flat[1::7] *= 1e6                                                    # scale overflows f16 (inf d)
+    flat[2::7] *= 1e-30                                                  # subnormal scale
+    flat[3::7] = torch.arange(32, device=dev, dtype=torch.float32) - 15.5  # v / scale lands on .5 ties
+    if nb > 5:
+        flat[5, 3] = float("nan")
+        flat[5, 4] = float("inf")
+    src = src.to(sdtype)
+    row = hd // 32 * 34
+    cache = torch.randint(0, 256, (n_kv, max_seq, row), generator=g, device=dev, dtype=torch.int32).to(torch.uint8)
+    before = to_np(cache).copy()
+    print(f"case kv_append q8_0 {sdtype} {n_kv}x{seq}x{hd} -> {max_seq} @ {pos}", flush=True)
+    ops.kv_append(src, cache, pos)
+    want = before.copy()
+    orc.kv_append(widen(src, orc).reshape(n_kv, seq, hd), want, orc.Q8_0, n_kv, seq, hd, max_seq, pos)
+    assert np.array_equal(to_np(cache), want)
+
+
+def test_kv_append_q8_0_rejects_bad_shapes(dev):
+    from sapient_amd._lib import EINVAL, ERANGE, Q8_0, lib
+    src = torch.zeros(2, 3, 48, device=dev)
+    cache = torch.zeros(2, 8, 64, dtype=torch.uint8, device=dev)
+    s = torch.cuda.current_stream().cuda_stream
+    assert lib().sph_kv_append(src.data_ptr(), 0, cache.data_ptr(), Q8_0, 2, 3, 48, 8, 0, s) == EINVAL  # 48 % 32
+    src = torch.zeros(2, 3, 64, device=dev)
+    assert lib().sph_kv_append(src.data_ptr(), 0, cache.data_ptr(), Q8_0, 2, 3, 64, 8, 6, s) == ERANGE  # 6 + 3 > 8

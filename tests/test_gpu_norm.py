@@ -54,14 +54,17 @@ def test_rms_norm_matches_wgpu_test_vectors(dev, orc):
     assert np.abs(got - want).max() < 1e-4
 
 
-@pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: str(d).split(".")[-1])
+# (input dtype, weight dtype mode, output dtype mode): every distinct combination (for f32 input, "same"
+# weight / output is the f32 case itself).
+_RMS_MODES = [pytest.param(dt, wm, om, id=f"{str(dt).split('.')[-1]}-w{wm}-out{om}")
+              for dt in DTYPES for wm in ("f32", "same", "none") for om in ("same", "f32")
+              if not (dt == torch.float32 and (wm == "same" or om == "f32"))]
+
+
 @pytest.mark.parametrize("rows,dim", [(1, 896), (3, 896), (512, 896), (7, 64), (2, 4), (5, 1536), (33, 4096),
                                       (4, 8192), (3, 8200), (2, 16384), (3, 100), (1, 1)])
-@pytest.mark.parametrize("wmode", ["f32", "same", "none"])
-@pytest.mark.parametrize("outmode", ["same", "f32"])
+@pytest.mark.parametrize("dtype,wmode,outmode", _RMS_MODES)
 def test_rms_norm_shapes(dev, orc, dtype, rows, dim, wmode, outmode):
-    if dtype == torch.float32 and (wmode == "same" or outmode == "f32"):
-        pytest.skip("identical to the f32 case")
     print(f"case rms_norm {dtype} {rows}x{dim} w={wmode} out={outmode}", flush=True)
     x = _gen((rows, dim), 1000 + dim, dev, dtype=dtype)
     w = None if wmode == "none" else _gen((dim,), 7, dev, 1.0, 0.1, torch.float32 if wmode == "f32" else dtype)

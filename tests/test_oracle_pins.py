@@ -588,6 +588,23 @@ def test_row_bytes_match_dtype_byte_count():
     assert oracle.row_bytes(oracle.Q8_0, 48) == 0   # not a whole number of blocks
 
 
+def test_kv_append_q8_0_rows_are_quantized_blocks():
+    """common.rs:449-508: each appended row of the quantized cache is quantize_f32_to_q8_0_block
+    (common.rs:336-348) of its 32-element blocks — the quantizer pinned above against the wgpu tests'
+    quantizer (resident.rs:506-524) — at byte (h · max_seq + position) · row_bytes; other rows untouched."""
+    n_kv, seq, hd, max_seq, pos = 3, 5, 64, 12, 4
+    src = WgpuLcg().take(n_kv * seq * hd).reshape(n_kv, seq, hd)
+    row = hd // 32 * 34
+    cache = np.full((n_kv, max_seq, row), 0xAB, np.uint8)
+    oracle.kv_append(src, cache, oracle.Q8_0, n_kv, seq, hd, max_seq, pos)
+    for h in range(n_kv):
+        for s_ in range(seq):
+            blocks, _ = quantize_q8_0_blocks(src[h, s_])
+            assert np.array_equal(cache[h, pos + s_], blocks.reshape(-1))
+    untouched = [p for p in range(max_seq) if not pos <= p < pos + seq]
+    assert (cache[:, untouched] == 0xAB).all()
+
+
 def test_transpose_heads_is_the_axis_permutation():
     """wgpu tests/resident.rs:956-982 (7 x 5 x 16, lcg): out[h][s][c] = x[s][h][c] and the round
     trip is the identity; numpy's axis permutation is the independent statement; half tensors
