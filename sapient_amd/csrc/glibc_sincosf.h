@@ -105,15 +105,17 @@ __host__ __device__ inline double reduce_large(uint32_t xi, int* np, const uint3
 }  // namespace sincosf_detail
 
 // sinf(y) and cosf(y) at once, each bit-identical to glibc's. glibc branches
-// three ways on |y|; here the branches collapse for a wave whose lanes hold
-// different angles:
+// three ways on |y|; here:
 //  - below 0.75 glibc evaluates the polynomials on y itself; the fast
 //    reduction gives n = 0 and r = fma(-0, pi/2, y) = y exactly there, with
-//    the quadrant signs and coefficient set of n = 0 — the same evaluation;
+//    the quadrant signs and coefficient set of n = 0 — the same evaluation,
+//    so the two lower branches collapse into one;
 //  - below 2^-12 glibc returns y and 1.0f (kept as a select: the
 //    polynomials round to the same values except sin(-0), which they make +0);
-//  - both reductions are computed and the one glibc would use is selected
-//    (for |y| >= 120 the large one, whose quadrant also absorbs the sign).
+//  - for |y| >= 120 the large reduction replaces the fast one (its quadrant
+//    also absorbs the sign). On the GPU this is a branch a wave skips when
+//    none of its lanes holds such an argument, so callers that give a wave
+//    angles of similar size pay for the large reduction only where it is used.
 // sincosf_poly and sinf_poly/cosf_poly evaluate identical expressions, so
 // one pair of polynomials serves both results.
 __host__ __device__ inline void glibc_sincosf_tab(float y, const uint32_t* inv_pio4, float* sin_out, float* cos_out) {
@@ -124,14 +126,17 @@ __host__ __device__ inline void glibc_sincosf_tab(float y, const uint32_t* inv_p
         return;
     }
     const uint32_t xi = __builtin_bit_cast(uint32_t, y);
-    int nf, nl;
-    const double rf = reduce_fast((double)y, &nf);
-    const double rl = reduce_large(xi, &nl, inv_pio4);
-    const bool large = top >= abstop12(120.0f);
-    const double x = large ? rl : rf;
-    const int n = large ? nl : nf;
-    const int q = large ? nl + (int)(xi >> 31) : nf;  // quadrant of the signs and coefficient set
-    const double sgn = ((q + 1) & 2) ? -1.0 : 1.0;     // signs {1, -1, -1, 1} by q mod 4
+    int n;
+    double x;
+    int q;  // quadrant of the signs and coefficient set
+    if (top >= abstop12(120.0f)) {
+        x = reduce_large(xi, &n, inv_pio4);
+        q = n + (int)(xi >> 31);
+    } else {
+        x = reduce_fast((double)y, &n);
+        q = n;
+    }
+    const double sgn = ((q + 1) & 2) ? -1.0 : 1.0;  // signs {1, -1, -1, 1} by q mod 4
     const double x2 = x * x;
     const float sp = poly(x * sgn, x2, false, 0);
     const float cp = poly(x * sgn, x2, (q & 2) != 0, 1);

@@ -58,69 +58,217 @@ __device__ __forceinline__ const uint32_t* stage_inv_pio4(uint32_t (&tab)[24]) {
     return tab;
 }
 
-template <typename T, int P, bool INTERLEAVED>
-__global__ __launch_bounds__(kThreads) void rope_kernel(T* q, int nq, T* k, int nk, const int32_t* __restrict__ pos,
-                                                        int64_t ntok, int64_t seq, int head_dim, int half,
-                                                        int lanes_per_tok, int toks_per_block, int heads_per_group,
-                                                        float pos_scale, DenTable den) {
-    __shared__ uint32_t inv_pio4[24];
-    const uint32_t* tab = stage_inv_pio4(inv_pio4);
-    const int tib = threadIdx.x / lanes_per_tok;
-    const int lit = threadIdx.x - tib * lanes_per_tok;
-    if (tib >= toks_per_block) return;
-    const int64_t t = (int64_t)blockIdx.x * toks_per_block + tib;
-    if (t >= ntok) return;
-    const int i0 = lit * P;
-    const int64_t b = t / seq;
-    const int64_t s = t - b * seq;
+// L consecutive elements of one row held as they sit in memory (32-bit words,
+// or single elements when the run is narrower than a word), so that a batch of
+// rows can be in flight while the previous batch is rotated and stored.
+template <typename T, int L>
+struct RawRun {
+    static constexpr bool kWords = (L * (int)sizeof(T)) % 4 == 0;
+    uint32_t w[kWords ? words_of<T, L>::n : 1];
+    T e[kWords ? 1 : L];
 
-    const float p = (float)pos[s] / pos_scale;
-    float cs[P], sn[P];
+    __device__ __forceinline__ void load(const T* p) {
+        if constexpr (kWords) {
+            load_words<T, L, true>(p, w);
+        } else {
 #pragma unroll
-    for (int j = 0; j < P; ++j) {
-        const float freq = p / den.v[i0 + j];
-        glibc_sincosf_tab(freq, tab, &sn[j], &cs[j]);
+            for (int i = 0; i < L; ++i) e[i] = p[i];
+        }
+    }
+    __device__ __forceinline__ void to_f32(float (&v)[L]) const {
+        if constexpr (kWords) {
+            words_to_f32<T, L>(w, v);
+        } else {
+#pragma unroll
+            for (int i = 0; i < L; ++i) v[i] = widen(e[i]);
+        }
+    }
+};
+
+template <typename T, int L>
+__device__ __forceinline__ void store_run(T* p, const float (&v)[L]) {
+    if constexpr ((L * (int)sizeof(T)) % 4 == 0) {
+        store_f32<T, L, true>(p, v);
+    } else {
+#pragma unroll
+        for (int i = 0; i < L; ++i) p[i] = narrow<T>(v[i]);
+    }
+}
+
+// One thread: pairs of one token, over the heads [h_begin, h_end) of its
+// group (split into HS runs of heads, one per 256-thread subgroup of the
+// block), U heads per batch. Each row is read as R runs of L elements:
+//  - NEOX: runs of P at i0 and i0 + half, rotating pairs (i0 + j, i0 + half + j);
+//  - interleaved: one run of 2P at 2·i0, pairs i0 .. i0 + P;
+//  - interleaved, SPLIT: runs of 2P at 2·i0 and 2·i0 + half, pairs i0 .. i0 + P
+//    and i0 + half/2 .. i0 + half/2 + P — two requests per head like NEOX,
+//    which streams faster than one request of twice the size (f32 at the
+//    Llama-3-8B shape: 61.2 µs with one 16-byte run per thread, 58.0 µs split).
+// NA = the distinct angles a thread applies (P, or 2P when SPLIT). Two
+// batches of U heads are requested before the angles are computed, and from
+// then on one batch is in flight while the other is rotated and stored.
+//
+// PAIR_MAJOR: angles are computed pair-major over the block (slot j of
+// thread x takes angle j·blockDim + x of the [pair][token] order), not per
+// thread: the lanes of a wave then hold a few adjacent pairs, all with similar
+// angles, and only the waves whose pairs are low enough to see |angle| >= 120
+// (at long sequences, the first ~20 of 64 pairs) run glibc's large-argument
+// reduction. Per-thread angles (pairs i0 .. i0+P of one token) put low pairs
+// in every wave, which made every wave pay for both reductions. sin and cos
+// reach the threads that apply them through LDS. Measured at 32 + 8 heads x
+// 8192 tokens x 128 on MI355X (one box): f16 NEOX 31.5 us per-thread, 28.4 us
+// with no angles at all, 28.6 us pair-major with two batches in flight. f32,
+// whose angles are shared by all 40 heads of a thread, is ~0.5 us faster
+// per-thread (the two block barriers cost about what the reductions save).
+template <typename T, int P, bool INTERLEAVED, bool SPLIT, int U, bool PAIR_MAJOR, int HS>
+__global__ __launch_bounds__(kThreads * HS) void rope_kernel(T* q, int nq, T* k, int nk, const int32_t* __restrict__ pos,
+                                                             int64_t ntok, int64_t seq, int head_dim, int half,
+                                                             int lanes_per_tok, int toks_per_block,
+                                                             int heads_per_group, float pos_scale, DenTable den) {
+    static_assert(INTERLEAVED || !SPLIT, "SPLIT is an interleaved layout");
+    constexpr int R = (!INTERLEAVED || SPLIT) ? 2 : 1;
+    constexpr int L = INTERLEAVED ? 2 * P : P;
+    constexpr int NA = SPLIT ? 2 * P : P;
+    // [pair][token] with a row stride of toks_per_block + 1 floats: the
+    // pair-major writes and the token-major reads both spread over the banks.
+    // toks_per_block · half <= kThreads · NA, so kThreads · NA + kMaxHalf covers it.
+    constexpr int kAngles = kThreads * NA + kMaxHalf;
+    __shared__ uint32_t inv_pio4[24];
+    __shared__ int32_t pos_s[kThreads];
+    __shared__ float cs_s[kAngles], sn_s[kAngles];
+    const int tid = threadIdx.x;
+    const int sub = tid / kThreads;  // head subgroup of the block
+    const int ltid = tid - sub * kThreads;
+    const int tib = ltid / lanes_per_tok;
+    const int lit = ltid - tib * lanes_per_tok;
+    const int64_t t_first = (int64_t)blockIdx.x * toks_per_block;
+    const int64_t t = t_first + tib;
+    const bool active = tib < toks_per_block && t < ntok;
+    const int i0 = lit * P;
+    const int off[2] = {INTERLEAVED ? 2 * i0 : i0, INTERLEAVED ? 2 * i0 + half : i0 + half};
+    // Pair of angle a (0 <= a < NA) of this thread.
+    auto pair_of = [&](int a) { return SPLIT ? i0 + (a / P) * (half / 2) + a % P : i0 + a; };
+    const int64_t b = active ? t / seq : 0;
+    const int64_t s = active ? t - b * seq : 0;
+    // The group's heads, split into HS contiguous runs, one per subgroup.
+    const int g_begin = blockIdx.y * heads_per_group;
+    int g_end = g_begin + heads_per_group;
+    if (g_end > nq + nk) g_end = nq + nk;
+    const int per_sub = (g_end - g_begin + HS - 1) / HS;
+    const int h_begin = g_begin + sub * per_sub;
+    const int h_end = h_begin + per_sub < g_end ? h_begin + per_sub : g_end;
+
+    auto row_of = [&](int hh) -> T* {
+        return hh < nq ? q + ((size_t)(b * nq + hh) * (size_t)seq + (size_t)s) * (size_t)head_dim
+                       : k + ((size_t)(b * nk + (hh - nq)) * (size_t)seq + (size_t)s) * (size_t)head_dim;
+    };
+    auto load_batch = [&](int h0, RawRun<T, L> (&buf)[U][R]) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            if (h0 + u < h_end) {
+                const T* row = row_of(h0 + u);
+#pragma unroll
+                for (int r = 0; r < R; ++r) buf[u][r].load(row + off[r]);
+            }
+        }
+    };
+    auto rotate_batch = [&](int h0, const RawRun<T, L> (&buf)[U][R], const float (&cs)[NA], const float (&sn)[NA]) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            if (h0 + u < h_end) {
+                T* row = row_of(h0 + u);
+                if constexpr (!INTERLEAVED) {
+                    float x0[P], x1[P], o0[P], o1[P];
+                    buf[u][0].to_f32(x0);
+                    buf[u][1].to_f32(x1);
+#pragma unroll
+                    for (int j = 0; j < P; ++j) {
+                        o0[j] = x0[j] * cs[j] - x1[j] * sn[j];
+                        o1[j] = x1[j] * cs[j] + x0[j] * sn[j];
+                    }
+                    store_run<T, P>(row + off[0], o0);
+                    store_run<T, P>(row + off[1], o1);
+                } else {
+#pragma unroll
+                    for (int r = 0; r < R; ++r) {
+                        float x[2 * P], o[2 * P];
+                        buf[u][r].to_f32(x);
+#pragma unroll
+                        for (int j = 0; j < P; ++j) {
+                            o[2 * j] = x[2 * j] * cs[r * P + j] - x[2 * j + 1] * sn[r * P + j];
+                            o[2 * j + 1] = x[2 * j + 1] * cs[r * P + j] + x[2 * j] * sn[r * P + j];
+                        }
+                        store_run<T, 2 * P>(row + off[r], o);
+                    }
+                }
+            }
+        }
+    };
+
+    // The position load goes first: loads complete in order, so staging it
+    // waits for it alone while the first two batches stay in flight.
+    float cs[NA], sn[NA];
+    RawRun<T, L> ba[U][R], bb[U][R];
+    if constexpr (PAIR_MAJOR) {
+        int32_t pv = 0;
+        if (tid < toks_per_block && t_first + tid < ntok) pv = pos[(t_first + tid) % seq];
+        if (active) {
+            load_batch(h_begin, ba);
+            load_batch(h_begin + U, bb);
+        }
+        if (tid < toks_per_block) pos_s[tid] = pv;
+        if (tid < 24) inv_pio4[tid] = kInvPio4.w[tid];
+        __syncthreads();
+
+        const int stride = toks_per_block + 1;
+        const int n_angles = toks_per_block * half;
+#pragma unroll
+        for (int j = 0; j < (NA + HS - 1) / HS; ++j) {
+            const int a = j * kThreads * HS + tid;
+            if (a < n_angles) {
+                const int pair = a / toks_per_block;
+                const int tk = a - pair * toks_per_block;
+                const float p = (float)pos_s[tk] / pos_scale;
+                const float freq = p / den.v[pair];
+                float sv, cv;
+                glibc_sincosf_tab(freq, inv_pio4, &sv, &cv);
+                cs_s[pair * stride + tk] = cv;
+                sn_s[pair * stride + tk] = sv;
+            }
+        }
+        __syncthreads();
+        if (!active) return;
+#pragma unroll
+        for (int a = 0; a < NA; ++a) {
+            cs[a] = cs_s[pair_of(a) * stride + tib];
+            sn[a] = sn_s[pair_of(a) * stride + tib];
+        }
+    } else {
+        int32_t ps = 0;
+        if (active) {
+            ps = pos[s];
+            load_batch(h_begin, ba);
+            load_batch(h_begin + U, bb);
+        }
+        if (tid < 24) inv_pio4[tid] = kInvPio4.w[tid];
+        __syncthreads();
+        if (!active) return;
+        const float p = (float)ps / pos_scale;
+#pragma unroll
+        for (int a = 0; a < NA; ++a) {
+            const float freq = p / den.v[pair_of(a)];
+            glibc_sincosf_tab(freq, inv_pio4, &sn[a], &cs[a]);
+        }
     }
 
-    const int h_begin = blockIdx.y * heads_per_group;
-    int h_end = h_begin + heads_per_group;
-    if (h_end > nq + nk) h_end = nq + nk;
-    for (int hh = h_begin; hh < h_end; ++hh) {
-        T* row = hh < nq ? q + ((size_t)(b * nq + hh) * (size_t)seq + (size_t)s) * (size_t)head_dim
-                         : k + ((size_t)(b * nk + (hh - nq)) * (size_t)seq + (size_t)s) * (size_t)head_dim;
-        if constexpr (!INTERLEAVED) {
-            float x0[P], x1[P];
-            if constexpr (P == 1) {
-                x0[0] = widen(row[i0]);
-                x1[0] = widen(row[i0 + half]);
-            } else {
-                load_f32<T, P, true>(row + i0, x0);
-                load_f32<T, P, true>(row + i0 + half, x1);
-            }
-            float o0[P], o1[P];
-#pragma unroll
-            for (int j = 0; j < P; ++j) {
-                o0[j] = x0[j] * cs[j] - x1[j] * sn[j];
-                o1[j] = x1[j] * cs[j] + x0[j] * sn[j];
-            }
-            if constexpr (P == 1) {
-                row[i0] = narrow<T>(o0[0]);
-                row[i0 + half] = narrow<T>(o1[0]);
-            } else {
-                store_f32<T, P, true>(row + i0, o0);
-                store_f32<T, P, true>(row + i0 + half, o1);
-            }
-        } else {
-            float x[2 * P];
-            load_f32<T, 2 * P, true>(row + 2 * i0, x);
-            float o[2 * P];
-#pragma unroll
-            for (int j = 0; j < P; ++j) {
-                o[2 * j] = x[2 * j] * cs[j] - x[2 * j + 1] * sn[j];
-                o[2 * j + 1] = x[2 * j + 1] * cs[j] + x[2 * j] * sn[j];
-            }
-            store_f32<T, 2 * P, true>(row + 2 * i0, o);
-        }
+    // Two batches alternate: while one is rotated and stored, the other's
+    // loads are in flight.
+    for (int h0 = h_begin; h0 < h_end; h0 += 2 * U) {
+        rotate_batch(h0, ba, cs, sn);
+        if (h0 + 2 * U < h_end) load_batch(h0 + 2 * U, ba);
+        if (h0 + U >= h_end) break;
+        rotate_batch(h0 + U, bb, cs, sn);
+        if (h0 + 3 * U < h_end) load_batch(h0 + 3 * U, bb);
     }
 }
 
@@ -273,35 +421,49 @@ __global__ __launch_bounds__(kThreads) void rope_kv_kernel(const T* q, T* qo, in
 #undef SPH_LOAD_HEAD
 }
 
-// Blocks to aim for in total (head groups × token blocks). Each head group
-// recomputes its sin/cos, so fewer, longer-running groups stream faster, down
-// to the point where too few waves are left in flight. Measured optimum at the
-// Llama-3-8B shape on MI355X (32 + 8 heads × 8192 tokens × 128):
-//   f32 NEOX 58.4 µs at 512 (60.8 at 1024), interleaved 58.9 at 512;
-//   f16 NEOX 34.3 µs at 512 (35.8 at 1024), interleaved 34.3 at 1536
-//   (35.4 at 1024, 41.1 at 512, where one group holds all 40 heads).
+// Launch shape of rope_kernel per storage type and layout, chosen by
+// round-robin timing at the Llama-3-8B shape on MI355X (32 + 8 heads × 8192
+// tokens × 128, in place), beside an in-place 16-byte copy of the same bytes
+// (two launches, q and k) as the ceiling; medians of 12 rounds on one box:
+//  - half types: NEOX P = 4 (8-byte runs), interleaved split with P = 2
+//    (two 8-byte runs), U = 2, pair-major angles, 2048 units in all (four
+//    head groups, each recomputing its angles: more waves in flight outweigh
+//    the repeated angle work). f16 NEOX 31.0 µs, interleaved 30.6 µs, copy
+//    30.2 µs. U = 4 cost 2–3 µs, P = 8 or one run of P = 4 0.3–4 µs.
+//  - f32: P = 4 NEOX, interleaved split with P = 2 (16-byte runs), U = 1,
+//    per-thread angles, 512 units (one group holds all 40 heads). NEOX
+//    57.5 µs, interleaved 58.0 µs (one 16-byte run: 61.2 µs), copy 56.3 µs.
+// Boxes differ by up to ±5 % in absolute speed; the ordering held on each.
 template <typename T, bool IL>
-constexpr int rope_grid_target() {
-    return sizeof(T) == 4 ? 512 : (IL ? 1536 : 512);
-}
+struct RopeShape {
+    static constexpr bool kHalf = sizeof(T) == 2;
+    static constexpr int P = IL ? 2 : 4;  // preferred pairs per run
+    static constexpr bool kSplit = IL;
+    static constexpr int U = kHalf ? 2 : 1;
+    static constexpr bool kPairMajor = kHalf;
+    static constexpr int HS = 1;
+    static constexpr int kTarget = kHalf ? 2048 : 512;
+};
 
-template <typename T, int P, bool IL>
+// target: 256-thread units to aim for in all (token blocks × HS × head groups).
+template <typename T, int P, bool IL, bool SPLIT = RopeShape<T, IL>::kSplit, int U = RopeShape<T, IL>::U,
+          bool PM = RopeShape<T, IL>::kPairMajor, int HS = RopeShape<T, IL>::HS>
 int launch_rope_p(T* q, int nq, T* k, int nk, const int32_t* pos, int64_t ntok, int64_t seq, int head_dim,
-                  int half, float pos_scale, const DenTable& den, hipStream_t stream) {
-    const int lanes_per_tok = half / P;
+                  int half, float pos_scale, const DenTable& den, hipStream_t stream,
+                  int target = RopeShape<T, IL>::kTarget) {
+    const int lanes_per_tok = half / (SPLIT ? 2 * P : P);
     const int toks_per_block = kThreads / lanes_per_tok;
     const int64_t blocks_x = (ntok + toks_per_block - 1) / toks_per_block;
     const int heads = nq + nk;
-    const int target = rope_grid_target<T, IL>();
-    int groups = (int)((target + blocks_x - 1) / blocks_x);
+    int groups = (int)((target + blocks_x * HS - 1) / (blocks_x * HS));
     if (groups > heads) groups = heads;
     if (groups < 1) groups = 1;
     const int heads_per_group = (heads + groups - 1) / groups;
     groups = (heads + heads_per_group - 1) / heads_per_group;
     if (blocks_x > INT32_MAX) return SPH_EINVAL;
     const dim3 grid((unsigned)blocks_x, (unsigned)groups);
-    rope_kernel<T, P, IL><<<grid, kThreads, 0, stream>>>(q, nq, k, nk, pos, ntok, seq, head_dim, half, lanes_per_tok,
-                                                         toks_per_block, heads_per_group, pos_scale, den);
+    rope_kernel<T, P, IL, SPLIT, U, PM, HS><<<grid, kThreads * HS, 0, stream>>>(
+        q, nq, k, nk, pos, ntok, seq, head_dim, half, lanes_per_tok, toks_per_block, heads_per_group, pos_scale, den);
     return launch_status();
 }
 
@@ -320,7 +482,9 @@ int launch_rope_kv_p(const T* q, T* qo, int nq, const T* k, const T* v, int nkv,
     const int toks_per_block = kThreads / lanes_per_tok;
     const int64_t blocks_x = (seq + toks_per_block - 1) / toks_per_block;
     const int heads = nq + nkv;
-    const int target = rope_grid_target<T, IL>();
+    // Blocks to aim for (head groups × token blocks), swept at the Llama-3-8B
+    // shape: f32 512; half types 512 NEOX, 1536 interleaved.
+    const int target = sizeof(T) == 4 ? 512 : (IL ? 1536 : 512);
     int groups = (int)((target + blocks_x - 1) / blocks_x);
     if (groups > heads) groups = heads;
     if (groups < 1) groups = 1;
@@ -397,20 +561,30 @@ int launch_rope(void* qv, int nq, void* kv, int nk, int layout, const int32_t* p
         if (elems_per_access > 1 && bytes % 4 != 0) return false;
         return aligned(q, bytes < 16 ? bytes : 16) && (k == nullptr || aligned(k, bytes < 16 ? bytes : 16));
     };
-    constexpr int V = vec16<T>::n;  // elements per 16-byte access
     if (layout == SPH_ROPE_NEOX) {
-        if (ok(V, V)) return launch_rope_p<T, V, false>(q, nq, k, nk, pos, ntok, seq, head_dim, half, pos_scale, den, stream);
-        if (ok(V / 2, V / 2)) return launch_rope_p<T, V / 2, false>(q, nq, k, nk, pos, ntok, seq, head_dim, half, pos_scale, den, stream);
-        if constexpr (V / 4 >= 2) {
-            if (ok(V / 4, V / 4)) return launch_rope_p<T, V / 4, false>(q, nq, k, nk, pos, ntok, seq, head_dim, half, pos_scale, den, stream);
+        // The preferred P (a run of P elements per access), then narrower runs.
+        constexpr int PN = RopeShape<T, false>::P;
+        if (ok(PN, PN)) return launch_rope_p<T, PN, false>(q, nq, k, nk, pos, ntok, seq, head_dim, half, pos_scale, den, stream);
+        if constexpr (PN / 2 >= 2) {
+            if (ok(PN / 2, PN / 2)) return launch_rope_p<T, PN / 2, false>(q, nq, k, nk, pos, ntok, seq, head_dim, half, pos_scale, den, stream);
+        }
+        if constexpr (PN / 4 >= 2) {
+            if (ok(PN / 4, PN / 4)) return launch_rope_p<T, PN / 4, false>(q, nq, k, nk, pos, ntok, seq, head_dim, half, pos_scale, den, stream);
         }
         return launch_rope_p<T, 1, false>(q, nq, k, nk, pos, ntok, seq, head_dim, half, pos_scale, den, stream);
     }
-    if (ok(V / 2, V)) return launch_rope_p<T, V / 2, true>(q, nq, k, nk, pos, ntok, seq, head_dim, half, pos_scale, den, stream);
+
+    // Interleaved: split runs (two per thread, from both halves of the pairs)
+    // when half divides into them, else one run per thread.
+    constexpr int PI = RopeShape<T, true>::P;
+    if (half % (2 * PI) == 0 && ok(PI, 2 * PI))
+        return launch_rope_p<T, PI, true, true>(q, nq, k, nk, pos, ntok, seq, head_dim, half, pos_scale, den, stream);
+    constexpr int V = vec16<T>::n;  // elements per 16-byte access
+    if (ok(V / 2, V)) return launch_rope_p<T, V / 2, true, false>(q, nq, k, nk, pos, ntok, seq, head_dim, half, pos_scale, den, stream);
     if constexpr (V / 4 >= 1) {
-        if (ok(V / 4, V / 2)) return launch_rope_p<T, V / 4, true>(q, nq, k, nk, pos, ntok, seq, head_dim, half, pos_scale, den, stream);
+        if (ok(V / 4, V / 2)) return launch_rope_p<T, V / 4, true, false>(q, nq, k, nk, pos, ntok, seq, head_dim, half, pos_scale, den, stream);
     }
-    return launch_rope_p<T, 1, true>(q, nq, k, nk, pos, ntok, seq, head_dim, half, pos_scale, den, stream);
+    return launch_rope_p<T, 1, true, false>(q, nq, k, nk, pos, ntok, seq, head_dim, half, pos_scale, den, stream);
 }
 
 }  // namespace

@@ -58,13 +58,14 @@ __device__ __forceinline__ void vstore(V* p, V v) {
     else *p = v;
 }
 
-// Load N consecutive elements of T (N * sizeof(T) a multiple of 4 bytes and
-// the address aligned to min(16, N * sizeof(T))) into f32 registers.
+// Raw 32-bit words of N consecutive elements of T: N * sizeof(T) a multiple
+// of 4 bytes, the address aligned to min(16, N * sizeof(T)).
+template <typename T, int N> struct words_of { static constexpr int n = N * (int)sizeof(T) / 4; };
+
 template <typename T, int N, bool NT = false>
-__device__ __forceinline__ void load_f32(const T* __restrict__ p, float (&v)[N]) {
+__device__ __forceinline__ void load_words(const T* __restrict__ p, uint32_t (&raw)[words_of<T, N>::n]) {
     constexpr int bytes = N * (int)sizeof(T);
     static_assert(bytes % 4 == 0, "vector access must be whole dwords");
-    uint32_t raw[bytes / 4];
     if constexpr (bytes % 16 == 0) {
 #pragma unroll
         for (int c = 0; c < bytes / 16; ++c) {
@@ -81,6 +82,10 @@ __device__ __forceinline__ void load_f32(const T* __restrict__ p, float (&v)[N])
 #pragma unroll
         for (int c = 0; c < bytes / 4; ++c) raw[c] = vload<NT>(reinterpret_cast<const uint32_t*>(p) + c);
     }
+}
+
+template <typename T, int N>
+__device__ __forceinline__ void words_to_f32(const uint32_t (&raw)[words_of<T, N>::n], float (&v)[N]) {
     if constexpr (sizeof(T) == 4) {
 #pragma unroll
         for (int i = 0; i < N; ++i) v[i] = __uint_as_float(raw[i]);
@@ -93,12 +98,8 @@ __device__ __forceinline__ void load_f32(const T* __restrict__ p, float (&v)[N])
     }
 }
 
-// Store N f32 values as consecutive elements of T (same alignment rule).
-template <typename T, int N, bool NT = false>
-__device__ __forceinline__ void store_f32(T* __restrict__ p, const float (&v)[N]) {
-    constexpr int bytes = N * (int)sizeof(T);
-    static_assert(bytes % 4 == 0, "vector access must be whole dwords");
-    uint32_t raw[bytes / 4];
+template <typename T, int N>
+__device__ __forceinline__ void f32_to_words(const float (&v)[N], uint32_t (&raw)[words_of<T, N>::n]) {
     if constexpr (sizeof(T) == 4) {
 #pragma unroll
         for (int i = 0; i < N; ++i) raw[i] = __float_as_uint(v[i]);
@@ -107,6 +108,12 @@ __device__ __forceinline__ void store_f32(T* __restrict__ p, const float (&v)[N]
         for (int i = 0; i < N; i += 2)
             raw[i / 2] = (uint32_t)narrow<T>(v[i]).bits | ((uint32_t)narrow<T>(v[i + 1]).bits << 16);
     }
+}
+
+template <typename T, int N, bool NT = false>
+__device__ __forceinline__ void store_words(T* __restrict__ p, const uint32_t (&raw)[words_of<T, N>::n]) {
+    constexpr int bytes = N * (int)sizeof(T);
+    static_assert(bytes % 4 == 0, "vector access must be whole dwords");
     if constexpr (bytes % 16 == 0) {
 #pragma unroll
         for (int c = 0; c < bytes / 16; ++c) {
@@ -123,6 +130,22 @@ __device__ __forceinline__ void store_f32(T* __restrict__ p, const float (&v)[N]
 #pragma unroll
         for (int c = 0; c < bytes / 4; ++c) vstore<NT>(reinterpret_cast<uint32_t*>(p) + c, raw[c]);
     }
+}
+
+// Load N consecutive elements of T (same alignment rule) into f32 registers.
+template <typename T, int N, bool NT = false>
+__device__ __forceinline__ void load_f32(const T* __restrict__ p, float (&v)[N]) {
+    uint32_t raw[words_of<T, N>::n];
+    load_words<T, N, NT>(p, raw);
+    words_to_f32<T, N>(raw, v);
+}
+
+// Store N f32 values as consecutive elements of T (same alignment rule).
+template <typename T, int N, bool NT = false>
+__device__ __forceinline__ void store_f32(T* __restrict__ p, const float (&v)[N]) {
+    uint32_t raw[words_of<T, N>::n];
+    f32_to_words<T, N>(v, raw);
+    store_words<T, N, NT>(p, raw);
 }
 
 template <int CTRL>

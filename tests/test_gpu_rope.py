@@ -81,12 +81,34 @@ def test_rope_matches_wgpu_test_vectors(dev, orc, H, S, D, rd):
     (1, 3, 0, 5, 80, 32),        # Phi partial rotary
     (1, 2, 1, 3, 6, 6),          # odd half: scalar path
     (1, 2, 2, 4, 12, 8),
+    (1, 3, 2, 37, 16, 12),       # half = 6: interleaved one run per thread (no split), NEOX with 2-pair runs
+    (1, 5, 1, 300, 40, 40),      # half = 20: more tokens than one block, split interleaved
 ])
 def test_rope_shapes(dev, orc, dtype, interleaved, B, Hq, Hk, S, D, rd):
     positions = [int(p) for p in np.random.default_rng(S).integers(0, 8192, S)] if S > 1 else [4095]
     base = 1e6 if D == 64 else 5e5
     print(f"case rope {dtype} il={interleaved} {B},{Hq},{Hk},{S},{D},{rd}", flush=True)
     _run(dev, orc, dtype, B, Hq, Hk, S, D, rd, base, positions, interleaved)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16], ids=lambda d: str(d).split(".")[-1])
+@pytest.mark.parametrize("interleaved", [False, True], ids=["neox", "interleaved"])
+@pytest.mark.parametrize("offset", [1, 2, 4])
+def test_rope_unaligned_rows(dev, orc, dtype, interleaved, offset):
+    """q and k starting `offset` elements into their buffers: narrower accesses than the 16-byte paths."""
+    B, Hq, Hk, S, D = 1, 5, 3, 11, 32
+    g = torch.Generator(device=dev).manual_seed(offset)
+    bq = torch.randn(offset + B * Hq * S * D, generator=g, device=dev).to(dtype)
+    bk = torch.randn(offset + B * Hk * S * D, generator=g, device=dev).to(dtype)
+    q, k = bq[offset:].view(B, Hq, S, D), bk[offset:].view(B, Hk, S, D)
+    q32, k32 = widen(q.contiguous(), orc).reshape(B, Hq, S, D), widen(k.contiguous(), orc).reshape(B, Hk, S, D)
+    positions = [int(p) for p in np.random.default_rng(offset).integers(0, 8192, S)]
+    print(f"case rope unaligned {dtype} il={interleaved} offset {offset}", flush=True)
+    ops.rope_(q, k, torch.tensor(positions, dtype=torch.int32, device=dev), 5e5, interleaved=interleaved)
+    torch.cuda.synchronize()
+    what = f"rope unaligned {dtype} il={interleaved} offset {offset}"
+    _check(q, orc.apply_rope_partial_scaled(q32, positions, 5e5, D, 1.0, interleaved), orc, what + " q")
+    _check(k, orc.apply_rope_partial_scaled(k32, positions, 5e5, D, 1.0, interleaved), orc, what + " k")
 
 
 def test_rope_linear_position_scale(dev, orc):
