@@ -158,7 +158,7 @@ template <int OP> constexpr bool binary_op() { return OP == OP_ADD || OP == OP_M
 // B_SCALAR_B / B_SCALAR_A read element 0 of the broadcast operand. `out` may
 // alias a full-length input: each element is read before it is written, by
 // the same thread.
-template <typename T, int OP, int BC>
+template <typename T, int OP, int BC, int U = kUnroll>
 __global__ __launch_bounds__(kThreads) void ew_vec(const T* a, const T* b, T* out, int64_t nvec) {
     constexpr int E = vec16<T>::n;
     __shared__ uint64_t exp_tab[needs_exp_table<OP, T>() ? 32 : 1];
@@ -166,11 +166,11 @@ __global__ __launch_bounds__(kThreads) void ew_vec(const T* a, const T* b, T* ou
     float sa = 0.0f, sb = 0.0f;
     if constexpr (BC == B_SCALAR_A) sa = widen(a[0]);
     if constexpr (BC == B_SCALAR_B) sb = widen(b[0]);
-    const int64_t stride = (int64_t)gridDim.x * kThreads * kUnroll;
-    for (int64_t base = (int64_t)blockIdx.x * kThreads * kUnroll + threadIdx.x; base < nvec; base += stride) {
-        float va[kUnroll][E], vb[kUnroll][E];
+    const int64_t stride = (int64_t)gridDim.x * kThreads * U;
+    for (int64_t base = (int64_t)blockIdx.x * kThreads * U + threadIdx.x; base < nvec; base += stride) {
+        float va[U][E], vb[U][E];
 #pragma unroll
-        for (int u = 0; u < kUnroll; ++u) {
+        for (int u = 0; u < U; ++u) {
             const int64_t i = base + (int64_t)u * kThreads;
             if (i < nvec) {
                 if constexpr (BC != B_SCALAR_A) load_f32<T, E, true>(a + i * E, va[u]);
@@ -178,7 +178,7 @@ __global__ __launch_bounds__(kThreads) void ew_vec(const T* a, const T* b, T* ou
             }
         }
 #pragma unroll
-        for (int u = 0; u < kUnroll; ++u) {
+        for (int u = 0; u < U; ++u) {
             const int64_t i = base + (int64_t)u * kThreads;
             if (i < nvec) {
                 float o[E];
@@ -316,6 +316,7 @@ __global__ __launch_bounds__(kThreads) void gelu_lut_build(int which) {
 }
 
 constexpr int kLutThreads = 512;
+constexpr int kLutBatch = 2;  // 16-byte vectors per thread per trip
 
 template <typename T>
 __device__ __forceinline__ uint32_t gelu_lookup(const uint16_t* tab, uint32_t h) {
@@ -323,12 +324,15 @@ __device__ __forceinline__ uint32_t gelu_lookup(const uint16_t* tab, uint32_t h)
 }
 
 // Two 512-thread blocks per CU, both resident (LDS-bound), each staging the
-// band table in LDS once and then streaming 16-byte vectors, grid-stride.
-// Measured on MI355X at [8192, 10240] f16: 60.9 µs, against 61.6 with four
-// blocks per CU (the table staged twice per slot), 58.7 for a table-free copy
-// of the same loop shape, and 63-65 with 1024-thread blocks or with the next
-// trip's loads issued ahead (software pipelining).
-template <typename T>
+// band table in LDS once and then streaming 16-byte vectors, grid-stride, U
+// per thread per trip. Measured on MI355X at [8192, 10240] f16, round-robin
+// with a 16-byte copy of the same bytes (53.9 µs in this loop shape, 53.1 as
+// a flat grid): U = 2 56.8 µs, U = 3 58.6, U = 4 59.4, U = 1 62.8; four
+// blocks per CU (the table staged twice per slot) 59.4 at U = 2; the first
+// trip's loads issued before the table is staged: no change. Earlier:
+// 1024-thread blocks or the next trip's loads issued ahead (software
+// pipelining) 63-65.
+template <typename T, int U>
 __global__ __launch_bounds__(kLutThreads) void gelu_lut_apply(const uint16_t* in, uint16_t* out, int64_t nvec, int which) {
     __shared__ __align__(16) uint16_t tab[kLutEntries];
     {
@@ -340,7 +344,6 @@ __global__ __launch_bounds__(kLutThreads) void gelu_lut_apply(const uint16_t* in
     __syncthreads();
     const u32x4* vin = reinterpret_cast<const u32x4*>(in);
     u32x4* vout = reinterpret_cast<u32x4*>(out);
-    constexpr int U = 4;
     const int64_t stride = (int64_t)gridDim.x * kLutThreads * U;
     for (int64_t base = (int64_t)blockIdx.x * kLutThreads * U + threadIdx.x; base < nvec; base += stride) {
         u32x4 q[U];
@@ -409,7 +412,7 @@ int gelu_half(const uint16_t* x, uint16_t* out, int which, int64_t n, hipStream_
     if (aligned(x, 16) && aligned(out, 16)) {
         const int64_t nvec = n / 8;
         if (nvec > 0) {
-            gelu_lut_apply<T><<<grid_for(nvec, (int64_t)kLutThreads * 4, 2 * cus), kLutThreads, 0, stream>>>(x, out, nvec, which);
+            gelu_lut_apply<T, kLutBatch><<<grid_for(nvec, (int64_t)kLutThreads * kLutBatch, 2 * cus), kLutThreads, 0, stream>>>(x, out, nvec, which);
             if (launch_status() != SPH_OK) return SPH_EHIP;
         }
         done = nvec * 8;
