@@ -290,35 +290,66 @@ void launch_vec(int W, dim3 grid, int threads, const TX* xp, TX* rp, const TW* w
     }
 }
 
+// One launch of the vector kernel with VPT 16-byte vectors per lane: W waves
+// per row (the fewest that cover it), LOOP blocks capped at `waves_per_cu`
+// resident waves per CU (at least one block). Returns false, launching
+// nothing, when a row is wider than 16 waves cover.
+template <typename TX, typename TW, typename TO, int KIND, int VPT, bool LOOP>
+bool launch_shape(const TX* xp, TX* rp, const TW* wp, const TW* bp, TO* op, int64_t nr, int dim, float eps,
+                  int waves_per_cu, hipStream_t stream) {
+    constexpr int E = vec16<TX>::n;
+    const int64_t nvec = dim / E;
+    int W = 1;
+    while (W < 16 && nvec > (int64_t)kWave * VPT * W) W *= 2;
+    if (nvec > (int64_t)kWave * VPT * W) return false;
+    const int rpb = W >= 4 ? 1 : 4 / W;
+    const int threads = W >= 4 ? kWave * W : 256;
+    int64_t nb = (nr + rpb - 1) / rpb;
+    if (LOOP) {
+        const int cus = device_cu_count();
+        const int per_cu = waves_per_cu / (threads / kWave);
+        if (cus > 0) {
+            const int64_t cap = (int64_t)cus * (per_cu > 1 ? per_cu : 1);
+            if (nb > cap) nb = cap;
+        }
+    }
+    launch_vec<TX, TW, TO, KIND, VPT, LOOP>(W, dim3((unsigned)nb), threads, xp, rp, wp, bp, op, nr, dim, eps, stream);
+    return true;
+}
+
+// Launch shapes, measured at 16384 x 4096 on MI355X (round-robin medians on
+// two boxes; one-block-per-row shapes listed as VPT):
+//  - fused add + RMSNorm: row-looping blocks, one vector per lane, 16 (f32)
+//    or 8 (half) resident waves per CU: f32 171.8 µs (one block per row,
+//    VPT 2: 175.0), f16 85.4 µs (VPT 1: 87.6), bf16 85.8 µs (84.9);
+//  - plain RMSNorm, half: row-looping, four vectors per lane, 8 resident
+//    waves per CU: f16 44.6 µs, bf16 47.0 (one block per row: 47.0, 48.7;
+//    two vectors per lane looping: 44.8, 54.5);
+//  - plain RMSNorm, f32: one block per row, two vectors per lane (85.0 µs;
+//    looping: 86.8);
+//  - LayerNorm: row-looping, 16 resident waves per CU, weight and bias held in
+//    registers (f16 63.8 -> 51.9 µs against one block per row).
+// A row too wide for the looping shape takes the one-block-per-row kernel
+// (twice the values per lane past 16 waves); unaligned rows, or rows wider
+// than that, the generic kernel.
 template <typename TX, typename TW, typename TO, int KIND>
 int launch_rms(const void* x, void* residual, const void* w, const void* bias, void* out, int64_t rows, int64_t dim,
                float eps, hipStream_t stream) {
     if (rows == 0 || dim == 0) return SPH_OK;
     constexpr int E = vec16<TX>::n;
     constexpr bool FUSED = KIND == K_ADD_RMS;
-    // Values per lane (measured at 16384 x 4096 on MI355X): 8 for f32 and for
-    // the fused half kernel, 16 for the other half kernels; twice that for rows
-    // too wide for 16 waves.
-    constexpr int VPT = (sizeof(TX) == 2 && KIND != K_ADD_RMS) ? 2 : 8 / E;
+    constexpr bool HALF = sizeof(TX) == 2;
+    // One-block-per-row (or LayerNorm's looping) shape: values per lane.
+    constexpr int VPT = (HALF && KIND != K_ADD_RMS) ? 2 : 8 / E;
+    constexpr bool kLoop = KIND == K_LAYER;
+    // The looping shape of the RMSNorm kinds (VPT_L = 0: none).
+    constexpr int VPT_L = FUSED ? 1 : (HALF ? 4 : 0);
+    constexpr int kLoopWaves = FUSED && !HALF ? 16 : 8;
     const int64_t nvec = dim / E;
-    int W = 1;
-    while (W < 16 && nvec > (int64_t)kWave * VPT * W) W *= 2;
-    const bool wide = nvec > (int64_t)kWave * VPT * W;  // needs 2 VPT at W = 16
     const bool vec_ok = dim % E == 0 && aligned(x, 16) && aligned(out, 16) &&
                         (!FUSED || aligned(residual, 16)) && (w == nullptr || aligned(w, 16)) &&
                         (bias == nullptr || aligned(bias, 16)) && nvec <= (int64_t)kWave * 2 * VPT * 16 &&
                         dim <= INT32_MAX;
-    const int rpb = W >= 4 ? 1 : 4 / W;
-    const int threads = W >= 4 ? kWave * W : 256;
-    // LayerNorm loops each block over rows (16 resident waves per CU), keeping
-    // weight and bias in registers; the RMSNorm kernels give every block one row.
-    constexpr bool kLoop = KIND == K_LAYER;  // the wide variant never loops (register budget)
-    int64_t max_blocks = INT64_MAX;
-    if (kLoop && !wide) {
-        const int cus = device_cu_count();
-        const int waves_per_block = threads / kWave;  // 4, 8 or 16
-        if (cus > 0) max_blocks = (int64_t)cus * (16 / waves_per_block);
-    }
     // A launch covers at most 2^22 rows, keeping grid x block below 2^32 work-items.
     constexpr int64_t kChunk = int64_t(1) << 22;
     for (int64_t r0 = 0; r0 < rows; r0 += kChunk) {
@@ -330,13 +361,16 @@ int launch_rms(const void* x, void* residual, const void* w, const void* bias, v
         const TW* bp = static_cast<const TW*>(bias);
         TO* op = static_cast<TO*>(out) + off;
         if (vec_ok) {
-            int64_t nb = (nr + rpb - 1) / rpb;
-            if (nb > max_blocks) nb = max_blocks;
-            const dim3 grid((unsigned)nb);
-            if (!wide)
-                launch_vec<TX, TW, TO, KIND, VPT, kLoop>(W, grid, threads, xp, rp, wp, bp, op, nr, (int)dim, eps, stream);
-            else
-                launch_vec<TX, TW, TO, KIND, 2 * VPT, false>(16, grid, threads, xp, rp, wp, bp, op, nr, (int)dim, eps, stream);
+            bool done = false;
+            if constexpr (VPT_L > 0)
+                done = launch_shape<TX, TW, TO, KIND, VPT_L, true>(xp, rp, wp, bp, op, nr, (int)dim, eps, kLoopWaves,
+                                                                   stream);
+            if (!done)
+                done = launch_shape<TX, TW, TO, KIND, VPT, kLoop>(xp, rp, wp, bp, op, nr, (int)dim, eps, 16, stream);
+            if (!done)  // wider than 16 waves at VPT: twice the values per lane, one block per row
+                done = launch_shape<TX, TW, TO, KIND, 2 * VPT, false>(xp, rp, wp, bp, op, nr, (int)dim, eps, 16,
+                                                                      stream);
+            if (!done) return SPH_EINVAL;  // unreachable: vec_ok bounds the width
         } else {
             rms_rows_generic<TX, TW, TO, KIND><<<dim3((unsigned)nr), 256, 0, stream>>>(xp, rp, wp, bp, op, nr, dim, eps);
         }
