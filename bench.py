@@ -30,13 +30,17 @@ sys.path.insert(0, str(ROOT))
 METRIC = "fused-op HBM GB/s & % of 8 TB/s peak (RMSNorm/RoPE/SwiGLU/embed)"
 PEAK_GBS = 8000.0
 PROFILES = ROOT / "profiles"
+# The headline's kernel instantiation (fused add + RMSNorm, f32, 16 waves per row, one
+# 16-byte vector per lane, row-looping blocks), as rocprofv3 names it.
+HEADLINE_KERNEL = "rms_rows_vec<float, float, float, 1, 16, 1, true>"
 
 
 def parse():
     p = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=50)
-    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--warmup", type=int, default=100, help="untimed headline launches before the timed ones "
+                   "(100: ~17 ms, enough for the GPU to reach steady clocks)")
     p.add_argument("--no-ops", action="store_true", help="skip the per-op table")
     p.add_argument("--only", default=None, help="comma list of op names for the per-op table")
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU-baseline time budget")
@@ -88,6 +92,27 @@ def time_region(torch, fn, sets, warmup: int, steps: int):
 
 def median(xs):
     return float(np.median(np.asarray(xs)))
+
+
+def warm(torch, fn, sets, min_launches: int = 3, min_ms: float = 25.0):
+    """Untimed launches until at least `min_launches` ran and `min_ms` of GPU time passed, so that
+    the row is timed at steady clocks (the GPU idles while the CPU columns are measured)."""
+    t0 = time.perf_counter()
+    i = 0
+    while True:
+        fn(sets[i % len(sets)])
+        i += 1
+        if i >= min_launches and i % len(sets) == 0:
+            torch.cuda.synchronize()
+            if (time.perf_counter() - t0) * 1e3 >= min_ms:
+                return
+
+
+def time_regions(torch, fn, sets, regions: int = 5, steps: int = 20):
+    """Steady-state per-launch ms: after `warm`, `regions` regions of `steps` back-to-back launches,
+    each between one HIP event pair; the median region / steps."""
+    warm(torch, fn, sets)
+    return median([time_region(torch, fn, sets, 0, steps)[0] for _ in range(regions)]) / steps
 
 
 def cpu_time(fn, budget_s: float, min_reps: int = 1):
@@ -181,8 +206,9 @@ def engine_rows(torch, dev, table, vocab):
 
 
 def op_table(torch, ops, dev, only=None, cpu_budget=0.0):
-    """Per-op GB/s at each configuration shape (20 back-to-back launches after 3 warm-ups between one
-    event pair; latency-bound rows: the median of 20 individually bracketed launches), and beside it
+    """Per-op GB/s at each configuration shape (after >= 25 ms of warm-up launches, the median of 5
+    regions of 20 back-to-back launches between one event pair; latency-bound rows: the median of 20
+    individually bracketed launches), and beside it
     the oracle — the reference's algorithm restated in C, one thread — on a sample of the same shape's
     rows (or tokens, ids), `cpu_budget` seconds each, reported in the same units."""
     import sapient_amd._lib as L
@@ -202,10 +228,11 @@ def op_table(torch, ops, dev, only=None, cpu_budget=0.0):
             return
         sets = make_sets()
         if latency_bound:  # one call's latency: the median of 20 event-bracketed launches
-            per, _ = time_launches(torch, fn, sets, 3, 20)
+            warm(torch, fn, sets)
+            per, _ = time_launches(torch, fn, sets, 0, 20)
             ms = median(per)
-        else:  # throughput: 20 back-to-back launches between one event pair
-            ms = time_region(torch, fn, sets, 3, 20)[0] / 20
+        else:  # throughput: the median of 5 regions of 20 back-to-back launches between one event pair
+            ms = time_regions(torch, fn, sets)
         gbs = alg_bytes / (ms * 1e-3) / 1e9
         row = {"op": name, "shape": shape_desc, "dtype": dtype_s, "us": round(ms * 1e3, 2),
                "GB/s": round(gbs, 1), "pct_peak": round(100 * gbs / PEAK_GBS, 1),
@@ -231,6 +258,15 @@ def op_table(torch, ops, dev, only=None, cpu_budget=0.0):
             lambda s, w=w: ops.add_rms_norm(s[0], s[1], w, 1e-5, out=s[2]),
             cpu=lambda: (lambda x=nrm(256, dim), r=nrm(256, dim), w=nrm(dim, scale=0.1, mean=1.0):
                          orc.add_rms_norm(x, r, w, 1e-5), 256))
+    # Plain RMSNorm at the same width (the norm the fused kernel's second half is)
+    for dt, tag in ((f32, "f32"), (f16, "f16"), (bf16, "bf16")):
+        w = gen(torch, (dim,), 3, dev, f32, 0.1, 1.0)
+        es = 4 if dt == f32 else 2
+        run("rms_norm", f"{rows}x{dim}", tag + " (f32 w)", 2 * rows * dim * es + dim * 4, rows, "rows",
+            lambda dt=dt: [(gen(torch, (rows, dim), 20 + i, dev, dt), torch.empty(rows, dim, device=dev, dtype=dt))
+                           for i in range(3 if dt == f32 else 5)],
+            lambda s, w=w: ops.rms_norm(s[0], w, 1e-5, out=s[1]),
+            cpu=lambda: (lambda x=nrm(256, dim), w=nrm(dim, scale=0.1, mean=1.0): orc.rms_norm(x, w, 1e-5), 256))
     # C3: RoPE, Q 32 + K 8 heads, T 8192, head_dim 128, in place
     T, D = 8192, 128
     for dt, tag in ((f32, "f32"), (f16, "f16")):
@@ -453,7 +489,7 @@ def main():
                    "rows_per_s": round(rows / (avg_ms * 1e-3), 1), "pct_of_peak": round(100 * value / PEAK_GBS, 1)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / PEAK_GBS, 4), "traffic": committed_traffic("add_rms_norm_f32_16384x4096"),
-                     "kernel": "rms_rows_vec<float, float, float, 1, 8, 2, false>", "alg_bytes_per_launch": alg_bytes,
+                     "kernel": HEADLINE_KERNEL, "alg_bytes_per_launch": alg_bytes,
                      "avg_launch_us": round(avg_ms * 1e3, 2)},
         "cpu_baseline": cpu,
         "timing": {"region_ms": round(region_ms, 3), "host_wall_ms": round(wall * 1e3, 3),
