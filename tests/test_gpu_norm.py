@@ -75,8 +75,11 @@ def test_rms_norm_shapes(dev, orc, dtype, rows, dim, wmode, outmode):
 
 
 @pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: str(d).split(".")[-1])
-@pytest.mark.parametrize("rows,dim", [(1, 896), (512, 896), (33, 4096), (4, 8192), (3, 8200), (3, 100)])
+@pytest.mark.parametrize("rows,dim", [(1, 896), (512, 896), (33, 4096), (4, 8192), (3, 8200), (2, 12288), (2, 16384),
+                                      (600, 1024), (3, 100)])
 def test_add_rms_norm_shapes(dev, orc, dtype, rows, dim):
+    """Widths that take each launch shape: the row-looping one (up to 4096 f32 / 8192 half
+    elements), one block per row, twice the values per lane past 16 waves, and the generic kernel."""
     print(f"case add_rms_norm {dtype} {rows}x{dim}", flush=True)
     x = _gen((rows, dim), 11 + dim, dev, dtype=dtype)
     r = _gen((rows, dim), 13 + dim, dev, dtype=dtype)
