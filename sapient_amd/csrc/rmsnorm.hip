@@ -327,8 +327,10 @@ bool launch_shape(const TX* xp, TX* rp, const TW* wp, const TW* bp, TO* op, int6
 //    two vectors per lane looping: 44.8, 54.5);
 //  - plain RMSNorm, f32: one block per row, two vectors per lane (85.0 µs;
 //    looping: 86.8);
-//  - LayerNorm: row-looping, 16 resident waves per CU, weight and bias held in
-//    registers (f16 63.8 -> 51.9 µs against one block per row).
+//  - LayerNorm: row-looping with weight and bias held in registers, 8 resident
+//    waves per CU, two (f32) or four (half) vectors per lane: f32 85.9 µs,
+//    f16 47.4 µs (16 waves per CU with two vectors: 88.8, 48.9; one block per
+//    row: 92.0, 55.6).
 // A row too wide for the looping shape takes the one-block-per-row kernel
 // (twice the values per lane past 16 waves); unaligned rows, or rows wider
 // than that, the generic kernel.
@@ -342,8 +344,9 @@ int launch_rms(const void* x, void* residual, const void* w, const void* bias, v
     // One-block-per-row (or LayerNorm's looping) shape: values per lane.
     constexpr int VPT = (HALF && KIND != K_ADD_RMS) ? 2 : 8 / E;
     constexpr bool kLoop = KIND == K_LAYER;
-    // The looping shape of the RMSNorm kinds (VPT_L = 0: none).
-    constexpr int VPT_L = FUSED ? 1 : (HALF ? 4 : 0);
+    // The row-looping shape tried first (VPT_L values per lane, 0: none) and its
+    // resident waves per CU.
+    constexpr int VPT_L = FUSED ? 1 : (HALF ? 4 : (KIND == K_LAYER ? 2 : 0));
     constexpr int kLoopWaves = FUSED && !HALF ? 16 : 8;
     const int64_t nvec = dim / E;
     const bool vec_ok = dim % E == 0 && aligned(x, 16) && aligned(out, 16) &&
