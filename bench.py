@@ -47,7 +47,8 @@ def parse():
     p.add_argument("--op-cpu-seconds", type=float, default=0.3, help="CPU time budget per op-table row")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--profile-run", action="store_true",
-                   help="launch only the headline kernel (warmup + steps) and a calibration copy: for rocprofv3")
+                   help="launch only the headline kernel (warmup + steps) and a calibration copy: for rocprofv3; "
+                        "with --only, the named op-table rows instead of the headline")
     return p.parse_args()
 
 
@@ -205,12 +206,13 @@ def engine_rows(torch, dev, table, vocab):
     return rows
 
 
-def op_table(torch, ops, dev, only=None, cpu_budget=0.0):
+def op_table(torch, ops, dev, only=None, cpu_budget=0.0, profile_launches=0):
     """Per-op GB/s at each configuration shape (after >= 25 ms of warm-up launches, the median of 5
     regions of 20 back-to-back launches between one event pair; latency-bound rows: the median of 20
     individually bracketed launches), and beside it
     the oracle — the reference's algorithm restated in C, one thread — on a sample of the same shape's
-    rows (or tokens, ids), `cpu_budget` seconds each, reported in the same units."""
+    rows (or tokens, ids), `cpu_budget` seconds each, reported in the same units.
+    profile_launches > 0: only launch each selected row that many times (for rocprofv3), time nothing."""
     import sapient_amd._lib as L
     f32, f16, bf16 = torch.float32, torch.float16, torch.bfloat16
     res = []
@@ -227,6 +229,13 @@ def op_table(torch, ops, dev, only=None, cpu_budget=0.0):
         if only and name.split()[0] not in only:
             return
         sets = make_sets()
+        if profile_launches > 0:
+            for i in range(profile_launches):
+                fn(sets[i % len(sets)])
+            torch.cuda.synchronize()
+            del sets
+            torch.cuda.empty_cache()
+            return
         if latency_bound:  # one call's latency: the median of 20 event-bracketed launches
             warm(torch, fn, sets)
             per, _ = time_launches(torch, fn, sets, 0, 20)
@@ -440,6 +449,18 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
 
+    if args.profile_run and args.only:
+        # Launch the selected op-table rows (warmup + steps launches each), then the calibration copy.
+        op_table(torch, ops, dev, set(args.only.split(",")), 0.0, profile_launches=args.warmup + args.steps)
+        rows, dim = 16384, 4096
+        n = 2 * rows * dim
+        a = [gen(torch, (n,), 90 + i, dev, torch.float32) for i in range(2)]
+        o = [torch.empty(n, device=dev) for _ in range(2)]
+        zero = torch.zeros(1, device=dev)
+        time_launches(torch, lambda i: ops.add(a[i], zero, out=o[i]), [0, 1], args.warmup, args.steps)
+        print(json.dumps({"profile_run": True, "ops": args.only, "launches_per_row": args.warmup + args.steps,
+                          "copy_bytes_read": n * 4, "copy_bytes_written": n * 4}))
+        return
     rows, dim, alg_bytes, region_ms, wall = headline(torch, ops, dev, args)
     if args.profile_run:
         # Calibration for the HBM counters: a copy of known size through the

@@ -23,16 +23,15 @@
 //    4 consecutive outputs per step, so every store instruction writes 1 KiB
 //    contiguous (16 bytes per lane), non-temporal (non-temporal stores and the
 //    larger block measured 4.8 → 6.5 TB/s on the Q4_K gather).
-//  - The packed blocks are read in place — no repacking. Q4_K: each step covers
-//    one 256-element super-block; a lane reads the 16-byte header (d, dmin,
-//    12 scale bytes; wave-uniform, so a scalar load) and the dword of nibbles
-//    it needs, and unpacks its (sc, m) pair in registers. A row's loads are
-//    all issued before the first is consumed (16 super-blocks per batch).
-//  - Q4_0 / Q8_0 / Q6_K blocks are 2-byte aligned only (18 / 34 / 210 bytes),
-//    so lanes read them in 16-bit pieces — except Q8_0, whose rows are staged
-//    through LDS with wide loads first (embed_q8_0_staged); Q5_K blocks (176
-//    bytes) stay 16-byte aligned, so a lane reads its header, nibble dword and
-//    high-bit dword whole.
+//  - The packed blocks are consumed as stored — no repacking. Q4_K and Q8_0
+//    rows are first copied into LDS with 16-byte (Q8_0: the widest aligned)
+//    loads, each cache line requested by one lane (embed_q4_k_staged,
+//    embed_q8_0_staged); Q4_K then takes one 256-element super-block per step:
+//    a lane reads the 16-byte header (d, dmin, 12 scale bytes) and the dword of
+//    nibbles it needs and unpacks its (sc, m) pair in registers.
+//  - Q4_0 / Q6_K blocks are 2-byte aligned only (18 / 210 bytes), so lanes
+//    read them in place in 16-bit pieces; Q5_K blocks (176 bytes) stay 16-byte
+//    aligned, so a lane reads its header, nibble dword and high-bit dword whole.
 //  - An id >= vocab zero-fills its row and raises `bad_id_flag`; the table is
 //    never read out of bounds.
 #include "sph_common.h"
@@ -185,11 +184,6 @@ __device__ __forceinline__ void dequant_q4k_lane(const u32x4 hdr, uint32_t qw, i
     for (int c = 0; c < 4; ++c) o[c] = __builtin_fmaf(d1, (float)((nib >> (8 * c)) & 0xFF), -m1);
 }
 
-// Super-blocks of one Q4_K row handled per batch: all their loads are issued
-// before any is consumed, so a wave has 2 x kQ4kBatch requests in flight
-// instead of one dependent load per step.
-constexpr int kQ4kBatch = 16;
-
 template <int DT>
 __global__ __launch_bounds__(kThreads) void embed_rows(const uint8_t* __restrict__ table, int64_t vocab,
                                                        int hidden, int64_t row_bytes, const uint32_t* __restrict__ ids,
@@ -208,35 +202,10 @@ __global__ __launch_bounds__(kThreads) void embed_rows(const uint8_t* __restrict
         return;
     }
     const uint8_t* row = table + (size_t)id * (size_t)row_bytes;
-    if constexpr (DT == SPH_Q4_K) {
-        const int nblk = hidden / 256;
-        const int qoff = 16 + 32 * (lane >> 4) + 4 * (lane & 7);  // this lane's nibble dword in a block
-        for (int b0 = 0; b0 < nblk; b0 += kQ4kBatch) {
-            u32x4 hdr[kQ4kBatch];
-            uint32_t qw[kQ4kBatch];
-#pragma unroll
-            for (int j = 0; j < kQ4kBatch; ++j) {
-                if (b0 + j < nblk) {
-                    const uint8_t* b = row + (size_t)(b0 + j) * 144;
-                    hdr[j] = *reinterpret_cast<const u32x4*>(b);
-                    qw[j] = *reinterpret_cast<const uint32_t*>(b + qoff);
-                }
-            }
-#pragma unroll
-            for (int j = 0; j < kQ4kBatch; ++j) {
-                if (b0 + j < nblk) {
-                    float o[4];
-                    dequant_q4k_lane(hdr[j], qw[j], lane, o);
-                    store4(dst + 256 * (b0 + j) + 4 * lane, o[0], o[1], o[2], o[3]);
-                }
-            }
-        }
-    } else {
-        for (int e4 = lane; e4 < n4; e4 += kWave) {
-            float o[4];
-            dequant4<DT>(row, e4, o);
-            store4(dst + 4 * e4, o[0], o[1], o[2], o[3]);
-        }
+    for (int e4 = lane; e4 < n4; e4 += kWave) {
+        float o[4];
+        dequant4<DT>(row, e4, o);
+        store4(dst + 4 * e4, o[0], o[1], o[2], o[3]);
     }
 }
 
@@ -298,6 +267,73 @@ __global__ __launch_bounds__(kThreads) void embed_q8_0_staged(const uint8_t* __r
         }
         __syncthreads();
     }
+}
+
+// Q4_K rows staged through LDS: a 144-byte super-block spans two cache lines,
+// one of them shared with its neighbour, and per-block loads fetched ~35 % of
+// each row twice (rocprofv3 FETCH_SIZE at 65536 uniform ids of a 128256 x
+// 4096 table: 1.35x the row bytes). A wave instead copies up to
+// kQ4kChunkBlocks super-blocks of its row into LDS with 16-byte loads (every
+// line requested once, by one lane) and dequantizes from there with the same
+// per-lane arithmetic as embed_rows. Every wave of a block runs the same
+// number of chunk steps, so the block barriers are reached by all.
+constexpr int kQ4kChunkBlocks = 16;
+constexpr int kQ4kChunkBytes = kQ4kChunkBlocks * 144;  // a multiple of 16
+
+__global__ __launch_bounds__(kThreads) void embed_q4_k_staged(const uint8_t* __restrict__ table, int64_t vocab,
+                                                              int hidden, int64_t row_bytes,
+                                                              const uint32_t* __restrict__ ids, int64_t n_ids,
+                                                              float* __restrict__ out, int32_t* bad_id_flag) {
+    __shared__ __align__(16) uint8_t stage[kTokPerBlock][kQ4kChunkBytes];
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wv = threadIdx.x / kWave;
+    const int64_t t = (int64_t)blockIdx.x * kTokPerBlock + wv;
+    const bool active = t < n_ids;
+    const uint32_t id = active ? __builtin_amdgcn_readfirstlane(ids[t]) : 0u;
+    const bool valid = active && (int64_t)id < vocab;
+    float* dst = out + (size_t)(active ? t : 0) * (size_t)hidden;
+    if (active && !valid) {
+        for (int e4 = lane; e4 < hidden / 4; e4 += kWave) store4(dst + 4 * e4, 0.f, 0.f, 0.f, 0.f);
+        if (lane == 0 && bad_id_flag != nullptr) *bad_id_flag = 1;
+    }
+    const uint8_t* row = table + (size_t)(valid ? id : 0u) * (size_t)row_bytes;
+    uint8_t* buf = stage[wv];
+    const int nblk = hidden / 256;
+    const int qoff = 16 + 32 * (lane >> 4) + 4 * (lane & 7);  // this lane's nibble dword in a block
+    for (int c0 = 0; c0 < nblk; c0 += kQ4kChunkBlocks) {
+        const int nb = nblk - c0 < kQ4kChunkBlocks ? nblk - c0 : kQ4kChunkBlocks;
+        if (valid) {
+            const uint8_t* src = row + (size_t)c0 * 144;
+            for (int o = lane * 16; o < nb * 144; o += kWave * 16)
+                *reinterpret_cast<u32x4*>(buf + o) = *reinterpret_cast<const u32x4*>(src + o);
+        }
+        __syncthreads();
+        if (valid) {
+            for (int j = 0; j < nb; ++j) {
+                const uint8_t* b = buf + j * 144;
+                float o[4];
+                dequant_q4k_lane(*reinterpret_cast<const u32x4*>(b), *reinterpret_cast<const uint32_t*>(b + qoff),
+                                 lane, o);
+                store4(dst + 256 * (c0 + j) + 4 * lane, o[0], o[1], o[2], o[3]);
+            }
+        }
+        __syncthreads();
+    }
+}
+
+int launch_q4_k_staged(const void* table, int64_t vocab, int64_t hidden, int64_t row_bytes, const uint32_t* ids,
+                       int64_t n_ids, float* out, int32_t* flag, hipStream_t stream) {
+    constexpr int64_t kChunk = int64_t(1) << 24;  // tokens per launch
+    for (int64_t t0 = 0; t0 < n_ids; t0 += kChunk) {
+        const int64_t nt = n_ids - t0 < kChunk ? n_ids - t0 : kChunk;
+        const dim3 grid((unsigned)((nt + kTokPerBlock - 1) / kTokPerBlock));
+        embed_q4_k_staged<<<grid, kThreads, 0, stream>>>(static_cast<const uint8_t*>(table), vocab, (int)hidden,
+                                                         row_bytes, ids + t0, nt, out + (size_t)t0 * (size_t)hidden,
+                                                         flag);
+        const int st = launch_status();
+        if (st != SPH_OK) return st;
+    }
+    return SPH_OK;
 }
 
 template <int W>
@@ -369,7 +405,7 @@ extern "C" int sph_embed(const void* table, int table_dtype, int64_t vocab, int6
         if (row_bytes % 4 == 0 && aligned(table, 4))
             return launch_q8_0_staged<4>(table, vocab, hidden, row_bytes, ids, n_ids, out, bad_id_flag, s);
         return launch_embed<SPH_Q8_0>(table, vocab, hidden, row_bytes, ids, n_ids, out, bad_id_flag, s);
-    case SPH_Q4_K: return launch_embed<SPH_Q4_K>(table, vocab, hidden, row_bytes, ids, n_ids, out, bad_id_flag, s);
+    case SPH_Q4_K: return launch_q4_k_staged(table, vocab, hidden, row_bytes, ids, n_ids, out, bad_id_flag, s);
     case SPH_Q5_K: return launch_embed<SPH_Q5_K>(table, vocab, hidden, row_bytes, ids, n_ids, out, bad_id_flag, s);
     case SPH_Q6_K: return launch_embed<SPH_Q6_K>(table, vocab, hidden, row_bytes, ids, n_ids, out, bad_id_flag, s);
     }
