@@ -124,9 +124,10 @@ def test_rope_llama3_8b_full(dev, orc, dtype, interleaved):
     _run(dev, orc, dtype, 1, 32, 8, 8192, 128, 128, 5e5, list(range(8192)), interleaved, seed=7)
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16], ids=lambda d: str(d).split(".")[-1])
 @pytest.mark.parametrize("interleaved", [False, True], ids=["neox", "interleaved"])
 @pytest.mark.parametrize("pos_scale", [1.0, 7.5, 2.0 ** -7, 3.0e-5, 2.0 ** -20, 1e-30])
-def test_rope_device_sin_cos_equal_glibc(dev, orc, pos_scale, interleaved):
+def test_rope_device_sin_cos_equal_glibc(dev, orc, pos_scale, interleaved, dtype):
     """A (1, 0) pair with head_dim 2 rotates to exactly (cos θ, sin θ), θ = (pos / pos_scale) / base⁰. Over 2^20
     positions in [0, 2^31) — random, plus the first 4096 — and pos_scales from 7.5 down to 1e-30, the angles span
     zero, both reduction ranges (below and above 120, every window of the 4/pi table) and overflow to inf: every
@@ -138,14 +139,20 @@ def test_rope_device_sin_cos_equal_glibc(dev, orc, pos_scale, interleaved):
     pos[:4096] = np.arange(4096, dtype=np.int32)
     x = np.zeros((1, 1, S, 2), np.float32)
     x[..., 0] = 1.0
-    t = torch.from_numpy(x).to(dev)
-    print(f"case rope sin/cos pos_scale {pos_scale} il={interleaved}", flush=True)
+    t = torch.from_numpy(x).to(dev).to(dtype)  # 1 and 0 are exact in every type
+    print(f"case rope sin/cos pos_scale {pos_scale} il={interleaved} {dtype}", flush=True)
     ops.rope_(t, None, torch.from_numpy(pos).to(dev), 1e4, pos_scale=pos_scale, interleaved=interleaved)
     ref = orc.apply_rope_partial_scaled(x, pos, 1e4, 2, pos_scale, interleaved).reshape(-1)
-    got = to_np(t).reshape(-1)
     nan = np.isnan(ref)
-    assert np.array_equal(np.isnan(got), nan)
-    bad = np.flatnonzero(got[~nan].view(np.uint32) != ref[~nan].view(np.uint32))
+    if dtype == torch.float32:
+        got = to_np(t).reshape(-1)
+        assert np.array_equal(np.isnan(got), nan)
+        bad = np.flatnonzero(got[~nan].view(np.uint32) != ref[~nan].view(np.uint32))
+    else:  # the half types' angles take the block-cooperative (pair-major) path
+        got = widen(t, orc).reshape(-1)
+        assert np.array_equal(np.isnan(got), nan)
+        want = narrow_bits(np.ascontiguousarray(ref[~nan]), dtype, orc)
+        bad = np.flatnonzero(to_np(t).reshape(-1)[~nan] != want)
     assert bad.size == 0, f"{bad.size} outputs differ; first at {np.flatnonzero(~nan)[bad[:5]].tolist()}"
     if pos_scale == 1.0:
         assert not nan.any()
