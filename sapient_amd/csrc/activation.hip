@@ -336,10 +336,24 @@ template <typename T, int U>
 __global__ __launch_bounds__(kLutThreads) void gelu_lut_apply(const uint16_t* in, uint16_t* out, int64_t nvec, int which) {
     __shared__ __align__(16) uint16_t tab[kLutEntries];
     {
+        // All of a thread's table chunks are requested before any is written
+        // to LDS: one L2 round trip per block instead of one per chunk (a
+        // load-wait-store loop serialised ten of them).
         constexpr int nq = (int)(2 * gelu_band<T>::kLimit * 2 / 16);  // 16-byte chunks of this type's table
+        constexpr int per = (nq + kLutThreads - 1) / kLutThreads;
         const u32x4* src = reinterpret_cast<const u32x4*>(gelu_lut[which]);
         u32x4* dst = reinterpret_cast<u32x4*>(tab);
-        for (int k = threadIdx.x; k < nq; k += kLutThreads) dst[k] = src[k];
+        u32x4 tmp[per];
+#pragma unroll
+        for (int i = 0; i < per; ++i) {
+            const int k = (int)threadIdx.x + i * kLutThreads;
+            if (k < nq) tmp[i] = src[k];
+        }
+#pragma unroll
+        for (int i = 0; i < per; ++i) {
+            const int k = (int)threadIdx.x + i * kLutThreads;
+            if (k < nq) dst[k] = tmp[i];
+        }
     }
     __syncthreads();
     const u32x4* vin = reinterpret_cast<const u32x4*>(in);
