@@ -308,6 +308,12 @@ def op_table(torch, ops, dev, only=None, cpu_budget=0.0, profile_launches=0):
                  for i in range(3)],
         lambda s: ops.gelu_tanh(s[0], out=s[1]),
         cpu=lambda: (lambda x=nrm(64, 10240, scale=2.0): orc.gelu(x), 64))
+    # the same GELU in f32, the reference's own activation type (compute-bound: glibc's tanhf per element)
+    run("gelu_tanh", "8192x10240", "f32", 2 * n * 4, 8192, "rows",
+        lambda: [(gen(torch, (8192, 10240), 95 + i, dev, f32, 2.0), torch.empty(8192, 10240, device=dev))
+                 for i in range(2)],
+        lambda s: ops.gelu_tanh(s[0], out=s[1]),
+        cpu=lambda: (lambda x=nrm(64, 10240, scale=2.0): orc.gelu(x), 64))
     # LayerNorm (+ bias), erf-GELU and the bias add: the encoder-family norm / activation path
     rows, dim = 16384, 4096
     wl, bl = gen(torch, (dim,), 4, dev, f32, 0.1, 1.0), gen(torch, (dim,), 5, dev, f32, 0.1)
