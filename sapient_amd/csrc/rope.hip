@@ -96,8 +96,7 @@ __device__ __forceinline__ void store_run(T* p, const float (&v)[L]) {
 }
 
 // One thread: pairs of one token, over the heads [h_begin, h_end) of its
-// group (split into HS runs of heads, one per 256-thread subgroup of the
-// block), U heads per batch. Each row is read as R runs of L elements:
+// group, U heads per batch. Each row is read as R runs of L elements:
 //  - NEOX: runs of P at i0 and i0 + half, rotating pairs (i0 + j, i0 + half + j);
 //  - interleaved: one run of 2P at 2·i0, pairs i0 .. i0 + P;
 //  - interleaved, SPLIT: runs of 2P at 2·i0 and 2·i0 + half, pairs i0 .. i0 + P
@@ -120,8 +119,8 @@ __device__ __forceinline__ void store_run(T* p, const float (&v)[L]) {
 // with no angles at all, 28.6 us pair-major with two batches in flight. f32,
 // whose angles are shared by all 40 heads of a thread, is ~0.5 us faster
 // per-thread (the two block barriers cost about what the reductions save).
-template <typename T, int P, bool INTERLEAVED, bool SPLIT, int U, bool PAIR_MAJOR, int HS>
-__global__ __launch_bounds__(kThreads * HS) void rope_kernel(T* q, int nq, T* k, int nk, const int32_t* __restrict__ pos,
+template <typename T, int P, bool INTERLEAVED, bool SPLIT, int U, bool PAIR_MAJOR>
+__global__ __launch_bounds__(kThreads) void rope_kernel(T* q, int nq, T* k, int nk, const int32_t* __restrict__ pos,
                                                              int64_t ntok, int64_t seq, int head_dim, int half,
                                                              int lanes_per_tok, int toks_per_block,
                                                              int heads_per_group, float pos_scale, DenTable den) {
@@ -137,10 +136,8 @@ __global__ __launch_bounds__(kThreads * HS) void rope_kernel(T* q, int nq, T* k,
     __shared__ int32_t pos_s[kThreads];
     __shared__ float cs_s[kAngles], sn_s[kAngles];
     const int tid = threadIdx.x;
-    const int sub = tid / kThreads;  // head subgroup of the block
-    const int ltid = tid - sub * kThreads;
-    const int tib = ltid / lanes_per_tok;
-    const int lit = ltid - tib * lanes_per_tok;
+    const int tib = tid / lanes_per_tok;
+    const int lit = tid - tib * lanes_per_tok;
     const int64_t t_first = (int64_t)blockIdx.x * toks_per_block;
     const int64_t t = t_first + tib;
     const bool active = tib < toks_per_block && t < ntok;
@@ -150,13 +147,9 @@ __global__ __launch_bounds__(kThreads * HS) void rope_kernel(T* q, int nq, T* k,
     auto pair_of = [&](int a) { return SPLIT ? i0 + (a / P) * (half / 2) + a % P : i0 + a; };
     const int64_t b = active ? t / seq : 0;
     const int64_t s = active ? t - b * seq : 0;
-    // The group's heads, split into HS contiguous runs, one per subgroup.
-    const int g_begin = blockIdx.y * heads_per_group;
-    int g_end = g_begin + heads_per_group;
-    if (g_end > nq + nk) g_end = nq + nk;
-    const int per_sub = (g_end - g_begin + HS - 1) / HS;
-    const int h_begin = g_begin + sub * per_sub;
-    const int h_end = h_begin + per_sub < g_end ? h_begin + per_sub : g_end;
+    const int h_begin = blockIdx.y * heads_per_group;
+    int h_end = h_begin + heads_per_group;
+    if (h_end > nq + nk) h_end = nq + nk;
 
     auto row_of = [&](int hh) -> T* {
         return hh < nq ? q + ((size_t)(b * nq + hh) * (size_t)seq + (size_t)s) * (size_t)head_dim
@@ -223,8 +216,8 @@ __global__ __launch_bounds__(kThreads * HS) void rope_kernel(T* q, int nq, T* k,
         const int stride = toks_per_block + 1;
         const int n_angles = toks_per_block * half;
 #pragma unroll
-        for (int j = 0; j < (NA + HS - 1) / HS; ++j) {
-            const int a = j * kThreads * HS + tid;
+        for (int j = 0; j < NA; ++j) {
+            const int a = j * kThreads + tid;
             if (a < n_angles) {
                 const int pair = a / toks_per_block;
                 const int tk = a - pair * toks_per_block;
@@ -441,13 +434,12 @@ struct RopeShape {
     static constexpr bool kSplit = IL;
     static constexpr int U = kHalf ? 2 : 1;
     static constexpr bool kPairMajor = kHalf;
-    static constexpr int HS = 1;
     static constexpr int kTarget = kHalf ? 2048 : 512;
 };
 
-// target: 256-thread units to aim for in all (token blocks × HS × head groups).
+// target: blocks to aim for in all (token blocks × head groups).
 template <typename T, int P, bool IL, bool SPLIT = RopeShape<T, IL>::kSplit, int U = RopeShape<T, IL>::U,
-          bool PM = RopeShape<T, IL>::kPairMajor, int HS = RopeShape<T, IL>::HS>
+          bool PM = RopeShape<T, IL>::kPairMajor>
 int launch_rope_p(T* q, int nq, T* k, int nk, const int32_t* pos, int64_t ntok, int64_t seq, int head_dim,
                   int half, float pos_scale, const DenTable& den, hipStream_t stream,
                   int target = RopeShape<T, IL>::kTarget) {
@@ -455,14 +447,14 @@ int launch_rope_p(T* q, int nq, T* k, int nk, const int32_t* pos, int64_t ntok, 
     const int toks_per_block = kThreads / lanes_per_tok;
     const int64_t blocks_x = (ntok + toks_per_block - 1) / toks_per_block;
     const int heads = nq + nk;
-    int groups = (int)((target + blocks_x * HS - 1) / (blocks_x * HS));
+    int groups = (int)((target + blocks_x - 1) / blocks_x);
     if (groups > heads) groups = heads;
     if (groups < 1) groups = 1;
     const int heads_per_group = (heads + groups - 1) / groups;
     groups = (heads + heads_per_group - 1) / heads_per_group;
     if (blocks_x > INT32_MAX) return SPH_EINVAL;
     const dim3 grid((unsigned)blocks_x, (unsigned)groups);
-    rope_kernel<T, P, IL, SPLIT, U, PM, HS><<<grid, kThreads * HS, 0, stream>>>(
+    rope_kernel<T, P, IL, SPLIT, U, PM><<<grid, kThreads, 0, stream>>>(
         q, nq, k, nk, pos, ntok, seq, head_dim, half, lanes_per_tok, toks_per_block, heads_per_group, pos_scale, den);
     return launch_status();
 }
