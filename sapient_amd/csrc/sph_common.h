@@ -34,11 +34,17 @@ template <> __device__ __forceinline__ f16 narrow<f16>(float v) {
     return f16{__builtin_bit_cast(uint16_t, (_Float16)v)};
 }
 template <> __device__ __forceinline__ bf16 narrow<bf16>(float v) {
-    uint32_t x = __float_as_uint(v);
-    if ((x & 0x7FFFFFFFu) > 0x7F800000u) return bf16{(uint16_t)((x >> 16) | 0x40u)};
-    // round to nearest, ties to even: add 0x7FFF plus the kept lsb
-    x += 0x7FFFu + ((x >> 16) & 1u);
-    return bf16{(uint16_t)(x >> 16)};
+    // v_cvt_pk_bf16_f32 (gfx950): round to nearest-even under the default
+    // MODE, subnormals kept, NaN quieted as (bits >> 16) | 0x40. Over all 2^32
+    // f32 inputs on gfx950 it gives exactly the integer sequence
+    // x += 0x7FFF + ((x >> 16) & 1), x >> 16, with that NaN rule.
+    return bf16{__builtin_bit_cast(uint16_t, (__bf16)v)};
+}
+// Two values in one v_cvt_pk_bf16_f32, v0 in the low half.
+__device__ __forceinline__ uint32_t narrow2_bf16(float v0, float v1) {
+    typedef float f32x2_t __attribute__((ext_vector_type(2)));
+    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){v0, v1}, bf16x2_t));
 }
 
 // Elements of T that fill one 16-byte access.
@@ -103,6 +109,9 @@ __device__ __forceinline__ void f32_to_words(const float (&v)[N], uint32_t (&raw
     if constexpr (sizeof(T) == 4) {
 #pragma unroll
         for (int i = 0; i < N; ++i) raw[i] = __float_as_uint(v[i]);
+    } else if constexpr (sizeof(T) == 2 && __is_same(T, bf16)) {
+#pragma unroll
+        for (int i = 0; i < N; i += 2) raw[i / 2] = narrow2_bf16(v[i], v[i + 1]);
     } else {
 #pragma unroll
         for (int i = 0; i < N; i += 2)

@@ -75,3 +75,42 @@ def test_f32_activation_every_input(dev, orc, name):
                 print(f"case {name} f32 every input: {c + 1} of 32 chunks, mismatches {bad}, NaN mismatches {nan_bad}",
                       flush=True)
     assert bad == 0 and nan_bad == 0, f"{name}: {bad} outputs differ, {nan_bad} NaN mismatches; first (x, got, want) {first}"
+
+
+@pytest.mark.parametrize("half", ["f16", "bf16"])
+def test_f32_to_half_every_input(dev, orc, half):
+    """Every kernel that stores f16 / bf16 narrows with the same device helper
+    (v_cvt_f16_f32 / v_cvt_pk_bf16_f32). kv_append from an f32 source into a half
+    cache is that narrowing alone; the oracle's is half's from_f32 (round bit and
+    sticky bits, NaN quieted with 0x40 for bf16). Bar: bit-exact, NaN included."""
+    tdt = torch.float16 if half == "f16" else torch.bfloat16
+    fn = getattr(orc.lib(), "sor_f32_to_f16_n" if half == "f16" else "sor_f32_to_bf16_n")
+    nthreads = max(1, min(16, os.cpu_count() or 1))
+    ops.init(dev)
+    hd = 128
+    cache = torch.empty((1, CHUNK // hd, hd), dtype=tdt, device=dev)
+    bad = 0
+    first = None
+    with ThreadPoolExecutor(nthreads) as pool:
+        for c in range((1 << 32) // CHUNK):
+            start = c * CHUNK if c * CHUNK < (1 << 31) else c * CHUNK - (1 << 32)
+            xb = torch.arange(start, start + CHUNK, dtype=torch.int32, device=dev)
+            ops.kv_append(xb.view(torch.float32).view(1, CHUNK // hd, hd), cache, 0)
+            got = cache.view(torch.int16).flatten()
+            x_np = np.arange(start, start + CHUNK, dtype=np.int32).view(np.float32)
+            ref_np = np.empty(CHUNK, dtype=np.uint16)
+            step = (CHUNK + nthreads - 1) // nthreads
+            futs = [pool.submit(fn, x_np[i:i + step].ctypes.data, ref_np[i:i + step].ctypes.data, x_np[i:i + step].size)
+                    for i in range(0, CHUNK, step)]
+            for f in futs:
+                f.result()
+            ref = torch.from_numpy(ref_np.view(np.int16)).to(dev)
+            diff = got != ref
+            nd = int(diff.sum())
+            if nd and first is None:
+                i = int(torch.nonzero(diff)[0])
+                first = (hex((start + i) & 0xFFFFFFFF), hex(int(got[i]) & 0xFFFF), hex(int(ref[i]) & 0xFFFF))
+            bad += nd
+            if c % 8 == 7:
+                print(f"case f32 -> {half} every input: {c + 1} of 32 chunks, mismatches {bad}", flush=True)
+    assert bad == 0, f"f32 -> {half}: {bad} outputs differ; first (x, got, want) {first}"
