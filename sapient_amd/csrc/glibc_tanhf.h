@@ -124,21 +124,31 @@ __host__ __device__ inline float div_tanh(float n, float d) {
 //   |x| >= 1:  t = expm1f(2|x|),  z = 1 - 2/(t + 2)
 //   |x| <  1:  t = expm1f(-2|x|), z = -t/(t + 2)
 // and returns z with x's sign (|x| >= 22: 1 - 1e-30; |x| < 2^-55: x(1 + x);
-// inf: +-1; NaN: NaN). Here one expm1f runs per element, on the argument fdlibm
-// would pass, and one division serves both formulas. The expm1f is fdlibm's
-// (glibc_expm1f above) for the arguments tanhf passes, |a| in [2^-54, 44):
-//  - its three reductions are one formula: k = 0 and k = -1 are the general
+// inf: +-1; NaN: NaN). tanhf_core returns fdlibm's value for every input but
+// NaN, with one expm1f per element on the argument fdlibm would pass and one
+// division for both formulas. Its expm1f is fdlibm's (glibc_expm1f above),
+// reorganised for the arguments tanhf passes:
+//  - |x| is clamped to 9.5: from |x| = 9.02 up, 2/(t + 2) < 2^-25 and fdlibm's
+//    z rounds to exactly 1, as does 1 - 1e-30 beyond 22, so the clamped
+//    evaluation gives fdlibm's result there, infinities included. expm1f's
+//    argument a then lies in (-2, 19], where k <= 27;
+//  - the three reductions are one formula: k = 0 and k = -1 are the general
 //    hi = a - k·ln2_hi, lo = k·ln2_lo at that k (k·ln2_hi is exact; at k = 0,
 //    hi = a, lo = +0, so the reduced argument is a and c = +0, as fdlibm has);
-//  - its reconstruction cases that these arguments reach (k = 0, -1, <= -2 or
-//    > 56, < 23, else) are all evaluated and the one fdlibm takes is selected;
-//  - |a| < 2^-25 returns a, as fdlibm's 1e30-trick does.
-// Every operation is fdlibm's, in its order, rounded on its own, so the result
-// equals glibc_tanhf's (checked against the host libm over all 2^32 inputs).
-// Lanes whose result comes from a special case still run the main formula on
-// a clamped argument (no out-of-range float-to-int conversion); that value is
-// discarded.
-__host__ __device__ inline float glibc_tanhf(float x) {
+//  - every reconstruction starts from d = xr - e2 with
+//    e2 = (xr·(e - c) - c) - hxs: at k = 0 (c = +0) e2 is fdlibm's
+//    xr·e - hxs and its result is d; k = -1 gives 0.5·d - 0.5; for k <= -2,
+//    2^k·(1 + d) - 1, and for k >= 2, 2^k·((1 - 2^-k) + d), fdlibm's
+//    1 - (e - x) and t - (e - x) with e - x = -d exactly. fdlibm's k >= 23
+//    form, (x - (e + 2^-k)) + 1, rounds differently from the k < 23 one, but
+//    the two give the same tanhf for every input (for |x| >= 7.97, where
+//    k >= 23, 2/(t + 2) <= 2^-21 and a last-place change in t does not move
+//    1 - 2/(t + 2); checked exhaustively);
+//  - |a| < 2^-25, where fdlibm returns a, is the k = 0 formula: d rounds to a;
+//    so is |x| < 2^-55, where the quotient 2|x| / 2 is |x| exactly.
+// Every operation is fdlibm's, in its order, rounded on its own; z >= +0, so
+// x's sign is ORed in.
+__host__ __device__ inline float tanhf_core(float x) {
     const float ln2_hi = 6.9313812256e-01f;  // 0x3f317180
     const float ln2_lo = 9.0580006145e-06f;  // 0x3717f7d1
     const float invln2 = 1.4426950216e+00f;  // 0x3fb8aa3b
@@ -146,18 +156,16 @@ __host__ __device__ inline float glibc_tanhf(float x) {
                 Q4 = 4.0082177293e-06f, Q5 = -2.0109921195e-07f;
     const uint32_t jx = fbits(x);
     const uint32_t ix = jx & 0x7fffffffu;
-    const bool big = ix >= 0x3f800000u;                     // |x| >= 1
-    const float ax = bitsf(ix < 0x41b00000u ? ix : 0x41a80000u);  // |x|, or 21 off the main range
-    const float a = big ? 2.0f * ax : -2.0f * ax;           // expm1f's argument (exact)
-    const uint32_t ha = fbits(a) & 0x7fffffffu;
-
-    // expm1f(a)
-    // A positive argument is >= 2 (|x| >= 1), past 1.5 ln2, so fdlibm's k = 1
-    // case never arises here: k is -1 below 1.5 ln2, else the general k.
-    int32_t k = 0;
-    if (ha > 0x3eb17218u)                                   // |a| > 0.5 ln2
-        k = ha < 0x3F851592u ? -1                           // |a| < 1.5 ln2 (a < 0 here)
-                             : (int32_t)(invln2 * a + (big ? 0.5f : -0.5f));  // truncating conversion
+    const bool big = ix >= 0x3f800000u;                          // |x| >= 1
+    const float ax = bitsf(ix < 0x41180000u ? ix : 0x41180000u);  // |x|, at most 9.5
+    const float a2 = 2.0f * ax;                                  // |a| (exact)
+    const float a = big ? a2 : -a2;                              // expm1f's argument
+    const uint32_t ha = fbits(a2);
+    // k: 0 up to 0.5 ln2, else fdlibm's rounding of a / ln2 (truncating
+    // conversion). Below 1.5 ln2, where fdlibm sets k = -1 without it, the
+    // rounding gives -1 as well (a < 0 there: a positive argument is >= 2).
+    int32_t k = (int32_t)(invln2 * a + (big ? 0.5f : -0.5f));
+    if (ha <= 0x3eb17218u) k = 0;
     const float tk = (float)k;
     const float hi = a - tk * ln2_hi;
     const float lo = tk * ln2_lo;
@@ -168,36 +176,32 @@ __host__ __device__ inline float glibc_tanhf(float x) {
     const float r1 = 1.0f + hxs * (Q1 + hxs * (Q2 + hxs * (Q3 + hxs * (Q4 + hxs * Q5))));
     const float t3 = 3.0f - r1 * hfx;
     const float e = hxs * div_tanh(r1 - t3, 6.0f - xr * t3);
-    const float y0 = xr - (xr * e - hxs);                   // k == 0
     const float e2 = (xr * (e - c) - c) - hxs;
-    const float ym1 = 0.5f * (xr - e2) - 0.5f;              // k == -1
-    const uint32_t kexp = (uint32_t)k << 23;                // k added to an exponent field
-    const float ya = bitsf(fbits(1.0f - (e2 - xr)) + kexp) - 1.0f;  // k <= -2 or k > 56
-    const int ks = k < 0 ? 0 : (k > 31 ? 31 : k);          // shift count in range (used for 2 <= k < 23)
-    const float yb = bitsf(fbits(bitsf(0x3f800000u - (0x1000000u >> ks)) - (e2 - xr)) + kexp);  // k < 23
-    const float yc = bitsf(fbits((xr - (e2 + bitsf((uint32_t)(0x7f - k) << 23))) + 1.0f) + kexp);  // else
-    float em1 = k == 0 ? y0 : (k == -1 ? ym1 : ((k <= -2 || k > 56) ? ya : (k < 23 ? yb : yc)));
-    if (ha < 0x33000000u) em1 = a;                          // |a| < 2^-25
-
+    const float d = xr - e2;
+    const float tt = k >= 2 ? bitsf(0x3f800000u - (0x1000000u >> (k & 31))) : 1.0f;  // 1 - 2^-k, or 1
+    const float w = bitsf(fbits(tt + d) + ((uint32_t)k << 23));                        // scaled by 2^k
+    const float em1 = k == 0 ? d : (k == -1 ? 0.5f * d - 0.5f : (k < 0 ? w - 1.0f : w));
     // tanh from expm1
     const float q = div_tanh(big ? 2.0f : -em1, em1 + 2.0f);
     const float z = big ? 1.0f - q : q;
-    float r = (jx >> 31) ? -z : z;
-    if (ix >= 0x41b00000u) r = (jx >> 31) ? -(1.0f - 1.0e-30f) : 1.0f - 1.0e-30f;  // |x| >= 22
-    if (ix < 0x24000000u) r = x * (1.0f + x);               // |x| < 2^-55 (and +-0)
-    // fdlibm returns 1/x -+ 1: +-1 at +-inf, a NaN for a NaN (written without
-    // the division, which would otherwise run on every lane).
-    if (ix == 0x7f800000u) r = (jx >> 31) ? -1.0f : 1.0f;
-    if (ix > 0x7f800000u) r = x + x;
-    return r;
+    return bitsf(fbits(z) | (jx & 0x80000000u));
+}
+
+// glibc's tanhf for every f32 input: NaN gives a quiet NaN (fdlibm's x + x).
+__host__ __device__ inline float glibc_tanhf(float x) {
+    const float r = tanhf_core(x);
+    return (fbits(x) & 0x7fffffffu) > 0x7f800000u ? x + x : r;
 }
 
 // GELU, tanh form, in the reference's operation order (elementwise.rs:120-127):
 //   inner = 0.797_884_56 * (v + 0.044_715 * v * v * v);  y = 0.5 * v * (1 + tanh(inner))
+// inner is NaN only for a NaN v (a finite or infinite v gives a finite or
+// same-signed infinite inner), and then y is NaN whatever tanh returns, so
+// tanh's NaN case is not needed here.
 __host__ __device__ inline float gelu_tanh_ref_order(float v) {
     const float S = 0.79788456f, C = 0.044715f;
     const float inner = S * (v + C * v * v * v);
-    return 0.5f * v * (1.0f + glibc_tanhf(inner));
+    return 0.5f * v * (1.0f + tanhf_core(inner));
 }
 
 }  // namespace sph
