@@ -1,5 +1,6 @@
 """GPU parity over every f32 input: the f32 SiLU, GELU-tanh and erf-GELU kernels
-against the oracle, all 2^32 bit patterns each.
+against the oracle, all 2^32 bit patterns each, and the device's f32 -> f16 /
+bf16 narrowing (through kv_append) against the oracle's half conversion.
 
 Reference: crates/sapient-backends/cpu/src/kernels/elementwise.rs:141-143 (silu),
 :120-127 (gelu, tanh form), :135-138 with erf_approx :163-174 (gelu_erf).
