@@ -79,6 +79,35 @@ __host__ __device__ inline float glibc_expf_tab(float x, const uint64_t* tab) {
     return (float)y;
 }
 
+// glibc_expf_tab for a <= 0 or NaN (erf's exp(−x²)), written without
+// branches: the special cases such arguments reach are −inf and underflow
+// below −0x1.9fe368p6, both 0, and NaN; every other argument, −103.97 ≤ a < −88
+// included, takes glibc's main path. The main path runs on the argument clamped
+// at the underflow bound (its value is then discarded for 0) and carries a NaN
+// through to a NaN (the table index stays in range: it is taken mod 32).
+__host__ __device__ inline float glibc_expf_nonpos_tab(float a, const uint64_t* tab) {
+    constexpr float kUnder = -0x1.9fe368p6f;
+    const bool under = a < kUnder;
+    const double inv_ln2_n = 0x1.71547652b82fep+0 * 32;
+    const double shift = 0x1.8p+52;
+    const double c0 = 0x1.c6af84b912394p-5 / 32 / 32 / 32;
+    const double c1 = 0x1.ebfce50fac4f3p-3 / 32 / 32;
+    const double c2 = 0x1.62e42ff0c52d6p-1 / 32;
+    const double xd = (double)(under ? kUnder : a);
+    double kd = __builtin_fma(inv_ln2_n, xd, shift);
+    const uint64_t ki = __builtin_bit_cast(uint64_t, kd);
+    kd -= shift;
+    const double r = __builtin_fma(inv_ln2_n, xd, -kd);
+    const uint64_t t = tab[ki % 32] + (ki << 47);
+    const double s = __builtin_bit_cast(double, t);
+    const double z = __builtin_fma(c0, r, c1);
+    const double r2 = r * r;
+    double y = __builtin_fma(c2, r, 1.0);
+    y = __builtin_fma(z, r2, y);
+    y = y * s;
+    return under ? 0.0f : (float)y;
+}
+
 __host__ inline float glibc_expf(float x) {
     constexpr Exp2fTable t = exp2f_table();
     return glibc_expf_tab(x, t.tab);
@@ -116,7 +145,7 @@ __host__ __device__ inline float erf_ref_order(float x, const uint64_t* tab) {
     const float t = recip_erf(1.0f + 0.3275911f * x);
     const float poly =
         0.25482959f + (-0.28449674f + (1.42141374f + (-1.45315203f + 1.06140543f * t) * t) * t) * t;
-    const float y = 1.0f - poly * t * glibc_expf_tab(-x * x, tab);
+    const float y = 1.0f - poly * t * glibc_expf_nonpos_tab(-x * x, tab);
     return sign * y;
 }
 

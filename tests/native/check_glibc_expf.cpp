@@ -33,24 +33,26 @@ static float gelu_erf_libm(float v) { return 0.5f * v * (1.0f + erf_libm(v * 0.7
 int main(int argc, char** argv) {
     const int nthreads = argc > 1 ? atoi(argv[1]) : 8;
     constexpr sph::Exp2fTable table = sph::exp2f_table();
-    std::atomic<uint64_t> bad_e{0}, bad_s{0}, bad_g{0};
+    std::atomic<uint64_t> bad_e{0}, bad_n{0}, bad_s{0}, bad_g{0};
     std::vector<std::thread> pool;
     for (int t = 0; t < nthreads; ++t) {
         pool.emplace_back([&, t] {
-            uint64_t be = 0, bs = 0, bg = 0;
+            uint64_t be = 0, bn = 0, bs = 0, bg = 0;
             for (uint64_t u = t; u < (1ull << 32); u += nthreads) {
                 float x;
                 uint32_t w = (uint32_t)u;
                 memcpy(&x, &w, 4);
                 if (!same(sph::glibc_expf_tab(x, table.tab), expf(x))) ++be;
+                if ((w >> 31 || isnan(x)) && !same(sph::glibc_expf_nonpos_tab(x, table.tab), expf(x))) ++bn;
                 if (!same(sph::silu_ref_order(x, table.tab), silu_libm(x))) ++bs;
                 if (!same(sph::gelu_erf_ref_order(x, table.tab), gelu_erf_libm(x))) ++bg;
             }
-            bad_e += be; bad_s += bs; bad_g += bg;
+            bad_e += be; bad_n += bn; bad_s += bs; bad_g += bg;
         });
     }
     for (auto& th : pool) th.join();
-    printf("expf mismatches %llu\nsilu mismatches %llu\ngelu_erf mismatches %llu\n",
-           (unsigned long long)bad_e.load(), (unsigned long long)bad_s.load(), (unsigned long long)bad_g.load());
-    return (bad_e || bad_s || bad_g) ? 1 : 0;
+    printf("expf mismatches %llu\nexpf_nonpos mismatches %llu\nsilu mismatches %llu\ngelu_erf mismatches %llu\n",
+           (unsigned long long)bad_e.load(), (unsigned long long)bad_n.load(), (unsigned long long)bad_s.load(),
+           (unsigned long long)bad_g.load());
+    return (bad_e || bad_n || bad_s || bad_g) ? 1 : 0;
 }
