@@ -47,21 +47,22 @@ __host__ __device__ constexpr Exp2fTable exp2f_table() {
 // expf with the 2^(i/32) table passed in: device code keeps it in LDS or
 // registers, host code uses exp2f_table().
 __host__ __device__ inline float glibc_expf_tab(float x, const uint64_t* tab) {
-    const uint32_t ux = __builtin_bit_cast(uint32_t, x);
-    const uint32_t abstop = (ux >> 20) & 0x7ff;
-    if (abstop >= 0x42b) {  // |x| >= 88 or x is NaN
-        if (ux == 0xff800000u) return 0.0f;     // -inf
-        if (abstop >= 0x7f8) return x + x;       // +inf, NaN
-        if (x > 0x1.62e42ep6f) return __builtin_bit_cast(float, 0x7f800000u);  // overflow
-        if (x < -0x1.9fe368p6f) return 0.0f;     // underflow
-    }
+    // glibc branches to its special cases for |x| >= 88 or NaN: overflow above
+    // 0x1.62e42ep6 and +inf give +inf, underflow below -0x1.9fe368p6 and -inf
+    // give 0, NaN gives NaN, and the rest of that range falls through to the
+    // main path. Here those are selects after the main path has run on x
+    // clamped into [underflow bound, overflow bound] (a NaN passes through it
+    // to a NaN; the table index is taken mod 32), so lanes never diverge.
+    constexpr float kUnder = -0x1.9fe368p6f, kOver = 0x1.62e42ep6f;
+    const bool under = x < kUnder, over = x > kOver;
+    const float xc = under ? kUnder : (over ? kOver : x);
     const double inv_ln2_n = 0x1.71547652b82fep+0 * 32;
     const double shift = 0x1.8p+52;
     const double c0 = 0x1.c6af84b912394p-5 / 32 / 32 / 32;
     const double c1 = 0x1.ebfce50fac4f3p-3 / 32 / 32;
     const double c2 = 0x1.62e42ff0c52d6p-1 / 32;
 
-    const double xd = (double)x;
+    const double xd = (double)xc;
     // z = x·N/ln2 feeds two additions, and the contracting build fuses the
     // product into both: kd = RN(z + shift) rounds z to an integer (ties to
     // even) and r = z − k is formed from the exact product.
@@ -76,7 +77,7 @@ __host__ __device__ inline float glibc_expf_tab(float x, const uint64_t* tab) {
     double y = __builtin_fma(c2, r, 1.0);
     y = __builtin_fma(z, r2, y);
     y = y * s;
-    return (float)y;
+    return over ? __builtin_bit_cast(float, 0x7f800000u) : (under ? 0.0f : (float)y);
 }
 
 // glibc_expf_tab for a <= 0 or NaN (erf's exp(−x²)), written without
