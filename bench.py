@@ -10,15 +10,26 @@ on their stream) against MI355X's 8 TB/s,
 the single-thread CPU oracle on a bounded sample of the same workload, and
 (``ops``) the same measurement for every other op at its configuration shape.
 
+Every throughput row rotates buffer sets totalling at least 512 MiB
+(``rotation_bytes``), so the 256 MB Infinity Cache cannot serve a repeat; the
+gather rows rotate whole tables and id sets. The latency-bound Qwen2.5-0.5B
+rows report kernel durations from a rocprofv3 kernel trace of a child process
+(``us``), beside the per-launch time of a replayed HIP graph of back-to-back
+launches (``graph_us``) and one call's latency from the host (``call_us``).
+
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-ops] [--cpu-seconds S]
 """
 from __future__ import annotations
 
 import argparse
+import csv
 import json
 import os
 import re
+import shutil
+import subprocess
 import sys
+import tempfile
 import time
 from pathlib import Path
 
@@ -33,6 +44,11 @@ PROFILES = ROOT / "profiles"
 # The headline's kernel instantiation (fused add + RMSNorm, f32, 16 waves per row, one
 # 16-byte vector per lane, row-looping blocks), as rocprofv3 names it.
 HEADLINE_KERNEL = "rms_rows_vec<float, float, float, 1, 16, 1, true>"
+# Every throughput row rotates at least this many bytes of distinct buffers (twice the
+# 256 MB Infinity Cache), so no launch can be served from the previous launches' lines.
+ROTATION_MIN = 1 << 29
+# Launches per latency-bound row in the kernel-trace child (the first C1_SKIP are warm-up).
+C1_LAUNCHES, C1_SKIP = 220, 20
 
 
 def parse():
@@ -46,9 +62,12 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU-baseline time budget")
     p.add_argument("--op-cpu-seconds", type=float, default=0.3, help="CPU time budget per op-table row")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    p.add_argument("--no-kernel-trace", action="store_true",
+                   help="latency-bound rows: skip the rocprofv3 child (us = graph replay per launch)")
     p.add_argument("--profile-run", action="store_true",
-                   help="launch only the headline kernel (warmup + steps) and a calibration copy: for rocprofv3; "
-                        "with --only, the named op-table rows instead of the headline")
+                   help="launch only the headline kernel (warmup + steps) and the calibration copies: for "
+                        "rocprofv3; with --only, the named op-table rows instead of the headline")
+    p.add_argument("--latency-child", action="store_true", help=argparse.SUPPRESS)
     return p.parse_args()
 
 
@@ -113,7 +132,33 @@ def time_regions(torch, fn, sets, regions: int = 5, steps: int = 20):
     """Steady-state per-launch ms: after `warm`, `regions` regions of `steps` back-to-back launches,
     each between one HIP event pair; the median region / steps."""
     warm(torch, fn, sets)
+    steps = max(steps, len(sets))  # every region walks the whole rotation at least once
     return median([time_region(torch, fn, sets, 0, steps)[0] for _ in range(regions)]) / steps
+
+
+def time_graph(torch, fn, sets, launches: int = 200, replays: int = 5):
+    """Per-launch ms of `launches` back-to-back launches captured into one HIP graph and replayed
+    (kernel time plus the dispatch gap between dependent kernels); the median of `replays`."""
+    for i in range(4):
+        fn(sets[i % len(sets)])
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(launches):
+            fn(sets[i % len(sets)])
+    g.replay()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    per = []
+    for _ in range(replays):
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        g.replay()
+        end.record(stream)
+        torch.cuda.synchronize()
+        per.append(start.elapsed_time(end) / launches)
+    del g
+    return median(per)
 
 
 def cpu_time(fn, budget_s: float, min_reps: int = 1):
@@ -138,6 +183,31 @@ def committed_traffic(kernel_tag: str):
     return float(m.group(1)) if m else None
 
 
+# ───────────────────────────── buffer sets ─────────────────────────────
+def set_bytes(torch, s) -> int:
+    """Bytes of the distinct tensors one buffer set holds."""
+    seen = {}
+
+    def walk(o):
+        if isinstance(o, torch.Tensor):
+            seen[o.data_ptr()] = o.numel() * o.element_size()
+        elif isinstance(o, (list, tuple)):
+            for x in o:
+                walk(x)
+    walk(s)
+    return sum(seen.values())
+
+
+def rotation(torch, make_set, min_bytes: int = ROTATION_MIN, min_sets: int = 2):
+    """Buffer sets make_set(0), make_set(1), ... until they hold at least `min_bytes` (and at least
+    `min_sets` sets). Returns (sets, bytes rotated)."""
+    sets = [make_set(0)]
+    per = set_bytes(torch, sets[0])
+    n = max(min_sets, -(-min_bytes // max(per, 1)))
+    sets += [make_set(i) for i in range(1, n)]
+    return sets, sum(set_bytes(torch, s) for s in sets)
+
+
 # ───────────────────────────── workloads ─────────────────────────────
 def gen(torch, shape, seed, dev, dtype, std=1.0, mean=0.0):
     g = torch.Generator(device=dev).manual_seed(seed)
@@ -157,11 +227,10 @@ def headline(torch, ops, dev, args):
 
     region_ms, wall = time_region(torch, fn, sets, args.warmup, args.steps)
     alg_bytes = 4 * rows * dim * 4 + dim * 4  # read x, residual, weight; write y, residual
-    return rows, dim, alg_bytes, region_ms, wall
+    return rows, dim, alg_bytes, region_ms, wall, sum(set_bytes(torch, s) for s in sets)
 
 
 def engine_rows(torch, dev, table, vocab):
-    import time
     import sapient_amd._lib as L
     from sapient_amd.engine import Engine
     f32 = torch.float32
@@ -206,12 +275,133 @@ def engine_rows(torch, dev, table, vocab):
     return rows
 
 
-def op_table(torch, ops, dev, only=None, cpu_budget=0.0, profile_launches=0):
+class Row:
+    """One op-table row: name, shape, dtype label, algorithmic bytes per launch, units per launch
+    (rows / tokens / ids), make_set(i) -> the i-th buffer set, fn(set) -> one launch, and cpu() ->
+    (oracle call, units it covers) for the CPU column."""
+
+    def __init__(self, name, shape, dtype, alg_bytes, units, unit_name, make_set, fn, cpu=None, latency=False):
+        self.name, self.shape, self.dtype, self.alg_bytes = name, shape, dtype, alg_bytes
+        self.units, self.unit_name, self.make_set, self.fn, self.cpu = units, unit_name, make_set, fn, cpu
+        self.latency = latency
+
+
+def q_table(torch, dev, g, vocab, hidden, block, nbytes, d_off, nd, dmin=0.0005, dmax=0.02, signed_q=False):
+    """A raw GGUF table [vocab, hidden] of `block`-element blocks of `nbytes` bytes: random quant
+    bytes (int8 in [-127, 127] when signed_q) with `nd` f16 scales ~U(dmin, dmax) at byte d_off."""
+    nb = vocab * hidden // block
+    if signed_q:
+        t = torch.randint(-127, 128, (nb, nbytes), generator=g, device=dev, dtype=torch.int32).to(torch.int8)
+        t = t.view(torch.uint8)
+    else:
+        t = torch.randint(0, 256, (nb, nbytes), generator=g, device=dev, dtype=torch.int32).to(torch.uint8)
+    dd = (torch.rand((nb, nd), generator=g, device=dev) * (dmax - dmin) + dmin).to(torch.float16)
+    t[:, d_off:d_off + 2 * nd] = dd.view(torch.uint8).view(nb, 2 * nd)
+    return t.reshape(-1)
+
+
+def latency_rows(torch, ops, dev, orc, nrm, cpu_gather):
+    """The Qwen2.5-0.5B (config 1) layer ops at T = 1 and T = 512: latency-bound, reported only."""
+    import sapient_amd._lib as L
+    f32, f16 = torch.float32, torch.float16
+    H = 896
+    rows = []
+    for T1 in (1, 512):
+        w = gen(torch, (H,), 3, dev, f32, 0.1, 1.0)
+        rows.append(Row(f"rms_norm qwen T={T1}", f"{T1}x{H}", "f32", T1 * H * 8 + H * 4, T1, "rows",
+                        lambda i, T1=T1: (gen(torch, (T1, H), 100 + i, dev, f32), torch.empty(T1, H, device=dev)),
+                        lambda s, w=w: ops.rms_norm(s[0], w, 1e-6, out=s[1]),
+                        lambda T1=T1: (lambda x=nrm(T1, H), w=nrm(H, scale=0.1, mean=1.0):
+                                       orc.rms_norm(x, w, 1e-6), T1), latency=True))
+        pos = torch.arange(T1, dtype=torch.int32, device=dev)
+        rows.append(Row(f"rope_neox qwen T={T1}", f"q14+k2 x {T1} x 64", "f32", 2 * 16 * T1 * 64 * 4, T1, "tokens",
+                        lambda i, T1=T1: (gen(torch, (1, 14, T1, 64), 110 + i, dev, f32),
+                                          gen(torch, (1, 2, T1, 64), 120 + i, dev, f32)),
+                        lambda s, pos=pos: ops.rope_(s[0], s[1], pos, 1e6),
+                        lambda T1=T1: (lambda q=nrm(1, 16, T1, 64), p=np.arange(T1): orc.apply_rope(q, p, 1e6), T1),
+                        latency=True))
+        rows.append(Row(f"swiglu qwen T={T1}", f"{T1}x4864", "f32", 3 * T1 * 4864 * 4, T1, "rows",
+                        lambda i, T1=T1: (gen(torch, (T1, 4864), 130 + i, dev, f32),
+                                          gen(torch, (T1, 4864), 140 + i, dev, f32), torch.empty(T1, 4864, device=dev)),
+                        lambda s: ops.swiglu(s[0], s[1], out=s[2]),
+                        lambda T1=T1: (lambda g=nrm(T1, 4864), u=nrm(T1, 4864): orc.swiglu(g, u), T1), latency=True))
+    vocab_q, hid_q = 151936, 896
+    g = torch.Generator(device=dev).manual_seed(11)
+    tq = q_table(torch, dev, g, vocab_q, hid_q, 32, 34, 0, 1, 0.001, 0.05, signed_q=True)
+    rng = np.random.default_rng(12)
+    for T1 in (1, 512):
+        ids = [torch.from_numpy(rng.integers(0, vocab_q, T1).astype(np.int32)).to(dev) for _ in range(2)]
+        rows.append(Row(f"embed_q8_0 qwen T={T1}", f"{vocab_q}x{hid_q} -> {T1} ids", "q8_0->f32",
+                        T1 * (952 + 4 + hid_q * 4), T1, "rows",
+                        lambda i, T1=T1, ids=ids: (ids[i % 2], torch.empty(T1, hid_q, device=dev)),
+                        lambda s: ops.embed(tq, L.Q8_0, vocab_q, hid_q, s[0], out=s[1]),
+                        lambda T1=T1: cpu_gather(L.Q8_0, 32, 34, 0, 1, hid_q, T1), latency=True))
+    return rows, tq, vocab_q
+
+
+def latency_kernel_times(rows_names):
+    """Kernel durations of the latency-bound rows: this script re-run as a child under
+    `rocprofv3 --kernel-trace` (each row's kernel launched C1_LAUNCHES times in order, one library
+    kernel per launch); returns ({row name: median µs over the last C1_LAUNCHES - C1_SKIP}, note),
+    or (None, reason) when the profiler is unavailable or its trace does not match the plan."""
+    prof = shutil.which("rocprofv3")
+    if prof is None:
+        return None, "rocprofv3 not found"
+    with tempfile.TemporaryDirectory(prefix="sph_c1_") as tmp:
+        env = dict(os.environ, TMPDIR=tmp)
+        cmd = [prof, "--kernel-trace", "--output-format", "csv", "-d", tmp, "-o", "c1", "--",
+               sys.executable, str(ROOT / "bench.py"), "--latency-child"]
+        try:
+            res = subprocess.run(cmd, cwd=tmp, env=env, capture_output=True, text=True, timeout=300)
+        except subprocess.TimeoutExpired:
+            return None, "kernel-trace child timed out"
+        plan = None
+        for line in res.stdout.splitlines():
+            if line.startswith('{"latency_child"'):
+                plan = json.loads(line)
+        traces = list(Path(tmp).rglob("c1_kernel_trace.csv"))
+        if plan is None or not traces:
+            return None, f"kernel-trace child failed (rc {res.returncode})"
+        with open(traces[0], newline="") as f:
+            recs = [r for r in csv.DictReader(f) if "sph::" in r["Kernel_Name"]]
+        recs.sort(key=lambda r: int(r["Dispatch_Id"]))
+        n = plan["launches"]
+        if len(recs) != n * len(plan["rows"]) or plan["rows"] != rows_names:
+            return None, f"kernel trace holds {len(recs)} library dispatches, expected {n * len(plan['rows'])}"
+        out = {}
+        for k, name in enumerate(plan["rows"]):
+            durs = [(int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3 for r in recs[k * n:(k + 1) * n]]
+            names = {r["Kernel_Name"] for r in recs[k * n:(k + 1) * n]}
+            if len(names) != 1:
+                return None, f"row {name}: more than one kernel per launch"
+            kernel = names.pop().replace("sph::(anonymous namespace)::", "")
+            out[name] = (median(durs[C1_SKIP:]), re.sub(r"^void |\(.*$", "", kernel))
+        return out, f"rocprofv3 kernel trace of a child process, median of {n - C1_SKIP} launches per row"
+
+
+def latency_child():
+    """Child of latency_kernel_times: launch each latency-bound row's op C1_LAUNCHES times, in order."""
+    import torch
+
+    import sapient_amd.ops as ops
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    rows, _, _ = latency_rows(torch, ops, dev, None, None, None)
+    for r in rows:
+        sets = [r.make_set(i) for i in range(2)]
+        torch.cuda.synchronize()
+        for i in range(C1_LAUNCHES):
+            r.fn(sets[i % 2])
+        torch.cuda.synchronize()
+    print(json.dumps({"latency_child": True, "launches": C1_LAUNCHES, "rows": [r.name for r in rows]}), flush=True)
+
+
+def op_table(torch, ops, dev, only=None, cpu_budget=0.0, profile_launches=0, kernel_trace=True):
     """Per-op GB/s at each configuration shape (after >= 25 ms of warm-up launches, the median of 5
-    regions of 20 back-to-back launches between one event pair; latency-bound rows: the median of 20
-    individually bracketed launches), and beside it
-    the oracle — the reference's algorithm restated in C, one thread — on a sample of the same shape's
-    rows (or tokens, ids), `cpu_budget` seconds each, reported in the same units.
+    regions of back-to-back launches between one event pair, over buffer sets rotating >= 512 MiB;
+    latency-bound rows: kernel durations from a rocprofv3 trace, graph replay and one call's latency),
+    and beside it the oracle — the reference's algorithm restated in C, one thread — on a sample of the
+    same shape's rows (or tokens, ids), `cpu_budget` seconds each, reported in the same units.
     profile_launches > 0: only launch each selected row that many times (for rocprofv3), time nothing."""
     import sapient_amd._lib as L
     f32, f16, bf16 = torch.float32, torch.float16, torch.bfloat16
@@ -224,35 +414,47 @@ def op_table(torch, ops, dev, only=None, cpu_budget=0.0, profile_launches=0):
     def nrm(*shape, scale=1.0, mean=0.0):
         return crng.standard_normal(shape, dtype=np.float32) * np.float32(scale) + np.float32(mean)
 
-    def run(name, shape_desc, dtype_s, alg_bytes, units, unit_name, make_sets, fn, latency_bound=False, cpu=None):
-        """cpu: a factory returning (oracle call, units it covers) for the CPU column."""
-        if only and name.split()[0] not in only:
+    def selected(name):
+        """--only names ops by their first word; the latency-bound Qwen rows only come with `qwen`."""
+        if not only:
+            return True
+        return "qwen" in only if " qwen " in name else name.split()[0] in only
+
+    def run(r: Row, min_bytes=ROTATION_MIN):
+        if not selected(r.name):
             return
-        sets = make_sets()
+        if r.latency:
+            sets, rot = [r.make_set(i) for i in range(2)], None
+        else:
+            sets, rot = rotation(torch, r.make_set, min_bytes)
         if profile_launches > 0:
             for i in range(profile_launches):
-                fn(sets[i % len(sets)])
+                r.fn(sets[i % len(sets)])
             torch.cuda.synchronize()
             del sets
             torch.cuda.empty_cache()
             return
-        if latency_bound:  # one call's latency: the median of 20 event-bracketed launches
-            warm(torch, fn, sets)
-            per, _ = time_launches(torch, fn, sets, 0, 20)
-            ms = median(per)
-        else:  # throughput: the median of 5 regions of 20 back-to-back launches between one event pair
-            ms = time_regions(torch, fn, sets)
-        gbs = alg_bytes / (ms * 1e-3) / 1e9
-        row = {"op": name, "shape": shape_desc, "dtype": dtype_s, "us": round(ms * 1e3, 2),
-               "GB/s": round(gbs, 1), "pct_peak": round(100 * gbs / PEAK_GBS, 1),
-               f"{unit_name}/s": round(units / (ms * 1e-3), 1), "alg_bytes": alg_bytes,
-               "latency_bound": latency_bound}
-        if cpu is not None and orc is not None:
-            call, sample = cpu()
+        row = {"op": r.name, "shape": r.shape, "dtype": r.dtype}
+        if r.latency:  # kernel time filled in from the kernel trace; graph replay and one call meanwhile
+            warm(torch, r.fn, sets)
+            per, _ = time_launches(torch, r.fn, sets, 0, 20)
+            row["graph_us"] = round(time_graph(torch, r.fn, sets) * 1e3, 2)
+            row["call_us"] = round(median(per) * 1e3, 2)
+            ms = row["graph_us"] * 1e-3
+        else:  # throughput: the median of 5 regions of back-to-back launches between one event pair
+            ms = time_regions(torch, r.fn, sets)
+        gbs = r.alg_bytes / (ms * 1e-3) / 1e9
+        row.update({"us": round(ms * 1e3, 2), "GB/s": round(gbs, 1), "pct_peak": round(100 * gbs / PEAK_GBS, 1),
+                    f"{r.unit_name}/s": round(r.units / (ms * 1e-3), 1), "alg_bytes": r.alg_bytes,
+                    "latency_bound": r.latency})
+        if rot is not None:
+            row["rotation_bytes"], row["sets"] = rot, len(sets)
+        if r.cpu is not None and orc is not None:
+            call, sample = r.cpu()
             sec, _ = cpu_time(call, cpu_budget)
-            row[f"cpu_{unit_name}/s"] = round(sample / sec, 1)
+            row[f"cpu_{r.unit_name}/s"] = round(sample / sec, 1)
             row["cpu_sample"] = sample
-            row["gpu_vs_cpu"] = round((units / (ms * 1e-3)) / (sample / sec), 1)
+            row["gpu_vs_cpu"] = round((r.units / (ms * 1e-3)) / (sample / sec), 1)
         res.append(row)
         del sets
         torch.cuda.empty_cache()
@@ -261,95 +463,85 @@ def op_table(torch, ops, dev, only=None, cpu_budget=0.0, profile_launches=0):
     rows, dim = 16384, 4096
     for dt, tag in ((f16, "f16"), (bf16, "bf16")):
         w = gen(torch, (dim,), 3, dev, f32, 0.1, 1.0)
-        run("add_rms_norm", f"{rows}x{dim}", tag + " (f32 w)", 4 * rows * dim * 2 + dim * 4, rows, "rows",
-            lambda dt=dt: [(gen(torch, (rows, dim), 30 + i, dev, dt), gen(torch, (rows, dim), 40 + i, dev, dt),
-                            torch.empty(rows, dim, device=dev, dtype=dt)) for i in range(3)],
-            lambda s, w=w: ops.add_rms_norm(s[0], s[1], w, 1e-5, out=s[2]),
-            cpu=lambda: (lambda x=nrm(256, dim), r=nrm(256, dim), w=nrm(dim, scale=0.1, mean=1.0):
-                         orc.add_rms_norm(x, r, w, 1e-5), 256))
+        run(Row("add_rms_norm", f"{rows}x{dim}", tag + " (f32 w)", 4 * rows * dim * 2 + dim * 4, rows, "rows",
+                lambda i, dt=dt: (gen(torch, (rows, dim), 30 + i, dev, dt), gen(torch, (rows, dim), 40 + i, dev, dt),
+                                  torch.empty(rows, dim, device=dev, dtype=dt)),
+                lambda s, w=w: ops.add_rms_norm(s[0], s[1], w, 1e-5, out=s[2]),
+                lambda: (lambda x=nrm(256, dim), r=nrm(256, dim), w=nrm(dim, scale=0.1, mean=1.0):
+                         orc.add_rms_norm(x, r, w, 1e-5), 256)))
     # Plain RMSNorm at the same width (the norm the fused kernel's second half is)
     for dt, tag in ((f32, "f32"), (f16, "f16"), (bf16, "bf16")):
         w = gen(torch, (dim,), 3, dev, f32, 0.1, 1.0)
         es = 4 if dt == f32 else 2
-        run("rms_norm", f"{rows}x{dim}", tag + " (f32 w)", 2 * rows * dim * es + dim * 4, rows, "rows",
-            lambda dt=dt: [(gen(torch, (rows, dim), 20 + i, dev, dt), torch.empty(rows, dim, device=dev, dtype=dt))
-                           for i in range(3 if dt == f32 else 5)],
-            lambda s, w=w: ops.rms_norm(s[0], w, 1e-5, out=s[1]),
-            cpu=lambda: (lambda x=nrm(256, dim), w=nrm(dim, scale=0.1, mean=1.0): orc.rms_norm(x, w, 1e-5), 256))
+        run(Row("rms_norm", f"{rows}x{dim}", tag + " (f32 w)", 2 * rows * dim * es + dim * 4, rows, "rows",
+                lambda i, dt=dt: (gen(torch, (rows, dim), 20 + i, dev, dt), torch.empty(rows, dim, device=dev, dtype=dt)),
+                lambda s, w=w: ops.rms_norm(s[0], w, 1e-5, out=s[1]),
+                lambda: (lambda x=nrm(256, dim), w=nrm(dim, scale=0.1, mean=1.0): orc.rms_norm(x, w, 1e-5), 256)))
     # C3: RoPE, Q 32 + K 8 heads, T 8192, head_dim 128, in place
     T, D = 8192, 128
+    pos = torch.arange(T, dtype=torch.int32, device=dev)
     for dt, tag in ((f32, "f32"), (f16, "f16")):
         for il in (False, True):
-            pos = torch.arange(T, dtype=torch.int32, device=dev)
             n_el = (32 + 8) * T * D
-            run("rope_" + ("interleaved" if il else "neox"), f"q32+k8 x {T} x {D}", tag, 2 * n_el * (4 if dt == f32 else 2),
-                T, "tokens",
-                lambda dt=dt: [(gen(torch, (1, 32, T, D), 50 + i, dev, dt), gen(torch, (1, 8, T, D), 60 + i, dev, dt))
-                               for i in range(4 if dt == f16 else 2)],
-                lambda s, il=il, pos=pos: ops.rope_(s[0], s[1], pos, 5e5, interleaved=il),
-                cpu=lambda il=il: (lambda x=nrm(1, 40, 32, D), p=np.arange(4000, 4032):
-                                   orc.apply_rope_partial_scaled(x, p, 5e5, D, 1.0, il), 32))
+            run(Row("rope_" + ("interleaved" if il else "neox"), f"q32+k8 x {T} x {D}", tag,
+                    2 * n_el * (4 if dt == f32 else 2), T, "tokens",
+                    lambda i, dt=dt: (gen(torch, (1, 32, T, D), 50 + i, dev, dt), gen(torch, (1, 8, T, D), 60 + i, dev, dt)),
+                    lambda s, il=il: ops.rope_(s[0], s[1], pos, 5e5, interleaved=il),
+                    lambda il=il: (lambda x=nrm(1, 40, 32, D), p=np.arange(4000, 4032):
+                                   orc.apply_rope_partial_scaled(x, p, 5e5, D, 1.0, il), 32)))
     # C4: SwiGLU [8192, 14336] f16, GELU-tanh [8192, 10240] f16
     n = 8192 * 14336
-    run("swiglu", "8192x14336", "f16", 3 * n * 2, 8192, "rows",
-        lambda: [(gen(torch, (8192, 14336), 70 + i, dev, f16, 2.0), gen(torch, (8192, 14336), 80 + i, dev, f16, 2.0),
-                  torch.empty(8192, 14336, device=dev, dtype=f16)) for i in range(2)],
-        lambda s: ops.swiglu(s[0], s[1], out=s[2]),
-        cpu=lambda: (lambda g=nrm(64, 14336, scale=2.0), u=nrm(64, 14336, scale=2.0): orc.swiglu(g, u), 64))
-    run("swiglu", "8192x14336", "f32", 3 * n * 4, 8192, "rows",
-        lambda: [(gen(torch, (8192, 14336), 75 + i, dev, f32, 2.0), gen(torch, (8192, 14336), 85 + i, dev, f32, 2.0),
-                  torch.empty(8192, 14336, device=dev, dtype=f32)) for i in range(2)],
-        lambda s: ops.swiglu(s[0], s[1], out=s[2]),
-        cpu=lambda: (lambda g=nrm(64, 14336, scale=2.0), u=nrm(64, 14336, scale=2.0): orc.swiglu(g, u), 64))
-    ops.init(dev)
+    for dt, tag, es, seed in ((f16, "f16", 2, 70), (f32, "f32", 4, 75)):
+        run(Row("swiglu", "8192x14336", tag, 3 * n * es, 8192, "rows",
+                lambda i, dt=dt, seed=seed: (gen(torch, (8192, 14336), seed + i, dev, dt, 2.0),
+                                             gen(torch, (8192, 14336), seed + 10 + i, dev, dt, 2.0),
+                                             torch.empty(8192, 14336, device=dev, dtype=dt)),
+                lambda s: ops.swiglu(s[0], s[1], out=s[2]),
+                lambda: (lambda g=nrm(64, 14336, scale=2.0), u=nrm(64, 14336, scale=2.0): orc.swiglu(g, u), 64)))
+    if profile_launches == 0 or not only or "gelu_tanh" in only or "gelu_erf" in only:
+        ops.init(dev)
     n = 8192 * 10240
-    run("gelu_tanh", "8192x10240", "f16", 2 * n * 2, 8192, "rows",
-        lambda: [(gen(torch, (8192, 10240), 90 + i, dev, f16, 2.0), torch.empty(8192, 10240, device=dev, dtype=f16))
-                 for i in range(3)],
-        lambda s: ops.gelu_tanh(s[0], out=s[1]),
-        cpu=lambda: (lambda x=nrm(64, 10240, scale=2.0): orc.gelu(x), 64))
-    # the same GELU in f32, the reference's own activation type (compute-bound: glibc's tanhf per element)
-    run("gelu_tanh", "8192x10240", "f32", 2 * n * 4, 8192, "rows",
-        lambda: [(gen(torch, (8192, 10240), 95 + i, dev, f32, 2.0), torch.empty(8192, 10240, device=dev))
-                 for i in range(2)],
-        lambda s: ops.gelu_tanh(s[0], out=s[1]),
-        cpu=lambda: (lambda x=nrm(64, 10240, scale=2.0): orc.gelu(x), 64))
+    # f32 is the reference's own activation type (glibc's tanhf per element)
+    for dt, tag, es, seed in ((f16, "f16", 2, 90), (f32, "f32", 4, 95)):
+        run(Row("gelu_tanh", "8192x10240", tag, 2 * n * es, 8192, "rows",
+                lambda i, dt=dt, seed=seed: (gen(torch, (8192, 10240), seed + i, dev, dt, 2.0),
+                                             torch.empty(8192, 10240, device=dev, dtype=dt)),
+                lambda s: ops.gelu_tanh(s[0], out=s[1]),
+                lambda: (lambda x=nrm(64, 10240, scale=2.0): orc.gelu(x), 64)))
     # LayerNorm (+ bias), erf-GELU and the bias add: the encoder-family norm / activation path
-    rows, dim = 16384, 4096
     wl, bl = gen(torch, (dim,), 4, dev, f32, 0.1, 1.0), gen(torch, (dim,), 5, dev, f32, 0.1)
     for dt, tag, es in ((f32, "f32", 4), (f16, "f16 (f32 w,b)", 2)):
-        run("layer_norm", f"{rows}x{dim}", tag, 2 * rows * dim * es + 2 * dim * 4, rows, "rows",
-            lambda dt=dt: [(gen(torch, (rows, dim), 150 + i, dev, dt, 2.0, 0.5), torch.empty(rows, dim, device=dev, dtype=dt))
-                           for i in range(3)],
-            lambda s: ops.layer_norm(s[0], wl, bl, 1e-5, out=s[1]),
-            cpu=lambda: (lambda x=nrm(256, dim, scale=2.0, mean=0.5), w=nrm(dim, scale=0.1, mean=1.0),
-                         b=nrm(dim, scale=0.1): orc.layer_norm(x, w, b, 1e-5), 256))
-    run("add_bias", f"{rows}x{dim}", "f32", 2 * rows * dim * 4 + dim * 4, rows, "rows",
-        lambda: [(gen(torch, (rows, dim), 160 + i, dev, f32), torch.empty(rows, dim, device=dev)) for i in range(3)],
-        lambda s: ops.add_bias(s[0], bl, out=s[1]),
-        cpu=lambda: (lambda y=nrm(256, dim), b=nrm(dim, scale=0.1): orc.add_bias_last_dim(y, b), 256))
+        run(Row("layer_norm", f"{rows}x{dim}", tag, 2 * rows * dim * es + 2 * dim * 4, rows, "rows",
+                lambda i, dt=dt: (gen(torch, (rows, dim), 150 + i, dev, dt, 2.0, 0.5),
+                                  torch.empty(rows, dim, device=dev, dtype=dt)),
+                lambda s: ops.layer_norm(s[0], wl, bl, 1e-5, out=s[1]),
+                lambda: (lambda x=nrm(256, dim, scale=2.0, mean=0.5), w=nrm(dim, scale=0.1, mean=1.0),
+                         b=nrm(dim, scale=0.1): orc.layer_norm(x, w, b, 1e-5), 256)))
+    run(Row("add_bias", f"{rows}x{dim}", "f32", 2 * rows * dim * 4 + dim * 4, rows, "rows",
+            lambda i: (gen(torch, (rows, dim), 160 + i, dev, f32), torch.empty(rows, dim, device=dev)),
+            lambda s: ops.add_bias(s[0], bl, out=s[1]),
+            lambda: (lambda y=nrm(256, dim), b=nrm(dim, scale=0.1): orc.add_bias_last_dim(y, b), 256)))
     n = 12000 * 5120
     for dt, tag, es in ((f32, "f32", 4), (f16, "f16", 2)):
-        run("gelu_erf", "12000x5120", tag, 2 * n * es, 12000, "rows",
-            lambda dt=dt: [(gen(torch, (12000, 5120), 170 + i, dev, dt, 2.0), torch.empty(12000, 5120, device=dev, dtype=dt))
-                           for i in range(3)],
-            lambda s: ops.gelu_erf(s[0], out=s[1]),
-            cpu=lambda: (lambda x=nrm(64, 5120, scale=2.0): orc.gelu_erf(x), 64))
+        run(Row("gelu_erf", "12000x5120", tag, 2 * n * es, 12000, "rows",
+                lambda i, dt=dt: (gen(torch, (12000, 5120), 170 + i, dev, dt, 2.0),
+                                  torch.empty(12000, 5120, device=dev, dtype=dt)),
+                lambda s: ops.gelu_erf(s[0], out=s[1]),
+                lambda: (lambda x=nrm(64, 5120, scale=2.0): orc.gelu_erf(x), 64)))
     # Decode-chain helpers: head transpose of a Llama-3-8B prefill Q, KV-cache append of its K
     T, H, D = 8192, 32, 128
     for dt, tag, es in ((f32, "f32", 4), (f16, "f16", 2)):
-        run("transpose_heads", f"{T}x{H}x{D}", tag, 2 * T * H * D * es, T, "tokens",
-            lambda dt=dt: [(gen(torch, (T, H, D), 180 + i, dev, dt), torch.empty(H, T, D, device=dev, dtype=dt))
-                           for i in range(3)],
-            lambda s: ops.transpose_heads(s[0], out=s[1]),
-            cpu=lambda es=es: (lambda x=(nrm(64, H, D) if es == 4 else crng.integers(0, 65536, (64, H, D), dtype=np.uint16)):
-                               orc.transpose_heads(x, 64, H, D), 64))
-    run("kv_append", f"8x{T}x{D} -> cache 8x{T}x{D}", "f32->f16", 8 * T * D * (4 + 2), T, "tokens",
-        lambda: [(gen(torch, (8, T, D), 190 + i, dev, f32), torch.empty(8, T, D, device=dev, dtype=f16))
-                 for i in range(3)],
-        lambda s: ops.kv_append(s[0], s[1], 0),
-        cpu=lambda: (lambda x=nrm(8, 64, D), c=np.zeros((8, T, D), np.uint16):
-                     orc.kv_append(x, c, L.F16, 8, 64, D, T, 0), 64))
+        run(Row("transpose_heads", f"{T}x{H}x{D}", tag, 2 * T * H * D * es, T, "tokens",
+                lambda i, dt=dt: (gen(torch, (T, H, D), 180 + i, dev, dt), torch.empty(H, T, D, device=dev, dtype=dt)),
+                lambda s: ops.transpose_heads(s[0], out=s[1]),
+                lambda es=es: (lambda x=(nrm(64, H, D) if es == 4 else
+                                         crng.integers(0, 65536, (64, H, D), dtype=np.uint16)):
+                               orc.transpose_heads(x, 64, H, D), 64)))
+    run(Row("kv_append", f"8x{T}x{D} -> cache 8x{T}x{D}", "f32->f16", 8 * T * D * (4 + 2), T, "tokens",
+            lambda i: (gen(torch, (8, T, D), 190 + i, dev, f32), torch.empty(8, T, D, device=dev, dtype=f16)),
+            lambda s: ops.kv_append(s[0], s[1], 0),
+            lambda: (lambda x=nrm(8, 64, D), c=np.zeros((8, T, D), np.uint16):
+                     orc.kv_append(x, c, L.F16, 8, 64, D, T, 0), 64)))
 
     def cpu_gather(dt, block, nbytes, d_off, nd, hidden, n):
         """The oracle's gather of n ids from a 2048-row table of the same format (cost per row does not
@@ -361,80 +553,72 @@ def op_table(torch, ops, dev, only=None, cpu_budget=0.0, profile_launches=0):
             t[:, d_off:d_off + 2 * nd] = crng.uniform(0.0005, 0.02, (nb_c, nd)).astype(np.float16).view(np.uint8)
         ids_c = crng.integers(0, vocab_c, n).astype(np.uint32)
         return (lambda: orc.embed_tokens(t, dt, vocab_c, hidden, ids_c)), n
-    # C5: Q4_K embedding gather, 128256 x 4096 table, 65536 ids (uniform, Zipf 1.1)
+
+    # C5 and the other table formats: 128256 x 4096 tables, 65536 ids. Each buffer set is a table of
+    # its own, an id set of its own and an output, so no launch reads rows the previous one left in cache.
     vocab, hidden, n_ids = 128256, 4096, 65536
-    nb = vocab * hidden // 256
     g = torch.Generator(device=dev).manual_seed(7)
-    table = torch.randint(0, 256, (nb, 144), generator=g, device=dev, dtype=torch.int32).to(torch.uint8)
-    dd = (torch.rand((nb, 2), generator=g, device=dev) * (0.02 - 0.0005) + 0.0005).to(f16)
-    table[:, 0:4] = dd.view(torch.uint8).view(nb, 4)
-    table = table.reshape(-1)
     rng = np.random.default_rng(8)
     p = 1.0 / np.arange(1, vocab + 1) ** 1.1
-    zipf = rng.permutation(vocab)[np.minimum(np.searchsorted(np.cumsum(p / p.sum()), rng.random(n_ids)), vocab - 1)]
-    for dist, ids_np in (("uniform", rng.integers(0, vocab, n_ids)), ("zipf1.1", zipf)):
-        ids = torch.from_numpy(ids_np.astype(np.int32)).to(dev)
-        run(f"embed_q4_k {dist}", f"{vocab}x{hidden} -> {n_ids} ids", "q4_k->f32",
-            n_ids * (2304 + 4 + hidden * 4), n_ids, "rows",
-            lambda: [torch.empty(n_ids, hidden, device=dev) for _ in range(2)],
-            lambda o, ids=ids: ops.embed(table, L.Q4_K, vocab, hidden, ids, out=o),
-            cpu=lambda: cpu_gather(L.Q4_K, 256, 144, 0, 2, hidden, 1024))
-    del table
-    # The other GGUF table formats at the same shape and uniform ids (f1 and the data formats around C5)
-    ids = torch.from_numpy(rng.integers(0, vocab, n_ids).astype(np.int32)).to(dev)
-    for dt, name, block, nbytes, d_off in ((L.Q8_0, "q8_0", 32, 34, 0), (L.Q4_0, "q4_0", 32, 18, 0),
-                                           (L.Q5_K, "q5_k", 256, 176, 0), (L.Q6_K, "q6_k", 256, 210, 208)):
-        nb = vocab * hidden // block
-        table = torch.randint(0, 256, (nb, nbytes), generator=g, device=dev, dtype=torch.int32).to(torch.uint8)
-        nd = 2 if dt == L.Q5_K else 1  # d (and dmin) as f16 in [0.0005, 0.02)
-        dd = (torch.rand((nb, nd), generator=g, device=dev) * (0.02 - 0.0005) + 0.0005).to(f16)
-        table[:, d_off:d_off + 2 * nd] = dd.view(torch.uint8).view(nb, 2 * nd)
-        table = table.reshape(-1)
-        row_bytes = hidden // block * nbytes
-        run(f"embed_{name} uniform", f"{vocab}x{hidden} -> {n_ids} ids", f"{name}->f32",
-            n_ids * (row_bytes + 4 + hidden * 4), n_ids, "rows",
-            lambda: [torch.empty(n_ids, hidden, device=dev) for _ in range(2)],
-            lambda o, table=table, dt=dt: ops.embed(table, dt, vocab, hidden, ids, out=o),
-            cpu=lambda dt=dt, block=block, nbytes=nbytes, d_off=d_off, nd=nd:
-                cpu_gather(dt, block, nbytes, d_off, nd, hidden, 1024))
-        del table
+    cdf = np.cumsum(p / p.sum())
+
+    def zipf_ids(i):
+        prng = np.random.default_rng(80 + i)
+        return prng.permutation(vocab)[np.minimum(np.searchsorted(cdf, prng.random(n_ids)), vocab - 1)]
+
+    formats = ((L.Q4_K, "q4_k", 256, 144, 0, 2), (L.Q8_0, "q8_0", 32, 34, 0, 1), (L.Q4_0, "q4_0", 32, 18, 0, 1),
+               (L.Q5_K, "q5_k", 256, 176, 0, 2), (L.Q6_K, "q6_k", 256, 210, 208, 1))
+    for dt, name, block, nbytes, d_off, nd in formats:
+        dists = ("uniform", "zipf1.1") if dt == L.Q4_K else ("uniform",)
+        for dist in dists:
+            def make_set(i, dist=dist, block=block, nbytes=nbytes, d_off=d_off, nd=nd):
+                ids_np = zipf_ids(i) if dist == "zipf1.1" else rng.integers(0, vocab, n_ids)
+                return (q_table(torch, dev, g, vocab, hidden, block, nbytes, d_off, nd),
+                        torch.from_numpy(ids_np.astype(np.int32)).to(dev), torch.empty(n_ids, hidden, device=dev))
+            row_bytes = hidden // block * nbytes
+            run(Row(f"embed_{name} {dist}", f"{vocab}x{hidden} -> {n_ids} ids", f"{name}->f32",
+                    n_ids * (row_bytes + 4 + hidden * 4), n_ids, "rows", make_set,
+                    lambda s, dt=dt: ops.embed(s[0], dt, vocab, hidden, s[1], out=s[2]),
+                    lambda dt=dt, block=block, nbytes=nbytes, d_off=d_off, nd=nd:
+                        cpu_gather(dt, block, nbytes, d_off, nd, hidden, 1024)))
     # C1: Qwen2.5-0.5B layer ops (latency-bound, reported only)
-    H = 896
-    for T1 in (1, 512):
-        w = gen(torch, (H,), 3, dev, f32, 0.1, 1.0)
-        run(f"rms_norm qwen T={T1}", f"{T1}x{H}", "f32", T1 * H * 8 + H * 4, T1, "rows",
-            lambda T1=T1: [(gen(torch, (T1, H), 100 + i, dev, f32), torch.empty(T1, H, device=dev)) for i in range(2)],
-            lambda s, w=w: ops.rms_norm(s[0], w, 1e-6, out=s[1]), latency_bound=True,
-            cpu=lambda T1=T1: (lambda x=nrm(T1, H), w=nrm(H, scale=0.1, mean=1.0): orc.rms_norm(x, w, 1e-6), T1))
-        pos = torch.arange(T1, dtype=torch.int32, device=dev)
-        run(f"rope_neox qwen T={T1}", f"q14+k2 x {T1} x 64", "f32", 2 * 16 * T1 * 64 * 4, T1, "tokens",
-            lambda T1=T1: [(gen(torch, (1, 14, T1, 64), 110 + i, dev, f32), gen(torch, (1, 2, T1, 64), 120 + i, dev, f32))
-                           for i in range(2)],
-            lambda s, pos=pos: ops.rope_(s[0], s[1], pos, 1e6), latency_bound=True,
-            cpu=lambda T1=T1: (lambda q=nrm(1, 16, T1, 64), p=np.arange(T1): orc.apply_rope(q, p, 1e6), T1))
-        run(f"swiglu qwen T={T1}", f"{T1}x4864", "f32", 3 * T1 * 4864 * 4, T1, "rows",
-            lambda T1=T1: [(gen(torch, (T1, 4864), 130 + i, dev, f32), gen(torch, (T1, 4864), 140 + i, dev, f32),
-                            torch.empty(T1, 4864, device=dev)) for i in range(2)],
-            lambda s: ops.swiglu(s[0], s[1], out=s[2]), latency_bound=True,
-            cpu=lambda T1=T1: (lambda g=nrm(T1, 4864), u=nrm(T1, 4864): orc.swiglu(g, u), T1))
-    vocab_q, hid_q = 151936, 896
-    nbq = vocab_q * hid_q // 32
-    tq = torch.randint(-127, 128, (nbq, 34), generator=g, device=dev, dtype=torch.int32).to(torch.int8).view(torch.uint8)
-    dq = (torch.rand((nbq, 1), generator=g, device=dev) * (0.05 - 0.001) + 0.001).to(f16)
-    tq[:, 0:2] = dq.view(torch.uint8).view(nbq, 2)
-    tq = tq.reshape(-1)
-    for T1 in (1, 512):
-        ids = torch.from_numpy(rng.integers(0, vocab_q, T1).astype(np.int32)).to(dev)
-        run(f"embed_q8_0 qwen T={T1}", f"{vocab_q}x{hid_q} -> {T1} ids", "q8_0->f32", T1 * (952 + 4 + hid_q * 4),
-            T1, "rows", lambda T1=T1: [torch.empty(T1, hid_q, device=dev) for _ in range(2)],
-            lambda o, ids=ids: ops.embed(tq, L.Q8_0, vocab_q, hid_q, ids, out=o), latency_bound=True,
-            cpu=lambda T1=T1: cpu_gather(L.Q8_0, 32, 34, 0, 1, hid_q, T1))
+    lrows, tq, vocab_q = latency_rows(torch, ops, dev, orc, nrm, cpu_gather)
+    first_latency = len(res)
+    for r in lrows:
+        run(r)
+    if profile_launches == 0 and kernel_trace and any(selected(r.name) for r in lrows):
+        times, note = latency_kernel_times([r.name for r in lrows])
+        for row in res[first_latency:]:
+            if times is not None and row["op"] in times:
+                us, kernel = times[row["op"]]
+                lr = next(r for r in lrows if r.name == row["op"])
+                gbs = lr.alg_bytes / (us * 1e-6) / 1e9
+                row.update({"us": round(us, 2), "GB/s": round(gbs, 1), "pct_peak": round(100 * gbs / PEAK_GBS, 1),
+                            f"{lr.unit_name}/s": round(lr.units / (us * 1e-6), 1), "kernel": kernel})
+                if "cpu_sample" in row:
+                    row["gpu_vs_cpu"] = round((lr.units / (us * 1e-6)) / row[f"cpu_{lr.unit_name}/s"], 1)
+            row["us_method"] = note if times is not None else f"graph replay per launch ({note})"
     # Device-resident decode engine at Qwen2.5-0.5B shape (24 layers, 896 hidden, 14 + 2 heads x 64,
     # 4864 intermediate, f16 KV cache, Q8_0 embedding): this library's part of a token
     # (projections / attention skipped), launched eagerly and replayed from a HIP graph.
-    if not only or "engine" in only:
+    if profile_launches == 0 and (not only or "engine" in only):
         res.extend(engine_rows(torch, dev, tq, vocab_q))
     return res
+
+
+def calibration_copies(torch, ops, dev, warmup, steps):
+    """Copies of known size for the HBM counters (2 x 16384 x 4096 f32 = 512 MiB read and 512 MiB
+    written per launch): torch's `copy_` and `neg` (kernels this library did not write), then the
+    library's own element-wise add of a length-1 zero operand."""
+    n = 2 * 16384 * 4096
+    a = [gen(torch, (n,), 90 + i, dev, torch.float32) for i in range(2)]
+    o = [torch.empty(n, device=dev) for _ in range(2)]
+    zero = torch.zeros(1, device=dev)
+    time_launches(torch, lambda i: o[i].copy_(a[i]), [0, 1], warmup, steps)
+    time_launches(torch, lambda i: torch.neg(a[i], out=o[i]), [0, 1], warmup, steps)
+    time_launches(torch, lambda i: ops.add(a[i], zero, out=o[i]), [0, 1], warmup, steps)
+    return {"copy_bytes_read": n * 4, "copy_bytes_written": n * 4,
+            "calibration_kernels": ["torch copy_", "torch neg", "sph add (a + 0)"]}
 
 
 def main():
@@ -444,6 +628,9 @@ def main():
               "N copies of the one-GPU kernel on 1/N of the rows (no exchange step). Run with --gpus 1.",
               file=sys.stderr)
         sys.exit(2)
+    if args.latency_child:
+        latency_child()
+        return
     import torch
 
     import sapient_amd
@@ -456,28 +643,16 @@ def main():
     torch.cuda.set_device(dev)
 
     if args.profile_run and args.only:
-        # Launch the selected op-table rows (warmup + steps launches each), then the calibration copy.
+        # Launch the selected op-table rows (warmup + steps launches each), then the calibration copies.
         op_table(torch, ops, dev, set(args.only.split(",")), 0.0, profile_launches=args.warmup + args.steps)
-        rows, dim = 16384, 4096
-        n = 2 * rows * dim
-        a = [gen(torch, (n,), 90 + i, dev, torch.float32) for i in range(2)]
-        o = [torch.empty(n, device=dev) for _ in range(2)]
-        zero = torch.zeros(1, device=dev)
-        time_launches(torch, lambda i: ops.add(a[i], zero, out=o[i]), [0, 1], args.warmup, args.steps)
-        print(json.dumps({"profile_run": True, "ops": args.only, "launches_per_row": args.warmup + args.steps,
-                          "copy_bytes_read": n * 4, "copy_bytes_written": n * 4}))
+        cal = calibration_copies(torch, ops, dev, args.warmup, args.steps)
+        print(json.dumps({"profile_run": True, "ops": args.only, "launches_per_row": args.warmup + args.steps, **cal}))
         return
-    rows, dim, alg_bytes, region_ms, wall = headline(torch, ops, dev, args)
+    rows, dim, alg_bytes, region_ms, wall, rot_bytes = headline(torch, ops, dev, args)
     if args.profile_run:
-        # Calibration for the HBM counters: a copy of known size through the
-        # library's own element-wise kernel (out = a + 0, 512 MiB in, 512 MiB out).
-        n = 2 * rows * dim
-        a = [gen(torch, (n,), 90 + i, dev, torch.float32) for i in range(2)]
-        o = [torch.empty(n, device=dev) for _ in range(2)]
-        zero = torch.zeros(1, device=dev)
-        time_launches(torch, lambda i: ops.add(a[i], zero, out=o[i]), [0, 1], args.warmup, args.steps)
+        cal = calibration_copies(torch, ops, dev, args.warmup, args.steps)
         print(json.dumps({"profile_run": True, "headline_avg_us": round(region_ms / args.steps * 1e3, 2),
-                          "headline_alg_bytes": alg_bytes, "copy_bytes_read": n * 4, "copy_bytes_written": n * 4}))
+                          "headline_alg_bytes": alg_bytes, **cal}))
         return
     avg_ms = region_ms / args.steps
     achieved = alg_bytes / (avg_ms * 1e-3) / 1e9
@@ -520,11 +695,13 @@ def main():
                      "avg_launch_us": round(avg_ms * 1e3, 2)},
         "cpu_baseline": cpu,
         "timing": {"region_ms": round(region_ms, 3), "host_wall_ms": round(wall * 1e3, 3),
+                   "rotation_bytes": rot_bytes,
                    "method": "one HIP event pair around the timed launches on their stream"},
     }
     if not args.no_ops:
         only = set(args.only.split(",")) if args.only else None
-        line["ops"] = op_table(torch, ops, dev, only, 0.0 if args.no_cpu else args.op_cpu_seconds)
+        line["ops"] = op_table(torch, ops, dev, only, 0.0 if args.no_cpu else args.op_cpu_seconds,
+                               kernel_trace=not args.no_kernel_trace)
         if not args.no_cpu:
             line["ops_cpu"] = ("cpu_*/s: the oracle (the reference's algorithm restated in C, f32, one thread) on "
                                "cpu_sample rows / tokens / ids of each shape, timed on this host; gpu_vs_cpu = the "
