@@ -23,17 +23,20 @@
 //    4 consecutive outputs per step, so every store instruction writes 1 KiB
 //    contiguous (16 bytes per lane), non-temporal (non-temporal stores and the
 //    larger block measured 4.8 → 6.5 TB/s on the Q4_K gather).
-//  - The packed blocks are consumed as stored — no repacking. Q4_K and Q8_0
-//    rows are first copied into LDS with 16-byte (Q8_0: the widest aligned)
-//    loads, each cache line requested by one lane (embed_q4_k_staged,
-//    embed_q8_0_staged); Q4_K then takes one 256-element super-block per step:
-//    a lane reads the 16-byte header (d, dmin, 12 scale bytes) and the dword of
-//    nibbles it needs and unpacks its (sc, m) pair in registers.
-//  - Q4_0 / Q6_K blocks are 2-byte aligned only (18 / 210 bytes), so lanes
-//    read them in place in 16-bit pieces; Q5_K blocks (176 bytes) stay 16-byte
-//    aligned, so a lane reads its header, nibble dword and high-bit dword whole.
+//  - The packed blocks are consumed as stored — no repacking. A wave first
+//    copies its row (a chunk of whole blocks at a time) into LDS with the
+//    widest loads the row length and table address allow (16, 8 or 4 bytes),
+//    each cache line requested by one lane and a chunk's loads all in flight
+//    together, then dequantizes from LDS (embed_staged; Q4_K: embed_q4_k_staged,
+//    which takes one 256-element super-block per step: a lane reads the
+//    16-byte header (d, dmin, 12 scale bytes) and the dword of nibbles it needs
+//    and unpacks its (sc, m) pair in registers).
+//  - Rows whose length or address admits only 2-byte loads (Q4_0, Q8_0 and
+//    Q6_K blocks are 18, 34 and 210 bytes) are read in place (embed_rows).
 //  - An id >= vocab zero-fills its row and raises `bad_id_flag`; the table is
 //    never read out of bounds.
+#include <type_traits>
+
 #include "sph_common.h"
 
 namespace sph {
@@ -209,28 +212,44 @@ __global__ __launch_bounds__(kThreads) void embed_rows(const uint8_t* __restrict
     }
 }
 
-// Q8_0 rows staged through LDS: 34-byte blocks leave every block 2-byte
-// aligned, so reading them in place costs three 2-byte loads per 4 outputs.
-// A wave instead copies a chunk of its row (up to 128 blocks, 4352 bytes) into
-// LDS with W-byte loads — W the widest power of two dividing both the row
-// length and the table's alignment — and dequantizes from there. Every wave of
-// a block runs the same number of chunk steps (hidden is uniform), so the
-// block barriers are reached by all, tokens past n_ids included.
-constexpr int kQ8ChunkBlocks = 128;
-constexpr int kQ8ChunkBytes = kQ8ChunkBlocks * 34;  // a multiple of 16
+// Rows staged through LDS (every table type but Q4_K, which has its own lane
+// mapping below). Reading blocks in place waits on memory once per step of
+// four outputs per lane: at 65536 random ids of a 128256 x 4096 table whose
+// rows come from HBM, Q4_0 / Q5_K / Q6_K in place ran at 54-60 % of HBM peak.
+// A wave instead copies a chunk of its row (whole blocks, at most kStageBytes)
+// into LDS with W-byte loads — W the widest power of two dividing both the row
+// length and the table's alignment, so every line is requested once and all of
+// a chunk's loads are in flight together — and dequantizes from there with
+// the same per-element arithmetic as embed_rows. Every wave of a block runs
+// the same number of chunk steps (hidden is uniform), so the block barriers
+// are reached by all, tokens past n_ids included.
+constexpr int kStageBytes = 4608;  // per wave: 16 waves x 4608 B leave room for two blocks per CU
 
 template <int W> struct StageWord;
 template <> struct StageWord<16> { using type = u32x4; };
 template <> struct StageWord<8> { using type = u32x2; };
 template <> struct StageWord<4> { using type = uint32_t; };
 
-template <int W>
-__global__ __launch_bounds__(kThreads) void embed_q8_0_staged(const uint8_t* __restrict__ table, int64_t vocab,
-                                                              int hidden, int64_t row_bytes,
-                                                              const uint32_t* __restrict__ ids, int64_t n_ids,
-                                                              float* __restrict__ out, int32_t* bad_id_flag) {
+// Bytes and elements of the unit a staged chunk is cut in: a quantization
+// block, or four elements of a plain table (hidden is a multiple of 4).
+template <int DT> struct StageUnit;
+template <> struct StageUnit<SPH_F32> { static constexpr int bytes = 16, elems = 4; };
+template <> struct StageUnit<SPH_F16> { static constexpr int bytes = 8, elems = 4; };
+template <> struct StageUnit<SPH_BF16> { static constexpr int bytes = 8, elems = 4; };
+template <> struct StageUnit<SPH_Q4_0> { static constexpr int bytes = 18, elems = 32; };
+template <> struct StageUnit<SPH_Q8_0> { static constexpr int bytes = 34, elems = 32; };
+template <> struct StageUnit<SPH_Q5_K> { static constexpr int bytes = 176, elems = 256; };
+template <> struct StageUnit<SPH_Q6_K> { static constexpr int bytes = 210, elems = 256; };
+
+// chunk_units: units per chunk, chunk_units * bytes <= kStageBytes and a multiple of W.
+template <int DT, int W>
+__global__ __launch_bounds__(kThreads) void embed_staged(const uint8_t* __restrict__ table, int64_t vocab, int hidden,
+                                                         int64_t row_bytes, const uint32_t* __restrict__ ids,
+                                                         int64_t n_ids, float* __restrict__ out, int32_t* bad_id_flag,
+                                                         int chunk_units) {
     using Word = typename StageWord<W>::type;
-    __shared__ __align__(16) uint8_t stage[kTokPerBlock][kQ8ChunkBytes];
+    using U = StageUnit<DT>;
+    __shared__ __align__(16) uint8_t stage[kTokPerBlock][kStageBytes];
     const int lane = threadIdx.x & (kWave - 1);
     const int wv = threadIdx.x / kWave;
     const int64_t t = (int64_t)blockIdx.x * kTokPerBlock + wv;
@@ -244,25 +263,22 @@ __global__ __launch_bounds__(kThreads) void embed_q8_0_staged(const uint8_t* __r
     }
     const uint8_t* row = table + (size_t)(valid ? id : 0u) * (size_t)row_bytes;
     uint8_t* buf = stage[wv];
-    const int nblk = hidden / 32;
-    for (int c0 = 0; c0 < nblk; c0 += kQ8ChunkBlocks) {
-        const int nb = nblk - c0 < kQ8ChunkBlocks ? nblk - c0 : kQ8ChunkBlocks;
-        const int bytes = nb * 34;  // a multiple of W: so are row_bytes and kQ8ChunkBytes
+    const int nunits = hidden / U::elems;
+    for (int c0 = 0; c0 < nunits; c0 += chunk_units) {
+        const int nu = nunits - c0 < chunk_units ? nunits - c0 : chunk_units;
+        const int bytes = nu * U::bytes;  // a multiple of W: so are row_bytes and chunk_units * U::bytes
         if (valid) {
-            const uint8_t* src = row + (size_t)c0 * 34;
+            const uint8_t* src = row + (size_t)c0 * U::bytes;
             for (int o = lane * W; o < bytes; o += kWave * W)
                 *reinterpret_cast<Word*>(buf + o) = *reinterpret_cast<const Word*>(src + o);
         }
         __syncthreads();
         if (valid) {
-            for (int e4 = lane; e4 < nb * 8; e4 += kWave) {
-                const uint8_t* b = buf + (e4 >> 3) * 34;
-                const int j = (e4 & 7) * 4;
-                const float d = widen(f16{*reinterpret_cast<const uint16_t*>(b)});
-                const uint32_t lo = *reinterpret_cast<const uint16_t*>(b + 2 + j);
-                const uint32_t hi = *reinterpret_cast<const uint16_t*>(b + 4 + j);
-                store4(dst + 32 * c0 + 4 * e4, (float)(int8_t)(lo & 0xFF) * d, (float)(int8_t)(lo >> 8) * d,
-                       (float)(int8_t)(hi & 0xFF) * d, (float)(int8_t)(hi >> 8) * d);
+            float* d0 = dst + (size_t)c0 * U::elems;
+            for (int e4 = lane; e4 < nu * (U::elems / 4); e4 += kWave) {
+                float o[4];
+                dequant4<DT>(buf, e4, o);
+                store4(d0 + 4 * e4, o[0], o[1], o[2], o[3]);
             }
         }
         __syncthreads();
@@ -327,26 +343,33 @@ int launch_q4_k_staged(const void* table, int64_t vocab, int64_t hidden, int64_t
     for (int64_t t0 = 0; t0 < n_ids; t0 += kChunk) {
         const int64_t nt = n_ids - t0 < kChunk ? n_ids - t0 : kChunk;
         const dim3 grid((unsigned)((nt + kTokPerBlock - 1) / kTokPerBlock));
-        embed_q4_k_staged<<<grid, kThreads, 0, stream>>>(static_cast<const uint8_t*>(table), vocab, (int)hidden,
-                                                         row_bytes, ids + t0, nt, out + (size_t)t0 * (size_t)hidden,
-                                                         flag);
-        const int st = launch_status();
+        const int st = launch(embed_q4_k_staged, grid, kThreads, stream, static_cast<const uint8_t*>(table), vocab,
+                              (int)hidden, row_bytes, ids + t0, nt, out + (size_t)t0 * (size_t)hidden, flag);
         if (st != SPH_OK) return st;
     }
     return SPH_OK;
 }
 
-template <int W>
-int launch_q8_0_staged(const void* table, int64_t vocab, int64_t hidden, int64_t row_bytes, const uint32_t* ids,
-                       int64_t n_ids, float* out, int32_t* flag, hipStream_t stream) {
+// Units per staged chunk: as many as fit kStageBytes with chunk bytes a multiple of W
+// (W / gcd(unit bytes, W) <= 16 units always qualify and fit).
+template <int DT>
+int stage_chunk_units(int W) {
+    int cu = kStageBytes / StageUnit<DT>::bytes;
+    while (cu > 1 && (cu * StageUnit<DT>::bytes) % W != 0) --cu;
+    return cu;
+}
+
+template <int DT, int W>
+int launch_staged(const void* table, int64_t vocab, int64_t hidden, int64_t row_bytes, const uint32_t* ids,
+                  int64_t n_ids, float* out, int32_t* flag, hipStream_t stream) {
+    const int cu = stage_chunk_units<DT>(W);
+    if ((cu * StageUnit<DT>::bytes) % W != 0 || row_bytes % W != 0) return SPH_EINVAL;
     constexpr int64_t kChunk = int64_t(1) << 24;  // tokens per launch
     for (int64_t t0 = 0; t0 < n_ids; t0 += kChunk) {
         const int64_t nt = n_ids - t0 < kChunk ? n_ids - t0 : kChunk;
         const dim3 grid((unsigned)((nt + kTokPerBlock - 1) / kTokPerBlock));
-        embed_q8_0_staged<W><<<grid, kThreads, 0, stream>>>(static_cast<const uint8_t*>(table), vocab, (int)hidden,
-                                                            row_bytes, ids + t0, nt, out + (size_t)t0 * (size_t)hidden,
-                                                            flag);
-        const int st = launch_status();
+        const int st = launch(embed_staged<DT, W>, grid, kThreads, stream, static_cast<const uint8_t*>(table), vocab,
+                              (int)hidden, row_bytes, ids + t0, nt, out + (size_t)t0 * (size_t)hidden, flag, cu);
         if (st != SPH_OK) return st;
     }
     return SPH_OK;
@@ -359,9 +382,8 @@ int launch_embed(const void* table, int64_t vocab, int64_t hidden, int64_t row_b
     for (int64_t t0 = 0; t0 < n_ids; t0 += kChunk) {
         const int64_t nt = n_ids - t0 < kChunk ? n_ids - t0 : kChunk;
         const dim3 grid((unsigned)((nt + kTokPerBlock - 1) / kTokPerBlock));
-        embed_rows<DT><<<grid, kThreads, 0, stream>>>(static_cast<const uint8_t*>(table), vocab, (int)hidden, row_bytes,
-                                                      ids + t0, nt, out + (size_t)t0 * (size_t)hidden, flag);
-        const int st = launch_status();
+        const int st = launch(embed_rows<DT>, grid, kThreads, stream, static_cast<const uint8_t*>(table), vocab,
+                              (int)hidden, row_bytes, ids + t0, nt, out + (size_t)t0 * (size_t)hidden, flag);
         if (st != SPH_OK) return st;
     }
     return SPH_OK;
@@ -391,23 +413,30 @@ extern "C" int sph_embed(const void* table, int table_dtype, int64_t vocab, int6
     if (ids == nullptr || out == nullptr || (vocab > 0 && table == nullptr)) return SPH_EINVAL;
     if (!aligned(table, align) || !aligned(out, 16) || !aligned(ids, 4)) return SPH_EINVAL;
     hipStream_t s = static_cast<hipStream_t>(stream);
+    if (table_dtype == SPH_Q4_K)
+        return launch_q4_k_staged(table, vocab, hidden, row_bytes, ids, n_ids, out, bad_id_flag, s);
+    // Every other type: staged through LDS with the widest loads the row length and table
+    // address allow, or read in place when only 2-byte loads would do.
+    const int W = (row_bytes % 16 == 0 && aligned(table, 16)) ? 16
+                : (row_bytes % 8 == 0 && aligned(table, 8))   ? 8
+                : (row_bytes % 4 == 0 && aligned(table, 4))   ? 4 : 0;
+    auto go = [&](auto dt) -> int {
+        constexpr int DT = decltype(dt)::value;
+        switch (W) {
+        case 16: return launch_staged<DT, 16>(table, vocab, hidden, row_bytes, ids, n_ids, out, bad_id_flag, s);
+        case 8: return launch_staged<DT, 8>(table, vocab, hidden, row_bytes, ids, n_ids, out, bad_id_flag, s);
+        case 4: return launch_staged<DT, 4>(table, vocab, hidden, row_bytes, ids, n_ids, out, bad_id_flag, s);
+        default: return launch_embed<DT>(table, vocab, hidden, row_bytes, ids, n_ids, out, bad_id_flag, s);
+        }
+    };
     switch (table_dtype) {
-    case SPH_F32: return launch_embed<SPH_F32>(table, vocab, hidden, row_bytes, ids, n_ids, out, bad_id_flag, s);
-    case SPH_F16: return launch_embed<SPH_F16>(table, vocab, hidden, row_bytes, ids, n_ids, out, bad_id_flag, s);
-    case SPH_BF16: return launch_embed<SPH_BF16>(table, vocab, hidden, row_bytes, ids, n_ids, out, bad_id_flag, s);
-    case SPH_Q4_0: return launch_embed<SPH_Q4_0>(table, vocab, hidden, row_bytes, ids, n_ids, out, bad_id_flag, s);
-    case SPH_Q8_0:
-        // Staged through LDS with the widest aligned loads the row layout allows.
-        if (row_bytes % 16 == 0 && aligned(table, 16))
-            return launch_q8_0_staged<16>(table, vocab, hidden, row_bytes, ids, n_ids, out, bad_id_flag, s);
-        if (row_bytes % 8 == 0 && aligned(table, 8))
-            return launch_q8_0_staged<8>(table, vocab, hidden, row_bytes, ids, n_ids, out, bad_id_flag, s);
-        if (row_bytes % 4 == 0 && aligned(table, 4))
-            return launch_q8_0_staged<4>(table, vocab, hidden, row_bytes, ids, n_ids, out, bad_id_flag, s);
-        return launch_embed<SPH_Q8_0>(table, vocab, hidden, row_bytes, ids, n_ids, out, bad_id_flag, s);
-    case SPH_Q4_K: return launch_q4_k_staged(table, vocab, hidden, row_bytes, ids, n_ids, out, bad_id_flag, s);
-    case SPH_Q5_K: return launch_embed<SPH_Q5_K>(table, vocab, hidden, row_bytes, ids, n_ids, out, bad_id_flag, s);
-    case SPH_Q6_K: return launch_embed<SPH_Q6_K>(table, vocab, hidden, row_bytes, ids, n_ids, out, bad_id_flag, s);
+    case SPH_F32: return go(std::integral_constant<int, SPH_F32>{});
+    case SPH_F16: return go(std::integral_constant<int, SPH_F16>{});
+    case SPH_BF16: return go(std::integral_constant<int, SPH_BF16>{});
+    case SPH_Q4_0: return go(std::integral_constant<int, SPH_Q4_0>{});
+    case SPH_Q8_0: return go(std::integral_constant<int, SPH_Q8_0>{});
+    case SPH_Q5_K: return go(std::integral_constant<int, SPH_Q5_K>{});
+    case SPH_Q6_K: return go(std::integral_constant<int, SPH_Q6_K>{});
     }
     return SPH_EINVAL;
 }

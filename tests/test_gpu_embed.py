@@ -297,3 +297,40 @@ def test_embed_q8_0_every_staging_width(dev, orc, hidden, offset):
     assert flag.item() == 1
     assert (out[~ok] == 0).all()
     assert_bits_equal(out[ok], orc.embed_tokens(blocks, Q8_0, vocab, hidden, ids[ok]), f"q8_0 {hidden} +{offset}")
+
+
+_FORMATS = {  # dtype: (elements per block, bytes per block, f16 scale byte offsets, table alignment the ABI needs)
+    "q4_0": (Q4_0, 32, 18, (0,), 2), "q5_k": (Q5_K, 256, 176, (0, 2), 16), "q6_k": (Q6_K, 256, 210, (208,), 2),
+    "f16": (F16, 4, 8, (), 8), "bf16": (BF16, 4, 8, (), 8), "f32": (F32, 4, 16, (), 16),
+}
+_WIDTHS = {"q4_0": (32, 64, 128, 4096, 8448), "q5_k": (256, 4096, 8448), "q6_k": (256, 512, 1024, 2048, 8192),
+           "f16": (4, 8, 3000), "bf16": (2600,), "f32": (4, 4100)}
+
+
+@pytest.mark.parametrize("fmt,hidden,offset", [(f, h, o) for f, hs in _WIDTHS.items() for h in hs
+                                               for o in (0, 2, 4, 8) if o % _FORMATS[f][4] == 0])
+def test_embed_every_format_every_staging_width(dev, orc, fmt, hidden, offset):
+    """Every table type but Q4_K is staged through LDS with 16-, 8- or 4-byte loads, whichever divides both
+    the row length and the table address, and read in place otherwise; rows longer than one staging chunk
+    (4608 bytes) take several. Widths chosen per format to reach each load width, a single block, one
+    chunk and several chunks; the table shifted by each offset its alignment allows; one out-of-range id
+    (zero row, flag raised). Bar: bit-exact with the oracle."""
+    dt, blk, nbytes, scale_offs, _ = _FORMATS[fmt]
+    vocab = 48
+    rng = np.random.default_rng(hidden * 16 + offset)
+    nb = vocab * hidden // blk
+    blocks = rng.integers(0, 256, (nb, nbytes), dtype=np.uint8)
+    for so in scale_offs:
+        blocks[:, so:so + 2] = np.frombuffer(rng.uniform(-0.05, 0.05, nb).astype(np.float16).tobytes(),
+                                             np.uint8).reshape(nb, 2)
+    raw = torch.zeros(nb * nbytes + 16, dtype=torch.uint8, device=dev)
+    table = raw[offset:offset + nb * nbytes]
+    table.copy_(torch.from_numpy(blocks.reshape(-1)).to(dev))
+    ids = np.array(list(rng.permutation(vocab)[:30]) + [vocab + 7, 0, vocab - 1, 3, 3], np.uint32)
+    flag = torch.zeros(1, dtype=torch.int32, device=dev)
+    print(f"case embed {fmt} staging hidden {hidden} offset {offset}", flush=True)
+    out = to_np(ops.embed(table, dt, vocab, hidden, _ids(ids, dev), bad_id_flag=flag))
+    ok = ids < vocab
+    assert flag.item() == 1
+    assert (out[~ok] == 0).all()
+    assert_bits_equal(out[ok], orc.embed_tokens(blocks, dt, vocab, hidden, ids[ok]), f"{fmt} {hidden} +{offset}")
