@@ -37,9 +37,12 @@ extern "C" {
 #define SPH_EHIP (-2)    /* the HIP runtime reported an error while enqueueing */
 #define SPH_ERANGE (-3)  /* a token id is outside [0, vocab), or cache positions past max_seq */
 #define SPH_ENODEV (-4)  /* no usable gfx950 device is current */
+#define SPH_ESTATE (-5)  /* one-time set-up cannot run now: the stream is being captured (call sph_init first) */
 
-/* Element / table types. The values are GGUF tensor type ids
- * (crates/sapient-io/src/gguf.rs:90-104), so a caller can pass them through. */
+/* Element / table types, numbered as GGUF tensor type ids
+ * (crates/sapient-io/src/gguf.rs:90-104). That enum is private to the
+ * reference's loader, so a caller maps its own dtype enum
+ * (sapient_core::DType, crates/sapient-core/src/dtype.rs:16) to these codes. */
 #define SPH_F32 0
 #define SPH_F16 1
 #define SPH_Q4_0 2
@@ -58,8 +61,10 @@ int sph_abi_version(void);
 const char* sph_status_string(int status);
 
 /* One-time per-device set-up (the GELU lookup tables). Optional: the first
- * sph_gelu_tanh call on a device does it lazily; call it first when later
- * calls will be captured into a HIP graph. Synchronizes `stream` once. */
+ * half-precision sph_gelu_tanh / sph_gelu_erf call on a device does it lazily;
+ * call it first when later calls will be captured into a HIP graph (a lazy
+ * set-up under capture returns SPH_ESTATE and enqueues nothing). Synchronizes
+ * `stream` once. */
 int sph_init(void* stream);
 
 /* RMSNorm over the last dimension, `rows` rows of `dim` elements:

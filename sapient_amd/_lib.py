@@ -12,7 +12,7 @@ from pathlib import Path
 LIB_PATH = Path(__file__).resolve().with_name("libsapient_hip.so")
 
 # status codes
-OK, EINVAL, EHIP, ERANGE, ENODEV = 0, -1, -2, -3, -4
+OK, EINVAL, EHIP, ERANGE, ENODEV, ESTATE = 0, -1, -2, -3, -4, -5
 # dtype codes: GGUF tensor type ids
 F32, F16, Q4_0, Q8_0, Q4_K, Q5_K, Q6_K, BF16 = 0, 1, 2, 8, 12, 13, 14, 30
 ROPE_NEOX, ROPE_INTERLEAVED = 0, 1

@@ -13,6 +13,7 @@ extern "C" const char* sph_status_string(int status) {
     case SPH_EHIP: return "HIP runtime error while enqueueing work";
     case SPH_ERANGE: return "index out of range (token id >= vocab, or cache positions past max_seq)";
     case SPH_ENODEV: return "no usable gfx950 device";
+    case SPH_ESTATE: return "one-time device set-up cannot run while the stream is being captured (call sph_init first)";
     default: return "unknown status";
     }
 }

@@ -227,14 +227,16 @@ int launch_ew(const void* a, const void* b, void* out, int64_t n, hipStream_t st
     if (vec_ok) {
         const int64_t nvec = n / E;
         if (nvec > 0) {
-            ew_vec<T, OP, BC><<<grid_for(nvec, (int64_t)kThreads * kUnroll, kMaxGrid), kThreads, 0, stream>>>(ap, bp, op, nvec);
-            if (launch_status() != SPH_OK) return SPH_EHIP;
+            const int st = launch(ew_vec<T, OP, BC>, grid_for(nvec, (int64_t)kThreads * kUnroll, kMaxGrid), kThreads,
+                                  stream, ap, bp, op, nvec);
+            if (st != SPH_OK) return st;
         }
         done = nvec * E;
     }
     if (done < n) {
-        ew_scalar<T, OP, BC><<<grid_for(n - done, kThreads, 4096), kThreads, 0, stream>>>(ap, bp, op, done, n);
-        if (launch_status() != SPH_OK) return SPH_EHIP;
+        const int st = launch(ew_scalar<T, OP, BC>, grid_for(n - done, kThreads, 4096), kThreads, stream, ap, bp, op,
+                              done, n);
+        if (st != SPH_OK) return st;
     }
     return SPH_OK;
 }
@@ -401,15 +403,20 @@ int ensure_device_ready(hipStream_t stream, int* cus) {
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return SPH_ENODEV;
     std::lock_guard<std::mutex> lock(g_init_mu);
     if (!g_lut_ready[dev]) {
+        // The build waits for its kernels: under stream capture they would be
+        // recorded instead of run and the wait would invalidate the capture.
+        hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+        if (hipStreamIsCapturing(stream, &cap) != hipSuccess) return SPH_EHIP;
+        if (cap != hipStreamCaptureStatusNone) return SPH_ESTATE;
         int n = 0;
         if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
             return SPH_ENODEV;
         g_num_cus[dev] = n;
+        const dim3 grid((kLutEntries + kThreads - 1) / kThreads);
         for (int form = 0; form < 2; ++form) {
-            gelu_lut_build<f16><<<(kLutEntries + kThreads - 1) / kThreads, kThreads, 0, stream>>>(form * 2);
-            gelu_lut_build<bf16><<<(kLutEntries + kThreads - 1) / kThreads, kThreads, 0, stream>>>(form * 2 + 1);
+            if (launch(gelu_lut_build<f16>, grid, kThreads, stream, form * 2) != SPH_OK) return SPH_EHIP;
+            if (launch(gelu_lut_build<bf16>, grid, kThreads, stream, form * 2 + 1) != SPH_OK) return SPH_EHIP;
         }
-        if (launch_status() != SPH_OK) return SPH_EHIP;
         if (hipStreamSynchronize(stream) != hipSuccess) return SPH_EHIP;
         g_lut_ready[dev] = true;
     }
@@ -426,14 +433,16 @@ int gelu_half(const uint16_t* x, uint16_t* out, int which, int64_t n, hipStream_
     if (aligned(x, 16) && aligned(out, 16)) {
         const int64_t nvec = n / 8;
         if (nvec > 0) {
-            gelu_lut_apply<T, kLutBatch><<<grid_for(nvec, (int64_t)kLutThreads * kLutBatch, 2 * cus), kLutThreads, 0, stream>>>(x, out, nvec, which);
-            if (launch_status() != SPH_OK) return SPH_EHIP;
+            st = launch(gelu_lut_apply<T, kLutBatch>, grid_for(nvec, (int64_t)kLutThreads * kLutBatch, 2 * cus),
+                        kLutThreads, stream, x, out, nvec, which);
+            if (st != SPH_OK) return st;
         }
         done = nvec * 8;
     }
     if (done < n) {
-        gelu_lut_apply_scalar<T><<<grid_for(n - done, kThreads, 4096), kThreads, 0, stream>>>(x, out, done, n, which);
-        if (launch_status() != SPH_OK) return SPH_EHIP;
+        st = launch(gelu_lut_apply_scalar<T>, grid_for(n - done, kThreads, 4096), kThreads, stream, x, out, done, n,
+                    which);
+        if (st != SPH_OK) return st;
     }
     return SPH_OK;
 }
@@ -512,13 +521,11 @@ int launch_bias(const void* y, const void* bias, void* out, int64_t total, int64
         const int64_t groups = (rows + kBiasRowsPerBlock - 1) / kBiasRowsPerBlock;
         // The grid is one launch: ntiles · groups < 2^32 blocks is checked here.
         if ((int64_t)ntiles * groups < ((int64_t)1 << 31)) {
-            bias_rows_vec<T, TB><<<dim3((unsigned)(ntiles * groups)), tile, 0, stream>>>(yp, bp, op, rows, (int)nvr,
-                                                                                          ntiles, tile);
-            return launch_status();
+            return launch(bias_rows_vec<T, TB>, dim3((unsigned)(ntiles * groups)), tile, stream, yp, bp, op, rows,
+                          (int)nvr, ntiles, tile);
         }
     }
-    bias_scalar<T, TB><<<grid_for(total, kThreads, 65536), kThreads, 0, stream>>>(yp, bp, op, total, n);
-    return launch_status();
+    return launch(bias_scalar<T, TB>, grid_for(total, kThreads, 65536), kThreads, stream, yp, bp, op, total, n);
 }
 
 int dispatch_bias(const void* y, const void* bias, int b_dt, void* out, int dt, int64_t total, int64_t n,

@@ -124,11 +124,10 @@ int launch_move(const void* src, void* dst, uint64_t rows, uint64_t hd, RowMap m
         const uint64_t nr = rows - r0 < rows_per_launch ? rows - r0 : rows_per_launch;
         const uint32_t items = (uint32_t)(nr * per_row);
         const dim3 grid((items + kThreads - 1) / kThreads);
-        if (vec)
-            move_rows_vec<TS, TD, MAP><<<grid, kThreads, 0, stream>>>(s, d, items, (uint32_t)per_row, (uint32_t)r0, m);
-        else
-            move_rows_scalar<TS, TD, MAP><<<grid, kThreads, 0, stream>>>(s, d, items, (uint32_t)hd, (uint32_t)r0, m);
-        const int st = launch_status();
+        const int st = vec ? launch(move_rows_vec<TS, TD, MAP>, grid, kThreads, stream, s, d, items, (uint32_t)per_row,
+                                    (uint32_t)r0, m)
+                           : launch(move_rows_scalar<TS, TD, MAP>, grid, kThreads, stream, s, d, items, (uint32_t)hd,
+                                    (uint32_t)r0, m);
         if (st != SPH_OK) return st;
     }
     return SPH_OK;
@@ -214,11 +213,9 @@ extern "C" int sph_kv_append(const void* src, int src_dtype, void* cache, int ca
             const uint64_t nblk = (blocks + sph::kThreads - 1) / sph::kThreads;
             if (nblk > INT32_MAX) return SPH_EINVAL;
             const dim3 grid((unsigned)nblk);
-            sph::kv_append_q8_0<TS><<<grid, sph::kThreads, 0, s>>>(static_cast<const TS*>(src),
-                                                                    static_cast<uint8_t*>(cache), blocks,
-                                                                    (uint32_t)bpr, (uint32_t)seq, (uint32_t)max_seq,
-                                                                    (uint64_t)pos);
-            return sph::launch_status();
+            return sph::launch(sph::kv_append_q8_0<TS>, grid, sph::kThreads, s, static_cast<const TS*>(src),
+                               static_cast<uint8_t*>(cache), blocks, (uint32_t)bpr, (uint32_t)seq, (uint32_t)max_seq,
+                               (uint64_t)pos);
         });
     }
     const sph::RowMap m{(uint32_t)seq, (uint32_t)max_seq, (uint64_t)pos};

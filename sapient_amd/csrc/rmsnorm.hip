@@ -279,29 +279,32 @@ __global__ __launch_bounds__(256) void rms_rows_generic(const TX* __restrict__ x
 }
 
 template <typename TX, typename TW, typename TO, int KIND, int VPT, bool LOOP>
-void launch_vec(int W, dim3 grid, int threads, const TX* xp, TX* rp, const TW* wp, const TW* bp, TO* op, int64_t nr, int d,
-                float eps, hipStream_t stream) {
+int launch_vec(int W, dim3 grid, int threads, const TX* xp, TX* rp, const TW* wp, const TW* bp, TO* op, int64_t nr, int d,
+               float eps, hipStream_t stream) {
     switch (W) {
-    case 1: rms_rows_vec<TX, TW, TO, KIND, 1, VPT, LOOP><<<grid, threads, 0, stream>>>(xp, rp, wp, bp, op, nr, d, eps); break;
-    case 2: rms_rows_vec<TX, TW, TO, KIND, 2, VPT, LOOP><<<grid, threads, 0, stream>>>(xp, rp, wp, bp, op, nr, d, eps); break;
-    case 4: rms_rows_vec<TX, TW, TO, KIND, 4, VPT, LOOP><<<grid, threads, 0, stream>>>(xp, rp, wp, bp, op, nr, d, eps); break;
-    case 8: rms_rows_vec<TX, TW, TO, KIND, 8, VPT, LOOP><<<grid, threads, 0, stream>>>(xp, rp, wp, bp, op, nr, d, eps); break;
-    default: rms_rows_vec<TX, TW, TO, KIND, 16, VPT, LOOP><<<grid, threads, 0, stream>>>(xp, rp, wp, bp, op, nr, d, eps); break;
+    case 1: return launch(rms_rows_vec<TX, TW, TO, KIND, 1, VPT, LOOP>, grid, threads, stream, xp, rp, wp, bp, op, nr, d, eps);
+    case 2: return launch(rms_rows_vec<TX, TW, TO, KIND, 2, VPT, LOOP>, grid, threads, stream, xp, rp, wp, bp, op, nr, d, eps);
+    case 4: return launch(rms_rows_vec<TX, TW, TO, KIND, 4, VPT, LOOP>, grid, threads, stream, xp, rp, wp, bp, op, nr, d, eps);
+    case 8: return launch(rms_rows_vec<TX, TW, TO, KIND, 8, VPT, LOOP>, grid, threads, stream, xp, rp, wp, bp, op, nr, d, eps);
+    default: return launch(rms_rows_vec<TX, TW, TO, KIND, 16, VPT, LOOP>, grid, threads, stream, xp, rp, wp, bp, op, nr, d, eps);
     }
 }
 
+// launch_shape's result when the shape does not cover the row (nothing launched).
+constexpr int kNoShape = 1;
+
 // One launch of the vector kernel with VPT 16-byte vectors per lane: W waves
 // per row (the fewest that cover it), LOOP blocks capped at `waves_per_cu`
-// resident waves per CU (at least one block). Returns false, launching
-// nothing, when a row is wider than 16 waves cover.
+// resident waves per CU (at least one block). Returns the launch's status, or
+// kNoShape, launching nothing, when a row is wider than 16 waves cover.
 template <typename TX, typename TW, typename TO, int KIND, int VPT, bool LOOP>
-bool launch_shape(const TX* xp, TX* rp, const TW* wp, const TW* bp, TO* op, int64_t nr, int dim, float eps,
+int launch_shape(const TX* xp, TX* rp, const TW* wp, const TW* bp, TO* op, int64_t nr, int dim, float eps,
                   int waves_per_cu, hipStream_t stream) {
     constexpr int E = vec16<TX>::n;
     const int64_t nvec = dim / E;
     int W = 1;
     while (W < 16 && nvec > (int64_t)kWave * VPT * W) W *= 2;
-    if (nvec > (int64_t)kWave * VPT * W) return false;
+    if (nvec > (int64_t)kWave * VPT * W) return kNoShape;
     const int rpb = W >= 4 ? 1 : 4 / W;
     const int threads = W >= 4 ? kWave * W : 256;
     int64_t nb = (nr + rpb - 1) / rpb;
@@ -313,8 +316,8 @@ bool launch_shape(const TX* xp, TX* rp, const TW* wp, const TW* bp, TO* op, int6
             if (nb > cap) nb = cap;
         }
     }
-    launch_vec<TX, TW, TO, KIND, VPT, LOOP>(W, dim3((unsigned)nb), threads, xp, rp, wp, bp, op, nr, dim, eps, stream);
-    return true;
+    return launch_vec<TX, TW, TO, KIND, VPT, LOOP>(W, dim3((unsigned)nb), threads, xp, rp, wp, bp, op, nr, dim, eps,
+                                                   stream);
 }
 
 // Launch shapes, measured at 16384 x 4096 on MI355X (round-robin medians on
@@ -363,21 +366,20 @@ int launch_rms(const void* x, void* residual, const void* w, const void* bias, v
         const TW* wp = static_cast<const TW*>(w);
         const TW* bp = static_cast<const TW*>(bias);
         TO* op = static_cast<TO*>(out) + off;
+        int st = kNoShape;
         if (vec_ok) {
-            bool done = false;
             if constexpr (VPT_L > 0)
-                done = launch_shape<TX, TW, TO, KIND, VPT_L, true>(xp, rp, wp, bp, op, nr, (int)dim, eps, kLoopWaves,
-                                                                   stream);
-            if (!done)
-                done = launch_shape<TX, TW, TO, KIND, VPT, kLoop>(xp, rp, wp, bp, op, nr, (int)dim, eps, 16, stream);
-            if (!done)  // wider than 16 waves at VPT: twice the values per lane, one block per row
-                done = launch_shape<TX, TW, TO, KIND, 2 * VPT, false>(xp, rp, wp, bp, op, nr, (int)dim, eps, 16,
-                                                                      stream);
-            if (!done) return SPH_EINVAL;  // unreachable: vec_ok bounds the width
+                st = launch_shape<TX, TW, TO, KIND, VPT_L, true>(xp, rp, wp, bp, op, nr, (int)dim, eps, kLoopWaves,
+                                                                 stream);
+            if (st == kNoShape)
+                st = launch_shape<TX, TW, TO, KIND, VPT, kLoop>(xp, rp, wp, bp, op, nr, (int)dim, eps, 16, stream);
+            if (st == kNoShape)  // wider than 16 waves at VPT: twice the values per lane, one block per row
+                st = launch_shape<TX, TW, TO, KIND, 2 * VPT, false>(xp, rp, wp, bp, op, nr, (int)dim, eps, 16, stream);
+            if (st == kNoShape) return SPH_EINVAL;  // unreachable: vec_ok bounds the width
         } else {
-            rms_rows_generic<TX, TW, TO, KIND><<<dim3((unsigned)nr), 256, 0, stream>>>(xp, rp, wp, bp, op, nr, dim, eps);
+            st = launch(rms_rows_generic<TX, TW, TO, KIND>, dim3((unsigned)nr), 256, stream, xp, rp, wp, bp, op, nr,
+                        dim, eps);
         }
-        const int st = launch_status();
         if (st != SPH_OK) return st;
     }
     return SPH_OK;

@@ -59,11 +59,12 @@ __device__ __forceinline__ const uint32_t* stage_inv_pio4(uint32_t (&tab)[24]) {
 }
 
 // L consecutive elements of one row held as they sit in memory (32-bit words,
-// or single elements when the run is narrower than a word), so that a batch of
-// rows can be in flight while the previous batch is rotated and stored.
-template <typename T, int L>
+// or single elements when the run is narrower than a word or ELEM asks for
+// element accesses: rows only element-aligned), so that a batch of rows can be
+// in flight while the previous batch is rotated and stored.
+template <typename T, int L, bool ELEM = false>
 struct RawRun {
-    static constexpr bool kWords = (L * (int)sizeof(T)) % 4 == 0;
+    static constexpr bool kWords = !ELEM && (L * (int)sizeof(T)) % 4 == 0;
     uint32_t w[kWords ? words_of<T, L>::n : 1];
     T e[kWords ? 1 : L];
 
@@ -85,9 +86,9 @@ struct RawRun {
     }
 };
 
-template <typename T, int L>
+template <typename T, int L, bool ELEM = false>
 __device__ __forceinline__ void store_run(T* p, const float (&v)[L]) {
-    if constexpr ((L * (int)sizeof(T)) % 4 == 0) {
+    if constexpr (!ELEM && (L * (int)sizeof(T)) % 4 == 0) {
         store_f32<T, L, true>(p, v);
     } else {
 #pragma unroll
@@ -119,7 +120,8 @@ __device__ __forceinline__ void store_run(T* p, const float (&v)[L]) {
 // with no angles at all, 28.6 us pair-major with two batches in flight. f32,
 // whose angles are shared by all 40 heads of a thread, is ~0.5 us faster
 // per-thread (the two block barriers cost about what the reductions save).
-template <typename T, int P, bool INTERLEAVED, bool SPLIT, int U, bool PAIR_MAJOR>
+// ELEM: element-wise loads and stores (rows that are only element-aligned).
+template <typename T, int P, bool INTERLEAVED, bool SPLIT, int U, bool PAIR_MAJOR, bool ELEM>
 __global__ __launch_bounds__(kThreads) void rope_kernel(T* q, int nq, T* k, int nk, const int32_t* __restrict__ pos,
                                                              int64_t ntok, int64_t seq, int head_dim, int half,
                                                              int lanes_per_tok, int toks_per_block,
@@ -155,7 +157,7 @@ __global__ __launch_bounds__(kThreads) void rope_kernel(T* q, int nq, T* k, int 
         return hh < nq ? q + ((size_t)(b * nq + hh) * (size_t)seq + (size_t)s) * (size_t)head_dim
                        : k + ((size_t)(b * nk + (hh - nq)) * (size_t)seq + (size_t)s) * (size_t)head_dim;
     };
-    auto load_batch = [&](int h0, RawRun<T, L> (&buf)[U][R]) {
+    auto load_batch = [&](int h0, RawRun<T, L, ELEM> (&buf)[U][R]) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             if (h0 + u < h_end) {
@@ -165,7 +167,8 @@ __global__ __launch_bounds__(kThreads) void rope_kernel(T* q, int nq, T* k, int 
             }
         }
     };
-    auto rotate_batch = [&](int h0, const RawRun<T, L> (&buf)[U][R], const float (&cs)[NA], const float (&sn)[NA]) {
+    auto rotate_batch = [&](int h0, const RawRun<T, L, ELEM> (&buf)[U][R], const float (&cs)[NA],
+                            const float (&sn)[NA]) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             if (h0 + u < h_end) {
@@ -179,8 +182,8 @@ __global__ __launch_bounds__(kThreads) void rope_kernel(T* q, int nq, T* k, int 
                         o0[j] = x0[j] * cs[j] - x1[j] * sn[j];
                         o1[j] = x1[j] * cs[j] + x0[j] * sn[j];
                     }
-                    store_run<T, P>(row + off[0], o0);
-                    store_run<T, P>(row + off[1], o1);
+                    store_run<T, P, ELEM>(row + off[0], o0);
+                    store_run<T, P, ELEM>(row + off[1], o1);
                 } else {
 #pragma unroll
                     for (int r = 0; r < R; ++r) {
@@ -191,7 +194,7 @@ __global__ __launch_bounds__(kThreads) void rope_kernel(T* q, int nq, T* k, int 
                             o[2 * j] = x[2 * j] * cs[r * P + j] - x[2 * j + 1] * sn[r * P + j];
                             o[2 * j + 1] = x[2 * j + 1] * cs[r * P + j] + x[2 * j] * sn[r * P + j];
                         }
-                        store_run<T, 2 * P>(row + off[r], o);
+                        store_run<T, 2 * P, ELEM>(row + off[r], o);
                     }
                 }
             }
@@ -201,7 +204,7 @@ __global__ __launch_bounds__(kThreads) void rope_kernel(T* q, int nq, T* k, int 
     // The position load goes first: loads complete in order, so staging it
     // waits for it alone while the first two batches stay in flight.
     float cs[NA], sn[NA];
-    RawRun<T, L> ba[U][R], bb[U][R];
+    RawRun<T, L, ELEM> ba[U][R], bb[U][R];
     if constexpr (PAIR_MAJOR) {
         int32_t pv = 0;
         if (tid < toks_per_block && t_first + tid < ntok) pv = pos[(t_first + tid) % seq];
@@ -439,7 +442,7 @@ struct RopeShape {
 
 // target: blocks to aim for in all (token blocks × head groups).
 template <typename T, int P, bool IL, bool SPLIT = RopeShape<T, IL>::kSplit, int U = RopeShape<T, IL>::U,
-          bool PM = RopeShape<T, IL>::kPairMajor>
+          bool PM = RopeShape<T, IL>::kPairMajor, bool ELEM = false>
 int launch_rope_p(T* q, int nq, T* k, int nk, const int32_t* pos, int64_t ntok, int64_t seq, int head_dim,
                   int half, float pos_scale, const DenTable& den, hipStream_t stream,
                   int target = RopeShape<T, IL>::kTarget) {
@@ -454,9 +457,8 @@ int launch_rope_p(T* q, int nq, T* k, int nk, const int32_t* pos, int64_t ntok, 
     groups = (heads + heads_per_group - 1) / heads_per_group;
     if (blocks_x > INT32_MAX) return SPH_EINVAL;
     const dim3 grid((unsigned)blocks_x, (unsigned)groups);
-    rope_kernel<T, P, IL, SPLIT, U, PM><<<grid, kThreads, 0, stream>>>(
-        q, nq, k, nk, pos, ntok, seq, head_dim, half, lanes_per_tok, toks_per_block, heads_per_group, pos_scale, den);
-    return launch_status();
+    return launch(rope_kernel<T, P, IL, SPLIT, U, PM, ELEM>, grid, kThreads, stream, q, nq, k, nk, pos, ntok, seq, head_dim,
+                  half, lanes_per_tok, toks_per_block, heads_per_group, pos_scale, den);
 }
 
 // Denominators powf(base, 2i / rotary_dim) from the host libm, the call the reference makes.
@@ -484,10 +486,9 @@ int launch_rope_kv_p(const T* q, T* qo, int nq, const T* k, const T* v, int nkv,
     groups = (heads + heads_per_group - 1) / heads_per_group;
     if (blocks_x > INT32_MAX) return SPH_EINVAL;
     const dim3 grid((unsigned)blocks_x, (unsigned)groups);
-    rope_kv_kernel<T, TC, TB, P, IL, TM><<<grid, kThreads, 0, stream>>>(q, qo, nq, k, v, nkv, pos, seq, head_dim, half,
-                                                                        lanes_per_tok, toks_per_block, heads_per_group,
-                                                                        pos_scale, kc, vc, max_seq, flag, bq, bk, bv, den);
-    return launch_status();
+    return launch(rope_kv_kernel<T, TC, TB, P, IL, TM>, grid, kThreads, stream, q, qo, nq, k, v, nkv, pos, seq,
+                  head_dim, half, lanes_per_tok, toks_per_block, heads_per_group, pos_scale, kc, vc, max_seq, flag, bq,
+                  bk, bv, den);
 }
 
 // P: pairs per thread, the widest whose accesses of q/k/v (type T) and of the
@@ -576,7 +577,9 @@ int launch_rope(void* qv, int nq, void* kv, int nk, int layout, const int32_t* p
     if constexpr (V / 4 >= 1) {
         if (ok(V / 4, V / 2)) return launch_rope_p<T, V / 4, true, false>(q, nq, k, nk, pos, ntok, seq, head_dim, half, pos_scale, den, stream);
     }
-    return launch_rope_p<T, 1, true, false>(q, nq, k, nk, pos, ntok, seq, head_dim, half, pos_scale, den, stream);
+    // Rows only element-aligned: element accesses (a 2-element run would not be word-aligned).
+    return launch_rope_p<T, 1, true, false, RopeShape<T, true>::U, RopeShape<T, true>::kPairMajor, true>(
+        q, nq, k, nk, pos, ntok, seq, head_dim, half, pos_scale, den, stream);
 }
 
 }  // namespace

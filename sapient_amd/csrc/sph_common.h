@@ -6,6 +6,9 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <tuple>
+#include <utility>
+
 #include "sapient_hip.h"
 
 namespace sph {
@@ -188,9 +191,23 @@ inline bool aligned(const void* p, size_t a) { return ((uintptr_t)p & (a - 1)) =
 inline bool is_float_dtype(int dt) { return dt == SPH_F32 || dt == SPH_F16 || dt == SPH_BF16; }
 inline size_t dtype_size(int dt) { return dt == SPH_F32 ? 4 : 2; }
 
-inline int launch_status() {
-    hipError_t e = hipGetLastError();
-    return e == hipSuccess ? SPH_OK : SPH_EHIP;
+// Enqueue one launch of `kernel` and return that launch's own status.
+// hipLaunchKernel reports the launch's error directly; reading hipGetLastError
+// after a triple-chevron launch would also return (and clear) an error that an
+// earlier, unrelated HIP call left on this thread. Arguments are converted to
+// the kernel's parameter types, as a call would convert them.
+template <typename... KArgs, typename... Args>
+inline int launch(void (*kernel)(KArgs...), dim3 grid, dim3 block, hipStream_t stream, Args&&... args) {
+    static_assert(sizeof...(KArgs) == sizeof...(Args), "kernel argument count");
+    std::tuple<KArgs...> vals(static_cast<KArgs>(std::forward<Args>(args))...);
+    void* ptrs[sizeof...(KArgs)];
+    std::apply([&ptrs](auto&... v) {
+        int i = 0;
+        ((ptrs[i++] = static_cast<void*>(&v)), ...);
+    }, vals);
+    return hipLaunchKernel(reinterpret_cast<const void*>(kernel), grid, block, ptrs, 0, stream) == hipSuccess
+               ? SPH_OK
+               : SPH_EHIP;
 }
 
 // Dispatch a functor templated on the storage type of a float dtype code.

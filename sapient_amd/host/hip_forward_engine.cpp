@@ -85,7 +85,7 @@ bool dalloc(sph_engine* e, T** p, size_t bytes) {
 // through, anything else reads as a HIP failure.
 int callback_status(int st) {
     if (st == 0) return SPH_OK;
-    return (st == SPH_EINVAL || st == SPH_EHIP || st == SPH_ERANGE || st == SPH_ENODEV) ? st : SPH_EHIP;
+    return (st == SPH_EINVAL || st == SPH_EHIP || st == SPH_ERANGE || st == SPH_ENODEV || st == SPH_ESTATE) ? st : SPH_EHIP;
 }
 
 int proj(sph_engine* e, int layer, int which, const float* in, float* out, int64_t rows) {
