@@ -37,11 +37,12 @@ constexpr int kWave = 64;
 
 enum Kind { K_RMS = 0, K_ADD_RMS = 1, K_LAYER = 2 };
 
-// y for one element: RMSNorm (r·inv)·w; LayerNorm ((r−mean)·inv)·w + b.
+// y for one element: RMSNorm (r·inv)·w; LayerNorm (d·inv)·w + b, where the
+// caller passes the centred value d = r − mean for LayerNorm.
 template <int KIND>
-__device__ __forceinline__ float norm_out(float r, float mean, float inv, float w, float b, bool has_w, bool has_b) {
+__device__ __forceinline__ float norm_out(float r, float inv, float w, float b, bool has_w, bool has_b) {
     if constexpr (KIND == K_LAYER) {
-        const float normed = (r - mean) * inv;
+        const float normed = r * inv;
         if (has_w && has_b) return normed * w + b;
         if (has_w) return normed * w;
         if (has_b) return normed + b;
@@ -162,9 +163,11 @@ __global__ __launch_bounds__(W >= 4 ? 64 * W : 256) void rms_rows_vec(const TX* 
             }
         }
         ss = row_sum<W, WPB>(ss, partial[par], 0, lane, wv);
-        float mean = 0.0f, inv;
+        float inv;
         if constexpr (KIND == K_LAYER) {
-            mean = ss / (float)dim;
+            // The row is centred once, in registers: the variance and the
+            // output both use d = r − mean (the same f32 difference each time).
+            const float mean = ss / (float)dim;
             float vs = 0.0f;
             if (live) {
 #pragma unroll
@@ -172,7 +175,10 @@ __global__ __launch_bounds__(W >= 4 ? 64 * W : 256) void rms_rows_vec(const TX* 
                     const int v = (sub * VPT + j) * kWave + lane;
                     if (v < nvec) {
 #pragma unroll
-                        for (int e = 0; e < E; ++e) vs = vs + (r[j][e] - mean) * (r[j][e] - mean);
+                        for (int e = 0; e < E; ++e) {
+                            r[j][e] = r[j][e] - mean;
+                            vs = vs + r[j][e] * r[j][e];
+                        }
                     }
                 }
             }
@@ -198,7 +204,7 @@ __global__ __launch_bounds__(W >= 4 ? 64 * W : 256) void rms_rows_vec(const TX* 
                 }
                 float y[E];
 #pragma unroll
-                for (int e = 0; e < E; ++e) y[e] = norm_out<KIND>(r[j][e], mean, inv, wj[e], bj[e], has_w, has_b);
+                for (int e = 0; e < E; ++e) y[e] = norm_out<KIND>(r[j][e], inv, wj[e], bj[e], has_w, has_b);
                 store_f32<TO, E, true>(out + base + (size_t)v * E, y);
             }
         }
@@ -274,7 +280,7 @@ __global__ __launch_bounds__(256) void rms_rows_generic(const TX* __restrict__ x
         if constexpr (KIND == K_ADD_RMS) residual[base + i] = narrow<TX>(r);
         const float wv_ = has_w ? widen(w[i]) : 1.0f;
         const float bv = (KIND == K_LAYER && has_b) ? widen(bias[i]) : 0.0f;
-        out[base + i] = narrow<TO>(norm_out<KIND>(r, mean, inv, wv_, bv, has_w, has_b));
+        out[base + i] = narrow<TO>(norm_out<KIND>(KIND == K_LAYER ? r - mean : r, inv, wv_, bv, has_w, has_b));
     }
 }
 

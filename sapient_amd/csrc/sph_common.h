@@ -49,6 +49,14 @@ __device__ __forceinline__ uint32_t narrow2_bf16(float v0, float v1) {
     typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
     return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){v0, v1}, bf16x2_t));
 }
+// Two values in one v_cvt_pk_f16_f32 (gfx950), v0 in the low half: the same
+// bits as two v_cvt_f16_f32 (round to nearest-even under the default MODE,
+// subnormals kept) for every f32 input, in one instruction instead of three.
+__device__ __forceinline__ uint32_t narrow2_f16(float v0, float v1) {
+    typedef float f32x2_t __attribute__((ext_vector_type(2)));
+    typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){v0, v1}, f16x2_t));
+}
 
 // Elements of T that fill one 16-byte access.
 template <typename T> struct vec16 { static constexpr int n = 16 / (int)sizeof(T); };
@@ -117,8 +125,7 @@ __device__ __forceinline__ void f32_to_words(const float (&v)[N], uint32_t (&raw
         for (int i = 0; i < N; i += 2) raw[i / 2] = narrow2_bf16(v[i], v[i + 1]);
     } else {
 #pragma unroll
-        for (int i = 0; i < N; i += 2)
-            raw[i / 2] = (uint32_t)narrow<T>(v[i]).bits | ((uint32_t)narrow<T>(v[i + 1]).bits << 16);
+        for (int i = 0; i < N; i += 2) raw[i / 2] = narrow2_f16(v[i], v[i + 1]);
     }
 }
 
