@@ -239,6 +239,24 @@ int sph_transpose_heads(const void* x, void* out, int dtype, int64_t outer, int6
 int sph_kv_append(const void* src, int src_dtype, void* cache, int cache_dtype, int64_t n_kv, int64_t seq,
                   int64_t head_dim, int64_t max_seq, int64_t pos, void* stream);
 
+/* The trait path's KV-cache update, sliding window included. Replaces
+ * common::update_kv_cache (crates/sapient-models/src/forward/common.rs:355-434,
+ * called at llama.rs:489-490 and phi.rs:461-462) and its Q8_0 cache,
+ * update_kv_cache_q8 (:449-508). cache [n_kv, max_seq, head_dim] (the
+ * reference's [batch, heads, max_seq, head_dim] with batch · heads folded into
+ * n_kv) holds cur_len valid rows per head; src [n_kv, seq, head_dim] is
+ * appended after them. When cur_len + seq > max_seq the oldest
+ * shift = cur_len + seq - max_seq rows of every head are dropped first (rows
+ * [shift, cur_len) move to [0, cur_len - shift), common.rs:392-405) and src
+ * lands at cur_len - shift. *new_len (host int64) receives min(cur_len + seq,
+ * max_seq), the length of the view the reference returns. seq > max_seq
+ * returns SPH_ERANGE (the reference's "new tokens exceeds max cache size"),
+ * cur_len > max_seq SPH_EINVAL; nothing is written then. Types, conversion and
+ * the Q8_0 layout are sph_kv_append's. At most two launches on `stream` (the
+ * shift, then the append); the rows moved by the shift are copied bit for bit. */
+int sph_kv_cache_update(const void* src, int src_dtype, void* cache, int cache_dtype, int64_t n_kv, int64_t seq,
+                        int64_t head_dim, int64_t max_seq, int64_t cur_len, int64_t* new_len, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -66,6 +66,7 @@ def lib() -> C.CDLL:
             "sor_quantize_q8_0": (None, [vp, sz, vp]),
             "sor_transpose_heads": (None, [vp, vp, sz, sz, sz, sz]),
             "sor_kv_append": (C.c_int, [vp, vp, C.c_int, sz, sz, sz, sz, sz]),
+            "sor_kv_cache_update": (C.c_int, [vp, vp, C.c_int, sz, sz, sz, sz, sz, C.POINTER(sz)]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -306,3 +307,24 @@ def kv_append(src, cache: np.ndarray, cache_dtype: int, n_kv: int, seq: int, hea
     st = lib().sor_kv_append(_p(src), _p(cache), cache_dtype, n_kv, seq, head_dim, max_seq, pos)
     if st != 0:
         raise OracleError(st, "kv_append")
+
+
+def kv_cache_update(src, cache: np.ndarray, cache_dtype: int, n_kv: int, seq: int, head_dim: int, max_seq: int,
+                    cur_len: int) -> int:
+    """common.rs:355-434 (update_kv_cache) / :449-508 (update_kv_cache_q8), in place on
+    `cache` (layouts as kv_append): appends src after cur_len rows per head, first
+    sliding the window left by cur_len + seq - max_seq rows when that is positive.
+    Returns the new length, min(cur_len + seq, max_seq)."""
+    src = _f32(src)
+    row = head_dim // 32 * 34 if cache_dtype == Q8_0 else head_dim
+    if src.size != n_kv * seq * head_dim or cache.size != n_kv * max_seq * row or not cache.flags.c_contiguous:
+        raise ValueError("src / cache sizes do not match the layout")
+    want = {F32: np.float32, Q8_0: np.uint8}.get(cache_dtype, np.uint16)
+    if cache.dtype != want:
+        raise ValueError("cache dtype does not match cache_dtype")
+    n = C.c_size_t(0)
+    st = lib().sor_kv_cache_update(_p(src), _p(cache), cache_dtype, n_kv, seq, head_dim, max_seq, cur_len,
+                                   C.byref(n))
+    if st != 0:
+        raise OracleError(st, "kv_cache_update")
+    return n.value

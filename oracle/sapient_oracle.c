@@ -605,3 +605,48 @@ int sor_kv_append(const float* src, void* cache, int cache_dtype, size_t n_kv, s
             }
     return SOR_OK;
 }
+
+/* The trait path's cache update with its sliding window:
+ * crates/sapient-models/src/forward/common.rs:355-434 (update_kv_cache, f32
+ * cache) and :449-508 (update_kv_cache_q8). cache [n_kv, max_seq, hd] (the
+ * reference's [b, h, max_seq, hd] with b·h folded) holds cur_len rows per head.
+ * total = cur_len + seq; shift = total − max_seq when positive (:381-383,
+ * :465-466): rows [shift, cur_len) of every head move to [0, cur_len − shift),
+ * one row at a time in increasing order (copy_within, :392-405 / :475-485),
+ * then the new rows are written from insert_pos = cur_len − shift (:408-412,
+ * :488-492) — each new row converted as sor_kv_append converts it (Q8_0: the
+ * block quantizer of :336-348). Returns the length of the view the reference
+ * returns, min(total, max_seq) (:430-433, :510-512), through *new_len.
+ * seq > max_seq is the reference's bail (:378-379, :462-463): SOR_ERANGE;
+ * cur_len > max_seq, where its subtraction would underflow, SOR_EINVAL. */
+int sor_kv_cache_update(const float* src, void* cache, int cache_dtype, size_t n_kv, size_t seq, size_t hd,
+                        size_t max_seq, size_t cur_len, size_t* new_len) {
+    if (seq > max_seq) return SOR_ERANGE;
+    if (cur_len > max_seq) return SOR_EINVAL;
+    size_t row_bytes;
+    if (cache_dtype == SOR_Q8_0) {
+        if (hd % QK != 0) return SOR_EINVAL;
+        row_bytes = hd / QK * Q8_0_BYTES;
+    } else if (cache_dtype == SOR_F32) {
+        row_bytes = hd * 4;
+    } else if (cache_dtype == SOR_F16 || cache_dtype == SOR_BF16) {
+        row_bytes = hd * 2;
+    } else {
+        return SOR_EINVAL;
+    }
+    const size_t total = cur_len + seq;
+    const size_t shift = total > max_seq ? total - max_seq : 0;
+    if (shift > 0) {
+        const size_t keep = cur_len - shift;
+        for (size_t h = 0; h < n_kv; h++)
+            for (size_t si = 0; si < keep; si++) {
+                uint8_t* head = (uint8_t*)cache + h * max_seq * row_bytes;
+                memmove(head + si * row_bytes, head + (si + shift) * row_bytes, row_bytes);
+            }
+    }
+    const size_t insert_pos = cur_len - shift;
+    const int st = sor_kv_append(src, cache, cache_dtype, n_kv, seq, hd, max_seq, insert_pos);
+    if (st != SOR_OK) return st;
+    *new_len = total < max_seq ? total : max_seq;
+    return SOR_OK;
+}

@@ -64,6 +64,7 @@ SIGNATURES = {
                                          _vp, _i32, _i64, _vp, _vp, _vp, _i32, _vp, _vp]),
     "sph_transpose_heads": (_i32, [_vp, _vp, _i32, _i64, _i64, _i64, _vp]),
     "sph_kv_append": (_i32, [_vp, _i32, _vp, _i32, _i64, _i64, _i64, _i64, _i64, _vp]),
+    "sph_kv_cache_update": (_i32, [_vp, _i32, _vp, _i32, _i64, _i64, _i64, _i64, _i64, _vp, _vp]),
     # sapient_hip_engine.h
     "sph_engine_create": (_i32, [C.POINTER(EngineConfig), _vp, _i32, _i64, C.POINTER(EngineLayer), _vp, PROJECT_FN,
                                  ATTEND_FN, _vp, C.POINTER(_vp)]),

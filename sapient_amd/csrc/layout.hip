@@ -172,6 +172,66 @@ __global__ __launch_bounds__(kThreads) void kv_append_q8_0(const TS* __restrict_
     }
 }
 
+// Sliding-window shift of a KV cache (the trait path's update_kv_cache,
+// crates/sapient-models/src/forward/common.rs:392-405 and :475-485): in every
+// head, rows [shift, shift + keep) move to [0, keep), in place. A row is read
+// by the row `shift` below it, so blocks cannot split a head's rows between
+// them; instead each block owns one column strip (up to kStripUnits units of
+// UT, the widest access the row width and alignment allow) of one head, over
+// all rows. It walks the strip in chunks of kThreads · kShiftR units, row-major:
+// a chunk's loads all complete (s_waitcnt and the block barrier) before any of
+// its stores, so a store never overtakes a load of the same row; later chunks
+// read only rows at least `shift` past the last row an earlier chunk wrote.
+// The strips of one head are placed on one XCD (workgroups go round-robin to
+// the 8 XCDs), so the partial-line accesses of its strips meet in one L2.
+constexpr int kShiftR = 8;            // units in flight per thread per chunk
+constexpr uint32_t kStripUnits = 16;  // units of a row per block
+constexpr uint32_t kXcds = 8;
+
+template <typename UT>
+__global__ __launch_bounds__(kThreads) void kv_shift_rows(UT* cache, uint32_t n_heads, uint32_t n_strips,
+                                                          uint32_t units_per_row, uint64_t max_seq, uint64_t shift,
+                                                          uint64_t keep) {
+    const uint32_t slot = blockIdx.x % kXcds, j = blockIdx.x / kXcds;
+    const uint32_t head = slot + kXcds * (j / n_strips);
+    const uint32_t strip = j % n_strips;
+    if (head >= n_heads) return;  // whole block: grid padding
+    const uint32_t u0 = strip * kStripUnits;
+    const uint32_t su = units_per_row - u0 < kStripUnits ? units_per_row - u0 : kStripUnits;
+    UT* base = cache + (uint64_t)head * max_seq * units_per_row + u0;
+    const uint64_t items = keep * su;
+    for (uint64_t c0 = 0; c0 < items; c0 += (uint64_t)kThreads * kShiftR) {
+        UT v[kShiftR];
+        uint64_t row[kShiftR];
+        uint32_t col[kShiftR];
+#pragma unroll
+        for (int r = 0; r < kShiftR; ++r) {
+            const uint64_t it = c0 + (uint64_t)r * kThreads + threadIdx.x;
+            row[r] = it / su;
+            col[r] = (uint32_t)(it - row[r] * su);
+            if (it < items) v[r] = base[(row[r] + shift) * units_per_row + col[r]];
+        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+#pragma unroll
+        for (int r = 0; r < kShiftR; ++r) {
+            const uint64_t it = c0 + (uint64_t)r * kThreads + threadIdx.x;
+            if (it < items) base[row[r] * units_per_row + col[r]] = v[r];
+        }
+    }
+}
+
+template <typename UT>
+int launch_shift(void* cache, uint64_t n_heads, uint64_t row_bytes, uint64_t max_seq, uint64_t shift, uint64_t keep,
+                 hipStream_t stream) {
+    const uint64_t upr = row_bytes / sizeof(UT);
+    const uint64_t n_strips = (upr + kStripUnits - 1) / kStripUnits;
+    const uint64_t blocks = kXcds * ((n_heads + kXcds - 1) / kXcds) * n_strips;
+    if (blocks > INT32_MAX || upr > UINT32_MAX || n_heads > UINT32_MAX) return SPH_EINVAL;
+    return launch(kv_shift_rows<UT>, dim3((unsigned)blocks), kThreads, stream, static_cast<UT*>(cache),
+                  (uint32_t)n_heads, (uint32_t)n_strips, (uint32_t)upr, max_seq, shift, keep);
+}
+
 }  // namespace
 }  // namespace sph
 
@@ -226,4 +286,39 @@ extern "C" int sph_kv_append(const void* src, int src_dtype, void* cache, int ca
             return sph::launch_move<TS, TD, sph::M_KV>(src, cache, rows, head_dim, m, s);
         });
     });
+}
+
+extern "C" int sph_kv_cache_update(const void* src, int src_dtype, void* cache, int cache_dtype, int64_t n_kv,
+                                   int64_t seq, int64_t head_dim, int64_t max_seq, int64_t cur_len, int64_t* new_len,
+                                   void* stream) {
+    if (n_kv < 0 || seq < 0 || head_dim < 0 || max_seq < 0 || cur_len < 0 || new_len == nullptr) return SPH_EINVAL;
+    const bool q8 = cache_dtype == SPH_Q8_0;
+    if (!sph::is_float_dtype(src_dtype) || !(q8 || sph::is_float_dtype(cache_dtype))) return SPH_EINVAL;
+    if (q8 && head_dim % 32 != 0) return SPH_EINVAL;
+    if (seq > max_seq) return SPH_ERANGE;      // the reference's "new tokens exceeds max cache size"
+    if (cur_len > max_seq) return SPH_EINVAL;  // more valid rows than the cache holds
+    const int64_t total = cur_len + seq;
+    const int64_t shift = total > max_seq ? total - max_seq : 0;
+    const int64_t keep = cur_len - shift;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (shift > 0 && keep > 0 && n_kv > 0 && head_dim > 0) {
+        if (cache == nullptr) return SPH_EINVAL;
+        const uint64_t row_bytes = q8 ? (uint64_t)head_dim / 32 * 34 : (uint64_t)head_dim * sph::dtype_size(cache_dtype);
+        int st;
+        if (row_bytes % 16 == 0 && sph::aligned(cache, 16))
+            st = sph::launch_shift<sph::u32x4>(cache, n_kv, row_bytes, max_seq, shift, keep, s);
+        else if (row_bytes % 8 == 0 && sph::aligned(cache, 8))
+            st = sph::launch_shift<sph::u32x2>(cache, n_kv, row_bytes, max_seq, shift, keep, s);
+        else if (row_bytes % 4 == 0 && sph::aligned(cache, 4))
+            st = sph::launch_shift<uint32_t>(cache, n_kv, row_bytes, max_seq, shift, keep, s);
+        else if (sph::aligned(cache, 2))
+            st = sph::launch_shift<uint16_t>(cache, n_kv, row_bytes, max_seq, shift, keep, s);
+        else
+            return SPH_EINVAL;
+        if (st != SPH_OK) return st;
+    }
+    const int st = sph_kv_append(src, src_dtype, cache, cache_dtype, n_kv, seq, head_dim, max_seq, keep, stream);
+    if (st != SPH_OK) return st;
+    *new_len = total < max_seq ? total : max_seq;
+    return SPH_OK;
 }

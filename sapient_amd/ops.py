@@ -6,6 +6,7 @@ tensors. Errors from the ABI raise :class:`SapientHipError`.
 """
 from __future__ import annotations
 
+import ctypes
 from typing import Optional, Tuple
 
 import torch
@@ -279,6 +280,28 @@ def kv_append(src: torch.Tensor, cache: torch.Tensor, pos: int) -> None:
     cdt = _lib.Q8_0 if q8 else dtype_code(cache.dtype)
     check(lib().sph_kv_append(src.data_ptr(), dtype_code(src.dtype), cache.data_ptr(), cdt,
                               n_kv, seq, hd, max_seq, int(pos), _stream(src)), "kv_append")
+
+
+def kv_cache_update(src: torch.Tensor, cache: torch.Tensor, cur_len: int) -> int:
+    """Append src [n_kv, seq, head_dim] after the cur_len valid rows of each head
+    of cache [n_kv, max_seq, row], sliding the window left first when the rows
+    would not fit, and return the new valid length min(cur_len + seq, max_seq):
+    common::update_kv_cache / update_kv_cache_q8 (common.rs:355-434, :449-508).
+    Cache dtypes as kv_append (a uint8 cache is Q8_0)."""
+    _dev(src, "src")
+    _dev(cache, "cache")
+    q8 = cache.dtype == torch.uint8
+    if src.dim() != 3 or cache.dim() != 3 or src.shape[0] != cache.shape[0]:
+        raise ValueError("src must be [n_kv, seq, head_dim] and cache [n_kv, max_seq, row]")
+    n_kv, seq, hd = src.shape
+    if cache.shape[2] != (hd // 32 * 34 if q8 else hd) or (q8 and hd % 32):
+        raise ValueError("cache rows must hold head_dim elements (Q8_0: head_dim / 32 blocks of 34 bytes)")
+    max_seq = cache.shape[1]
+    cdt = _lib.Q8_0 if q8 else dtype_code(cache.dtype)
+    n = ctypes.c_int64(0)
+    check(lib().sph_kv_cache_update(src.data_ptr(), dtype_code(src.dtype), cache.data_ptr(), cdt, n_kv, seq, hd,
+                                    max_seq, int(cur_len), ctypes.addressof(n), _stream(src)), "kv_cache_update")
+    return n.value
 
 
 def _rope_kv_args(Hq, Hkv, S, D, positions, kcache, vcache, bad_pos_flag, bq, bk, bv):

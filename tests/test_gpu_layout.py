@@ -166,3 +166,77 @@ def test_kv_append_q8_0_rejects_bad_shapes(dev):
     assert lib().sph_kv_append(src.data_ptr(), 0, cache.data_ptr(), Q8_0, 2, 3, 48, 8, 0, s) == EINVAL  # 48 % 32
     src = torch.zeros(2, 3, 64, device=dev)
     assert lib().sph_kv_append(src.data_ptr(), 0, cache.data_ptr(), Q8_0, 2, 3, 64, 8, 6, s) == ERANGE  # 6 + 3 > 8
+
+
+# Sliding-window cache update (common.rs:355-434, :449-508): (n_kv, hd, max_seq, cur_len, seq). Covers no shift,
+# a decode step on a full cache, a prefill chunk that slides, seq == max_seq (nothing kept), Llama-3-8B's
+# 8 x 8192 x 128 cache at full length, and row widths that take each access width of the shift kernel
+# (16-byte units, 8 (Q8_0 at hd 128: 136-byte rows), 4, 2 (hd 1 in f16, Q8_0 at hd 32: 34-byte rows)).
+_UPD_CASES = [(2, 64, 16, 5, 3), (2, 64, 16, 16, 1), (3, 64, 16, 12, 7), (2, 64, 16, 9, 16), (2, 64, 16, 16, 16),
+              (8, 128, 8192, 8192, 1), (8, 128, 8192, 8000, 512), (5, 3, 40, 40, 2), (4, 1, 33, 30, 5),
+              (1, 128, 4096, 4095, 3), (11, 64, 100, 100, 1)]
+
+
+@pytest.mark.parametrize("cdtype", [torch.float32, torch.float16, torch.bfloat16], ids=IDS)
+@pytest.mark.parametrize("n_kv,hd,max_seq,cur_len,seq", _UPD_CASES)
+def test_kv_cache_update_matches_oracle(dev, orc, cdtype, n_kv, hd, max_seq, cur_len, seq):
+    """update_kv_cache on the device: the shift moves rows bit for bit, the new rows are converted as
+    kv_append converts them, and the returned length is the reference view's; bit-exact with the oracle
+    over the whole cache (rows past the new length untouched)."""
+    print(f"case kv_cache_update {cdtype} {n_kv}x{hd} max {max_seq} cur {cur_len} seq {seq}", flush=True)
+    src = _gen((n_kv, seq, hd), seq * 7 + hd, dev)
+    cache = _gen((n_kv, max_seq, hd), 17 + hd, dev, cdtype)
+    ref = to_np(cache).copy()
+    n = ops.kv_cache_update(src, cache, cur_len)
+    want_n = orc.kv_cache_update(to_np(src), ref, CODE[cdtype], n_kv, seq, hd, max_seq, cur_len)
+    assert n == want_n == min(cur_len + seq, max_seq)
+    _same(cache, ref, f"kv_cache_update {cdtype}")
+
+
+@pytest.mark.parametrize("n_kv,hd,max_seq,cur_len,seq", [(2, 64, 16, 16, 1), (3, 32, 24, 20, 9), (8, 128, 512, 512, 1),
+                                                         (2, 128, 64, 40, 64), (2, 64, 16, 3, 4)])
+def test_kv_cache_update_q8_0(dev, orc, n_kv, hd, max_seq, cur_len, seq):
+    """The quantized cache (update_kv_cache_q8): 34-byte blocks moved by the shift as raw bytes, new rows
+    quantized on append; bit-exact with the oracle."""
+    print(f"case kv_cache_update q8_0 {n_kv}x{hd} max {max_seq} cur {cur_len} seq {seq}", flush=True)
+    g = torch.Generator(device=dev).manual_seed(max_seq + cur_len)
+    src = torch.randn(n_kv, seq, hd, generator=g, device=dev) * 3
+    row = hd // 32 * 34
+    cache = torch.randint(0, 256, (n_kv, max_seq, row), generator=g, device=dev, dtype=torch.int32).to(torch.uint8)
+    ref = to_np(cache).copy()
+    n = ops.kv_cache_update(src, cache, cur_len)
+    assert n == orc.kv_cache_update(to_np(src), ref, orc.Q8_0, n_kv, seq, hd, max_seq, cur_len)
+    assert np.array_equal(to_np(cache), ref)
+
+
+def test_kv_cache_update_decode_sequence(dev, orc):
+    """Thirty decode steps past a full f16 cache (the window slides one row per step), each step checked
+    against the oracle's cache after the same steps."""
+    n_kv, hd, max_seq = 4, 64, 48
+    cache = _gen((n_kv, max_seq, hd), 5, dev, torch.float16)
+    ref = to_np(cache).copy()
+    cur = 40
+    for t in range(30):
+        src = _gen((n_kv, 1, hd), 100 + t, dev)
+        print(f"case kv_cache_update decode step {t} cur {cur}", flush=True)
+        n = ops.kv_cache_update(src, cache, cur)
+        assert n == orc.kv_cache_update(to_np(src), ref, 1, n_kv, 1, hd, max_seq, cur)
+        _same(cache, ref, f"step {t}")
+        cur = n
+
+
+def test_kv_cache_update_rejects_bad_arguments(dev):
+    from sapient_amd._lib import EINVAL, ERANGE, lib
+    import ctypes
+    cache = torch.zeros(2, 8, 16, device=dev)
+    before = cache.clone()
+    src = torch.ones(2, 9, 16, device=dev)
+    n = ctypes.c_int64(-7)
+    s = torch.cuda.current_stream().cuda_stream
+    L = lib()
+    assert L.sph_kv_cache_update(src.data_ptr(), 0, cache.data_ptr(), 0, 2, 9, 16, 8, 0, ctypes.addressof(n), s) == ERANGE
+    assert L.sph_kv_cache_update(src.data_ptr(), 0, cache.data_ptr(), 0, 2, 1, 16, 8, 9, ctypes.addressof(n), s) == EINVAL
+    assert L.sph_kv_cache_update(src.data_ptr(), 0, cache.data_ptr(), 0, 2, 1, 16, 8, 2, None, s) == EINVAL
+    assert L.sph_kv_cache_update(src.data_ptr(), 0, cache.data_ptr(), 0, 2, 1, 16, 8, -1, ctypes.addressof(n), s) == EINVAL
+    torch.cuda.synchronize()
+    assert n.value == -7 and torch.equal(cache, before)

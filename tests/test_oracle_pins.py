@@ -644,3 +644,69 @@ def test_kv_append_is_a_slice_assignment(cache_dtype):
     assert (cache[:, steps:] == 0).all()
     with pytest.raises(oracle.OracleError):
         oracle.kv_append(np.zeros((n_kv, 2, hd), np.float32), cache, cache_dtype, n_kv, 2, hd, max_seq, 15)
+
+
+def test_kv_cache_update_reference_kat():
+    """crates/sapient-models/tests/inference_test.rs:10-61: an f32 cache [1, 2, 4, 2]; one token, then
+    two more at seq 1; views of length 1 and 3; the cache holds 1,3,4 / 2,5,6 and zeros past them."""
+    cache = np.zeros((2, 4, 2), np.float32)
+    assert oracle.kv_cache_update(np.array([1, 1, 2, 2], np.float32), cache, oracle.F32, 2, 1, 2, 4, 0) == 1
+    k2 = np.array([3, 3, 4, 4, 5, 5, 6, 6], np.float32)
+    assert oracle.kv_cache_update(k2, cache, oracle.F32, 2, 2, 2, 4, 1) == 3
+    assert np.array_equal(cache[0].reshape(-1), [1, 1, 3, 3, 4, 4, 0, 0])
+    assert np.array_equal(cache[1].reshape(-1), [2, 2, 5, 5, 6, 6, 0, 0])
+
+
+def _window_model(old_rows: np.ndarray, new_rows: np.ndarray, max_seq: int) -> np.ndarray:
+    """The sliding window stated as what it keeps: the last min(len, max_seq) rows of the valid
+    rows followed by the new ones (independent of the shift-then-insert loop of common.rs)."""
+    both = np.concatenate([old_rows, new_rows], axis=1)
+    return both[:, max(0, both.shape[1] - max_seq):]
+
+
+@pytest.mark.parametrize("cache_dtype", [0, 1, 30, 8])
+@pytest.mark.parametrize("max_seq,cur_len,seq", [(8, 0, 3), (8, 5, 3), (8, 8, 1), (8, 7, 3), (8, 6, 8), (8, 0, 8),
+                                                 (8, 8, 8), (5, 5, 4), (16, 16, 1), (16, 3, 15), (1, 1, 1)])
+def test_kv_cache_update_is_a_sliding_window(cache_dtype, max_seq, cur_len, seq):
+    """common.rs:355-434 / :449-508 (f32, f16, bf16 and Q8_0 caches): after the update the first
+    new_len = min(cur_len + seq, max_seq) rows of every head are the last new_len rows of
+    (old valid rows, new rows converted to the cache type); rows past new_len are untouched."""
+    n_kv, hd = 3, 64
+    rng = np.random.default_rng(max_seq * 100 + cur_len * 10 + seq + cache_dtype)
+    if cache_dtype == oracle.Q8_0:
+        row = hd // 32 * 34
+        cache = rng.integers(0, 256, (n_kv, max_seq, row), dtype=np.uint8)
+    elif cache_dtype == 0:
+        row = hd
+        cache = rng.standard_normal((n_kv, max_seq, row), dtype=np.float32)
+    else:
+        row = hd
+        cache = rng.integers(0, 1 << 16, (n_kv, max_seq, row), dtype=np.uint16)
+    before = cache.copy()
+    src = rng.standard_normal((n_kv, seq, hd), dtype=np.float32) * 3
+    if cache_dtype == oracle.Q8_0:
+        new = np.stack([np.stack([quantize_q8_0_blocks(src[h, s_])[0].reshape(-1) for s_ in range(seq)])
+                        for h in range(n_kv)])
+    elif cache_dtype == 0:
+        new = src
+    elif cache_dtype == 1:
+        new = src.astype(np.float16).view(np.uint16)
+    else:
+        new = torch.from_numpy(src).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    n = oracle.kv_cache_update(src, cache, cache_dtype, n_kv, seq, hd, max_seq, cur_len)
+    assert n == min(cur_len + seq, max_seq)
+    want = _window_model(before[:, :cur_len], new, max_seq)
+    assert np.array_equal(_bits(cache[:, :n]) if cache_dtype == 0 else cache[:, :n],
+                          _bits(want) if cache_dtype == 0 else want)
+    assert np.array_equal(cache[:, n:], before[:, n:])
+
+
+def test_kv_cache_update_errors():
+    """seq > max_seq is the reference's bail (common.rs:378-379); cur_len > max_seq has no valid
+    meaning (its subtraction would underflow); nothing is written in either case."""
+    cache = np.zeros((2, 4, 2), np.float32)
+    with pytest.raises(oracle.OracleError):
+        oracle.kv_cache_update(np.zeros(2 * 5 * 2, np.float32), cache, oracle.F32, 2, 5, 2, 4, 0)
+    with pytest.raises(oracle.OracleError):
+        oracle.kv_cache_update(np.zeros(2 * 1 * 2, np.float32), cache, oracle.F32, 2, 1, 2, 4, 5)
+    assert (cache == 0).all()
