@@ -10,11 +10,15 @@ and check, in order:
   1. graph replay = eager launches, bit for bit, at every decode step (the
      graph is replayed for several tokens, eager work and synchronizations in
      between);
-  2. the engine's hidden states and KV caches against the oracle's
-     restatement of the reference sequence: RMSNorm and SwiGLU compound over
-     the layers, so the bound is 1e-4 of the largest |value| (hidden) and
-     one f16 ulp plus that bound (caches);
-  3. the engine's refusals (full cache, id ≥ vocab, oversized chunk).
+  2. every op of every layer on the engine's own inputs (the stand-ins record
+     what each op received; the residual stream is rebuilt from the records
+     with the same f32 adds): the norms to 1e-5 relative, bias + RoPE, the
+     KV-cache rows and SwiGLU bit for bit;
+  3. the end-to-end hidden states and caches against the oracle's run of the
+     whole reference sequence on its own values, where the norms' last-bit
+     differences compound over the layers: 1e-4 of the largest |value|
+     (hidden), one f16 ulp plus that bound (caches);
+  4. the engine's refusals (full cache, id ≥ vocab, oversized chunk).
 """
 import numpy as np
 import pytest
@@ -189,4 +193,92 @@ def test_engine_refusals(dev, model):
     assert eng.position == 0
     eng.forward_token(2)
     torch.cuda.synchronize()
+    eng.close()
+
+
+class _Recorder:
+    """Projection and attention stand-ins (the module's) that also keep each call's input as the engine
+    handed it over, so every op of the sequence can be checked on the engine's own inputs."""
+
+    def __init__(self):
+        self.calls = []  # (layer, which, input clone); which = PROJ_* or "attend"
+
+    def project(self, layer, which, in_ptr, out_ptr, rows, stream):
+        n_in = _n_in(which)
+        with torch.cuda.stream(torch.cuda.ExternalStream(stream)):
+            self.calls.append((layer, which, _view(in_ptr, rows * n_in).view(rows, n_in).clone()))
+        return project(layer, which, in_ptr, out_ptr, rows, stream)
+
+    def attend(self, layer, q_ptr, kc, vc, kv_dtype, pos_ptr, n_tok, max_seq, out_ptr, stream):
+        n = NQ * n_tok * HD
+        with torch.cuda.stream(torch.cuda.ExternalStream(stream)):
+            self.calls.append((layer, "attend", _view(q_ptr, n).view(NQ, n_tok, HD).clone()))
+        return attend(layer, q_ptr, kc, vc, kv_dtype, pos_ptr, n_tok, max_seq, out_ptr, stream)
+
+
+def _rel_ok(got, want, what):
+    """RMSNorm outputs: <= 1e-5 relative per element (the sum's order differs from the serial fold)."""
+    err = np.abs(got - want)
+    assert np.all(err <= 1e-5 * np.abs(want)), f"{what}: max rel {float((err / np.maximum(np.abs(want), 1e-30)).max())}"
+
+
+def test_engine_each_op_on_its_own_inputs(dev, orc, model):
+    """Teacher-forced parity: the callbacks record what each op received, the test rebuilds the
+    residual stream x from those records with the same f32 adds (exact), and checks every op of every
+    layer on the engine's own inputs — RMSNorm (input, post-attention, final) to 1e-5 relative,
+    bias + RoPE of q (the attention input) and of k with the v rows (the caches) and SwiGLU bit for
+    bit — so no op's tolerance compounds over the layers. Reference sequence: wgpu_engine.rs:362-629."""
+    table, layers, final = model
+    tab = to_np(table)
+    lw = [{k: (None if v is None else widen(v, orc)) for k, v in Lw.items()} for Lw in layers]
+    fin = to_np(final)
+    rec = _Recorder()
+    t_, l_, f_ = model
+    cfg = L.EngineConfig(H, NQ, NKV, HD, INTER, LAYERS, MAX_SEQ, MAX_CHUNK, EPS, THETA, L.ROPE_NEOX, L.F16, L.F16)
+    eng = Engine(cfg, t_, L.F32, VOCAB, l_, f_, rec.project, rec.attend)
+    proj = lambda x, n_out: (0.5 * np.tile(x, (1, -(-n_out // x.shape[1])))[:, :n_out]).astype(np.float32)
+    caches = [(np.zeros((NKV, MAX_SEQ, HD), np.uint16), np.zeros((NKV, MAX_SEQ, HD), np.uint16)) for _ in range(LAYERS)]
+    steps = [PROMPT] + [[t] for t in DECODE]
+    pos0 = 0
+    for si, ids in enumerate(steps):
+        rec.calls.clear()
+        out = to_np(eng.forward_chunk(ids) if len(ids) > 1 else eng.forward_token(ids[0]))
+        torch.cuda.synchronize()
+        T = len(ids)
+        pos = np.arange(pos0, pos0 + T)
+        got = {}
+        for layer, which, t in rec.calls:
+            got[(layer, which)] = to_np(t)
+        print(f"case engine teacher-forced step {si} T {T}", flush=True)
+        x = orc.embed_tokens(tab.reshape(-1).view(np.uint8), L.F32, VOCAB, H, np.array(ids, np.uint32)).reshape(T, H)
+        down = None
+        for l in range(LAYERS):
+            if l > 0:
+                x = orc.add(x, down)
+            h1 = got[(l, L.PROJ_Q)]
+            _rel_ok(h1, orc.rms_norm(x, lw[l]["input_ln"], EPS), f"step {si} layer {l} input norm")
+            q = orc.add_bias_last_dim(proj(h1, NQ * HD), lw[l]["bq"])
+            k = orc.add_bias_last_dim(proj(got[(l, L.PROJ_K)], NKV * HD), lw[l]["bk"])
+            v = orc.add_bias_last_dim(proj(got[(l, L.PROJ_V)], NKV * HD), lw[l]["bv"])
+            qr = orc.apply_rope(np.ascontiguousarray(q.reshape(T, NQ, HD).transpose(1, 0, 2)[None]), pos, THETA)[0]
+            kr = orc.apply_rope(np.ascontiguousarray(k.reshape(T, NKV, HD).transpose(1, 0, 2)[None]), pos, THETA)[0]
+            assert np.array_equal(got[(l, "attend")].view(np.uint32), qr.view(np.uint32)), f"step {si} layer {l} rope q"
+            orc.kv_append(kr, caches[l][0], L.F16, NKV, T, HD, MAX_SEQ, pos0)
+            orc.kv_append(np.ascontiguousarray(v.reshape(T, NKV, HD).transpose(1, 0, 2)), caches[l][1], L.F16, NKV, T,
+                          HD, MAX_SEQ, pos0)
+            attn = got[(l, L.PROJ_O)]
+            assert np.array_equal(attn.view(np.uint32), qr.transpose(1, 0, 2).reshape(T, NQ * HD).view(np.uint32))
+            x = orc.add(x, proj(attn, H))
+            h2 = got[(l, L.PROJ_GATE)]
+            _rel_ok(h2, orc.rms_norm(x, lw[l]["post_ln"], EPS), f"step {si} layer {l} post-attention norm")
+            act = got[(l, L.PROJ_DOWN)]
+            assert np.array_equal(act.view(np.uint32), orc.swiglu(proj(h2, INTER), proj(h2, INTER)).view(np.uint32)), \
+                f"step {si} layer {l} swiglu"
+            down = proj(act, H)
+        _rel_ok(out, orc.rms_norm(orc.add(x[-1:], down[-1:]), fin, EPS)[0], f"step {si} final norm")
+        pos0 += T
+    for l in range(LAYERS):
+        for j, which in enumerate("kv"):
+            g = to_np(eng.cache(l, which)).view(np.uint16).reshape(NKV, MAX_SEQ, HD)
+            assert np.array_equal(g, caches[l][j]), f"layer {l} {which} cache"
     eng.close()
