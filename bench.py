@@ -542,6 +542,14 @@ def op_table(torch, ops, dev, only=None, cpu_budget=0.0, profile_launches=0, ker
             lambda s: ops.kv_append(s[0], s[1], 0),
             lambda: (lambda x=nrm(8, 64, D), c=np.zeros((8, T, D), np.uint16):
                      orc.kv_append(x, c, L.F16, 8, 64, D, T, 0), 64)))
+    # The trait path's cache update on a full cache (decode step past 8192 positions): the window
+    # slides one row — every head's 8191 kept rows move down (read + write) — then the new row lands.
+    run(Row("kv_cache_update", f"8x1x{D} -> full cache 8x{T}x{D}", "f32->f16",
+            2 * 8 * (T - 1) * D * 2 + 8 * D * (4 + 2), 1, "tokens",
+            lambda i: (gen(torch, (8, 1, D), 210 + i, dev, f32), gen(torch, (8, T, D), 220 + i, dev, f16)),
+            lambda s: ops.kv_cache_update(s[0], s[1], T),
+            lambda: (lambda x=nrm(8, 1, D), c=np.zeros((8, T, D), np.uint16):
+                     orc.kv_cache_update(x, c, L.F16, 8, 1, D, T, T), 1)))
 
     def cpu_gather(dt, block, nbytes, d_off, nd, hidden, n):
         """The oracle's gather of n ids from a 2048-row table of the same format (cost per row does not

@@ -176,47 +176,43 @@ __global__ __launch_bounds__(kThreads) void kv_append_q8_0(const TS* __restrict_
 // crates/sapient-models/src/forward/common.rs:392-405 and :475-485): in every
 // head, rows [shift, shift + keep) move to [0, keep), in place. A row is read
 // by the row `shift` below it, so blocks cannot split a head's rows between
-// them; instead each block owns one column strip (up to kStripUnits units of
-// UT, the widest access the row width and alignment allow) of one head, over
-// all rows. It walks the strip in chunks of kThreads · kShiftR units, row-major:
-// a chunk's loads all complete (s_waitcnt and the block barrier) before any of
-// its stores, so a store never overtakes a load of the same row; later chunks
-// read only rows at least `shift` past the last row an earlier chunk wrote.
-// The strips of one head are placed on one XCD (workgroups go round-robin to
-// the 8 XCDs), so the partial-line accesses of its strips meet in one L2.
-constexpr int kShiftR = 8;            // units in flight per thread per chunk
-constexpr uint32_t kStripUnits = 16;  // units of a row per block
+// them; instead each block owns one column of one head — one unit of UT (the
+// widest access the row width and alignment allow) in every row. It walks the
+// column in chunks of kThreads · R rows: a chunk's loads all complete (s_waitcnt
+// and the block barrier) before any of its stores, so a store never overtakes a
+// load of the same row, and later chunks read only rows at least `shift` past
+// the last row an earlier chunk wrote. The columns of one head are placed on
+// one XCD (workgroups go round-robin to the 8 XCDs), so the columns' accesses
+// to the same rows meet in one L2 and each line crosses HBM once.
 constexpr uint32_t kXcds = 8;
 
 template <typename UT>
-__global__ __launch_bounds__(kThreads) void kv_shift_rows(UT* cache, uint32_t n_heads, uint32_t n_strips,
-                                                          uint32_t units_per_row, uint64_t max_seq, uint64_t shift,
-                                                          uint64_t keep) {
+struct ShiftDepth {  // rows in flight per thread: up to 256 bytes of units, at most 32
+    static constexpr int r = 256 / (int)sizeof(UT) < 32 ? 256 / (int)sizeof(UT) : 32;
+};
+
+template <typename UT>
+__global__ __launch_bounds__(kThreads) void kv_shift_rows(UT* cache, uint32_t n_heads, uint32_t units_per_row,
+                                                          uint64_t max_seq, uint64_t shift, uint64_t keep) {
+    constexpr int R = ShiftDepth<UT>::r;
     const uint32_t slot = blockIdx.x % kXcds, j = blockIdx.x / kXcds;
-    const uint32_t head = slot + kXcds * (j / n_strips);
-    const uint32_t strip = j % n_strips;
+    const uint32_t head = slot + kXcds * (j / units_per_row);
+    const uint32_t col = j % units_per_row;
     if (head >= n_heads) return;  // whole block: grid padding
-    const uint32_t u0 = strip * kStripUnits;
-    const uint32_t su = units_per_row - u0 < kStripUnits ? units_per_row - u0 : kStripUnits;
-    UT* base = cache + (uint64_t)head * max_seq * units_per_row + u0;
-    const uint64_t items = keep * su;
-    for (uint64_t c0 = 0; c0 < items; c0 += (uint64_t)kThreads * kShiftR) {
-        UT v[kShiftR];
-        uint64_t row[kShiftR];
-        uint32_t col[kShiftR];
+    UT* base = cache + (uint64_t)head * max_seq * units_per_row + col;
+    for (uint64_t r0 = 0; r0 < keep; r0 += (uint64_t)kThreads * R) {  // trip count uniform over the block
+        UT v[R];
 #pragma unroll
-        for (int r = 0; r < kShiftR; ++r) {
-            const uint64_t it = c0 + (uint64_t)r * kThreads + threadIdx.x;
-            row[r] = it / su;
-            col[r] = (uint32_t)(it - row[r] * su);
-            if (it < items) v[r] = base[(row[r] + shift) * units_per_row + col[r]];
+        for (int r = 0; r < R; ++r) {
+            const uint64_t row = r0 + (uint64_t)r * kThreads + threadIdx.x;
+            if (row < keep) v[r] = base[(row + shift) * units_per_row];
         }
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
 #pragma unroll
-        for (int r = 0; r < kShiftR; ++r) {
-            const uint64_t it = c0 + (uint64_t)r * kThreads + threadIdx.x;
-            if (it < items) base[row[r] * units_per_row + col[r]] = v[r];
+        for (int r = 0; r < R; ++r) {
+            const uint64_t row = r0 + (uint64_t)r * kThreads + threadIdx.x;
+            if (row < keep) base[row * units_per_row] = v[r];
         }
     }
 }
@@ -225,11 +221,10 @@ template <typename UT>
 int launch_shift(void* cache, uint64_t n_heads, uint64_t row_bytes, uint64_t max_seq, uint64_t shift, uint64_t keep,
                  hipStream_t stream) {
     const uint64_t upr = row_bytes / sizeof(UT);
-    const uint64_t n_strips = (upr + kStripUnits - 1) / kStripUnits;
-    const uint64_t blocks = kXcds * ((n_heads + kXcds - 1) / kXcds) * n_strips;
+    const uint64_t blocks = kXcds * ((n_heads + kXcds - 1) / kXcds) * upr;
     if (blocks > INT32_MAX || upr > UINT32_MAX || n_heads > UINT32_MAX) return SPH_EINVAL;
     return launch(kv_shift_rows<UT>, dim3((unsigned)blocks), kThreads, stream, static_cast<UT*>(cache),
-                  (uint32_t)n_heads, (uint32_t)n_strips, (uint32_t)upr, max_seq, shift, keep);
+                  (uint32_t)n_heads, (uint32_t)upr, max_seq, shift, keep);
 }
 
 }  // namespace
