@@ -153,26 +153,30 @@ __global__ __launch_bounds__(kThreads) void rope_kernel(T* q, int nq, T* k, int 
     int h_end = h_begin + heads_per_group;
     if (h_end > nq + nk) h_end = nq + nk;
 
-    auto row_of = [&](int hh) -> T* {
-        return hh < nq ? q + ((size_t)(b * nq + hh) * (size_t)seq + (size_t)s) * (size_t)head_dim
-                       : k + ((size_t)(b * nk + (hh - nq)) * (size_t)seq + (size_t)s) * (size_t)head_dim;
-    };
-    auto load_batch = [&](int h0, RawRun<T, L, ELEM> (&buf)[U][R]) {
+    // This lane's row in head 0 of q and of k; heads lie seq · head_dim
+    // elements apart, so a head's row is the lane's base plus a block-uniform
+    // offset (scalar arithmetic and one 64-bit add per head, instead of the
+    // full per-lane index), computed once per head for its load and its store.
+    const size_t hs = (size_t)seq * (size_t)head_dim;
+    T* const qb = q + ((size_t)b * (size_t)nq * (size_t)seq + (size_t)s) * (size_t)head_dim;
+    T* const kb = nk > 0 ? k + ((size_t)b * (size_t)nk * (size_t)seq + (size_t)s) * (size_t)head_dim : qb;
+    auto row_of = [&](int hh) -> T* { return hh < nq ? qb + (size_t)hh * hs : kb + (size_t)(hh - nq) * hs; };
+    auto load_batch = [&](int h0, RawRun<T, L, ELEM> (&buf)[U][R], T* (&rows)[U]) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             if (h0 + u < h_end) {
-                const T* row = row_of(h0 + u);
+                rows[u] = row_of(h0 + u);
 #pragma unroll
-                for (int r = 0; r < R; ++r) buf[u][r].load(row + off[r]);
+                for (int r = 0; r < R; ++r) buf[u][r].load(rows[u] + off[r]);
             }
         }
     };
-    auto rotate_batch = [&](int h0, const RawRun<T, L, ELEM> (&buf)[U][R], const float (&cs)[NA],
-                            const float (&sn)[NA]) {
+    auto rotate_batch = [&](int h0, const RawRun<T, L, ELEM> (&buf)[U][R], T* const (&rows)[U],
+                            const float (&cs)[NA], const float (&sn)[NA]) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             if (h0 + u < h_end) {
-                T* row = row_of(h0 + u);
+                T* row = rows[u];
                 if constexpr (!INTERLEAVED) {
                     float x0[P], x1[P], o0[P], o1[P];
                     buf[u][0].to_f32(x0);
@@ -205,12 +209,14 @@ __global__ __launch_bounds__(kThreads) void rope_kernel(T* q, int nq, T* k, int 
     // waits for it alone while the first two batches stay in flight.
     float cs[NA], sn[NA];
     RawRun<T, L, ELEM> ba[U][R], bb[U][R];
+    T* ra[U];
+    T* rb[U];
     if constexpr (PAIR_MAJOR) {
         int32_t pv = 0;
         if (tid < toks_per_block && t_first + tid < ntok) pv = pos[(t_first + tid) % seq];
         if (active) {
-            load_batch(h_begin, ba);
-            load_batch(h_begin + U, bb);
+            load_batch(h_begin, ba, ra);
+            load_batch(h_begin + U, bb, rb);
         }
         if (tid < toks_per_block) pos_s[tid] = pv;
         if (tid < 24) inv_pio4[tid] = kInvPio4.w[tid];
@@ -243,8 +249,8 @@ __global__ __launch_bounds__(kThreads) void rope_kernel(T* q, int nq, T* k, int 
         int32_t ps = 0;
         if (active) {
             ps = pos[s];
-            load_batch(h_begin, ba);
-            load_batch(h_begin + U, bb);
+            load_batch(h_begin, ba, ra);
+            load_batch(h_begin + U, bb, rb);
         }
         if (tid < 24) inv_pio4[tid] = kInvPio4.w[tid];
         __syncthreads();
@@ -260,11 +266,11 @@ __global__ __launch_bounds__(kThreads) void rope_kernel(T* q, int nq, T* k, int 
     // Two batches alternate: while one is rotated and stored, the other's
     // loads are in flight.
     for (int h0 = h_begin; h0 < h_end; h0 += 2 * U) {
-        rotate_batch(h0, ba, cs, sn);
-        if (h0 + 2 * U < h_end) load_batch(h0 + 2 * U, ba);
+        rotate_batch(h0, ba, ra, cs, sn);
+        if (h0 + 2 * U < h_end) load_batch(h0 + 2 * U, ba, ra);
         if (h0 + U >= h_end) break;
-        rotate_batch(h0 + U, bb, cs, sn);
-        if (h0 + 3 * U < h_end) load_batch(h0 + 3 * U, bb);
+        rotate_batch(h0 + U, bb, rb, cs, sn);
+        if (h0 + 3 * U < h_end) load_batch(h0 + 3 * U, bb, rb);
     }
 }
 
