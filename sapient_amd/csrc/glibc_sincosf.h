@@ -22,6 +22,12 @@
 //
 // Declared __host__ __device__ so the test suite can compare this very code
 // with the host libm over all 2^32 inputs.
+//
+// Provenance and licence: the algorithm and its constants (the polynomial
+// coefficients, the 4/pi bit table) are those of ARM's optimized-routines
+// (Copyright (c) 2018 Arm Limited; MIT OR Apache-2.0 WITH LLVM-exception), as
+// carried by glibc (LGPL-2.1-or-later); they are restated here from the
+// published algorithm, not copied from either source tree.
 #pragma once
 
 #include <hip/hip_runtime.h>

@@ -14,6 +14,12 @@
 //
 // Declared __host__ __device__ so the test suite can compare the very same
 // code against the host libm over all 2^32 inputs.
+//
+// Provenance and licence: the algorithms and constants are fdlibm's (Copyright
+// (C) 1993 by Sun Microsystems, Inc.: "Permission to use, copy, modify, and
+// distribute this software is freely granted, provided that this notice is
+// preserved."; float conversion by Cygnus Support), as carried by glibc.
+// They are restated here step for step from the published algorithm.
 #pragma once
 
 #include <hip/hip_runtime.h>
