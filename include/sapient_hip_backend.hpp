@@ -57,6 +57,8 @@ class Tensor {
     const std::vector<uint8_t>& bytes() const { return bytes_; }
     // The same bytes under another shape of equal numel (Tensor::reshape).
     Tensor reshaped(std::vector<size_t> shape) const;
+    // The bytes, writable in place (Tensor::as_bytes_mut, tensor.rs:590).
+    std::vector<uint8_t>& bytes_mut() { return bytes_; }
     // The values of an F32 tensor (as_f32_slice); throws for other dtypes.
     std::vector<float> as_f32() const;
 
@@ -164,6 +166,16 @@ class HipLlmBackend final : public LlmBackend {
     std::pair<Tensor, Tensor> add_rms_norm(const Tensor& x, const Tensor& residual, const Tensor& weight,
                                            float eps) override;
     Tensor swiglu(const Tensor& gate, const Tensor& up) override;
+
+    // common::update_kv_cache / update_kv_cache_q8 (crates/sapient-models/src/forward/common.rs:355-434,
+    // :449-528), the trait path's cache update (llama.rs:489-490): new_k [b, h, new_seq, hd] (any float
+    // dtype) is appended after the current_seq_len valid rows of cache [b, h, max_seq, hd] (F32, F16,
+    // BF16, or Q8_0 blocks), sliding the window once the cache is full; the cache is updated in place
+    // and the live prefix is returned as F32 [b, h, min(current_seq_len + new_seq, max_seq), hd] (the
+    // view the F32 path returns, the dequantized copy the Q8_0 path returns). Errors as the reference's
+    // ("update_kv_cache expects 4-D tensors", "update_kv_cache shape mismatch", "new tokens … exceeds
+    // max cache size …").
+    Tensor update_kv_cache(Tensor& cache, size_t current_seq_len, const Tensor& new_k);
 
     // The switches as read at construction.
     bool disabled(const char* op) const;

@@ -584,6 +584,53 @@ Tensor HipLlmBackend::gather_rows(const Tensor& w, const std::vector<uint32_t>& 
     return Tensor::from_f32(out, {1, ids.size(), hidden});
 }
 
+// common.rs:355-434 / :449-528 over sph_kv_cache_update; the Q8_0 prefix is
+// dequantized by the gather kernel (its Q8_0 arm is the reference's
+// `q as i8 as f32 * d`, common.rs:518-524), reading the cache rows as a table.
+Tensor HipLlmBackend::update_kv_cache(Tensor& cache, size_t current_seq_len, const Tensor& new_k) {
+    const auto& cd = cache.shape();
+    const auto& nd = new_k.shape();
+    if (cd.size() != 4 || nd.size() != 4) throw Error("update_kv_cache expects 4-D tensors");
+    if (cd[0] != nd[0] || cd[1] != nd[1] || cd[3] != nd[3]) throw Error("update_kv_cache shape mismatch");
+    const size_t b = cd[0], h = cd[1], max_seq = cd[2], hd = cd[3], new_seq = nd[2];
+    if (new_seq > max_seq)
+        throw Error("new tokens " + std::to_string(new_seq) + " exceeds max cache size " + std::to_string(max_seq));
+    const DType cdt = cache.dtype();
+    if (cdt != DType::F32 && cdt != DType::F16 && cdt != DType::BF16 && cdt != DType::Q8_0)
+        throw Error(std::string("type mismatch: unsupported KV cache dtype ") + dtype_name(cdt));
+    if (current_seq_len > max_seq) throw Error("current length " + std::to_string(current_seq_len) + " exceeds the cache");
+    const Tensor src = f32_input(new_k);
+    std::lock_guard<std::mutex> lock(mu_);
+    DeviceBuf cdev = upload(cache.bytes().data(), cache.bytes().size());
+    DeviceBuf sdev = upload(src.bytes().data(), src.bytes().size());
+    int64_t total = 0;
+    int st = sph_kv_cache_update(sdev.ptr, SPH_F32, cdev.ptr, (int)cdt, (int64_t)(b * h), (int64_t)new_seq,
+                                 (int64_t)hd, (int64_t)max_seq, (int64_t)current_seq_len, &total, stream_);
+    if (st == SPH_OK) download(cdev, cache.bytes_mut().data(), cache.bytes().size());
+    release(sdev);
+    check(st, "update_kv_cache");
+    const size_t n = (size_t)total;
+    std::vector<float> out(b * h * n * hd);
+    if (cdt == DType::Q8_0) {
+        std::vector<uint32_t> ids(b * h * n);
+        for (size_t r = 0; r < b * h; ++r)
+            for (size_t s = 0; s < n; ++s) ids[r * n + s] = (uint32_t)(r * max_seq + s);
+        DeviceBuf idd = upload(ids.data(), ids.size() * 4);
+        DeviceBuf od = alloc(out.size() * 4);
+        st = sph_embed(cdev.ptr, SPH_Q8_0, (int64_t)(b * h * max_seq), (int64_t)hd,
+                       static_cast<const uint32_t*>(idd.ptr), (int64_t)ids.size(), static_cast<float*>(od.ptr),
+                       nullptr, stream_);
+        if (st == SPH_OK) download(od, out.data(), out.size() * 4);
+        check(st, "update_kv_cache (dequantize)");
+    } else {
+        const Tensor all = f32_input(cache);
+        const std::vector<float> v = all.as_f32();
+        for (size_t r = 0; r < b * h; ++r)
+            std::memcpy(out.data() + r * n * hd, v.data() + r * max_seq * hd, n * hd * 4);
+    }
+    return Tensor::from_f32(out, {b, h, n, hd});
+}
+
 // ── graph-side dispatch ─────────────────────────────────────────────────────
 
 bool HipExecutionBackend::supports_op(OpKind) { return true; }  // every kind of OpKind runs here

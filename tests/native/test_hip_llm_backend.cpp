@@ -1,7 +1,8 @@
 // GPU tests of the C++ LlmBackend mirror (include/sapient_hip_backend.hpp),
 // written after the reference's own unit tests so they read the same way:
 //   layernorm.rs:113-149, elementwise.rs:176-232, rope.rs:155-206,
-//   common.rs:556-569 and :669-718, the graph-side dispatch arms of
+//   common.rs:556-569 and :669-718, the KV-cache update (tests/inference_test.rs:10-61 and the
+//   sliding window of common.rs:355-528), the graph-side dispatch arms of
 //   crates/sapient-backends/cpu/src/backend.rs:239-487, the trait's validation errors (rope.rs:19-35,
 //   elementwise.rs:15-21, common.rs:171-173), and the debug switches of backend.rs:191-216.
 // Prints "test <name> ... ok|FAILED: <why>" per test; exits 1 if any failed.
@@ -435,6 +436,65 @@ static void verify_returns_the_device_result(HipLlmBackend&) {
     ASSERT(cpu.calls.size() == 64, "only the first 64 calls are cross-checked");
 }
 
+static void kv_cache_update_reference_test(HipLlmBackend& bk) {  // tests/inference_test.rs:10-61
+    Tensor cache = Tensor::from_f32(std::vector<float>(16, 0.0f), {1, 2, 4, 2});
+    const Tensor view1 = bk.update_kv_cache(cache, 0, Tensor::from_f32({1, 1, 2, 2}, {1, 2, 1, 2}));
+    ASSERT((view1.shape() == std::vector<size_t>{1, 2, 1, 2}), "view after the first token");
+    const Tensor view2 = bk.update_kv_cache(cache, 1, Tensor::from_f32({3, 3, 4, 4, 5, 5, 6, 6}, {1, 2, 2, 2}));
+    ASSERT((view2.shape() == std::vector<size_t>{1, 2, 3, 2}), "view after two more");
+    ASSERT((cache.as_f32() == std::vector<float>{1, 1, 3, 3, 4, 4, 0, 0, 2, 2, 5, 5, 6, 6, 0, 0}), "cache contents");
+    ASSERT((view2.as_f32() == std::vector<float>{1, 1, 3, 3, 4, 4, 2, 2, 5, 5, 6, 6}), "view contents");
+}
+
+static void kv_cache_update_slides_when_full(HipLlmBackend& bk) {  // common.rs:381-412
+    // Full cache (4 of 4 rows per head): one more token drops row 0; three more drop three.
+    Tensor cache = Tensor::from_f32({1, 1, 2, 2, 3, 3, 4, 4, 11, 11, 12, 12, 13, 13, 14, 14}, {1, 2, 4, 2});
+    const Tensor v = bk.update_kv_cache(cache, 4, Tensor::from_f32({5, 5, 15, 15}, {1, 2, 1, 2}));
+    ASSERT((v.shape() == std::vector<size_t>{1, 2, 4, 2}), "view stays at max_seq");
+    ASSERT((cache.as_f32() == std::vector<float>{2, 2, 3, 3, 4, 4, 5, 5, 12, 12, 13, 13, 14, 14, 15, 15}), "slid by one");
+    (void)bk.update_kv_cache(cache, 3, Tensor::from_f32({6, 6, 7, 7, 8, 8, 16, 16, 17, 17, 18, 18}, {1, 2, 3, 2}));
+    ASSERT((cache.as_f32() == std::vector<float>{4, 4, 6, 6, 7, 7, 8, 8, 14, 14, 16, 16, 17, 17, 18, 18}),
+           "cur 3 + 3 new: two dropped, the kept row first");
+    ASSERT(expect_error([&] { bk.update_kv_cache(cache, 4, Tensor::from_f32(std::vector<float>(20, 0.0f), {1, 2, 5, 2})); })
+               .find("new tokens 5 exceeds max cache size 4") != std::string::npos, "too many new tokens");
+    ASSERT(expect_error([&] { bk.update_kv_cache(cache, 0, Tensor::from_f32({1, 1, 1, 1}, {2, 1, 2})); })
+               .find("expects 4-D tensors") != std::string::npos, "rank");
+    ASSERT(expect_error([&] { bk.update_kv_cache(cache, 0, Tensor::from_f32({1, 1}, {1, 1, 1, 2})); })
+               .find("shape mismatch") != std::string::npos, "heads");
+}
+
+static void kv_cache_update_q8_0(HipLlmBackend& bk) {  // update_kv_cache_q8, common.rs:449-528
+    // [1, 1, 2, 32] Q8_0 cache holding one row; a full cache after a second, then a slide: rows are
+    // quantized by quantize_f32_to_q8_0_block (common.rs:336-348, the quantizer of quant.rs:223-235),
+    // moved as raw blocks, and the returned prefix is q · d in f32.
+    std::vector<float> r0(32), r1(32), r2(32);
+    for (int i = 0; i < 32; ++i) {
+        r0[i] = (float)(i - 16) * 0.25f;
+        r1[i] = std::sin((float)i);
+        r2[i] = (float)(i % 5) - 2.0f;
+    }
+    std::vector<uint8_t> bytes = quantize_q8_0(r0);
+    bytes.resize(68, 0);
+    Tensor cache = Tensor::from_quant_bytes(bytes, {1, 1, 2, 32}, DType::Q8_0);
+    const Tensor v1 = bk.update_kv_cache(cache, 1, Tensor::from_f32(r1, {1, 1, 1, 32}));
+    std::vector<uint8_t> want = quantize_q8_0(r0), q1 = quantize_q8_0(r1);
+    want.insert(want.end(), q1.begin(), q1.end());
+    ASSERT(cache.bytes() == want, "second row quantized in place");
+    const Tensor v2 = bk.update_kv_cache(cache, 2, Tensor::from_f32(r2, {1, 1, 1, 32}));
+    std::vector<uint8_t> q2 = quantize_q8_0(r2);
+    want.assign(q1.begin(), q1.end());
+    want.insert(want.end(), q2.begin(), q2.end());
+    ASSERT(cache.bytes() == want, "window slid by one block row");
+    ASSERT((v2.shape() == std::vector<size_t>{1, 1, 2, 32}), "prefix shape");
+    const std::vector<float> y = v2.as_f32();
+    for (int s = 0; s < 2; ++s) {
+        const uint8_t* blk = want.data() + 34 * s;
+        const float d = f16_to_f32((uint16_t)(blk[0] | (blk[1] << 8)));
+        for (int i = 0; i < 32; ++i) ASSERT(y[32 * s + i] == (float)(int8_t)blk[2 + i] * d, "dequantized prefix");
+    }
+    (void)v1;
+}
+
 static void quant_bytes_are_validated(HipLlmBackend&) {  // tensor.rs:143-169
     ASSERT(expect_error([] { Tensor::from_quant_bytes(std::vector<uint8_t>(33), {32}, DType::Q8_0); })
                .find("shape mismatch") != std::string::npos, "byte count");
@@ -470,6 +530,9 @@ int main() {
         {"add_rms_norm_is_add_then_rms_norm", add_rms_norm_is_add_then_rms_norm},
         {"embed_row_gather_matches_full_dequant", embed_row_gather_matches_full_dequant},
         {"quant_bytes_are_validated", quant_bytes_are_validated},
+        {"kv_cache_update_reference_test", kv_cache_update_reference_test},
+        {"kv_cache_update_slides_when_full", kv_cache_update_slides_when_full},
+        {"kv_cache_update_q8_0", kv_cache_update_q8_0},
         {"disable_routes_listed_ops", disable_routes_listed_ops},
         {"disable_without_backend_raises", disable_without_backend_raises},
         {"verify_returns_the_device_result", verify_returns_the_device_result},
