@@ -529,13 +529,21 @@ int launch_rope_kv(const void* qv, void* qov, int nq, const void* kv, const void
                aligned(vc, ac) && aligned(bq, ab) && aligned(bk, ab) && aligned(bv, ab);
     };
     constexpr int V = vec16<T>::n < vec16<TC>::n ? vec16<T>::n : vec16<TC>::n;
+    // A decode step (a few tokens) leaves most lanes of its blocks idle and its
+    // time is one dependent chain — position load, the thread's sin/cos, store —
+    // so it takes the narrowest runs that stay word-sized: fewer angles per lane.
+    const bool few = seq <= 4;
     if (!il) {
+        if (few && ok(V / 2)) return launch_rope_kv_p<T, TC, TB, V / 2, false, TM>(q, qo, nq, k, v, nkv, pos, seq, head_dim, pos_scale, kc, vc, max_seq, flag, bq, bk, bv, den, stream);
         if (ok(V)) return launch_rope_kv_p<T, TC, TB, V, false, TM>(q, qo, nq, k, v, nkv, pos, seq, head_dim, pos_scale, kc, vc, max_seq, flag, bq, bk, bv, den, stream);
         if (ok(V / 2)) return launch_rope_kv_p<T, TC, TB, V / 2, false, TM>(q, qo, nq, k, v, nkv, pos, seq, head_dim, pos_scale, kc, vc, max_seq, flag, bq, bk, bv, den, stream);
         if constexpr (V / 4 >= 2) {
             if (ok(V / 4)) return launch_rope_kv_p<T, TC, TB, V / 4, false, TM>(q, qo, nq, k, v, nkv, pos, seq, head_dim, pos_scale, kc, vc, max_seq, flag, bq, bk, bv, den, stream);
         }
     } else {
+        if constexpr (V / 4 >= 1) {
+            if (few && ok(V / 4)) return launch_rope_kv_p<T, TC, TB, V / 4, true, TM>(q, qo, nq, k, v, nkv, pos, seq, head_dim, pos_scale, kc, vc, max_seq, flag, bq, bk, bv, den, stream);
+        }
         if (ok(V / 2)) return launch_rope_kv_p<T, TC, TB, V / 2, true, TM>(q, qo, nq, k, v, nkv, pos, seq, head_dim, pos_scale, kc, vc, max_seq, flag, bq, bk, bv, den, stream);
         if constexpr (V / 4 >= 1) {
             if (ok(V / 4)) return launch_rope_kv_p<T, TC, TB, V / 4, true, TM>(q, qo, nq, k, v, nkv, pos, seq, head_dim, pos_scale, kc, vc, max_seq, flag, bq, bk, bv, den, stream);
