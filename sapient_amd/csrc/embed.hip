@@ -19,7 +19,8 @@
 // (d·sc·q is exact). The gather is therefore bit-exact.
 //
 // Design (write-dominated: 16 KiB of f32 out per 2.3 KiB Q4_K row in):
-//  - One wave64 per token, 16 tokens per 1024-thread block; each lane produces
+//  - One wave64 per token (16 tokens per 1024-thread block; 8 per 512-thread
+//    block in embed_staged, whose LDS footprint that keeps small); each lane produces
 //    4 consecutive outputs per step, so every store instruction writes 1 KiB
 //    contiguous (16 bytes per lane), non-temporal (non-temporal stores and the
 //    larger block measured 4.8 → 6.5 TB/s on the Q4_K gather).
@@ -223,7 +224,14 @@ __global__ __launch_bounds__(kThreads) void embed_rows(const uint8_t* __restrict
 // the same per-element arithmetic as embed_rows. Every wave of a block runs
 // the same number of chunk steps (hidden is uniform), so the block barriers
 // are reached by all, tokens past n_ids included.
-constexpr int kStageBytes = 4608;  // per wave: 16 waves x 4608 B leave room for two blocks per CU
+// Blocks of 8 waves (512 threads) x 4608 B: four blocks fit a CU's LDS, and
+// against 16-wave blocks (two per CU) they measured 0.6 to 1.9 points more of
+// HBM peak on every staged type at 65536 uniform ids of a 128256 x 4096 table
+// (Q5_K 75.8 -> 76.5 %, Q8_0 74.8 -> 75.6 %, f16 73.0 -> 74.9 %). The Q4_K
+// kernel below stages 2304 B per wave and gains nothing from the smaller block.
+constexpr int kStageBytes = 4608;
+constexpr int kStagedThreads = 512;
+constexpr int kStagedTokPerBlock = kStagedThreads / kWave;
 
 template <int W> struct StageWord;
 template <> struct StageWord<16> { using type = u32x4; };
@@ -243,16 +251,16 @@ template <> struct StageUnit<SPH_Q6_K> { static constexpr int bytes = 210, elems
 
 // chunk_units: units per chunk, chunk_units * bytes <= kStageBytes and a multiple of W.
 template <int DT, int W>
-__global__ __launch_bounds__(kThreads) void embed_staged(const uint8_t* __restrict__ table, int64_t vocab, int hidden,
+__global__ __launch_bounds__(kStagedThreads) void embed_staged(const uint8_t* __restrict__ table, int64_t vocab, int hidden,
                                                          int64_t row_bytes, const uint32_t* __restrict__ ids,
                                                          int64_t n_ids, float* __restrict__ out, int32_t* bad_id_flag,
                                                          int chunk_units) {
     using Word = typename StageWord<W>::type;
     using U = StageUnit<DT>;
-    __shared__ __align__(16) uint8_t stage[kTokPerBlock][kStageBytes];
+    __shared__ __align__(16) uint8_t stage[kStagedTokPerBlock][kStageBytes];
     const int lane = threadIdx.x & (kWave - 1);
     const int wv = threadIdx.x / kWave;
-    const int64_t t = (int64_t)blockIdx.x * kTokPerBlock + wv;
+    const int64_t t = (int64_t)blockIdx.x * kStagedTokPerBlock + wv;
     const bool active = t < n_ids;
     const uint32_t id = active ? __builtin_amdgcn_readfirstlane(ids[t]) : 0u;
     const bool valid = active && (int64_t)id < vocab;
@@ -367,8 +375,8 @@ int launch_staged(const void* table, int64_t vocab, int64_t hidden, int64_t row_
     constexpr int64_t kChunk = int64_t(1) << 24;  // tokens per launch
     for (int64_t t0 = 0; t0 < n_ids; t0 += kChunk) {
         const int64_t nt = n_ids - t0 < kChunk ? n_ids - t0 : kChunk;
-        const dim3 grid((unsigned)((nt + kTokPerBlock - 1) / kTokPerBlock));
-        const int st = launch(embed_staged<DT, W>, grid, kThreads, stream, static_cast<const uint8_t*>(table), vocab,
+        const dim3 grid((unsigned)((nt + kStagedTokPerBlock - 1) / kStagedTokPerBlock));
+        const int st = launch(embed_staged<DT, W>, grid, kStagedThreads, stream, static_cast<const uint8_t*>(table), vocab,
                               (int)hidden, row_bytes, ids + t0, nt, out + (size_t)t0 * (size_t)hidden, flag, cu);
         if (st != SPH_OK) return st;
     }
