@@ -287,7 +287,8 @@ __global__ __launch_bounds__(kThreads) void rope_kv_kernel(const T* q, T* qo, in
                                                            int half, int lanes_per_tok, int toks_per_block,
                                                            int heads_per_group, float pos_scale, TC* kc, TC* vc,
                                                            int64_t max_seq, int32_t* bad_pos_flag, const TB* bq,
-                                                           const TB* bk, const TB* bv, DenTable den) {
+                                                           const TB* bk, const TB* bv, DenTable den,
+                                                           const float* __restrict__ ang) {
     __shared__ uint32_t inv_pio4[24];
     const int tib = threadIdx.x / lanes_per_tok;
     const int lit = threadIdx.x - tib * lanes_per_tok;
@@ -361,19 +362,33 @@ __global__ __launch_bounds__(kThreads) void rope_kv_kernel(const T* q, T* qo, in
             load_row(row_of(v, nkv, h_), bv ? bv + (size_t)h_ * head_dim : nullptr, v0, v1);      \
         }                                                                                         \
     } while (0)
-    if (active) {
-        ps = pos[s];
-        if (h_begin < h_end) SPH_LOAD_HEAD(h_begin);
-    }
-    const uint32_t* tab = stage_inv_pio4(inv_pio4);
-    if (!active) return;
-
-    const float p = (float)ps / pos_scale;
     float cs[P], sn[P];
+    if (ang != nullptr) {
+        // Angles supplied per (token, pair) as (cos, sin): requested with the
+        // position and the rows, so the step waits on memory once and computes
+        // no sin/cos (the whole block takes this branch; no barrier follows).
+        if (!active) return;
+        ps = pos[s];
+        const float* a = ang + 2 * ((size_t)s * (size_t)half + (size_t)i0);
 #pragma unroll
-    for (int j = 0; j < P; ++j) {
-        const float freq = p / den.v[i0 + j];
-        glibc_sincosf_tab(freq, tab, &sn[j], &cs[j]);
+        for (int j = 0; j < P; ++j) {
+            cs[j] = a[2 * j];
+            sn[j] = a[2 * j + 1];
+        }
+        if (h_begin < h_end) SPH_LOAD_HEAD(h_begin);
+    } else {
+        if (active) {
+            ps = pos[s];
+            if (h_begin < h_end) SPH_LOAD_HEAD(h_begin);
+        }
+        const uint32_t* tab = stage_inv_pio4(inv_pio4);
+        if (!active) return;
+        const float p = (float)ps / pos_scale;
+#pragma unroll
+        for (int j = 0; j < P; ++j) {
+            const float freq = p / den.v[i0 + j];
+            glibc_sincosf_tab(freq, tab, &sn[j], &cs[j]);
+        }
     }
     const bool pos_ok = ps >= 0 && (int64_t)ps < max_seq;
     if (!pos_ok && bad_pos_flag != nullptr && lit == 0 && blockIdx.y == 0) *bad_pos_flag = 1;
@@ -476,7 +491,7 @@ inline void fill_dens(DenTable& den, int half, int rotary_dim, float base) {
 template <typename T, typename TC, typename TB, int P, bool IL, bool TM>
 int launch_rope_kv_p(const T* q, T* qo, int nq, const T* k, const T* v, int nkv, const int32_t* pos, int64_t seq, int head_dim,
                      float pos_scale, TC* kc, TC* vc, int64_t max_seq, int32_t* flag, const TB* bq, const TB* bk,
-                     const TB* bv, const DenTable& den, hipStream_t stream) {
+                     const TB* bv, const DenTable& den, const float* ang, hipStream_t stream) {
     const int half = head_dim / 2;
     const int lanes_per_tok = half / P;
     const int toks_per_block = kThreads / lanes_per_tok;
@@ -494,7 +509,7 @@ int launch_rope_kv_p(const T* q, T* qo, int nq, const T* k, const T* v, int nkv,
     const dim3 grid((unsigned)blocks_x, (unsigned)groups);
     return launch(rope_kv_kernel<T, TC, TB, P, IL, TM>, grid, kThreads, stream, q, qo, nq, k, v, nkv, pos, seq,
                   head_dim, half, lanes_per_tok, toks_per_block, heads_per_group, pos_scale, kc, vc, max_seq, flag, bq,
-                  bk, bv, den);
+                  bk, bv, den, ang);
 }
 
 // P: pairs per thread, the widest whose accesses of q/k/v (type T) and of the
@@ -502,7 +517,7 @@ int launch_rope_kv_p(const T* q, T* qo, int nq, const T* k, const T* v, int nkv,
 template <typename T, typename TC, typename TB, bool TM>
 int launch_rope_kv(const void* qv, void* qov, int nq, const void* kv, const void* vv, int nkv, int layout,
                    const int32_t* pos, int64_t seq, int head_dim, float base, float pos_scale, void* kcv, void* vcv,
-                   int64_t max_seq, int32_t* flag, const void* bqv, const void* bkv, const void* bvv,
+                   int64_t max_seq, int32_t* flag, const void* bqv, const void* bkv, const void* bvv, const float* ang,
                    hipStream_t stream) {
     const TB* bq = static_cast<const TB*>(bqv);
     const TB* bk = static_cast<const TB*>(bkv);
@@ -534,19 +549,19 @@ int launch_rope_kv(const void* qv, void* qov, int nq, const void* kv, const void
     // so it takes the narrowest runs that stay word-sized: fewer angles per lane.
     const bool few = seq <= 4;
     if (!il) {
-        if (few && ok(V / 2)) return launch_rope_kv_p<T, TC, TB, V / 2, false, TM>(q, qo, nq, k, v, nkv, pos, seq, head_dim, pos_scale, kc, vc, max_seq, flag, bq, bk, bv, den, stream);
-        if (ok(V)) return launch_rope_kv_p<T, TC, TB, V, false, TM>(q, qo, nq, k, v, nkv, pos, seq, head_dim, pos_scale, kc, vc, max_seq, flag, bq, bk, bv, den, stream);
-        if (ok(V / 2)) return launch_rope_kv_p<T, TC, TB, V / 2, false, TM>(q, qo, nq, k, v, nkv, pos, seq, head_dim, pos_scale, kc, vc, max_seq, flag, bq, bk, bv, den, stream);
+        if (few && ok(V / 2)) return launch_rope_kv_p<T, TC, TB, V / 2, false, TM>(q, qo, nq, k, v, nkv, pos, seq, head_dim, pos_scale, kc, vc, max_seq, flag, bq, bk, bv, den, ang, stream);
+        if (ok(V)) return launch_rope_kv_p<T, TC, TB, V, false, TM>(q, qo, nq, k, v, nkv, pos, seq, head_dim, pos_scale, kc, vc, max_seq, flag, bq, bk, bv, den, ang, stream);
+        if (ok(V / 2)) return launch_rope_kv_p<T, TC, TB, V / 2, false, TM>(q, qo, nq, k, v, nkv, pos, seq, head_dim, pos_scale, kc, vc, max_seq, flag, bq, bk, bv, den, ang, stream);
         if constexpr (V / 4 >= 2) {
-            if (ok(V / 4)) return launch_rope_kv_p<T, TC, TB, V / 4, false, TM>(q, qo, nq, k, v, nkv, pos, seq, head_dim, pos_scale, kc, vc, max_seq, flag, bq, bk, bv, den, stream);
+            if (ok(V / 4)) return launch_rope_kv_p<T, TC, TB, V / 4, false, TM>(q, qo, nq, k, v, nkv, pos, seq, head_dim, pos_scale, kc, vc, max_seq, flag, bq, bk, bv, den, ang, stream);
         }
     } else {
         if constexpr (V / 4 >= 1) {
-            if (few && ok(V / 4)) return launch_rope_kv_p<T, TC, TB, V / 4, true, TM>(q, qo, nq, k, v, nkv, pos, seq, head_dim, pos_scale, kc, vc, max_seq, flag, bq, bk, bv, den, stream);
+            if (few && ok(V / 4)) return launch_rope_kv_p<T, TC, TB, V / 4, true, TM>(q, qo, nq, k, v, nkv, pos, seq, head_dim, pos_scale, kc, vc, max_seq, flag, bq, bk, bv, den, ang, stream);
         }
-        if (ok(V / 2)) return launch_rope_kv_p<T, TC, TB, V / 2, true, TM>(q, qo, nq, k, v, nkv, pos, seq, head_dim, pos_scale, kc, vc, max_seq, flag, bq, bk, bv, den, stream);
+        if (ok(V / 2)) return launch_rope_kv_p<T, TC, TB, V / 2, true, TM>(q, qo, nq, k, v, nkv, pos, seq, head_dim, pos_scale, kc, vc, max_seq, flag, bq, bk, bv, den, ang, stream);
         if constexpr (V / 4 >= 1) {
-            if (ok(V / 4)) return launch_rope_kv_p<T, TC, TB, V / 4, true, TM>(q, qo, nq, k, v, nkv, pos, seq, head_dim, pos_scale, kc, vc, max_seq, flag, bq, bk, bv, den, stream);
+            if (ok(V / 4)) return launch_rope_kv_p<T, TC, TB, V / 4, true, TM>(q, qo, nq, k, v, nkv, pos, seq, head_dim, pos_scale, kc, vc, max_seq, flag, bq, bk, bv, den, ang, stream);
         }
     }
     return SPH_EINVAL;  // head_dim or alignment the vector paths do not cover
@@ -630,7 +645,8 @@ template <bool TM>
 int rope_kv_entry(const void* q, void* q_out, int64_t n_q_heads, const void* k, const void* v, int64_t n_kv_heads,
                   int dtype, int layout, const int32_t* positions, int64_t seq, int64_t head_dim, float base,
                   float pos_scale, void* kcache, void* vcache, int cache_dtype, int64_t max_seq, const void* bq,
-                  const void* bk, const void* bv, int bias_dtype, int32_t* bad_pos_flag, void* stream) {
+                  const void* bk, const void* bv, int bias_dtype, int32_t* bad_pos_flag, void* stream,
+                  const float* angles = nullptr) {
     if (layout != SPH_ROPE_NEOX && layout != SPH_ROPE_INTERLEAVED) return SPH_EINVAL;
     if (!is_float_dtype(dtype) || !is_float_dtype(cache_dtype)) return SPH_EINVAL;
     if ((bq || bk || bv) && !is_float_dtype(bias_dtype)) return SPH_EINVAL;
@@ -656,7 +672,7 @@ int rope_kv_entry(const void* q, void* q_out, int64_t n_q_heads, const void* k, 
                 using TB = decltype(tb);
                 return launch_rope_kv<T, TC, TB, TM>(q, q_out, (int)n_q_heads, k, v, (int)n_kv_heads, layout,
                                                      positions, seq, (int)head_dim, base, pos_scale, kcache, vcache,
-                                                     max_seq, bad_pos_flag, bq, bk, bv, s);
+                                                     max_seq, bad_pos_flag, bq, bk, bv, angles, s);
             });
         });
     });
@@ -673,6 +689,21 @@ extern "C" int sph_rope_kv_append(void* q, int64_t n_q_heads, const void* k, con
     return sph::rope_kv_entry<false>(q, q, n_q_heads, k, v, n_kv_heads, dtype, layout, positions, seq, head_dim, base,
                                      pos_scale, kcache, vcache, cache_dtype, max_seq, bq, bk, bv, bias_dtype,
                                      bad_pos_flag, stream);
+}
+
+// sph_rope_kv_append with the angles supplied: angles[2 (s·rotary_dim/2 + i)]
+// and [... + 1] hold cos and sin of positions[s] / pos_scale / base^(2i/head_dim),
+// evaluated by the caller with the libm the reference calls. For the decode
+// engine, which knows a step's position on the host; not exported.
+extern "C" __attribute__((visibility("hidden"))) int sph_rope_kv_append_angles(
+    void* q, int64_t n_q_heads, const void* k, const void* v, int64_t n_kv_heads, int dtype, int layout,
+    const int32_t* positions, const float* angles, int64_t seq, int64_t head_dim, void* kcache, void* vcache,
+    int cache_dtype, int64_t max_seq, const void* bq, const void* bk, const void* bv, int bias_dtype,
+    int32_t* bad_pos_flag, void* stream) {
+    if (angles == nullptr || !sph::aligned(angles, 8)) return SPH_EINVAL;
+    return sph::rope_kv_entry<false>(q, q, n_q_heads, k, v, n_kv_heads, dtype, layout, positions, seq, head_dim, 1.0f,
+                                     1.0f, kcache, vcache, cache_dtype, max_seq, bq, bk, bv, bias_dtype, bad_pos_flag,
+                                     stream, angles);
 }
 
 extern "C" int sph_rope_kv_append_tokens(const void* q, void* q_out, int64_t n_q_heads, const void* k, const void* v,

@@ -12,10 +12,15 @@
 //    (sph_rope_kv_append_tokens reads the projections' token-major rows);
 //  - forward_chunk adds the last layer's residual and normalises only the last
 //    row, the one the reference slices out before its final norm (:623-627).
+//  - a one-token step's RoPE angles, cos and sin of position / base^(2i/hd), are
+//    evaluated on the host with the libm the reference calls (the values its
+//    own rope computes) and staged with the token id and position, so the
+//    fused RoPE + KV launch reads them instead of evaluating sin/cos.
 // Decode steps can be captured into a HIP graph once and replayed: every
-// per-token value (token id, position) lives in device memory, refreshed by an
-// H2D copy from pinned staging before each launch.
+// per-token value (token id, position, angles) lives in device memory,
+// refreshed by one H2D copy from pinned staging before each launch.
 #include <hip/hip_runtime.h>
+#include <math.h>
 
 #include <cstring>
 #include <new>
@@ -23,6 +28,13 @@
 #include <vector>
 
 #include "sapient_hip_engine.h"
+
+// The fused RoPE + KV append with caller-evaluated angles (rope.hip; not exported).
+extern "C" int sph_rope_kv_append_angles(void* q, int64_t n_q_heads, const void* k, const void* v, int64_t n_kv_heads,
+                                         int dtype, int layout, const int32_t* positions, const float* angles,
+                                         int64_t seq, int64_t head_dim, void* kcache, void* vcache, int cache_dtype,
+                                         int64_t max_seq, const void* bq, const void* bk, const void* bv,
+                                         int bias_dtype, int32_t* bad_pos_flag, void* stream);
 
 struct sph_engine {
     sph_engine_config cfg{};
@@ -40,14 +52,16 @@ struct sph_engine {
     float *x = nullptr, *h = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *qt = nullptr, *attn = nullptr,
           *attn_sm = nullptr, *o = nullptr, *gate = nullptr, *up = nullptr, *act = nullptr, *down = nullptr,
           *out = nullptr;
-    uint32_t* ids = nullptr;
-    int32_t* positions = nullptr;
+    // Per-call inputs of T tokens, packed from byte 0: ids[T], positions[T],
+    // then (T = 1) the step's angles, head_dim/2 (cos, sin) pairs. A device
+    // buffer and its pinned host staging copy, moved by one H2D copy.
+    uint8_t* inputs = nullptr;
     int32_t* flags = nullptr;  // [0] bad token id, [1] bad cache position (both checked on the host first)
     std::vector<void*> kcache, vcache;
+    std::vector<float> dens;  // base^(2i/head_dim), i < head_dim/2, from the host libm
 
-    uint32_t* staged_ids = nullptr;  // pinned
-    int32_t* staged_pos = nullptr;   // pinned
-    hipEvent_t staged = nullptr;     // the last H2D copy out of the staging buffers
+    uint8_t* staged = nullptr;  // pinned
+    hipEvent_t staged_done = nullptr;  // the last H2D copy out of the staging buffer
     bool staged_pending = false;
 
     int64_t cur = 0;
@@ -65,9 +79,8 @@ void release(sph_engine* e) {
     if (e->stream) (void)hipStreamSynchronize(e->stream);
     if (e->graph) (void)hipGraphExecDestroy(e->graph);
     for (auto& a : e->device_allocs) (void)hipFree(a.first);
-    if (e->staged_ids) (void)hipHostFree(e->staged_ids);
-    if (e->staged_pos) (void)hipHostFree(e->staged_pos);
-    if (e->staged) (void)hipEventDestroy(e->staged);
+    if (e->staged) (void)hipHostFree(e->staged);
+    if (e->staged_done) (void)hipEventDestroy(e->staged_done);
     if (e->stream) (void)hipStreamDestroy(e->stream);
 }
 
@@ -99,12 +112,17 @@ int proj(sph_engine* e, int layer, int which, const float* in, float* out, int64
         if (st_ != SPH_OK) return st_; \
     } while (0)
 
+const uint32_t* ids_of(const sph_engine* e) { return reinterpret_cast<const uint32_t*>(e->inputs); }
+int32_t* positions_of(const sph_engine* e, int64_t T) { return reinterpret_cast<int32_t*>(e->inputs + 4 * T); }
+const float* angles_of(const sph_engine* e) { return reinterpret_cast<const float*>(e->inputs + 8); }  // T = 1
+
 // Everything one forward call enqueues after its inputs are staged: T tokens
-// whose ids and positions are already in device memory.
+// whose ids and positions (and, for one token, angles) are in device memory.
 int body(sph_engine* e, int64_t T) {
     const sph_engine_config& c = e->cfg;
     hipStream_t s = e->stream;
-    SPH_TRY(sph_embed(e->embed, e->embed_dtype, e->vocab, c.hidden, e->ids, T, e->x, e->flags, s));
+    int32_t* positions = positions_of(e, T);
+    SPH_TRY(sph_embed(e->embed, e->embed_dtype, e->vocab, c.hidden, ids_of(e), T, e->x, e->flags, s));
     for (int l = 0; l < (int)c.n_layers; ++l) {
         const sph_engine_layer& L = e->layers[l];
         // attention block: h = rms_norm(x) (layer 0) or x += down; h = rms_norm(x)
@@ -121,18 +139,19 @@ int body(sph_engine* e, int64_t T) {
         // are read token-major and q is written heads-major to qt, the transposes fused.
         float* qh = e->q;
         if (T == 1) {
-            SPH_TRY(sph_rope_kv_append(e->q, c.n_heads, e->k, e->v, c.n_kv_heads, SPH_F32, c.rope_layout,
-                                       e->positions, T, c.head_dim, c.rope_theta, 1.0f, e->kcache[l], e->vcache[l],
-                                       c.kv_dtype, c.max_seq, L.bq, L.bk, L.bv, c.bias_dtype, e->flags + 1, s));
+            SPH_TRY(sph_rope_kv_append_angles(e->q, c.n_heads, e->k, e->v, c.n_kv_heads, SPH_F32, c.rope_layout,
+                                              positions, angles_of(e), T, c.head_dim, e->kcache[l], e->vcache[l],
+                                              c.kv_dtype, c.max_seq, L.bq, L.bk, L.bv, c.bias_dtype, e->flags + 1,
+                                              s));
         } else {
             qh = e->qt;
             SPH_TRY(sph_rope_kv_append_tokens(e->q, e->qt, c.n_heads, e->k, e->v, c.n_kv_heads, SPH_F32,
-                                              c.rope_layout, e->positions, T, c.head_dim, c.rope_theta, 1.0f,
+                                              c.rope_layout, positions, T, c.head_dim, c.rope_theta, 1.0f,
                                               e->kcache[l], e->vcache[l], c.kv_dtype, c.max_seq, L.bq, L.bk, L.bv,
                                               c.bias_dtype, e->flags + 1, s));
         }
         if (e->attend)
-            SPH_TRY(callback_status(e->attend(e->user, l, qh, e->kcache[l], e->vcache[l], c.kv_dtype, e->positions, T,
+            SPH_TRY(callback_status(e->attend(e->user, l, qh, e->kcache[l], e->vcache[l], c.kv_dtype, positions, T,
                                               c.max_seq, e->attn, s)));
         float* att = e->attn;
         if (T > 1) {
@@ -160,12 +179,25 @@ int stage(sph_engine* e, const uint32_t* toks, int64_t n) {
     if (e->cur + n > e->cfg.max_seq) return SPH_ERANGE;
     for (int64_t i = 0; i < n; ++i)
         if ((int64_t)toks[i] >= e->vocab) return SPH_ERANGE;
-    if (e->staged_pending && hipEventSynchronize(e->staged) != hipSuccess) return SPH_EHIP;
-    std::memcpy(e->staged_ids, toks, (size_t)n * 4);
-    for (int64_t i = 0; i < n; ++i) e->staged_pos[i] = (int32_t)(e->cur + i);
-    if (hipMemcpyAsync(e->ids, e->staged_ids, (size_t)n * 4, hipMemcpyHostToDevice, e->stream) != hipSuccess ||
-        hipMemcpyAsync(e->positions, e->staged_pos, (size_t)n * 4, hipMemcpyHostToDevice, e->stream) != hipSuccess ||
-        hipEventRecord(e->staged, e->stream) != hipSuccess)
+    if (e->staged_pending && hipEventSynchronize(e->staged_done) != hipSuccess) return SPH_EHIP;
+    std::memcpy(e->staged, toks, (size_t)n * 4);
+    int32_t* pos = reinterpret_cast<int32_t*>(e->staged + 4 * n);
+    for (int64_t i = 0; i < n; ++i) pos[i] = (int32_t)(e->cur + i);
+    size_t bytes = (size_t)n * 8;
+    if (n == 1) {
+        // The reference's angle: freq = (f32)pos / base^(2i/d), then sinf / cosf
+        // (rope.rs:48-57); pos_scale 1 divides exactly.
+        float* ang = reinterpret_cast<float*>(e->staged + 8);
+        const float p = (float)e->cur;
+        for (size_t i = 0; i < e->dens.size(); ++i) {
+            const float freq = p / e->dens[i];
+            ang[2 * i] = cosf(freq);
+            ang[2 * i + 1] = sinf(freq);
+        }
+        bytes += e->dens.size() * 8;
+    }
+    if (hipMemcpyAsync(e->inputs, e->staged, bytes, hipMemcpyHostToDevice, e->stream) != hipSuccess ||
+        hipEventRecord(e->staged_done, e->stream) != hipSuccess)
         return SPH_EHIP;
     e->staged_pending = true;
     return SPH_OK;
@@ -209,6 +241,8 @@ extern "C" int sph_engine_create(const sph_engine_config* cfg, const void* embed
     sph_engine* e = new (std::nothrow) sph_engine;
     if (!e) return SPH_EINVAL;
     e->cfg = c;
+    e->dens.resize((size_t)(c.head_dim / 2));
+    for (size_t i = 0; i < e->dens.size(); ++i) e->dens[i] = powf(c.rope_theta, 2.0f * (float)i / (float)c.head_dim);
     e->embed = embed_table;
     e->embed_dtype = embed_dtype;
     e->vocab = vocab;
@@ -222,17 +256,16 @@ extern "C" int sph_engine_create(const sph_engine_config* cfg, const void* embed
     const size_t qd = (size_t)(c.n_heads * c.head_dim), kd = (size_t)(c.n_kv_heads * c.head_dim);
     const size_t cache_bytes = (size_t)c.n_kv_heads * (size_t)c.max_seq * (size_t)c.head_dim * elem_size(c.kv_dtype);
     bool ok = hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking) == hipSuccess &&
-              hipEventCreateWithFlags(&e->staged, hipEventDisableTiming) == hipSuccess &&
-              hipHostMalloc((void**)&e->staged_ids, T * 4, hipHostMallocDefault) == hipSuccess &&
-              hipHostMalloc((void**)&e->staged_pos, T * 4, hipHostMallocDefault) == hipSuccess &&
+              hipEventCreateWithFlags(&e->staged_done, hipEventDisableTiming) == hipSuccess &&
+              hipHostMalloc((void**)&e->staged, T * 8 + (size_t)c.head_dim * 4, hipHostMallocDefault) == hipSuccess &&
               dalloc(e, &e->x, T * c.hidden * 4) && dalloc(e, &e->h, T * c.hidden * 4) && dalloc(e, &e->q, T * qd * 4) &&
               dalloc(e, &e->k, T * kd * 4) && dalloc(e, &e->v, T * kd * 4) && dalloc(e, &e->qt, T * qd * 4) &&
               dalloc(e, &e->attn, T * qd * 4) &&
               dalloc(e, &e->attn_sm, T * qd * 4) && dalloc(e, &e->o, T * c.hidden * 4) &&
               dalloc(e, &e->gate, T * c.intermediate * 4) && dalloc(e, &e->up, T * c.intermediate * 4) &&
               dalloc(e, &e->act, T * c.intermediate * 4) && dalloc(e, &e->down, T * c.hidden * 4) &&
-              dalloc(e, &e->out, (size_t)c.hidden * 4) && dalloc(e, &e->ids, T * 4) &&
-              dalloc(e, &e->positions, T * 4) && dalloc(e, &e->flags, 2 * 4);
+              dalloc(e, &e->out, (size_t)c.hidden * 4) && dalloc(e, &e->inputs, T * 8 + (size_t)c.head_dim * 4) &&
+              dalloc(e, &e->flags, 2 * 4);
     for (int64_t l = 0; ok && l < c.n_layers; ++l) {
         void *kc = nullptr, *vc = nullptr;
         ok = dalloc(e, &kc, cache_bytes) && dalloc(e, &vc, cache_bytes);
