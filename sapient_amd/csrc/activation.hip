@@ -52,6 +52,7 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kUnroll = 2;       // vectors in flight per operand per thread
 constexpr int64_t kMaxGrid = 65536;  // ~one loop trip per thread at the configuration sizes
+constexpr int64_t kFewVecs = 16384;  // up to 64 blocks of one vector per thread
 
 enum Op { OP_ADD = 0, OP_MUL = 1, OP_SILU = 2, OP_SWIGLU = 3, OP_GELU = 4, OP_GELU_ERF = 5 };
 
@@ -226,7 +227,13 @@ int launch_ew(const void* a, const void* b, void* out, int64_t n, hipStream_t st
     int64_t done = 0;
     if (vec_ok) {
         const int64_t nvec = n / E;
-        if (nvec > 0) {
+        if (nvec > 0 && nvec <= kFewVecs) {
+            // A small launch (a decode step): one vector per thread, so each
+            // thread's dependent chain is as short as it can be.
+            const int st = launch(ew_vec<T, OP, BC, 1>, grid_for(nvec, (int64_t)kThreads, kMaxGrid), kThreads, stream,
+                                  ap, bp, op, nvec);
+            if (st != SPH_OK) return st;
+        } else if (nvec > 0) {
             const int st = launch(ew_vec<T, OP, BC>, grid_for(nvec, (int64_t)kThreads * kUnroll, kMaxGrid), kThreads,
                                   stream, ap, bp, op, nvec);
             if (st != SPH_OK) return st;
