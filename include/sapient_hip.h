@@ -252,8 +252,10 @@ int sph_kv_append(const void* src, int src_dtype, void* cache, int cache_dtype, 
  * max_seq), the length of the view the reference returns. seq > max_seq
  * returns SPH_ERANGE (the reference's "new tokens exceeds max cache size"),
  * cur_len > max_seq SPH_EINVAL; nothing is written then. Types, conversion and
- * the Q8_0 layout are sph_kv_append's. At most two launches on `stream` (the
- * shift, then the append); the rows moved by the shift are copied bit for bit. */
+ * the Q8_0 layout are sph_kv_append's. At most three launches on `stream` (the
+ * shift as two in-place passes, then the append); the rows moved by the shift
+ * are copied bit for bit, and the shift's rows past cur_len - shift hold
+ * intermediate values until the append overwrites them. */
 int sph_kv_cache_update(const void* src, int src_dtype, void* cache, int cache_dtype, int64_t n_kv, int64_t seq,
                         int64_t head_dim, int64_t max_seq, int64_t cur_len, int64_t* new_len, void* stream);
 
