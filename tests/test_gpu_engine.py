@@ -12,7 +12,8 @@ and check, in order:
      between);
   2. every op of every layer on the engine's own inputs (the stand-ins record
      what each op received; the residual stream is rebuilt from the records
-     with the same f32 adds): the norms to 1e-5 relative, bias + RoPE, the
+     with the same f32 adds): the norms to 1e-5 relative, bias + RoPE (NEOX
+     and interleaved; a one-token step's angles come from the host), the
      KV-cache rows and SwiGLU bit for bit;
   3. the end-to-end hidden states and caches against the oracle's run of the
      whole reference sequence on its own values, where the norms' last-bit
@@ -222,7 +223,8 @@ def _rel_ok(got, want, what):
     assert np.all(err <= 1e-5 * np.abs(want)), f"{what}: max rel {float((err / np.maximum(np.abs(want), 1e-30)).max())}"
 
 
-def test_engine_each_op_on_its_own_inputs(dev, orc, model):
+@pytest.mark.parametrize("layout", [L.ROPE_NEOX, L.ROPE_INTERLEAVED], ids=["neox", "interleaved"])
+def test_engine_each_op_on_its_own_inputs(dev, orc, model, layout):
     """Teacher-forced parity: the callbacks record what each op received, the test rebuilds the
     residual stream x from those records with the same f32 adds (exact), and checks every op of every
     layer on the engine's own inputs — RMSNorm (input, post-attention, final) to 1e-5 relative,
@@ -234,8 +236,12 @@ def test_engine_each_op_on_its_own_inputs(dev, orc, model):
     fin = to_np(final)
     rec = _Recorder()
     t_, l_, f_ = model
-    cfg = L.EngineConfig(H, NQ, NKV, HD, INTER, LAYERS, MAX_SEQ, MAX_CHUNK, EPS, THETA, L.ROPE_NEOX, L.F16, L.F16)
+    cfg = L.EngineConfig(H, NQ, NKV, HD, INTER, LAYERS, MAX_SEQ, MAX_CHUNK, EPS, THETA, layout, L.F16, L.F16)
     eng = Engine(cfg, t_, L.F32, VOCAB, l_, f_, rec.project, rec.attend)
+    if layout == L.ROPE_NEOX:
+        rope = lambda x, pos: orc.apply_rope(x, pos, THETA)
+    else:  # interleaved pairs (the GGUF q/k layout), full rotary dimension
+        rope = lambda x, pos: orc.apply_rope_partial_scaled(x, pos, THETA, HD, 1.0, True)
     proj = lambda x, n_out: (0.5 * np.tile(x, (1, -(-n_out // x.shape[1])))[:, :n_out]).astype(np.float32)
     caches = [(np.zeros((NKV, MAX_SEQ, HD), np.uint16), np.zeros((NKV, MAX_SEQ, HD), np.uint16)) for _ in range(LAYERS)]
     steps = [PROMPT] + [[t] for t in DECODE]
@@ -249,7 +255,7 @@ def test_engine_each_op_on_its_own_inputs(dev, orc, model):
         got = {}
         for layer, which, t in rec.calls:
             got[(layer, which)] = to_np(t)
-        print(f"case engine teacher-forced step {si} T {T}", flush=True)
+        print(f"case engine teacher-forced layout {layout} step {si} T {T}", flush=True)
         x = orc.embed_tokens(tab.reshape(-1).view(np.uint8), L.F32, VOCAB, H, np.array(ids, np.uint32)).reshape(T, H)
         down = None
         for l in range(LAYERS):
@@ -260,8 +266,8 @@ def test_engine_each_op_on_its_own_inputs(dev, orc, model):
             q = orc.add_bias_last_dim(proj(h1, NQ * HD), lw[l]["bq"])
             k = orc.add_bias_last_dim(proj(got[(l, L.PROJ_K)], NKV * HD), lw[l]["bk"])
             v = orc.add_bias_last_dim(proj(got[(l, L.PROJ_V)], NKV * HD), lw[l]["bv"])
-            qr = orc.apply_rope(np.ascontiguousarray(q.reshape(T, NQ, HD).transpose(1, 0, 2)[None]), pos, THETA)[0]
-            kr = orc.apply_rope(np.ascontiguousarray(k.reshape(T, NKV, HD).transpose(1, 0, 2)[None]), pos, THETA)[0]
+            qr = rope(np.ascontiguousarray(q.reshape(T, NQ, HD).transpose(1, 0, 2)[None]), pos)[0]
+            kr = rope(np.ascontiguousarray(k.reshape(T, NKV, HD).transpose(1, 0, 2)[None]), pos)[0]
             assert np.array_equal(got[(l, "attend")].view(np.uint32), qr.view(np.uint32)), f"step {si} layer {l} rope q"
             orc.kv_append(kr, caches[l][0], L.F16, NKV, T, HD, MAX_SEQ, pos0)
             orc.kv_append(np.ascontiguousarray(v.reshape(T, NKV, HD).transpose(1, 0, 2)), caches[l][1], L.F16, NKV, T,
