@@ -240,42 +240,53 @@ extern "C" int sph_engine_create(const sph_engine_config* cfg, const void* embed
 
     sph_engine* e = new (std::nothrow) sph_engine;
     if (!e) return SPH_EINVAL;
-    e->cfg = c;
-    e->dens.resize((size_t)(c.head_dim / 2));
-    for (size_t i = 0; i < e->dens.size(); ++i) e->dens[i] = powf(c.rope_theta, 2.0f * (float)i / (float)c.head_dim);
-    e->embed = embed_table;
-    e->embed_dtype = embed_dtype;
-    e->vocab = vocab;
-    e->layers.assign(layers, layers + c.n_layers);
-    e->final_norm = final_norm;
-    e->project = project;
-    e->attend = attend;
-    e->user = user;
+    // The host-side vectors below may throw std::bad_alloc; nothing may unwind
+    // through the C ABI, so a failed allocation of any kind returns SPH_EHIP.
+    bool ok = false;
+    try {
+        e->cfg = c;
+        e->dens.resize((size_t)(c.head_dim / 2));
+        for (size_t i = 0; i < e->dens.size(); ++i)
+            e->dens[i] = powf(c.rope_theta, 2.0f * (float)i / (float)c.head_dim);
+        e->embed = embed_table;
+        e->embed_dtype = embed_dtype;
+        e->vocab = vocab;
+        e->layers.assign(layers, layers + c.n_layers);
+        e->final_norm = final_norm;
+        e->project = project;
+        e->attend = attend;
+        e->user = user;
 
-    const size_t T = (size_t)c.max_chunk;
-    const size_t qd = (size_t)(c.n_heads * c.head_dim), kd = (size_t)(c.n_kv_heads * c.head_dim);
-    const size_t cache_bytes = (size_t)c.n_kv_heads * (size_t)c.max_seq * (size_t)c.head_dim * elem_size(c.kv_dtype);
-    bool ok = hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking) == hipSuccess &&
-              hipEventCreateWithFlags(&e->staged_done, hipEventDisableTiming) == hipSuccess &&
-              hipHostMalloc((void**)&e->staged, T * 8 + (size_t)c.head_dim * 4, hipHostMallocDefault) == hipSuccess &&
-              dalloc(e, &e->x, T * c.hidden * 4) && dalloc(e, &e->h, T * c.hidden * 4) && dalloc(e, &e->q, T * qd * 4) &&
-              dalloc(e, &e->k, T * kd * 4) && dalloc(e, &e->v, T * kd * 4) && dalloc(e, &e->qt, T * qd * 4) &&
-              dalloc(e, &e->attn, T * qd * 4) &&
-              dalloc(e, &e->attn_sm, T * qd * 4) && dalloc(e, &e->o, T * c.hidden * 4) &&
-              dalloc(e, &e->gate, T * c.intermediate * 4) && dalloc(e, &e->up, T * c.intermediate * 4) &&
-              dalloc(e, &e->act, T * c.intermediate * 4) && dalloc(e, &e->down, T * c.hidden * 4) &&
-              dalloc(e, &e->out, (size_t)c.hidden * 4) && dalloc(e, &e->inputs, T * 8 + (size_t)c.head_dim * 4) &&
-              dalloc(e, &e->flags, 2 * 4);
-    for (int64_t l = 0; ok && l < c.n_layers; ++l) {
-        void *kc = nullptr, *vc = nullptr;
-        ok = dalloc(e, &kc, cache_bytes) && dalloc(e, &vc, cache_bytes);
-        e->kcache.push_back(kc);
-        e->vcache.push_back(vc);
+        const size_t T = (size_t)c.max_chunk;
+        const size_t qd = (size_t)(c.n_heads * c.head_dim), kd = (size_t)(c.n_kv_heads * c.head_dim);
+        const size_t cache_bytes =
+            (size_t)c.n_kv_heads * (size_t)c.max_seq * (size_t)c.head_dim * elem_size(c.kv_dtype);
+        ok = hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking) == hipSuccess &&
+                  hipEventCreateWithFlags(&e->staged_done, hipEventDisableTiming) == hipSuccess &&
+                  hipHostMalloc((void**)&e->staged, T * 8 + (size_t)c.head_dim * 4, hipHostMallocDefault) ==
+                      hipSuccess &&
+                  dalloc(e, &e->x, T * c.hidden * 4) && dalloc(e, &e->h, T * c.hidden * 4) &&
+                  dalloc(e, &e->q, T * qd * 4) &&
+                  dalloc(e, &e->k, T * kd * 4) && dalloc(e, &e->v, T * kd * 4) && dalloc(e, &e->qt, T * qd * 4) &&
+                  dalloc(e, &e->attn, T * qd * 4) &&
+                  dalloc(e, &e->attn_sm, T * qd * 4) && dalloc(e, &e->o, T * c.hidden * 4) &&
+                  dalloc(e, &e->gate, T * c.intermediate * 4) && dalloc(e, &e->up, T * c.intermediate * 4) &&
+                  dalloc(e, &e->act, T * c.intermediate * 4) && dalloc(e, &e->down, T * c.hidden * 4) &&
+                  dalloc(e, &e->out, (size_t)c.hidden * 4) && dalloc(e, &e->inputs, T * 8 + (size_t)c.head_dim * 4) &&
+                  dalloc(e, &e->flags, 2 * 4);
+        for (int64_t l = 0; ok && l < c.n_layers; ++l) {
+            void *kc = nullptr, *vc = nullptr;
+            ok = dalloc(e, &kc, cache_bytes) && dalloc(e, &vc, cache_bytes);
+            e->kcache.push_back(kc);
+            e->vcache.push_back(vc);
+        }
+        // Buffers a NULL callback leaves untouched start at zero, as do the caches.
+        for (size_t i = 0; ok && i < e->device_allocs.size(); ++i)
+            ok = hipMemsetAsync(e->device_allocs[i].first, 0, e->device_allocs[i].second, e->stream) == hipSuccess;
+        ok = ok && hipStreamSynchronize(e->stream) == hipSuccess;
+    } catch (...) {
+        ok = false;
     }
-    // Buffers a NULL callback leaves untouched start at zero, as do the caches.
-    for (size_t i = 0; ok && i < e->device_allocs.size(); ++i)
-        ok = hipMemsetAsync(e->device_allocs[i].first, 0, e->device_allocs[i].second, e->stream) == hipSuccess;
-    ok = ok && hipStreamSynchronize(e->stream) == hipSuccess;
     if (!ok) {
         release(e);
         delete e;
