@@ -208,10 +208,17 @@ int launch_reverse(void* cache, uint64_t n_heads, uint64_t row_bytes, uint64_t m
     const uint64_t upr = row_bytes / sizeof(UT);
     const uint64_t items = (hi - lo) / 2 * upr;
     if (items == 0) return SPH_OK;
-    if (items > UINT32_MAX - kThreads || upr > UINT32_MAX || n_heads > 65535) return SPH_EINVAL;
-    const dim3 grid((unsigned)((items + kThreads - 1) / kThreads), (unsigned)n_heads);
-    return launch(kv_reverse_rows<UT>, grid, kThreads, stream, static_cast<UT*>(cache), (uint32_t)upr, max_seq, lo,
-                  hi, (uint32_t)items);
+    if (items > UINT32_MAX - kThreads || upr > UINT32_MAX) return SPH_EINVAL;
+    constexpr uint64_t kMaxY = 65535;  // heads per launch (grid y)
+    for (uint64_t h0 = 0; h0 < n_heads; h0 += kMaxY) {
+        const uint64_t nh = n_heads - h0 < kMaxY ? n_heads - h0 : kMaxY;
+        const dim3 grid((unsigned)((items + kThreads - 1) / kThreads), (unsigned)nh);
+        const int st = launch(kv_reverse_rows<UT>, grid, kThreads, stream,
+                              static_cast<UT*>(cache) + h0 * max_seq * upr, (uint32_t)upr, max_seq, lo, hi,
+                              (uint32_t)items);
+        if (st != SPH_OK) return st;
+    }
+    return SPH_OK;
 }
 
 // The two passes, with the widest unit the row width and the cache's alignment allow.

@@ -35,6 +35,7 @@
 
 #include "glibc_sincosf.h"
 #include "sph_common.h"
+#include "sph_internal.h"
 
 namespace sph {
 namespace {
@@ -691,15 +692,12 @@ extern "C" int sph_rope_kv_append(void* q, int64_t n_q_heads, const void* k, con
                                      bad_pos_flag, stream);
 }
 
-// sph_rope_kv_append with the angles supplied: angles[2 (s·rotary_dim/2 + i)]
-// and [... + 1] hold cos and sin of positions[s] / pos_scale / base^(2i/head_dim),
-// evaluated by the caller with the libm the reference calls. For the decode
-// engine, which knows a step's position on the host; not exported.
-extern "C" __attribute__((visibility("hidden"))) int sph_rope_kv_append_angles(
-    void* q, int64_t n_q_heads, const void* k, const void* v, int64_t n_kv_heads, int dtype, int layout,
-    const int32_t* positions, const float* angles, int64_t seq, int64_t head_dim, void* kcache, void* vcache,
-    int cache_dtype, int64_t max_seq, const void* bq, const void* bk, const void* bv, int bias_dtype,
-    int32_t* bad_pos_flag, void* stream) {
+// Declared in sph_internal.h (not exported).
+extern "C" int sph_rope_kv_append_angles(void* q, int64_t n_q_heads, const void* k, const void* v, int64_t n_kv_heads,
+                                         int dtype, int layout, const int32_t* positions, const float* angles,
+                                         int64_t seq, int64_t head_dim, void* kcache, void* vcache, int cache_dtype,
+                                         int64_t max_seq, const void* bq, const void* bk, const void* bv,
+                                         int bias_dtype, int32_t* bad_pos_flag, void* stream) {
     if (angles == nullptr || !sph::aligned(angles, 8)) return SPH_EINVAL;
     return sph::rope_kv_entry<false>(q, q, n_q_heads, k, v, n_kv_heads, dtype, layout, positions, seq, head_dim, 1.0f,
                                      1.0f, kcache, vcache, cache_dtype, max_seq, bq, bk, bv, bias_dtype, bad_pos_flag,

@@ -28,13 +28,7 @@
 #include <vector>
 
 #include "sapient_hip_engine.h"
-
-// The fused RoPE + KV append with caller-evaluated angles (rope.hip; not exported).
-extern "C" int sph_rope_kv_append_angles(void* q, int64_t n_q_heads, const void* k, const void* v, int64_t n_kv_heads,
-                                         int dtype, int layout, const int32_t* positions, const float* angles,
-                                         int64_t seq, int64_t head_dim, void* kcache, void* vcache, int cache_dtype,
-                                         int64_t max_seq, const void* bq, const void* bk, const void* bv,
-                                         int bias_dtype, int32_t* bad_pos_flag, void* stream);
+#include "sph_internal.h"
 
 struct sph_engine {
     sph_engine_config cfg{};
