@@ -7,8 +7,9 @@
 //                    of [n_kv, max_seq, hd], converted to the cache type (:645-711)
 //
 // Both are moves of hd-element rows between two row orders, so one kernel
-// serves both: each thread moves one 16-byte access of the wider side (f32: 4
-// elements, halves: 8; an f32 → half move reads 16 B and writes 8 B),
+// serves both: each thread moves 16 bytes of the narrower side (f32: 4
+// elements, halves: 8; an f32 → half move reads two 16-byte words and writes
+// one; 16 bytes of the wider side when hd is not a multiple of 8),
 // non-temporal, with a per-row index map. The transpose walks 8 × 8 tiles of
 // (outer, inner) rows, so a block's reads cover 8 runs of 8 consecutive
 // source rows and its writes 8 runs of 8 consecutive output rows (measured at
@@ -60,14 +61,17 @@ __device__ __forceinline__ bool map_row(uint32_t row, const RowMap& m, uint64_t&
     return true;
 }
 
+// Elements per thread of the vector path: 16 bytes of the narrower side (an
+// f32 <-> half move reads or writes two 16-byte words, so both sides stay
+// 16 bytes wide), or, when hd is not a multiple of that, 16 bytes of the wider side.
 template <typename TS, typename TD>
 struct MoveWidth {
-    static constexpr int n = 16 / (int)(sizeof(TS) > sizeof(TD) ? sizeof(TS) : sizeof(TD));
+    static constexpr int wide = 16 / (int)(sizeof(TS) < sizeof(TD) ? sizeof(TS) : sizeof(TD));
+    static constexpr int narrow = 16 / (int)(sizeof(TS) > sizeof(TD) ? sizeof(TS) : sizeof(TD));
 };
 
-template <typename TS, typename TD>
+template <typename TS, typename TD, int E>
 __device__ __forceinline__ void move_chunk(const TS* s, TD* d) {
-    constexpr int E = MoveWidth<TS, TD>::n;
     if constexpr (std::is_same<TS, TD>::value) {
         vstore<true>(reinterpret_cast<u32x4*>(d), vload<true>(reinterpret_cast<const u32x4*>(s)));
     } else {
@@ -77,12 +81,11 @@ __device__ __forceinline__ void move_chunk(const TS* s, TD* d) {
     }
 }
 
-// Vector path: hd a multiple of the chunk width, both bases 16-byte aligned;
+// Vector path: hd a multiple of the chunk width E, both bases 16-byte aligned;
 // rows [row0, row0 + items / cpr) of this launch, cpr chunks per row.
-template <typename TS, typename TD, int MAP>
+template <typename TS, typename TD, int MAP, int E>
 __global__ __launch_bounds__(kThreads) void move_rows_vec(const TS* __restrict__ src, TD* __restrict__ dst,
                                                           uint32_t items, uint32_t cpr, uint32_t row0, RowMap m) {
-    constexpr int E = MoveWidth<TS, TD>::n;
     const uint32_t k = blockIdx.x * kThreads + threadIdx.x;
     if (k >= items) return;
     const uint32_t r = k / cpr;
@@ -90,7 +93,7 @@ __global__ __launch_bounds__(kThreads) void move_rows_vec(const TS* __restrict__
     uint64_t srow, drow;
     if (!map_row<MAP>(row0 + r, m, srow, drow)) return;
     const uint64_t hd = (uint64_t)cpr * E;
-    move_chunk(src + srow * hd + c, dst + drow * hd + c);
+    move_chunk<TS, TD, E>(src + srow * hd + c, dst + drow * hd + c);
 }
 
 // Any hd / alignment: one element per thread.
@@ -112,11 +115,12 @@ template <typename TS, typename TD, int MAP>
 int launch_move(const void* src, void* dst, uint64_t rows, uint64_t hd, RowMap m, hipStream_t stream) {
     if (rows == 0 || hd == 0) return SPH_OK;
     if (hd > (1u << 24) || rows > UINT32_MAX) return SPH_EINVAL;
-    constexpr int E = MoveWidth<TS, TD>::n;
+    constexpr int EW = MoveWidth<TS, TD>::wide, EN = MoveWidth<TS, TD>::narrow;
     const TS* s = static_cast<const TS*>(src);
     TD* d = static_cast<TD*>(dst);
-    const bool vec = hd % E == 0 && aligned(src, 16) && aligned(dst, 16);
-    const uint64_t per_row = vec ? hd / E : hd;  // work items per row
+    const bool al = aligned(src, 16) && aligned(dst, 16);
+    const int E = !al ? 0 : hd % EW == 0 ? EW : hd % EN == 0 ? EN : 0;  // 0: scalar path
+    const uint64_t per_row = E ? hd / E : hd;  // work items per row
     // Each launch covers whole rows (whole tiles for the transpose) and fewer than 2^31 work items.
     uint64_t rows_per_launch = ((uint64_t)1 << 31) / per_row;
     if (MAP == M_TRANSPOSE) rows_per_launch -= rows_per_launch % (kTile * kTile);
@@ -124,10 +128,12 @@ int launch_move(const void* src, void* dst, uint64_t rows, uint64_t hd, RowMap m
         const uint64_t nr = rows - r0 < rows_per_launch ? rows - r0 : rows_per_launch;
         const uint32_t items = (uint32_t)(nr * per_row);
         const dim3 grid((items + kThreads - 1) / kThreads);
-        const int st = vec ? launch(move_rows_vec<TS, TD, MAP>, grid, kThreads, stream, s, d, items, (uint32_t)per_row,
-                                    (uint32_t)r0, m)
-                           : launch(move_rows_scalar<TS, TD, MAP>, grid, kThreads, stream, s, d, items, (uint32_t)hd,
-                                    (uint32_t)r0, m);
+        const int st = E == EW ? launch(move_rows_vec<TS, TD, MAP, EW>, grid, kThreads, stream, s, d, items,
+                                        (uint32_t)per_row, (uint32_t)r0, m)
+                     : E == EN ? launch(move_rows_vec<TS, TD, MAP, EN>, grid, kThreads, stream, s, d, items,
+                                        (uint32_t)per_row, (uint32_t)r0, m)
+                               : launch(move_rows_scalar<TS, TD, MAP>, grid, kThreads, stream, s, d, items,
+                                        (uint32_t)hd, (uint32_t)r0, m);
         if (st != SPH_OK) return st;
     }
     return SPH_OK;

@@ -92,12 +92,13 @@ def test_kv_append_matches_wgpu_test_sequence(dev, orc, cdtype):
     _same(cache, ref, f"kv cache {cdtype}")
 
 
-# Every (source, cache) dtype pair at the small shapes; the large prefill runs f32 sources into every
-# cache type and half sources into f16.
+# Every (source, cache) dtype pair at the small shapes (an f32 <-> half pair moves 8 elements per thread
+# at hd 64 and 128, 4 at hd 12; hd 6 and 1 take the one-element path); the large prefill runs f32 sources
+# into every cache type and half sources into f16.
 _KV_CASES = [pytest.param(sd, cd, *shape, id=f"{IDS(sd)}-{IDS(cd)}-{'x'.join(map(str, shape))}")
              for sd in DTYPES for cd in DTYPES
-             for shape in [(8, 8192, 128, 8192, 0), (8, 1, 128, 8192, 8191), (2, 5, 64, 40, 17), (3, 4, 6, 10, 6),
-                           (1, 1, 1, 1, 0)]
+             for shape in [(8, 8192, 128, 8192, 0), (8, 1, 128, 8192, 8191), (2, 5, 64, 40, 17), (2, 3, 12, 9, 2),
+                           (3, 4, 6, 10, 6), (1, 1, 1, 1, 0)]
              if not (shape[1] == 8192 and sd != torch.float32 and cd != torch.float16)]
 
 
