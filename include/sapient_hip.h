@@ -251,8 +251,9 @@ int sph_kv_append(const void* src, int src_dtype, void* cache, int cache_dtype, 
  * lands at cur_len - shift. *new_len (host int64) receives min(cur_len + seq,
  * max_seq), the length of the view the reference returns. seq > max_seq
  * returns SPH_ERANGE (the reference's "new tokens exceeds max cache size"),
- * cur_len > max_seq SPH_EINVAL; nothing is written then. Types, conversion and
- * the Q8_0 layout are sph_kv_append's. At most three launches on `stream` (the
+ * cur_len > max_seq SPH_EINVAL; nothing is written then, nor when the append
+ * itself would be rejected (its checks run before the shift). Types,
+ * conversion and the Q8_0 layout are sph_kv_append's. At most three launches on `stream` (the
  * shift as two in-place passes, then the append); the rows moved by the shift
  * are copied bit for bit, and the shift's rows past cur_len - shift hold
  * intermediate values until the append overwrites them. */

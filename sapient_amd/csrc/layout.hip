@@ -256,8 +256,13 @@ extern "C" int sph_transpose_heads(const void* x, void* out, int dtype, int64_t 
     return sph::launch_move<sph::f16, sph::f16, sph::M_TRANSPOSE>(x, out, walk, head_dim, m, s);
 }
 
-extern "C" int sph_kv_append(const void* src, int src_dtype, void* cache, int cache_dtype, int64_t n_kv, int64_t seq,
-                             int64_t head_dim, int64_t max_seq, int64_t pos, void* stream) {
+namespace {
+
+// Every argument check of sph_kv_append: SPH_OK when the append would launch (or
+// has nothing to do), else the error it returns. sph_kv_cache_update runs it
+// before shifting, so a rejected call leaves the cache untouched.
+int kv_append_check(const void* src, int src_dtype, const void* cache, int cache_dtype, int64_t n_kv, int64_t seq,
+                    int64_t head_dim, int64_t max_seq, int64_t pos) {
     if (n_kv < 0 || seq < 0 || head_dim < 0 || max_seq < 0 || pos < 0) return SPH_EINVAL;
     const bool q8 = cache_dtype == SPH_Q8_0;
     if (!sph::is_float_dtype(src_dtype) || !(q8 || sph::is_float_dtype(cache_dtype))) return SPH_EINVAL;
@@ -267,16 +272,32 @@ extern "C" int sph_kv_append(const void* src, int src_dtype, void* cache, int ca
     if (rows == 0 || head_dim == 0) return SPH_OK;
     if (src == nullptr || cache == nullptr) return SPH_EINVAL;
     if (seq > UINT32_MAX || max_seq > UINT32_MAX) return SPH_EINVAL;
-    hipStream_t s = static_cast<hipStream_t>(stream);
     if (q8) {
         if (!sph::aligned(cache, 2) || !sph::aligned(src, 16) || head_dim / 32 > UINT32_MAX) return SPH_EINVAL;
+        const uint64_t blocks = rows * ((uint64_t)head_dim / 32);
+        if ((blocks + sph::kThreads - 1) / sph::kThreads > INT32_MAX) return SPH_EINVAL;
+    } else if ((uint64_t)head_dim > (1u << 24) || rows > UINT32_MAX) {
+        return SPH_EINVAL;  // launch_move's limits
+    }
+    return SPH_OK;
+}
+
+}  // namespace
+
+extern "C" int sph_kv_append(const void* src, int src_dtype, void* cache, int cache_dtype, int64_t n_kv, int64_t seq,
+                             int64_t head_dim, int64_t max_seq, int64_t pos, void* stream) {
+    const int chk = kv_append_check(src, src_dtype, cache, cache_dtype, n_kv, seq, head_dim, max_seq, pos);
+    if (chk != SPH_OK) return chk;
+    const bool q8 = cache_dtype == SPH_Q8_0;
+    const uint64_t rows = (uint64_t)n_kv * (uint64_t)seq;
+    if (rows == 0 || head_dim == 0) return SPH_OK;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (q8) {
         const uint64_t bpr = (uint64_t)head_dim / 32;
         const uint64_t blocks = rows * bpr;
         return sph::with_float_type(src_dtype, [&](auto ts) -> int {
             using TS = decltype(ts);
-            const uint64_t nblk = (blocks + sph::kThreads - 1) / sph::kThreads;
-            if (nblk > INT32_MAX) return SPH_EINVAL;
-            const dim3 grid((unsigned)nblk);
+            const dim3 grid((unsigned)((blocks + sph::kThreads - 1) / sph::kThreads));
             return sph::launch(sph::kv_append_q8_0<TS>, grid, sph::kThreads, s, static_cast<const TS*>(src),
                                static_cast<uint8_t*>(cache), blocks, (uint32_t)bpr, (uint32_t)seq, (uint32_t)max_seq,
                                (uint64_t)pos);
@@ -304,6 +325,8 @@ extern "C" int sph_kv_cache_update(const void* src, int src_dtype, void* cache, 
     const int64_t total = cur_len + seq;
     const int64_t shift = total > max_seq ? total - max_seq : 0;
     const int64_t keep = cur_len - shift;
+    const int chk = kv_append_check(src, src_dtype, cache, cache_dtype, n_kv, seq, head_dim, max_seq, keep);
+    if (chk != SPH_OK) return chk;
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (shift > 0 && keep > 0 && n_kv > 0 && head_dim > 0) {
         if (cache == nullptr) return SPH_EINVAL;

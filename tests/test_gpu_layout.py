@@ -229,7 +229,7 @@ def test_kv_cache_update_decode_sequence(dev, orc):
 def test_kv_cache_update_rejects_bad_arguments(dev):
     from sapient_amd._lib import EINVAL, ERANGE, lib
     import ctypes
-    cache = torch.zeros(2, 8, 16, device=dev)
+    cache = torch.arange(2 * 8 * 16, device=dev, dtype=torch.float32).reshape(2, 8, 16)
     before = cache.clone()
     src = torch.ones(2, 9, 16, device=dev)
     n = ctypes.c_int64(-7)
@@ -239,5 +239,11 @@ def test_kv_cache_update_rejects_bad_arguments(dev):
     assert L.sph_kv_cache_update(src.data_ptr(), 0, cache.data_ptr(), 0, 2, 1, 16, 8, 9, ctypes.addressof(n), s) == EINVAL
     assert L.sph_kv_cache_update(src.data_ptr(), 0, cache.data_ptr(), 0, 2, 1, 16, 8, 2, None, s) == EINVAL
     assert L.sph_kv_cache_update(src.data_ptr(), 0, cache.data_ptr(), 0, 2, 1, 16, 8, -1, ctypes.addressof(n), s) == EINVAL
+    # A full cache whose append would be rejected: the window must not slide either.
+    assert L.sph_kv_cache_update(None, 0, cache.data_ptr(), 0, 2, 1, 16, 8, 8, ctypes.addressof(n), s) == EINVAL
+    q8 = (torch.arange(2 * 8 * 34, device=dev) % 251).to(torch.uint8).reshape(2, 8, 34)
+    q8_before = q8.clone()
+    raw = torch.ones(2 * 32 + 4, device=dev)
+    assert L.sph_kv_cache_update(raw.data_ptr() + 4, 0, q8.data_ptr(), 8, 2, 1, 32, 8, 8, ctypes.addressof(n), s) == EINVAL
     torch.cuda.synchronize()
-    assert n.value == -7 and torch.equal(cache, before)
+    assert n.value == -7 and torch.equal(cache, before) and torch.equal(q8, q8_before)
