@@ -38,18 +38,14 @@ constexpr int kWave = 64;
 enum Kind { K_RMS = 0, K_ADD_RMS = 1, K_LAYER = 2 };
 
 // y for one element: RMSNorm (r·inv)·w; LayerNorm (d·inv)·w + b, where the
-// caller passes the centred value d = r − mean for LayerNorm.
+// caller passes the centred value d = r − mean for LayerNorm. An absent weight
+// is passed as 1 and an absent bias as −0: x·1 and x + (−0) are x exactly
+// (signed zeros included, where + (+0) would turn −0 into +0), so one
+// branch-free expression gives each of the reference's four forms bit for bit.
 template <int KIND>
-__device__ __forceinline__ float norm_out(float r, float inv, float w, float b, bool has_w, bool has_b) {
-    if constexpr (KIND == K_LAYER) {
-        const float normed = r * inv;
-        if (has_w && has_b) return normed * w + b;
-        if (has_w) return normed * w;
-        if (has_b) return normed + b;
-        return normed;
-    } else {
-        return (r * inv) * w;  // w = 1 when absent: (r·inv)·1 is r·inv exactly
-    }
+__device__ __forceinline__ float norm_out(float r, float inv, float w, float b) {
+    if constexpr (KIND == K_LAYER) return (r * inv) * w + b;
+    else return (r * inv) * w;
 }
 
 // Sum of one value per wave of a row: the W partials meet in LDS and every
@@ -117,7 +113,7 @@ __global__ __launch_bounds__(W >= 4 ? 64 * W : 256) void rms_rows_vec(const TX* 
             load_f32<TW, E>(bias + (size_t)v * E, bj);
         } else {
 #pragma unroll
-            for (int e = 0; e < E; ++e) bj[e] = 0.0f;
+            for (int e = 0; e < E; ++e) bj[e] = -0.0f;
         }
     };
     auto fetch = [&](int64_t row, u32x4 (&vx)[VPT], u32x4 (&vres)[VPT]) {
@@ -204,7 +200,7 @@ __global__ __launch_bounds__(W >= 4 ? 64 * W : 256) void rms_rows_vec(const TX* 
                 }
                 float y[E];
 #pragma unroll
-                for (int e = 0; e < E; ++e) y[e] = norm_out<KIND>(r[j][e], inv, wj[e], bj[e], has_w, has_b);
+                for (int e = 0; e < E; ++e) y[e] = norm_out<KIND>(r[j][e], inv, wj[e], bj[e]);
                 store_f32<TO, E, true>(out + base + (size_t)v * E, y);
             }
         }
@@ -279,8 +275,8 @@ __global__ __launch_bounds__(256) void rms_rows_generic(const TX* __restrict__ x
         const float r = value(i);
         if constexpr (KIND == K_ADD_RMS) residual[base + i] = narrow<TX>(r);
         const float wv_ = has_w ? widen(w[i]) : 1.0f;
-        const float bv = (KIND == K_LAYER && has_b) ? widen(bias[i]) : 0.0f;
-        out[base + i] = narrow<TO>(norm_out<KIND>(KIND == K_LAYER ? r - mean : r, inv, wv_, bv, has_w, has_b));
+        const float bv = (KIND == K_LAYER && has_b) ? widen(bias[i]) : -0.0f;
+        out[base + i] = narrow<TO>(norm_out<KIND>(KIND == K_LAYER ? r - mean : r, inv, wv_, bv));
     }
 }
 

@@ -124,6 +124,36 @@ def test_layer_norm_full(dev, orc, dtype, rows, dim):
     _check(out, ref, x32, to_np(w), to_np(b), orc, f"layer_norm full {dtype}")
 
 
+@pytest.mark.parametrize("dtype", DTYPES, ids=IDS)
+@pytest.mark.parametrize("dim", [4096, 100, 64, 4])
+@pytest.mark.parametrize("mode", ["none", "w", "b", "wb"])
+def test_layer_norm_signed_zero_bit_exact(dev, orc, dtype, dim, mode):
+    """Rows of (k, -k) pairs (k = 1, 2, 3), one -0 and one +0, shuffled: every sum the kernel forms is an
+    exact integer in any order, so its mean (+0), variance and outputs equal the oracle's bit for bit. The
+    -0 element centres to -0 - (+0) = -0, and without a bias the reference writes -0·w
+    (layernorm.rs:17-69): an absent bias enters the kernel as -0, the identity of +, which keeps that
+    sign (+0 would not). Weights of both signs; 4096 takes the row-looping shape, 100 (halves) the
+    one-element kernel."""
+    rng = np.random.default_rng(dim * 8 + len(mode))
+    pairs = [np.float32(1 + i % 3) for i in range((dim - 2) // 2)]
+    proto = np.array([v for k in pairs for v in (k, -k)] + [-0.0, 0.0], np.float32)
+    x32 = np.stack([rng.permutation(proto) for _ in range(3)]).astype(np.float32)
+    x = torch.from_numpy(x32).to(dev).to(dtype)
+    w = torch.from_numpy(rng.normal(0.0, 1.0, dim).astype(np.float32)).to(dev).to(dtype) if "w" in mode else None
+    b = torch.from_numpy(rng.normal(0.0, 0.2, dim).astype(np.float32)).to(dev).to(dtype) if "b" in mode else None
+    print(f"case layer_norm signed zero {dtype} 3x{dim} {mode}", flush=True)
+    out = ops.layer_norm(x, w, b, 1e-5)
+    ref = orc.layer_norm(widen(x, orc), None if w is None else widen(w, orc), None if b is None else widen(b, orc), 1e-5)
+    if dtype == torch.float32:
+        got, want = to_np(out).view(np.uint32), ref.view(np.uint32)
+    else:
+        got, want = to_np(out), narrow_bits(ref, dtype, orc)
+    assert np.array_equal(got, want), f"{int((got != want).sum())} of {got.size} outputs differ in bits"
+    if mode == "none":
+        neg0 = np.signbit(x32) & (x32 == 0)
+        assert np.all(np.signbit(ref[neg0])) and np.all(ref[neg0] == 0)
+
+
 def test_layer_norm_unit_property(dev):
     """Size-independent check at the full shape: with no weight / bias and eps = 0
     every output row has mean 0 and variance 1 (to f32 rounding)."""
