@@ -157,27 +157,32 @@ __global__ __launch_bounds__(kThreads) void rope_kernel(T* q, int nq, T* k, int 
     // This lane's row in head 0 of q and of k; heads lie seq · head_dim
     // elements apart, so a head's row is the lane's base plus a block-uniform
     // offset (scalar arithmetic and one 64-bit add per head, instead of the
-    // full per-lane index), computed once per head for its load and its store.
+    // full per-lane index). The store recomputes it from the head index rather
+    // than carrying the load's pointer across the loop: a carried pointer lost
+    // its global address space and the half-type stores compiled to flat
+    // stores (also counted by the LDS counter the angle reads wait on; the
+    // loop-top wait for the next batch already drains every store, so the
+    // time measured the same either way).
     const size_t hs = (size_t)seq * (size_t)head_dim;
     T* const qb = q + ((size_t)b * (size_t)nq * (size_t)seq + (size_t)s) * (size_t)head_dim;
     T* const kb = nk > 0 ? k + ((size_t)b * (size_t)nk * (size_t)seq + (size_t)s) * (size_t)head_dim : qb;
     auto row_of = [&](int hh) -> T* { return hh < nq ? qb + (size_t)hh * hs : kb + (size_t)(hh - nq) * hs; };
-    auto load_batch = [&](int h0, RawRun<T, L, ELEM> (&buf)[U][R], T* (&rows)[U]) {
+    auto load_batch = [&](int h0, RawRun<T, L, ELEM> (&buf)[U][R]) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             if (h0 + u < h_end) {
-                rows[u] = row_of(h0 + u);
+                const T* row = row_of(h0 + u);
 #pragma unroll
-                for (int r = 0; r < R; ++r) buf[u][r].load(rows[u] + off[r]);
+                for (int r = 0; r < R; ++r) buf[u][r].load(row + off[r]);
             }
         }
     };
-    auto rotate_batch = [&](int h0, const RawRun<T, L, ELEM> (&buf)[U][R], T* const (&rows)[U],
-                            const float (&cs)[NA], const float (&sn)[NA]) {
+    auto rotate_batch = [&](int h0, const RawRun<T, L, ELEM> (&buf)[U][R], const float (&cs)[NA],
+                            const float (&sn)[NA]) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             if (h0 + u < h_end) {
-                T* row = rows[u];
+                T* row = row_of(h0 + u);
                 if constexpr (!INTERLEAVED) {
                     float x0[P], x1[P], o0[P], o1[P];
                     buf[u][0].to_f32(x0);
@@ -210,14 +215,12 @@ __global__ __launch_bounds__(kThreads) void rope_kernel(T* q, int nq, T* k, int 
     // waits for it alone while the first two batches stay in flight.
     float cs[NA], sn[NA];
     RawRun<T, L, ELEM> ba[U][R], bb[U][R];
-    T* ra[U];
-    T* rb[U];
     if constexpr (PAIR_MAJOR) {
         int32_t pv = 0;
         if (tid < toks_per_block && t_first + tid < ntok) pv = pos[(t_first + tid) % seq];
         if (active) {
-            load_batch(h_begin, ba, ra);
-            load_batch(h_begin + U, bb, rb);
+            load_batch(h_begin, ba);
+            load_batch(h_begin + U, bb);
         }
         if (tid < toks_per_block) pos_s[tid] = pv;
         if (tid < 24) inv_pio4[tid] = kInvPio4.w[tid];
@@ -250,8 +253,8 @@ __global__ __launch_bounds__(kThreads) void rope_kernel(T* q, int nq, T* k, int 
         int32_t ps = 0;
         if (active) {
             ps = pos[s];
-            load_batch(h_begin, ba, ra);
-            load_batch(h_begin + U, bb, rb);
+            load_batch(h_begin, ba);
+            load_batch(h_begin + U, bb);
         }
         if (tid < 24) inv_pio4[tid] = kInvPio4.w[tid];
         __syncthreads();
@@ -267,11 +270,11 @@ __global__ __launch_bounds__(kThreads) void rope_kernel(T* q, int nq, T* k, int 
     // Two batches alternate: while one is rotated and stored, the other's
     // loads are in flight.
     for (int h0 = h_begin; h0 < h_end; h0 += 2 * U) {
-        rotate_batch(h0, ba, ra, cs, sn);
-        if (h0 + 2 * U < h_end) load_batch(h0 + 2 * U, ba, ra);
+        rotate_batch(h0, ba, cs, sn);
+        if (h0 + 2 * U < h_end) load_batch(h0 + 2 * U, ba);
         if (h0 + U >= h_end) break;
-        rotate_batch(h0 + U, bb, rb, cs, sn);
-        if (h0 + 3 * U < h_end) load_batch(h0 + 3 * U, bb, rb);
+        rotate_batch(h0 + U, bb, cs, sn);
+        if (h0 + 3 * U < h_end) load_batch(h0 + 3 * U, bb);
     }
 }
 
