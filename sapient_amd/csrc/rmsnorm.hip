@@ -244,6 +244,7 @@ __global__ __launch_bounds__(256) void rms_rows_generic(const TX* __restrict__ x
     __shared__ float partial[2][256 / kWave];
     const int lane = threadIdx.x & (kWave - 1), wv = threadIdx.x / kWave;
     const int64_t row = blockIdx.x;
+    if (row >= rows) return;  // the grid is one block per row; block-uniform, before any barrier
     const size_t base = (size_t)row * (size_t)dim;
     auto value = [&](int64_t i) {
         float r = widen(x[base + i]);
