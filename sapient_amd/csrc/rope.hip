@@ -105,9 +105,15 @@ __device__ __forceinline__ void store_run(T* p, const float (&v)[L]) {
 //    and i0 + half/2 .. i0 + half/2 + P — two requests per head like NEOX,
 //    which streams faster than one request of twice the size (f32 at the
 //    Llama-3-8B shape: 61.2 µs with one 16-byte run per thread, 58.0 µs split).
-// NA = the distinct angles a thread applies (P, or 2P when SPLIT). Two
-// batches of U heads are requested before the angles are computed, and from
-// then on one batch is in flight while the other is rotated and stored.
+// NA = the distinct angles a thread applies (P, or 2P when SPLIT). kPre
+// batches of U heads are requested before the angles are computed, so the
+// angle phase overlaps their loads; from then on one batch is in flight while
+// the other is rotated and stored. The half types request four (eight heads:
+// f16 at the Llama-3-8B shape, NEOX 30.2 -> 28.4 us, interleaved 30.0 ->
+// 28.4, the speed of the same access pattern with no arithmetic at all;
+// three: 29.5 / 29.0; five need more than 64 VGPRs, lose half the resident
+// waves and run at 33.2). In steady state two stay best: more requests in
+// flight per wave slowed every stream measured on this GPU.
 //
 // PAIR_MAJOR: angles are computed pair-major over the block (slot j of
 // thread x takes angle j·blockDim + x of the [pair][token] order), not per
@@ -214,13 +220,14 @@ __global__ __launch_bounds__(kThreads) void rope_kernel(T* q, int nq, T* k, int 
     // The position load goes first: loads complete in order, so staging it
     // waits for it alone while the first two batches stay in flight.
     float cs[NA], sn[NA];
-    RawRun<T, L, ELEM> ba[U][R], bb[U][R];
+    constexpr int kPre = (PAIR_MAJOR && sizeof(T) == 2) ? 4 : 2;  // batches requested before the angles
+    RawRun<T, L, ELEM> bufs[kPre][U][R];
     if constexpr (PAIR_MAJOR) {
         int32_t pv = 0;
         if (tid < toks_per_block && t_first + tid < ntok) pv = pos[(t_first + tid) % seq];
         if (active) {
-            load_batch(h_begin, ba);
-            load_batch(h_begin + U, bb);
+#pragma unroll
+            for (int p = 0; p < kPre; ++p) load_batch(h_begin + p * U, bufs[p]);
         }
         if (tid < toks_per_block) pos_s[tid] = pv;
         if (tid < 24) inv_pio4[tid] = kInvPio4.w[tid];
@@ -253,8 +260,8 @@ __global__ __launch_bounds__(kThreads) void rope_kernel(T* q, int nq, T* k, int 
         int32_t ps = 0;
         if (active) {
             ps = pos[s];
-            load_batch(h_begin, ba);
-            load_batch(h_begin + U, bb);
+            load_batch(h_begin, bufs[0]);
+            load_batch(h_begin + U, bufs[1]);
         }
         if (tid < 24) inv_pio4[tid] = kInvPio4.w[tid];
         __syncthreads();
@@ -267,14 +274,26 @@ __global__ __launch_bounds__(kThreads) void rope_kernel(T* q, int nq, T* k, int 
         }
     }
 
+    // The batches requested before the angles, in order; the first two are
+    // refilled with the next two batches (load_batch and rotate_batch skip
+    // heads past the group's end).
+    int h_loop = h_begin;
+    if constexpr (kPre > 2) {
+#pragma unroll
+        for (int p = 0; p < kPre; ++p) {
+            rotate_batch(h_begin + p * U, bufs[p], cs, sn);
+            if (p < 2) load_batch(h_begin + (kPre + p) * U, bufs[p]);
+        }
+        h_loop = h_begin + kPre * U;
+    }
     // Two batches alternate: while one is rotated and stored, the other's
     // loads are in flight.
-    for (int h0 = h_begin; h0 < h_end; h0 += 2 * U) {
-        rotate_batch(h0, ba, cs, sn);
-        if (h0 + 2 * U < h_end) load_batch(h0 + 2 * U, ba);
+    for (int h0 = h_loop; h0 < h_end; h0 += 2 * U) {
+        rotate_batch(h0, bufs[0], cs, sn);
+        if (h0 + 2 * U < h_end) load_batch(h0 + 2 * U, bufs[0]);
         if (h0 + U >= h_end) break;
-        rotate_batch(h0 + U, bb, cs, sn);
-        if (h0 + 3 * U < h_end) load_batch(h0 + 3 * U, bb);
+        rotate_batch(h0 + U, bufs[1], cs, sn);
+        if (h0 + 3 * U < h_end) load_batch(h0 + 3 * U, bufs[1]);
     }
 }
 
@@ -450,7 +469,8 @@ __global__ __launch_bounds__(kThreads) void rope_kv_kernel(const T* q, T* qo, in
 //    (two 8-byte runs), U = 2, pair-major angles, 2048 units in all (four
 //    head groups, each recomputing its angles: more waves in flight outweigh
 //    the repeated angle work). f16 NEOX 31.0 µs, interleaved 30.6 µs, copy
-//    30.2 µs. U = 4 cost 2–3 µs, P = 8 or one run of P = 4 0.3–4 µs.
+//    30.2 µs with two batches requested before the angles; four: 28.4 µs
+//    both. U = 4 cost 2–3 µs, P = 8 or one run of P = 4 0.3–4 µs.
 //  - f32: P = 4 NEOX, interleaved split with P = 2 (16-byte runs), U = 1,
 //    per-thread angles, 512 units (one group holds all 40 heads). NEOX
 //    57.5 µs, interleaved 58.0 µs (one 16-byte run: 61.2 µs), copy 56.3 µs.
