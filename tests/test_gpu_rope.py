@@ -124,6 +124,16 @@ def test_rope_llama3_8b_full(dev, orc, dtype, interleaved):
     _run(dev, orc, dtype, 1, 32, 8, 8192, 128, 128, 5e5, list(range(8192)), interleaved, seed=7)
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["float16", "bfloat16"])
+@pytest.mark.parametrize("interleaved", [False, True], ids=["neox", "interleaved"])
+def test_rope_head_groups_with_a_single_head_batch(dev, orc, dtype, interleaved):
+    """32 + 4 heads x 8192 tokens: the half-type kernel splits the 36 heads into four groups of 9, so
+    after the eight heads requested before the angle phase (four batches of two) a group ends with a
+    batch holding one head. Bit-exact like every other shape."""
+    print(f"case rope 9-head groups {dtype} il={interleaved}", flush=True)
+    _run(dev, orc, dtype, 1, 32, 4, 8192, 128, 128, 5e5, list(range(8192)), interleaved, seed=9)
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16], ids=lambda d: str(d).split(".")[-1])
 @pytest.mark.parametrize("interleaved", [False, True], ids=["neox", "interleaved"])
 @pytest.mark.parametrize("pos_scale", [1.0, 7.5, 2.0 ** -7, 3.0e-5, 2.0 ** -20, 1e-30])
