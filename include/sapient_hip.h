@@ -159,6 +159,38 @@ int sph_rope(void* q, int64_t n_q_heads, void* k, int64_t n_k_heads, int dtype, 
              const int32_t* positions, int64_t batch, int64_t seq, int64_t head_dim,
              int64_t rotary_dim, float base, float pos_scale, void* stream);
 
+/* sph_rope with the angles read from tables instead of evaluated on the device:
+ * cos_table / sin_table are device f32 [table_rows, rotary_dim / 2] (4-byte
+ * aligned), row r holding cos / sin of row r's angle for each pair — the
+ * layout of rope::rope_cos_sin_cache (crates/sapient-backends/cpu/src/kernels/rope.rs:140-153),
+ * which sph_rope_table fills on the host. Token s reads row positions[s]
+ * (device int32[seq]), or row s when `positions` is NULL (tables built for
+ * this call's positions; then table_rows >= seq, else SPH_ERANGE). A row
+ * outside [0, table_rows) leaves that token's channels unchanged and stores 1
+ * to `bad_pos_flag` (device int32, optional). Replaces
+ * LlmBackend::apply_rope_positions / apply_rope_partial / apply_rope_interleaved
+ * (crates/sapient-models/src/forward/backend.rs:84-97), whose positions are on
+ * the host (`positions: &[usize]`) and whose angles the reference evaluates
+ * with host libm (rope.rs:49-50, :123-125): with tables from sph_rope_table
+ * the result is sph_rope's, bit for bit, and the kernel evaluates no sin/cos.
+ * Other arguments and rules are sph_rope's (base and pos_scale are in the tables). */
+int sph_rope_cached(void* q, int64_t n_q_heads, void* k, int64_t n_k_heads, int dtype, int layout,
+                    const float* cos_table, const float* sin_table, int64_t table_rows,
+                    const int32_t* positions, int64_t batch, int64_t seq, int64_t head_dim,
+                    int64_t rotary_dim, int32_t* bad_pos_flag, void* stream);
+
+/* Host function (no device work): fill HOST arrays cos_out / sin_out
+ * [n, rotary_dim / 2] with the RoPE angles of n positions, row r for
+ * positions[r] (or r when `positions` is NULL): the reference's
+ *   freq = (pos as f32 / pos_scale) / base.powf(2i / rotary_dim)
+ * (rope.rs:48-50, :123-125) and its sin / cos, by the host libm the
+ * reference's f32::powf / f32::sin_cos call. positions NULL, rotary_dim =
+ * head_dim and pos_scale = 1 give rope::rope_cos_sin_cache(n, head_dim, base)
+ * (rope.rs:140-153). Negative positions, odd rotary_dim or pos_scale 0 / NaN:
+ * SPH_EINVAL. */
+int sph_rope_table(const int64_t* positions, int64_t n, int64_t rotary_dim, float base, float pos_scale,
+                   float* cos_out, float* sin_out);
+
 /* Decode-step fusion of RoPE and the KV-cache append: q [n_q_heads, seq,
  * head_dim] is rotated in place; k and v [n_kv_heads, seq, head_dim] are read
  * (not modified), and for each token s the rotated k row and the v row are
@@ -253,12 +285,35 @@ int sph_kv_append(const void* src, int src_dtype, void* cache, int cache_dtype, 
  * returns SPH_ERANGE (the reference's "new tokens exceeds max cache size"),
  * cur_len > max_seq SPH_EINVAL; nothing is written then, nor when the append
  * itself would be rejected (its checks run before the shift). Types,
- * conversion and the Q8_0 layout are sph_kv_append's. At most three launches on `stream` (the
- * shift as two in-place passes, then the append); the rows moved by the shift
- * are copied bit for bit, and the shift's rows past cur_len - shift hold
- * intermediate values until the append overwrites them. */
+ * conversion and the Q8_0 layout are sph_kv_append's. The shift runs as two
+ * in-place row-reversal passes (one launch each for n_kv <= 65535, more for
+ * larger n_kv) and the append as one launch (more past 2^31 work items); the
+ * rows moved by the shift are copied bit for bit, and the shift's rows past
+ * cur_len - shift hold intermediate values until the append overwrites them.
+ * The in-place shift moves every kept row twice; sph_kv_cache_update_into
+ * moves it once, into a second buffer. */
 int sph_kv_cache_update(const void* src, int src_dtype, void* cache, int cache_dtype, int64_t n_kv, int64_t seq,
                         int64_t head_dim, int64_t max_seq, int64_t cur_len, int64_t* new_len, void* stream);
+
+/* sph_kv_cache_update into a second, caller-owned cache: `out` (same layout
+ * and type as `cache`) receives the updated cache — rows [0, *new_len) of
+ * every head: the kept rows cache[shift .. cur_len), then src converted to
+ * the cache type — and `cache` is only read. Rows of `out` past *new_len are
+ * left as they were. Replaces common::update_kv_cache / update_kv_cache_q8
+ * (crates/sapient-models/src/forward/common.rs:355-434, :449-508) for a
+ * caller that then replaces its cache tensor with `out`, which the reference's
+ * signature allows: it takes the cache as `&mut Tensor` (:355-359, :449-455).
+ * Each kept row crosses HBM once each way, and a float cache
+ * whose rows split into 16-byte units (16-byte aligned buffers) takes a
+ * single launch for the move and the append; other rows take two (the
+ * move as raw units, then sph_kv_append). Results equal sph_kv_cache_update's
+ * rows [0, *new_len) bit for bit. When no row is dropped (cur_len + seq <=
+ * max_seq) this still copies the cur_len rows: such a step is cheaper in
+ * place. Arguments and errors are sph_kv_cache_update's; `out` must not
+ * overlap `cache` or `src` (SPH_EINVAL). */
+int sph_kv_cache_update_into(const void* src, int src_dtype, const void* cache, void* out, int cache_dtype,
+                             int64_t n_kv, int64_t seq, int64_t head_dim, int64_t max_seq, int64_t cur_len,
+                             int64_t* new_len, void* stream);
 
 #ifdef __cplusplus
 }

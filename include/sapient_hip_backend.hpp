@@ -169,13 +169,17 @@ class HipLlmBackend final : public LlmBackend {
 
     // common::update_kv_cache / update_kv_cache_q8 (crates/sapient-models/src/forward/common.rs:355-434,
     // :449-528), the trait path's cache update (llama.rs:489-490): new_k [b, h, new_seq, hd] (any float
-    // dtype) is appended after the current_seq_len valid rows of cache [b, h, max_seq, hd] (F32, F16,
-    // BF16, or Q8_0 blocks), sliding the window once the cache is full; the cache is updated in place
-    // and the live prefix is returned as F32 [b, h, min(current_seq_len + new_seq, max_seq), hd] (the
-    // view the F32 path returns, the dequantized copy the Q8_0 path returns). Errors as the reference's
+    // dtype) is appended after the current_seq_len valid rows of cache [b, h, max_seq, hd] (F32, or
+    // Q8_0 blocks), sliding the window once the cache is full; the cache's bytes are updated and the
+    // live prefix is returned as F32 [b, h, min(current_seq_len + new_seq, max_seq), hd] (the view the
+    // F32 path returns, the dequantized copy the Q8_0 path returns). Errors as the reference's
     // ("update_kv_cache expects 4-D tensors", "update_kv_cache shape mismatch", "new tokens … exceeds
-    // max cache size …").
+    // max cache size …", and "Tensor dtype is not F32" for an F16 / BF16 cache, tensor.rs:599-602).
     Tensor update_kv_cache(Tensor& cache, size_t current_seq_len, const Tensor& new_k);
+
+    // RoPE calls with at most this many (token, pair) angles evaluate them on the host
+    // (sph_rope_table → sph_rope_cached); larger ones evaluate them on the device (sph_rope).
+    static constexpr size_t kHostAngleMax = 8192;
 
     // The switches as read at construction.
     bool disabled(const char* op) const;

@@ -57,6 +57,9 @@ SIGNATURES = {
     "sph_gelu_erf": (_i32, [_vp, _vp, _i32, _i64, _vp]),
     "sph_add_bias": (_i32, [_vp, _vp, _i32, _vp, _i32, _i64, _i64, _vp]),
     "sph_rope": (_i32, [_vp, _i64, _vp, _i64, _i32, _i32, _vp, _i64, _i64, _i64, _i64, _f, _f, _vp]),
+    "sph_rope_cached": (_i32, [_vp, _i64, _vp, _i64, _i32, _i32, _vp, _vp, _i64, _vp, _i64, _i64, _i64, _i64, _vp,
+                               _vp]),
+    "sph_rope_table": (_i32, [_vp, _i64, _i64, _f, _f, _vp, _vp]),
     "sph_embed": (_i32, [_vp, _i32, _i64, _i64, _vp, _i64, _vp, _vp, _vp]),
     "sph_rope_kv_append": (_i32, [_vp, _i64, _vp, _vp, _i64, _i32, _i32, _vp, _i64, _i64, _f, _f, _vp, _vp, _i32,
                                   _i64, _vp, _vp, _vp, _i32, _vp, _vp]),
@@ -65,6 +68,7 @@ SIGNATURES = {
     "sph_transpose_heads": (_i32, [_vp, _vp, _i32, _i64, _i64, _i64, _vp]),
     "sph_kv_append": (_i32, [_vp, _i32, _vp, _i32, _i64, _i64, _i64, _i64, _i64, _vp]),
     "sph_kv_cache_update": (_i32, [_vp, _i32, _vp, _i32, _i64, _i64, _i64, _i64, _i64, _vp, _vp]),
+    "sph_kv_cache_update_into": (_i32, [_vp, _i32, _vp, _vp, _i32, _i64, _i64, _i64, _i64, _i64, _vp, _vp]),
     # sapient_hip_engine.h
     "sph_engine_create": (_i32, [C.POINTER(EngineConfig), _vp, _i32, _i64, C.POINTER(EngineLayer), _vp, PROJECT_FN,
                                  ATTEND_FN, _vp, C.POINTER(_vp)]),

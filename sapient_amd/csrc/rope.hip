@@ -47,6 +47,18 @@ struct DenTable {
     float v[kMaxHalf];
 };
 
+// Angles read from caller-supplied tables instead of evaluated: row r of cs /
+// sn holds cos / sin of position r's angle for pairs 0 .. half - 1 (the layout
+// of rope_cos_sin_cache, crates/sapient-backends/cpu/src/kernels/rope.rs:140-153).
+// Token s reads row pos[s] (row s when pos is null); a row outside [0, rows)
+// leaves the token's channels unchanged and stores 1 to *bad (when not null).
+struct TableArgs {
+    const float* cs;
+    const float* sn;
+    int64_t rows;
+    int32_t* bad;
+};
+
 __constant__ InvPio4Table kInvPio4 = inv_pio4_table();
 
 // The large-argument reduction indexes the 4/pi table per lane; staged in LDS
@@ -128,12 +140,17 @@ __device__ __forceinline__ void store_run(T* p, const float (&v)[L]) {
 // whose angles are shared by all 40 heads of a thread, is ~0.5 us faster
 // per-thread (the two block barriers cost about what the reductions save).
 // ELEM: element-wise loads and stores (rows that are only element-aligned).
-template <typename T, int P, bool INTERLEAVED, bool SPLIT, int U, bool PAIR_MAJOR, bool ELEM>
+// A: DenTable (angles evaluated in-kernel from the denominators) or TableArgs
+// (angles read from tables; per-thread, no block barrier).
+template <typename T, int P, bool INTERLEAVED, bool SPLIT, int U, bool PAIR_MAJOR, bool ELEM, typename A, bool FOLD>
 __global__ __launch_bounds__(kThreads) void rope_kernel(T* q, int nq, T* k, int nk, const int32_t* __restrict__ pos,
                                                              int64_t ntok, int64_t seq, int head_dim, int half,
                                                              int lanes_per_tok, int toks_per_block,
-                                                             int heads_per_group, float pos_scale, DenTable den) {
+                                                             int heads_per_group, float pos_scale, A den) {
     static_assert(INTERLEAVED || !SPLIT, "SPLIT is an interleaved layout");
+    constexpr bool TAB = std::is_same<A, TableArgs>::value;
+    static_assert(!(TAB && PAIR_MAJOR), "table angles are read per thread");
+    static_assert(!(FOLD && PAIR_MAJOR), "pair-major angles are shared by a block's consecutive tokens");
     constexpr int R = (!INTERLEAVED || SPLIT) ? 2 : 1;
     constexpr int L = INTERLEAVED ? 2 * P : P;
     constexpr int NA = SPLIT ? 2 * P : P;
@@ -148,15 +165,29 @@ __global__ __launch_bounds__(kThreads) void rope_kernel(T* q, int nq, T* k, int 
     const int tib = tid / lanes_per_tok;
     const int lit = tid - tib * lanes_per_tok;
     const int64_t t_first = (int64_t)blockIdx.x * toks_per_block;
-    const int64_t t = t_first + tib;
-    const bool active = tib < toks_per_block && t < ntok;
+    // FOLD (launches of fewer tokens than a block holds): the block's token
+    // slots take (token, head group) units, unit = group · ntok + token, so a
+    // one-token step runs in one block instead of one block per head group.
+    int64_t t;
+    int h_begin;
+    bool active;
+    if constexpr (FOLD) {
+        const int unit = blockIdx.x * toks_per_block + tib;
+        const int grp = unit / (int)ntok;
+        t = unit - grp * ntok;
+        h_begin = grp * heads_per_group;
+        active = tib < toks_per_block && h_begin < nq + nk;
+    } else {
+        t = t_first + tib;
+        h_begin = blockIdx.y * heads_per_group;
+        active = tib < toks_per_block && t < ntok;
+    }
     const int i0 = lit * P;
     const int off[2] = {INTERLEAVED ? 2 * i0 : i0, INTERLEAVED ? 2 * i0 + half : i0 + half};
     // Pair of angle a (0 <= a < NA) of this thread.
     auto pair_of = [&](int a) { return SPLIT ? i0 + (a / P) * (half / 2) + a % P : i0 + a; };
     const int64_t b = active ? t / seq : 0;
     const int64_t s = active ? t - b * seq : 0;
-    const int h_begin = blockIdx.y * heads_per_group;
     int h_end = h_begin + heads_per_group;
     if (h_end > nq + nk) h_end = nq + nk;
 
@@ -222,7 +253,26 @@ __global__ __launch_bounds__(kThreads) void rope_kernel(T* q, int nq, T* k, int 
     float cs[NA], sn[NA];
     constexpr int kPre = (PAIR_MAJOR && sizeof(T) == 2) ? 4 : 2;  // batches requested before the angles
     RawRun<T, L, ELEM> bufs[kPre][U][R];
-    if constexpr (PAIR_MAJOR) {
+    if constexpr (TAB) {
+        // Token s's row of the tables: requested after the position (row pos[s])
+        // and alongside the first two batches, so the thread waits on memory
+        // for the position and then once more; no sin/cos, no block barrier.
+        if (!active) return;
+        const int32_t ps = pos != nullptr ? pos[s] : (int32_t)s;
+        load_batch(h_begin, bufs[0]);
+        load_batch(h_begin + U, bufs[1]);
+        if (ps < 0 || (int64_t)ps >= den.rows) {
+            if (den.bad != nullptr) *den.bad = 1;
+            return;
+        }
+        const float* crow = den.cs + (size_t)ps * (size_t)half;
+        const float* srow = den.sn + (size_t)ps * (size_t)half;
+#pragma unroll
+        for (int a = 0; a < NA; ++a) {
+            cs[a] = crow[pair_of(a)];
+            sn[a] = srow[pair_of(a)];
+        }
+    } else if constexpr (PAIR_MAJOR) {
         int32_t pv = 0;
         if (tid < toks_per_block && t_first + tid < ntok) pv = pos[(t_first + tid) % seq];
         if (active) {
@@ -486,11 +536,13 @@ struct RopeShape {
 };
 
 // target: blocks to aim for in all (token blocks × head groups).
+// Table angles are read per thread, so those launches never take the pair-major shape.
 template <typename T, int P, bool IL, bool SPLIT = RopeShape<T, IL>::kSplit, int U = RopeShape<T, IL>::U,
-          bool PM = RopeShape<T, IL>::kPairMajor, bool ELEM = false>
+          bool PM = RopeShape<T, IL>::kPairMajor, bool ELEM = false, typename A = DenTable>
 int launch_rope_p(T* q, int nq, T* k, int nk, const int32_t* pos, int64_t ntok, int64_t seq, int head_dim,
-                  int half, float pos_scale, const DenTable& den, hipStream_t stream,
+                  int half, float pos_scale, const A& den, hipStream_t stream,
                   int target = RopeShape<T, IL>::kTarget) {
+    constexpr bool kPM = PM && !std::is_same<A, TableArgs>::value;
     const int lanes_per_tok = half / (SPLIT ? 2 * P : P);
     const int toks_per_block = kThreads / lanes_per_tok;
     const int64_t blocks_x = (ntok + toks_per_block - 1) / toks_per_block;
@@ -501,9 +553,19 @@ int launch_rope_p(T* q, int nq, T* k, int nk, const int32_t* pos, int64_t ntok, 
     const int heads_per_group = (heads + groups - 1) / groups;
     groups = (heads + heads_per_group - 1) / heads_per_group;
     if (blocks_x > INT32_MAX) return SPH_EINVAL;
+    if constexpr (!kPM) {
+        // Fewer tokens than a block holds: (token, head group) units share blocks (FOLD).
+        if (ntok < toks_per_block) {
+            const int64_t units = ntok * (int64_t)groups;  // < toks_per_block · heads
+            const dim3 grid((unsigned)((units + toks_per_block - 1) / toks_per_block));
+            return launch(rope_kernel<T, P, IL, SPLIT, U, false, ELEM, A, true>, grid, kThreads, stream, q, nq, k, nk,
+                          pos, ntok, seq, head_dim, half, lanes_per_tok, toks_per_block, heads_per_group, pos_scale,
+                          den);
+        }
+    }
     const dim3 grid((unsigned)blocks_x, (unsigned)groups);
-    return launch(rope_kernel<T, P, IL, SPLIT, U, PM, ELEM>, grid, kThreads, stream, q, nq, k, nk, pos, ntok, seq, head_dim,
-                  half, lanes_per_tok, toks_per_block, heads_per_group, pos_scale, den);
+    return launch(rope_kernel<T, P, IL, SPLIT, U, kPM, ELEM, A, false>, grid, kThreads, stream, q, nq, k, nk, pos,
+                  ntok, seq, head_dim, half, lanes_per_tok, toks_per_block, heads_per_group, pos_scale, den);
 }
 
 // Denominators powf(base, 2i / rotary_dim) from the host libm, the call the reference makes.
@@ -591,15 +653,13 @@ int launch_rope_kv(const void* qv, void* qov, int nq, const void* kv, const void
     return SPH_EINVAL;  // head_dim or alignment the vector paths do not cover
 }
 
-template <typename T>
+// den: the denominators (DenTable) or the angle tables (TableArgs).
+template <typename T, typename A>
 int launch_rope(void* qv, int nq, void* kv, int nk, int layout, const int32_t* pos, int64_t batch, int64_t seq,
-                int head_dim, int rotary_dim, float base, float pos_scale, hipStream_t stream) {
+                int head_dim, int rotary_dim, float pos_scale, const A& den, hipStream_t stream) {
     T* q = static_cast<T*>(qv);
     T* k = static_cast<T*>(kv);
     const int half = rotary_dim / 2;
-    // The reference's denominators: base.powf(2.0 * i as f32 / rotary_dim as f32), host libm.
-    DenTable den;
-    fill_dens(den, half, rotary_dim, base);
     const int64_t ntok = batch * seq;
     auto ok = [&](int P, int elems_per_access) {
         const size_t bytes = (size_t)elems_per_access * sizeof(T);
@@ -654,11 +714,73 @@ extern "C" int sph_rope(void* q, int64_t n_q_heads, void* k, int64_t n_k_heads, 
     if (positions == nullptr || (n_q_heads > 0 && q == nullptr)) return SPH_EINVAL;
     if (!(pos_scale == pos_scale) || pos_scale == 0.0f) return SPH_EINVAL;
     hipStream_t s = static_cast<hipStream_t>(stream);
+    // The reference's denominators: base.powf(2.0 * i as f32 / rotary_dim as f32), host libm.
+    sph::DenTable den;
+    sph::fill_dens(den, (int)rotary_dim / 2, (int)rotary_dim, base);
     return sph::with_float_type(dtype, [&](auto t) -> int {
         using T = decltype(t);
         return sph::launch_rope<T>(q, (int)n_q_heads, k, (int)n_k_heads, layout, positions, batch, seq, (int)head_dim,
-                                   (int)rotary_dim, base, pos_scale, s);
+                                   (int)rotary_dim, pos_scale, den, s);
     });
+}
+
+extern "C" int sph_rope_cached(void* q, int64_t n_q_heads, void* k, int64_t n_k_heads, int dtype, int layout,
+                               const float* cos_table, const float* sin_table, int64_t table_rows,
+                               const int32_t* positions, int64_t batch, int64_t seq, int64_t head_dim,
+                               int64_t rotary_dim, int32_t* bad_pos_flag, void* stream) {
+    if (layout != SPH_ROPE_NEOX && layout != SPH_ROPE_INTERLEAVED) return SPH_EINVAL;
+    if (!sph::is_float_dtype(dtype)) return SPH_EINVAL;
+    if (k == nullptr) n_k_heads = 0;
+    if (n_q_heads < 0 || n_k_heads < 0 || batch < 0 || seq < 0 || table_rows < 0) return SPH_EINVAL;
+    if (head_dim <= 0 || head_dim % 2 != 0 || head_dim > INT32_MAX) return SPH_EINVAL;
+    if (rotary_dim <= 0 || rotary_dim % 2 != 0 || rotary_dim > head_dim || rotary_dim / 2 > sph::kMaxHalf)
+        return SPH_EINVAL;
+    if (n_q_heads + n_k_heads > INT32_MAX) return SPH_EINVAL;
+    const int64_t heads = n_q_heads + n_k_heads;
+    if (batch == 0 || seq == 0 || heads == 0) return SPH_OK;
+    if (n_q_heads > 0 && q == nullptr) return SPH_EINVAL;
+    if (cos_table == nullptr || sin_table == nullptr || !sph::aligned(cos_table, 4) || !sph::aligned(sin_table, 4))
+        return SPH_EINVAL;
+    // Without positions token s reads row s: the tables must hold seq rows.
+    if (positions == nullptr && table_rows < seq) return SPH_ERANGE;
+    if (seq > INT32_MAX) return SPH_EINVAL;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const sph::TableArgs tab{cos_table, sin_table, table_rows, bad_pos_flag};
+    return sph::with_float_type(dtype, [&](auto t) -> int {
+        using T = decltype(t);
+        return sph::launch_rope<T>(q, (int)n_q_heads, k, (int)n_k_heads, layout, positions, batch, seq, (int)head_dim,
+                                   (int)rotary_dim, 1.0f, tab, s);
+    });
+}
+
+// Host-side table builder: the reference's angle, (pos as f32 / pos_scale) /
+// base.powf(2i / rotary_dim) (rope.rs:48-50, :123-125), and its sin / cos, with
+// the host libm the reference's f32::sin_cos / powf bind to.
+extern "C" int sph_rope_table(const int64_t* positions, int64_t n, int64_t rotary_dim, float base, float pos_scale,
+                              float* cos_out, float* sin_out) {
+    if (n < 0 || rotary_dim <= 0 || rotary_dim % 2 != 0) return SPH_EINVAL;
+    if (!(pos_scale == pos_scale) || pos_scale == 0.0f) return SPH_EINVAL;
+    if (n == 0) return SPH_OK;
+    if (cos_out == nullptr || sin_out == nullptr) return SPH_EINVAL;
+    const int64_t half = rotary_dim / 2;
+    if (positions != nullptr)
+        for (int64_t r = 0; r < n; ++r)
+            if (positions[r] < 0) return SPH_EINVAL;
+    float den[sph::kMaxHalf];
+    const bool small = half <= sph::kMaxHalf;
+    if (small)
+        for (int64_t i = 0; i < half; ++i) den[i] = powf(base, 2.0f * (float)i / (float)rotary_dim);
+    for (int64_t r = 0; r < n; ++r) {
+        const int64_t pos = positions != nullptr ? positions[r] : r;
+        const float p = (float)pos / pos_scale;
+        for (int64_t i = 0; i < half; ++i) {
+            const float d = small ? den[i] : powf(base, 2.0f * (float)i / (float)rotary_dim);
+            const float freq = p / d;
+            cos_out[r * half + i] = cosf(freq);
+            sin_out[r * half + i] = sinf(freq);
+        }
+    }
+    return SPH_OK;
 }
 
 namespace sph {

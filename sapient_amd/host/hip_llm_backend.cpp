@@ -524,11 +524,33 @@ Tensor HipLlmBackend::rope(const Tensor& x0, const std::vector<size_t>& position
         pos[i] = (int32_t)positions[i];
     }
     const Tensor x = f32_input(x0);
+    // Short sequences (decode steps, small chunks) take their angles from the host, evaluated
+    // for exactly these positions by the libm the reference calls (rope.rs:49-50): the kernel
+    // then only reads them. Longer ones evaluate the same sin/cos on the device instead of
+    // spending host time on seq · rotary_dim / 2 of them.
+    const size_t half = rotary_dim / 2;
+    const bool host_angles = seq * half <= kHostAngleMax;
+    std::vector<float> tab;
+    if (host_angles) {
+        std::vector<int64_t> p64(positions.begin(), positions.end());
+        tab.resize(2 * seq * half);
+        check(sph_rope_table(p64.data(), (int64_t)seq, (int64_t)rotary_dim, base, 1.0f, tab.data(),
+                             tab.data() + seq * half),
+              "rope (angles)");
+    }
     std::lock_guard<std::mutex> lock(mu_);
     DeviceBuf xd = upload(x.bytes().data(), x.bytes().size());
-    DeviceBuf pd = upload(pos.data(), pos.size() * 4);
-    const int st = sph_rope(xd.ptr, (int64_t)n_heads, nullptr, 0, SPH_F32, layout, static_cast<const int32_t*>(pd.ptr),
-                            (int64_t)batch, (int64_t)seq, (int64_t)head_dim, (int64_t)rotary_dim, base, 1.0f, stream_);
+    DeviceBuf pd = host_angles ? upload(tab.data(), tab.size() * 4) : upload(pos.data(), pos.size() * 4);
+    int st;
+    if (host_angles) {
+        const float* cs = static_cast<const float*>(pd.ptr);
+        st = sph_rope_cached(xd.ptr, (int64_t)n_heads, nullptr, 0, SPH_F32, layout, cs, cs + seq * half,
+                             (int64_t)seq, nullptr, (int64_t)batch, (int64_t)seq, (int64_t)head_dim,
+                             (int64_t)rotary_dim, nullptr, stream_);
+    } else {
+        st = sph_rope(xd.ptr, (int64_t)n_heads, nullptr, 0, SPH_F32, layout, static_cast<const int32_t*>(pd.ptr),
+                      (int64_t)batch, (int64_t)seq, (int64_t)head_dim, (int64_t)rotary_dim, base, 1.0f, stream_);
+    }
     std::vector<float> out(x.numel());
     if (st == SPH_OK) download(xd, out.data(), out.size() * 4);
     release(xd);
@@ -596,16 +618,29 @@ Tensor HipLlmBackend::update_kv_cache(Tensor& cache, size_t current_seq_len, con
     if (new_seq > max_seq)
         throw Error("new tokens " + std::to_string(new_seq) + " exceeds max cache size " + std::to_string(max_seq));
     const DType cdt = cache.dtype();
-    if (cdt != DType::F32 && cdt != DType::F16 && cdt != DType::BF16 && cdt != DType::Q8_0)
-        throw Error(std::string("type mismatch: unsupported KV cache dtype ") + dtype_name(cdt));
+    // The reference's float path writes through cache.as_f32_slice_mut() (common.rs:378), which
+    // refuses any other dtype (tensor.rs:599-602); only Q8_0 has a path of its own.
+    if (cdt != DType::F32 && cdt != DType::Q8_0) throw Error("Tensor dtype is not F32");
     if (current_seq_len > max_seq) throw Error("current length " + std::to_string(current_seq_len) + " exceeds the cache");
     const Tensor src = f32_input(new_k);
     std::lock_guard<std::mutex> lock(mu_);
     DeviceBuf cdev = upload(cache.bytes().data(), cache.bytes().size());
     DeviceBuf sdev = upload(src.bytes().data(), src.bytes().size());
     int64_t total = 0;
-    int st = sph_kv_cache_update(sdev.ptr, SPH_F32, cdev.ptr, (int)cdt, (int64_t)(b * h), (int64_t)new_seq,
+    // When the window slides, the kept rows move once into a second buffer (the in-place shift
+    // moves them twice), which then becomes the cache; the first is freed after the download.
+    const bool slides = current_seq_len + new_seq > max_seq;
+    DeviceBuf next = slides ? alloc(cache.bytes().size()) : DeviceBuf();
+    int st;
+    if (slides) {
+        st = sph_kv_cache_update_into(sdev.ptr, SPH_F32, cdev.ptr, next.ptr, (int)cdt, (int64_t)(b * h),
+                                      (int64_t)new_seq, (int64_t)hd, (int64_t)max_seq, (int64_t)current_seq_len,
+                                      &total, stream_);
+        if (st == SPH_OK) std::swap(cdev.ptr, next.ptr);
+    } else {
+        st = sph_kv_cache_update(sdev.ptr, SPH_F32, cdev.ptr, (int)cdt, (int64_t)(b * h), (int64_t)new_seq,
                                  (int64_t)hd, (int64_t)max_seq, (int64_t)current_seq_len, &total, stream_);
+    }
     if (st == SPH_OK) download(cdev, cache.bytes_mut().data(), cache.bytes().size());
     release(sdev);
     check(st, "update_kv_cache");

@@ -217,6 +217,77 @@ def rope_(q: torch.Tensor, k: Optional[torch.Tensor], positions: torch.Tensor, b
                          positions.data_ptr(), B, S, D, rd, float(base), float(pos_scale), _stream(q)), "rope")
 
 
+def rope_table(positions, rotary_dim: int, base: float, pos_scale: float = 1.0, n: Optional[int] = None):
+    """Host cos / sin tables [n, rotary_dim / 2] (float32 numpy) of the RoPE angles of `positions` (a
+    sequence of ints, row r for positions[r]) or, with positions None, of 0 .. n - 1 — the layout of
+    rope_cos_sin_cache (rope.rs:140-153), evaluated by the library with the host libm (rope.rs:48-50)."""
+    import numpy as np
+    if positions is None:
+        if n is None:
+            raise ValueError("give positions or n")
+        pos, count = None, int(n)
+    else:
+        pos = np.ascontiguousarray(positions, dtype=np.int64)
+        count = pos.size
+    if rotary_dim <= 0 or rotary_dim % 2:
+        raise ValueError("rotary_dim must be even and positive")
+    cs = np.empty((count, rotary_dim // 2), np.float32)
+    sn = np.empty((count, rotary_dim // 2), np.float32)
+    check(lib().sph_rope_table(None if pos is None else pos.ctypes.data, count, rotary_dim, float(base),
+                               float(pos_scale), cs.ctypes.data, sn.ctypes.data), "rope_table")
+    return cs, sn
+
+
+def rope_cached_(q: torch.Tensor, k: Optional[torch.Tensor], cos_table: torch.Tensor, sin_table: torch.Tensor,
+                 positions: Optional[torch.Tensor] = None, rotary_dim: Optional[int] = None,
+                 interleaved: bool = False, bad_pos_flag: Optional[torch.Tensor] = None) -> None:
+    """RoPE in place on q [B, Hq, S, D] (and k) with the angles read from device f32 tables
+    [rows, rotary_dim / 2]: token s uses row positions[s] (int32 device tensor [S]), or row s when
+    positions is None."""
+    _dev(q, "q")
+    if q.dim() != 4:
+        raise ValueError("q must be [batch, heads, seq, head_dim]")
+    B, Hq, S, D = q.shape
+    Hk = 0
+    if k is not None:
+        _dev(k, "k")
+        if k.dim() != 4 or k.shape[0] != B or k.shape[2] != S or k.shape[3] != D or k.dtype != q.dtype:
+            raise ValueError("k must be [batch, kv_heads, seq, head_dim] like q")
+        Hk = k.shape[1]
+    rd = D if rotary_dim is None else rotary_dim
+    for t, name in ((cos_table, "cos_table"), (sin_table, "sin_table")):
+        _dev(t, name)
+        if t.dtype != torch.float32 or t.dim() != 2 or t.shape[1] != rd // 2:
+            raise ValueError(f"{name} must be f32 [rows, rotary_dim / 2]")
+    if cos_table.shape != sin_table.shape:
+        raise ValueError("cos_table and sin_table must have the same shape")
+    if positions is not None:
+        _dev(positions, "positions")
+        if positions.dtype != torch.int32 or positions.numel() != S:
+            raise ValueError("positions must be int32 with seq_len entries")
+    flag = None
+    if bad_pos_flag is not None:
+        flag = _dev(bad_pos_flag, "bad_pos_flag")
+        if flag.dtype != torch.int32 or flag.numel() < 1:
+            raise ValueError("bad_pos_flag must be an int32 device tensor")
+    layout = _lib.ROPE_INTERLEAVED if interleaved else _lib.ROPE_NEOX
+    check(lib().sph_rope_cached(q.data_ptr(), Hq, None if k is None else k.data_ptr(), Hk, dtype_code(q.dtype),
+                                layout, cos_table.data_ptr(), sin_table.data_ptr(), cos_table.shape[0],
+                                None if positions is None else positions.data_ptr(), B, S, D, rd,
+                                None if flag is None else flag.data_ptr(), _stream(q)), "rope_cached")
+
+
+def rope_host_positions_(q: torch.Tensor, k: Optional[torch.Tensor], positions, base: float,
+                         rotary_dim: Optional[int] = None, pos_scale: float = 1.0, interleaved: bool = False) -> None:
+    """The trait path's RoPE (apply_rope_positions, backend.rs:84): positions on the host, angles evaluated
+    on the host for exactly those positions (rope_table), uploaded, and applied by rope_cached_."""
+    rd = q.shape[-1] if rotary_dim is None else rotary_dim
+    cs, sn = rope_table(positions, rd, base, pos_scale)
+    cs_d = torch.from_numpy(cs).to(q.device, non_blocking=False)
+    sn_d = torch.from_numpy(sn).to(q.device, non_blocking=False)
+    rope_cached_(q, k, cs_d, sn_d, None, rd, interleaved)
+
+
 # Bytes per row as (bytes per block, elements per block) of each table type
 # (crates/sapient-core/src/dtype.rs:136-145).
 _ROW_BYTES = {_lib.F32: (4, 1), _lib.F16: (2, 1), _lib.BF16: (2, 1), _lib.Q4_0: (18, 32), _lib.Q8_0: (34, 32),
@@ -301,6 +372,30 @@ def kv_cache_update(src: torch.Tensor, cache: torch.Tensor, cur_len: int) -> int
     n = ctypes.c_int64(0)
     check(lib().sph_kv_cache_update(src.data_ptr(), dtype_code(src.dtype), cache.data_ptr(), cdt, n_kv, seq, hd,
                                     max_seq, int(cur_len), ctypes.addressof(n), _stream(src)), "kv_cache_update")
+    return n.value
+
+
+def kv_cache_update_into(src: torch.Tensor, cache: torch.Tensor, out: torch.Tensor, cur_len: int) -> int:
+    """kv_cache_update into a second cache: `out` (cache's shape and dtype) receives rows [0, new_len) of the
+    updated cache — cache's kept rows moved once, then src — and `cache` is only read. The caller then uses
+    `out` as its cache (common.rs:355-434, :449-508 take the cache as &mut Tensor). Returns new_len."""
+    _dev(src, "src")
+    _dev(cache, "cache")
+    _dev(out, "out")
+    q8 = cache.dtype == torch.uint8
+    if src.dim() != 3 or cache.dim() != 3 or src.shape[0] != cache.shape[0]:
+        raise ValueError("src must be [n_kv, seq, head_dim] and cache [n_kv, max_seq, row]")
+    if out.shape != cache.shape or out.dtype != cache.dtype:
+        raise ValueError("out must have the cache's shape and dtype")
+    n_kv, seq, hd = src.shape
+    if cache.shape[2] != (hd // 32 * 34 if q8 else hd) or (q8 and hd % 32):
+        raise ValueError("cache rows must hold head_dim elements (Q8_0: head_dim / 32 blocks of 34 bytes)")
+    max_seq = cache.shape[1]
+    cdt = _lib.Q8_0 if q8 else dtype_code(cache.dtype)
+    n = ctypes.c_int64(0)
+    check(lib().sph_kv_cache_update_into(src.data_ptr(), dtype_code(src.dtype), cache.data_ptr(), out.data_ptr(),
+                                         cdt, n_kv, seq, hd, max_seq, int(cur_len), ctypes.addressof(n),
+                                         _stream(src)), "kv_cache_update_into")
     return n.value
 
 

@@ -286,6 +286,25 @@ static void rope_rejects_bad_arguments(HipLlmBackend& bk) {  // rope.rs:19-35, :
     ASSERT(expect_error([&] { bk.apply_rope_partial(x, {0, 1}, 1e4f, 10); }).find("rotary_dim") != std::string::npos, "rd");
 }
 
+static void rope_host_and_device_angles_agree(HipLlmBackend& bk) {  // rope.rs:48-57
+    // 300 tokens x 32 pairs exceed the host-angle budget (device sin/cos); one token at a time stays
+    // within it (host libm angles): both routes give the reference's bits, so they agree exactly.
+    const size_t H = 2, S = 300, D = 64;
+    std::vector<float> x(H * S * D);
+    for (size_t i = 0; i < x.size(); ++i) x[i] = std::sin(0.37f * (float)i) * 3.0f;
+    std::vector<size_t> pos(S);
+    for (size_t s = 0; s < S; ++s) pos[s] = 7919 * s % 100003;
+    ASSERT(S * D / 2 > HipLlmBackend::kHostAngleMax, "the whole call takes the device route");
+    const std::vector<float> all = bk.apply_rope_positions(Tensor::from_f32(x, {1, H, S, D}), pos, 5e5f).as_f32();
+    for (size_t s = 0; s < S; s += 23) {
+        std::vector<float> one(H * D);
+        for (size_t h = 0; h < H; ++h) std::memcpy(&one[h * D], &x[(h * S + s) * D], D * 4);
+        const std::vector<float> o = bk.apply_rope_positions(Tensor::from_f32(one, {1, H, 1, D}), {pos[s]}, 5e5f).as_f32();
+        for (size_t h = 0; h < H; ++h)
+            ASSERT(std::memcmp(&o[h * D], &all[(h * S + s) * D], D * 4) == 0, "token rotated alike on both routes");
+    }
+}
+
 static void rope_interleaved_is_permuted_neox(HipLlmBackend& bk) {  // gguf_weights.rs:111-115
     const size_t D = 16;
     std::vector<float> x(2 * 3 * D);
@@ -463,6 +482,39 @@ static void kv_cache_update_slides_when_full(HipLlmBackend& bk) {  // common.rs:
                .find("shape mismatch") != std::string::npos, "heads");
 }
 
+static void kv_cache_update_refuses_half_caches(HipLlmBackend& bk) {  // common.rs:378 → tensor.rs:599-602
+    // The float path writes through as_f32_slice_mut, which refuses every dtype but F32.
+    Tensor cache = Tensor::from_f16_bytes(std::vector<uint8_t>(32, 0), {1, 2, 4, 2});
+    ASSERT(expect_error([&] { bk.update_kv_cache(cache, 0, Tensor::from_f32({1, 1, 2, 2}, {1, 2, 1, 2})); })
+               .find("Tensor dtype is not F32") != std::string::npos, "f16 cache");
+    Tensor cache_bf = Tensor::from_bf16_bytes(std::vector<uint8_t>(32, 0), {1, 2, 4, 2});
+    ASSERT(expect_error([&] { bk.update_kv_cache(cache_bf, 0, Tensor::from_f32({1, 1, 2, 2}, {1, 2, 1, 2})); })
+               .find("Tensor dtype is not F32") != std::string::npos, "bf16 cache");
+}
+
+static void kv_cache_update_long_decode(HipLlmBackend& bk) {  // common.rs:381-412, step by step
+    // Twelve one-token steps into a [1, 3, 5, 4] cache: the window slides from the sixth on; the
+    // cache always holds the last min(t, 5) tokens of each head, oldest first.
+    const size_t H = 3, S = 5, D = 4;
+    Tensor cache = Tensor::from_f32(std::vector<float>(H * S * D, 0.0f), {1, H, S, D});
+    size_t cur = 0;
+    for (int t = 1; t <= 12; ++t) {
+        std::vector<float> tok(H * D);
+        for (size_t h = 0; h < H; ++h)
+            for (size_t d = 0; d < D; ++d) tok[h * D + d] = (float)(100 * h + 10 * t) + (float)d;
+        const Tensor v = bk.update_kv_cache(cache, cur, Tensor::from_f32(tok, {1, H, 1, D}));
+        cur = v.shape()[2];
+        ASSERT(cur == std::min<size_t>((size_t)t, S), "view length");
+        const std::vector<float> c = cache.as_f32();
+        for (size_t h = 0; h < H; ++h)
+            for (size_t s = 0; s < cur; ++s) {
+                const int tt = t - (int)cur + 1 + (int)s;
+                for (size_t d = 0; d < D; ++d)
+                    ASSERT(c[(h * S + s) * D + d] == (float)(100 * h + 10 * tt) + (float)d, "cache row");
+            }
+    }
+}
+
 static void kv_cache_update_q8_0(HipLlmBackend& bk) {  // update_kv_cache_q8, common.rs:449-528
     // [1, 1, 2, 32] Q8_0 cache holding one row; a full cache after a second, then a slide: rows are
     // quantized by quantize_f32_to_q8_0_block (common.rs:336-348, the quantizer of quant.rs:223-235),
@@ -527,12 +579,15 @@ int main() {
         {"rope_position_zero_is_identity", rope_position_zero_is_identity},
         {"rope_rejects_bad_arguments", rope_rejects_bad_arguments},
         {"rope_interleaved_is_permuted_neox", rope_interleaved_is_permuted_neox},
+        {"rope_host_and_device_angles_agree", rope_host_and_device_angles_agree},
         {"add_rms_norm_is_add_then_rms_norm", add_rms_norm_is_add_then_rms_norm},
         {"embed_row_gather_matches_full_dequant", embed_row_gather_matches_full_dequant},
         {"quant_bytes_are_validated", quant_bytes_are_validated},
         {"kv_cache_update_reference_test", kv_cache_update_reference_test},
         {"kv_cache_update_slides_when_full", kv_cache_update_slides_when_full},
         {"kv_cache_update_q8_0", kv_cache_update_q8_0},
+        {"kv_cache_update_refuses_half_caches", kv_cache_update_refuses_half_caches},
+        {"kv_cache_update_long_decode", kv_cache_update_long_decode},
         {"disable_routes_listed_ops", disable_routes_listed_ops},
         {"disable_without_backend_raises", disable_without_backend_raises},
         {"verify_returns_the_device_result", verify_returns_the_device_result},

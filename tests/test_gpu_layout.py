@@ -247,3 +247,153 @@ def test_kv_cache_update_rejects_bad_arguments(dev):
     assert L.sph_kv_cache_update(raw.data_ptr() + 4, 0, q8.data_ptr(), 8, 2, 1, 32, 8, 8, ctypes.addressof(n), s) == EINVAL
     torch.cuda.synchronize()
     assert n.value == -7 and torch.equal(cache, before) and torch.equal(q8, q8_before)
+
+
+# The out-of-place form (sph_kv_cache_update_into): the updated cache lands in a second buffer, which the
+# caller then uses as its cache; the reference takes the cache as &mut Tensor (common.rs:355-359).
+def _sentinel(shape, dtype, dev):
+    """A buffer of a recognisable pattern, so rows the call must not touch can be checked."""
+    n = 1
+    for d in shape:
+        n *= d
+    if dtype == torch.uint8:
+        return (torch.arange(n, device=dev) % 253).to(torch.uint8).reshape(shape)
+    return (torch.arange(n, device=dev, dtype=torch.float32) * 0.5 - 7).to(dtype).reshape(shape)
+
+
+def _check_into(cache, out, before_cache, before_out, want, n, what):
+    """out rows [0, n) equal the oracle's cache rows [0, n) bit for bit, out rows past n are untouched, and
+    the source cache is unchanged."""
+    got = to_np(out)
+    if got.dtype == np.float32:
+        assert_bits_equal(got[:, :n], want[:, :n], what)
+    else:
+        assert np.array_equal(got[:, :n].view(np.uint8), want[:, :n].view(np.uint8)), what
+    assert np.array_equal(got[:, n:].view(np.uint8), before_out[:, n:].view(np.uint8)), f"{what}: rows past {n}"
+    assert np.array_equal(to_np(cache).view(np.uint8), before_cache.view(np.uint8)), f"{what}: source cache"
+
+
+@pytest.mark.parametrize("cdtype", [torch.float32, torch.float16, torch.bfloat16], ids=IDS)
+@pytest.mark.parametrize("n_kv,hd,max_seq,cur_len,seq", _UPD_CASES)
+def test_kv_cache_update_into_matches_oracle(dev, orc, cdtype, n_kv, hd, max_seq, cur_len, seq):
+    """The out-of-place update: rows [0, new_len) of out equal the in-place update's (the oracle's
+    update_kv_cache) bit for bit, whatever the shift; rows past new_len and the source cache keep their bytes."""
+    print(f"case kv_cache_update_into {cdtype} {n_kv}x{hd} max {max_seq} cur {cur_len} seq {seq}", flush=True)
+    src = _gen((n_kv, seq, hd), seq * 7 + hd, dev)
+    cache = _gen((n_kv, max_seq, hd), 17 + hd, dev, cdtype)
+    out = _sentinel((n_kv, max_seq, hd), cdtype, dev)
+    before_cache, before_out = to_np(cache).copy(), to_np(out).copy()
+    want = before_cache.copy()
+    n = ops.kv_cache_update_into(src, cache, out, cur_len)
+    want_n = orc.kv_cache_update(to_np(src), want, CODE[cdtype], n_kv, seq, hd, max_seq, cur_len)
+    assert n == want_n == min(cur_len + seq, max_seq)
+    _check_into(cache, out, before_cache, before_out, want, n, f"kv_cache_update_into {cdtype}")
+
+
+@pytest.mark.parametrize("sdtype,cdtype", [(torch.float16, torch.float32), (torch.bfloat16, torch.float32),
+                                           (torch.float16, torch.float16), (torch.bfloat16, torch.float16),
+                                           (torch.float32, torch.bfloat16), (torch.float16, torch.bfloat16)],
+                         ids=lambda d: IDS(d))
+@pytest.mark.parametrize("n_kv,hd,max_seq,cur_len,seq", [(8, 128, 1024, 1024, 1), (3, 64, 16, 12, 7),
+                                                         (2, 64, 16, 5, 3), (5, 3, 40, 40, 2)])
+def test_kv_cache_update_into_source_types(dev, orc, sdtype, cdtype, n_kv, hd, max_seq, cur_len, seq):
+    """Every source type into every cache type (the fused launch widens or narrows the new rows)."""
+    print(f"case kv_cache_update_into {sdtype}->{cdtype} {n_kv}x{hd} max {max_seq} cur {cur_len} seq {seq}",
+          flush=True)
+    src = _gen((n_kv, seq, hd), 3 * seq + hd, dev, sdtype)
+    cache = _gen((n_kv, max_seq, hd), 29 + hd, dev, cdtype)
+    out = _sentinel((n_kv, max_seq, hd), cdtype, dev)
+    before_cache, before_out = to_np(cache).copy(), to_np(out).copy()
+    want = before_cache.copy()
+    n = ops.kv_cache_update_into(src, cache, out, cur_len)
+    assert n == orc.kv_cache_update(widen(src, orc), want, CODE[cdtype], n_kv, seq, hd, max_seq, cur_len)
+    _check_into(cache, out, before_cache, before_out, want, n, f"{sdtype}->{cdtype}")
+
+
+@pytest.mark.parametrize("n_kv,hd,max_seq,cur_len,seq", [(2, 64, 16, 16, 1), (3, 32, 24, 20, 9), (8, 128, 512, 512, 1),
+                                                         (2, 128, 64, 40, 64), (2, 64, 16, 3, 4)])
+def test_kv_cache_update_into_q8_0(dev, orc, n_kv, hd, max_seq, cur_len, seq):
+    """The quantized cache: kept 34-byte blocks moved as raw bytes into out, new rows quantized there."""
+    print(f"case kv_cache_update_into q8_0 {n_kv}x{hd} max {max_seq} cur {cur_len} seq {seq}", flush=True)
+    g = torch.Generator(device=dev).manual_seed(max_seq + cur_len)
+    src = torch.randn(n_kv, seq, hd, generator=g, device=dev) * 3
+    row = hd // 32 * 34
+    cache = torch.randint(0, 256, (n_kv, max_seq, row), generator=g, device=dev, dtype=torch.int32).to(torch.uint8)
+    out = _sentinel((n_kv, max_seq, row), torch.uint8, dev)
+    before_cache, before_out = to_np(cache).copy(), to_np(out).copy()
+    want = before_cache.copy()
+    n = ops.kv_cache_update_into(src, cache, out, cur_len)
+    assert n == orc.kv_cache_update(to_np(src), want, orc.Q8_0, n_kv, seq, hd, max_seq, cur_len)
+    _check_into(cache, out, before_cache, before_out, want, n, "q8_0")
+
+
+@pytest.mark.parametrize("cdtype", [torch.float16, torch.uint8], ids=IDS)
+def test_kv_cache_update_into_decode_sequence(dev, orc, cdtype):
+    """Thirty decode steps past a full cache, alternating between two buffers as a caller that installs
+    each step's `out` as its cache would; every step checked against the oracle's in-place cache."""
+    n_kv, hd, max_seq = 4, 64, 48
+    q8 = cdtype == torch.uint8
+    row = hd // 32 * 34 if q8 else hd
+    if q8:
+        g = torch.Generator(device=dev).manual_seed(5)
+        cur_buf = torch.randint(0, 256, (n_kv, max_seq, row), generator=g, device=dev, dtype=torch.int32)
+        cur_buf = cur_buf.to(torch.uint8)
+    else:
+        cur_buf = _gen((n_kv, max_seq, hd), 5, dev, cdtype)
+    spare = _sentinel((n_kv, max_seq, row), cdtype, dev)
+    ref = to_np(cur_buf).copy()
+    cur = 40
+    for t in range(30):
+        src = _gen((n_kv, 1, hd), 100 + t, dev)
+        print(f"case kv_cache_update_into {cdtype} decode step {t} cur {cur}", flush=True)
+        n = ops.kv_cache_update_into(src, cur_buf, spare, cur)
+        assert n == orc.kv_cache_update(to_np(src), ref, orc.Q8_0 if q8 else 1, n_kv, 1, hd, max_seq, cur)
+        got = to_np(spare)
+        assert np.array_equal(got[:, :n].view(np.uint8), ref[:, :n].view(np.uint8)), f"step {t}"
+        cur_buf, spare = spare, cur_buf
+        cur = n
+
+
+@pytest.mark.parametrize("offset", [2, 4, 8])
+def test_kv_cache_update_into_unaligned_buffers(dev, orc, offset):
+    """Buffers off 16-byte alignment take the two-launch path (raw units as wide as the alignment allows)."""
+    n_kv, hd, max_seq, cur_len, seq = 3, 64, 20, 20, 2
+    print(f"case kv_cache_update_into f16 unaligned by {offset}", flush=True)
+    el = n_kv * max_seq * hd
+    cache_raw = _gen((el + 8,), 41, dev, torch.float16)
+    out_raw = _sentinel((el + 8,), torch.float16, dev)
+    cache = cache_raw[offset // 2:offset // 2 + el].view(n_kv, max_seq, hd)
+    out = out_raw[offset // 2:offset // 2 + el].view(n_kv, max_seq, hd)
+    src = _gen((n_kv, seq, hd), 43, dev)
+    before_cache, before_out = to_np(cache).copy(), to_np(out).copy()
+    want = before_cache.copy()
+    n = ops.kv_cache_update_into(src, cache, out, cur_len)
+    assert n == orc.kv_cache_update(to_np(src), want, 1, n_kv, seq, hd, max_seq, cur_len)
+    _check_into(cache, out, before_cache, before_out, want, n, f"offset {offset}")
+    assert torch.equal(out_raw[:offset // 2], _sentinel((el + 8,), torch.float16, dev)[:offset // 2])
+
+
+def test_kv_cache_update_into_rejects_bad_arguments(dev):
+    from sapient_amd._lib import EINVAL, ERANGE, lib
+    import ctypes
+    cache = torch.arange(2 * 8 * 16, device=dev, dtype=torch.float32).reshape(2, 8, 16)
+    out = torch.full((2, 8, 16), 3.0, device=dev)
+    before, out_before = cache.clone(), out.clone()
+    src = torch.ones(2, 9, 16, device=dev)
+    n = ctypes.c_int64(-7)
+    s = torch.cuda.current_stream().cuda_stream
+    L = lib()
+    a = ctypes.addressof(n)
+    c, o, x = cache.data_ptr(), out.data_ptr(), src.data_ptr()
+    assert L.sph_kv_cache_update_into(x, 0, c, o, 0, 2, 9, 16, 8, 0, a, s) == ERANGE     # seq > max_seq
+    assert L.sph_kv_cache_update_into(x, 0, c, o, 0, 2, 1, 16, 8, 9, a, s) == EINVAL     # cur_len > max_seq
+    assert L.sph_kv_cache_update_into(x, 0, c, o, 0, 2, 1, 16, 8, 2, None, s) == EINVAL  # no new_len
+    assert L.sph_kv_cache_update_into(x, 0, c, None, 0, 2, 1, 16, 8, 8, a, s) == EINVAL  # no out
+    assert L.sph_kv_cache_update_into(x, 0, None, o, 0, 2, 1, 16, 8, 8, a, s) == EINVAL  # kept rows, no cache
+    assert L.sph_kv_cache_update_into(None, 0, c, o, 0, 2, 1, 16, 8, 8, a, s) == EINVAL  # no src
+    assert L.sph_kv_cache_update_into(x, 0, c, c, 0, 2, 1, 16, 8, 8, a, s) == EINVAL     # out is cache
+    assert L.sph_kv_cache_update_into(x, 0, c, c + 64, 0, 2, 1, 16, 8, 8, a, s) == EINVAL  # out overlaps cache
+    assert L.sph_kv_cache_update_into(o, 0, c, o, 0, 2, 1, 16, 8, 8, a, s) == EINVAL     # src inside out
+    assert L.sph_kv_cache_update_into(x, 0, c, o, 8, 2, 1, 16, 8, 8, a, s) == EINVAL     # Q8_0 at hd 16
+    torch.cuda.synchronize()
+    assert n.value == -7 and torch.equal(cache, before) and torch.equal(out, out_before)
