@@ -3,19 +3,27 @@
 
 Headline step: one fused residual-add + RMSNorm launch over 16384 x 4096 f32
 (Llama-3-8B width, eps 1e-5) — x and residual in, normed rows and the updated
-residual out, every input resident in HBM before timing starts. The printed
+residual out, every input resident in HBM before timing starts. The last
 JSON line reports that kernel's achieved HBM bandwidth (algorithmic bytes x
 launches / the time of the K back-to-back launches between one HIP event pair
-on their stream) against MI355X's 8 TB/s,
-the single-thread CPU oracle on a bounded sample of the same workload, and
-(``ops``) the same measurement for every other op at its configuration shape.
+on their stream; one untimed launch goes ahead of the start event so the
+region holds GPU work only) against MI355X's 8 TB/s, the single-thread CPU
+oracle on a bounded sample of the same workload, and (``ops``, compact) the
+same measurement for the rows of the five benchmark configurations. The line
+before it (``ops_full``) holds every row in full, the configuration rows and
+the others (other dtypes and table formats, LayerNorm, erf-GELU, the layout
+helpers, the decode engine).
 
 Every throughput row rotates buffer sets totalling at least 512 MiB
 (``rotation_bytes``), so the 256 MB Infinity Cache cannot serve a repeat; the
-gather rows rotate whole tables and id sets. The latency-bound Qwen2.5-0.5B
-rows report kernel durations from a rocprofv3 kernel trace of a child process
-(``us``), beside the per-launch time of a replayed HIP graph of back-to-back
-launches (``graph_us``) and one call's latency from the host (``call_us``).
+gather rows rotate whole tables and id sets. Each starts after half a second
+of idle and at least 25 ms of warm-up launches. Rows whose launches take under
+25 us are timed as back-to-back launches replayed from a HIP graph (Python
+issues a launch in ~10 us, which would otherwise be what the events measure).
+The latency-bound Qwen2.5-0.5B rows report kernel durations from a rocprofv3
+kernel trace of a child process (``us``), beside the per-launch time of a
+replayed HIP graph of back-to-back launches (``graph_us``) and one call's
+latency from the host (``call_us``).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-ops] [--cpu-seconds S]
 """
@@ -27,6 +35,7 @@ import json
 import os
 import re
 import shutil
+import signal
 import subprocess
 import sys
 import tempfile
@@ -49,6 +58,10 @@ HEADLINE_KERNEL = "rms_rows_vec<float, float, float, 1, 16, 1, true>"
 ROTATION_MIN = 1 << 29
 # Launches per latency-bound row in the kernel-trace child (the first C1_SKIP are warm-up).
 C1_LAUNCHES, C1_SKIP = 220, 20
+# Throughput rows whose event-timed launches take less than this (ms) are re-timed from a HIP graph.
+SHORT_MS = 0.025
+# Idle seconds before each throughput row (see op_table).
+SETTLE_S = 0.5
 
 
 def parse():
@@ -95,16 +108,20 @@ def time_launches(torch, fn, sets, warmup: int, steps: int):
 def time_region(torch, fn, sets, warmup: int, steps: int):
     """Run fn(set) over rotating buffer sets: `warmup` untimed, then exactly `steps` timed launches
     between one HIP event pair on the current stream (the stream every op is enqueued on), with
-    synchronizations before and after. Returns (ms for the whole region, host wall seconds)."""
+    synchronizations before and after. One more untimed launch goes ahead of the start event: the GPU
+    runs it while the host queues the timed ones, so the region holds the `steps` launches back to
+    back and not the host's latency to queue the first of them. Returns (ms for the whole region,
+    host wall seconds)."""
     stream = torch.cuda.current_stream()
     for i in range(warmup):
         fn(sets[i % len(sets)])
     torch.cuda.synchronize()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
+    fn(sets[warmup % len(sets)])  # the lead launch (untimed)
     start.record(stream)
     for i in range(steps):
-        fn(sets[i % len(sets)])
+        fn(sets[(warmup + 1 + i) % len(sets)])
     end.record(stream)
     torch.cuda.synchronize()
     return start.elapsed_time(end), time.perf_counter() - t0
@@ -280,10 +297,12 @@ class Row:
     (rows / tokens / ids), make_set(i) -> the i-th buffer set, fn(set) -> one launch, and cpu() ->
     (oracle call, units it covers) for the CPU column."""
 
-    def __init__(self, name, shape, dtype, alg_bytes, units, unit_name, make_set, fn, cpu=None, latency=False):
+    def __init__(self, name, shape, dtype, alg_bytes, units, unit_name, make_set, fn, cpu=None, latency=False,
+                 cfg=None):
         self.name, self.shape, self.dtype, self.alg_bytes = name, shape, dtype, alg_bytes
         self.units, self.unit_name, self.make_set, self.fn, self.cpu = units, unit_name, make_set, fn, cpu
         self.latency = latency
+        self.cfg = cfg  # the benchmark configuration (1-5) this row measures, or None for an extra row
 
 
 def q_table(torch, dev, g, vocab, hidden, block, nbytes, d_off, nd, dmin=0.0005, dmax=0.02, signed_q=False):
@@ -312,19 +331,29 @@ def latency_rows(torch, ops, dev, orc, nrm, cpu_gather):
                         lambda i, T1=T1: (gen(torch, (T1, H), 100 + i, dev, f32), torch.empty(T1, H, device=dev)),
                         lambda s, w=w: ops.rms_norm(s[0], w, 1e-6, out=s[1]),
                         lambda T1=T1: (lambda x=nrm(T1, H), w=nrm(H, scale=0.1, mean=1.0):
-                                       orc.rms_norm(x, w, 1e-6), T1), latency=True))
+                                       orc.rms_norm(x, w, 1e-6), T1), latency=True, cfg=1))
+        # RoPE as the trait path's apply_rope_positions runs it: up to 8192 (token, pair) angles from the
+        # host (cos / sin tables for exactly these positions, device-resident), more evaluated on the
+        # device. Each row's other route is reported beside it as an extra row.
         pos = torch.arange(T1, dtype=torch.int32, device=dev)
-        rows.append(Row(f"rope_neox qwen T={T1}", f"q14+k2 x {T1} x 64", "f32", 2 * 16 * T1 * 64 * 4, T1, "tokens",
-                        lambda i, T1=T1: (gen(torch, (1, 14, T1, 64), 110 + i, dev, f32),
-                                          gen(torch, (1, 2, T1, 64), 120 + i, dev, f32)),
-                        lambda s, pos=pos: ops.rope_(s[0], s[1], pos, 1e6),
-                        lambda T1=T1: (lambda q=nrm(1, 16, T1, 64), p=np.arange(T1): orc.apply_rope(q, p, 1e6), T1),
-                        latency=True))
+        cs, sn = (torch.from_numpy(t).to(dev) for t in ops.rope_table(None, 64, 1e6, n=T1))
+        qk = (lambda i, T1=T1: (gen(torch, (1, 14, T1, 64), 110 + i, dev, f32),
+                                gen(torch, (1, 2, T1, 64), 120 + i, dev, f32)))
+        rope_cpu = (lambda T1=T1: (lambda q=nrm(1, 16, T1, 64), p=np.arange(T1): orc.apply_rope(q, p, 1e6), T1))
+        tab_row = Row(f"rope_neox qwen T={T1}" + (" tables" if T1 > 1 else ""), f"q14+k2 x {T1} x 64", "f32",
+                      2 * 16 * T1 * 64 * 4 + T1 * 32 * 8, T1, "tokens", qk,
+                      lambda s, cs=cs, sn=sn: ops.rope_cached_(s[0], s[1], cs, sn), rope_cpu, latency=True,
+                      cfg=1 if T1 * 32 <= 8192 else None)
+        dev_row = Row(f"rope_neox qwen T={T1}" + (" device-angles" if T1 * 32 <= 8192 else ""), f"q14+k2 x {T1} x 64",
+                      "f32", 2 * 16 * T1 * 64 * 4, T1, "tokens", qk, lambda s, pos=pos: ops.rope_(s[0], s[1], pos, 1e6),
+                      rope_cpu, latency=True, cfg=None if T1 * 32 <= 8192 else 1)
+        rows += [tab_row, dev_row] if tab_row.cfg else [dev_row, tab_row]
         rows.append(Row(f"swiglu qwen T={T1}", f"{T1}x4864", "f32", 3 * T1 * 4864 * 4, T1, "rows",
                         lambda i, T1=T1: (gen(torch, (T1, 4864), 130 + i, dev, f32),
                                           gen(torch, (T1, 4864), 140 + i, dev, f32), torch.empty(T1, 4864, device=dev)),
                         lambda s: ops.swiglu(s[0], s[1], out=s[2]),
-                        lambda T1=T1: (lambda g=nrm(T1, 4864), u=nrm(T1, 4864): orc.swiglu(g, u), T1), latency=True))
+                        lambda T1=T1: (lambda g=nrm(T1, 4864), u=nrm(T1, 4864): orc.swiglu(g, u), T1), latency=True,
+                        cfg=1))
     vocab_q, hid_q = 151936, 896
     g = torch.Generator(device=dev).manual_seed(11)
     tq = q_table(torch, dev, g, vocab_q, hid_q, 32, 34, 0, 1, 0.001, 0.05, signed_q=True)
@@ -335,7 +364,7 @@ def latency_rows(torch, ops, dev, orc, nrm, cpu_gather):
                         T1 * (952 + 4 + hid_q * 4), T1, "rows",
                         lambda i, T1=T1, ids=ids: (ids[i % 2], torch.empty(T1, hid_q, device=dev)),
                         lambda s: ops.embed(tq, L.Q8_0, vocab_q, hid_q, s[0], out=s[1]),
-                        lambda T1=T1: cpu_gather(L.Q8_0, 32, 34, 0, 1, hid_q, T1), latency=True))
+                        lambda T1=T1: cpu_gather(L.Q8_0, 32, 34, 0, 1, hid_q, T1), latency=True, cfg=1))
     return rows, tq, vocab_q
 
 
@@ -351,17 +380,22 @@ def latency_kernel_times(rows_names):
         env = dict(os.environ, TMPDIR=tmp)
         cmd = [prof, "--kernel-trace", "--output-format", "csv", "-d", tmp, "-o", "c1", "--",
                sys.executable, str(ROOT / "bench.py"), "--latency-child"]
+        # Its own process group, so a time-out ends the profiled program too, not only rocprofv3.
+        child = subprocess.Popen(cmd, cwd=tmp, env=env, stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True,
+                                 start_new_session=True)
         try:
-            res = subprocess.run(cmd, cwd=tmp, env=env, capture_output=True, text=True, timeout=300)
+            out, _ = child.communicate(timeout=300)
         except subprocess.TimeoutExpired:
+            os.killpg(child.pid, signal.SIGKILL)
+            child.communicate()
             return None, "kernel-trace child timed out"
         plan = None
-        for line in res.stdout.splitlines():
+        for line in out.splitlines():
             if line.startswith('{"latency_child"'):
                 plan = json.loads(line)
         traces = list(Path(tmp).rglob("c1_kernel_trace.csv"))
         if plan is None or not traces:
-            return None, f"kernel-trace child failed (rc {res.returncode})"
+            return None, f"kernel-trace child failed (rc {child.returncode})"
         with open(traces[0], newline="") as f:
             recs = [r for r in csv.DictReader(f) if "sph::" in r["Kernel_Name"]]
         recs.sort(key=lambda r: int(r["Dispatch_Id"]))
@@ -434,7 +468,7 @@ def op_table(torch, ops, dev, only=None, cpu_budget=0.0, profile_launches=0, ker
             del sets
             torch.cuda.empty_cache()
             return
-        row = {"op": r.name, "shape": r.shape, "dtype": r.dtype}
+        row = {"op": r.name, "shape": r.shape, "dtype": r.dtype, "cfg": r.cfg}
         if r.latency:  # kernel time filled in from the kernel trace; graph replay and one call meanwhile
             warm(torch, r.fn, sets)
             per, _ = time_launches(torch, r.fn, sets, 0, 20)
@@ -442,7 +476,18 @@ def op_table(torch, ops, dev, only=None, cpu_budget=0.0, profile_launches=0, ker
             row["call_us"] = round(median(per) * 1e3, 2)
             ms = row["graph_us"] * 1e-3
         else:  # throughput: the median of 5 regions of back-to-back launches between one event pair
+            # The GPU idles briefly first: a VALU-heavy row (f32 SwiGLU or GELU) leaves it in a lower
+            # power state for a while, which slowed the next row's table-lookup kernel by ~5 %; each row's
+            # warm-up then brings the GPU to that row's own steady state.
+            torch.cuda.synchronize()
+            time.sleep(SETTLE_S)
             ms = time_regions(torch, r.fn, sets)
+            if ms < SHORT_MS:
+                # Python issues a launch in ~10 us: below this the GPU waits on the host between launches,
+                # so time the same launches back to back from a replayed HIP graph instead.
+                row["event_us"] = round(ms * 1e3, 2)
+                ms = time_graph(torch, r.fn, sets)
+                row["us_method"] = "HIP graph replay, per launch"
         gbs = r.alg_bytes / (ms * 1e-3) / 1e9
         row.update({"us": round(ms * 1e3, 2), "GB/s": round(gbs, 1), "pct_peak": round(100 * gbs / PEAK_GBS, 1),
                     f"{r.unit_name}/s": round(r.units / (ms * 1e-3), 1), "alg_bytes": r.alg_bytes,
@@ -468,7 +513,7 @@ def op_table(torch, ops, dev, only=None, cpu_budget=0.0, profile_launches=0, ker
                                   torch.empty(rows, dim, device=dev, dtype=dt)),
                 lambda s, w=w: ops.add_rms_norm(s[0], s[1], w, 1e-5, out=s[2]),
                 lambda: (lambda x=nrm(256, dim), r=nrm(256, dim), w=nrm(dim, scale=0.1, mean=1.0):
-                         orc.add_rms_norm(x, r, w, 1e-5), 256)))
+                         orc.add_rms_norm(x, r, w, 1e-5), 256), cfg=2))
     # Plain RMSNorm at the same width (the norm the fused kernel's second half is)
     for dt, tag in ((f32, "f32"), (f16, "f16"), (bf16, "bf16")):
         w = gen(torch, (dim,), 3, dev, f32, 0.1, 1.0)
@@ -488,7 +533,7 @@ def op_table(torch, ops, dev, only=None, cpu_budget=0.0, profile_launches=0, ker
                     lambda i, dt=dt: (gen(torch, (1, 32, T, D), 50 + i, dev, dt), gen(torch, (1, 8, T, D), 60 + i, dev, dt)),
                     lambda s, il=il: ops.rope_(s[0], s[1], pos, 5e5, interleaved=il),
                     lambda il=il: (lambda x=nrm(1, 40, 32, D), p=np.arange(4000, 4032):
-                                   orc.apply_rope_partial_scaled(x, p, 5e5, D, 1.0, il), 32)))
+                                   orc.apply_rope_partial_scaled(x, p, 5e5, D, 1.0, il), 32), cfg=3))
     # C4: SwiGLU [8192, 14336] f16, GELU-tanh [8192, 10240] f16
     n = 8192 * 14336
     for dt, tag, es, seed in ((f16, "f16", 2, 70), (f32, "f32", 4, 75)):
@@ -497,7 +542,8 @@ def op_table(torch, ops, dev, only=None, cpu_budget=0.0, profile_launches=0, ker
                                              gen(torch, (8192, 14336), seed + 10 + i, dev, dt, 2.0),
                                              torch.empty(8192, 14336, device=dev, dtype=dt)),
                 lambda s: ops.swiglu(s[0], s[1], out=s[2]),
-                lambda: (lambda g=nrm(64, 14336, scale=2.0), u=nrm(64, 14336, scale=2.0): orc.swiglu(g, u), 64)))
+                lambda: (lambda g=nrm(64, 14336, scale=2.0), u=nrm(64, 14336, scale=2.0): orc.swiglu(g, u), 64),
+                cfg=4 if dt == f16 else None))
     if profile_launches == 0 or not only or "gelu_tanh" in only or "gelu_erf" in only:
         ops.init(dev)
     n = 8192 * 10240
@@ -507,7 +553,7 @@ def op_table(torch, ops, dev, only=None, cpu_budget=0.0, profile_launches=0, ker
                 lambda i, dt=dt, seed=seed: (gen(torch, (8192, 10240), seed + i, dev, dt, 2.0),
                                              torch.empty(8192, 10240, device=dev, dtype=dt)),
                 lambda s: ops.gelu_tanh(s[0], out=s[1]),
-                lambda: (lambda x=nrm(64, 10240, scale=2.0): orc.gelu(x), 64)))
+                lambda: (lambda x=nrm(64, 10240, scale=2.0): orc.gelu(x), 64), cfg=4 if dt == f16 else None))
     # LayerNorm (+ bias), erf-GELU and the bias add: the encoder-family norm / activation path
     wl, bl = gen(torch, (dim,), 4, dev, f32, 0.1, 1.0), gen(torch, (dim,), 5, dev, f32, 0.1)
     for dt, tag, es in ((f32, "f32", 4), (f16, "f16 (f32 w,b)", 2)):
@@ -550,6 +596,14 @@ def op_table(torch, ops, dev, only=None, cpu_budget=0.0, profile_launches=0, ker
             lambda s: ops.kv_cache_update(s[0], s[1], T),
             lambda: (lambda x=nrm(8, 1, D), c=np.zeros((8, T, D), np.uint16):
                      orc.kv_cache_update(x, c, L.F16, 8, 1, D, T, T), 1)))
+    # The same step into a second cache (the caller then uses it as its cache): each kept row moves once.
+    run(Row("kv_cache_update_into", f"8x1x{D} -> full cache 8x{T}x{D}", "f32->f16",
+            2 * 8 * (T - 1) * D * 2 + 8 * D * (4 + 2), 1, "tokens",
+            lambda i: (gen(torch, (8, 1, D), 210 + i, dev, f32), gen(torch, (8, T, D), 220 + i, dev, f16),
+                       torch.empty(8, T, D, device=dev, dtype=f16)),
+            lambda s: ops.kv_cache_update_into(s[0], s[1], s[2], T),
+            lambda: (lambda x=nrm(8, 1, D), c=np.zeros((8, T, D), np.uint16):
+                     orc.kv_cache_update(x, c, L.F16, 8, 1, D, T, T), 1)))
 
     def cpu_gather(dt, block, nbytes, d_off, nd, hidden, n):
         """The oracle's gather of n ids from a 2048-row table of the same format (cost per row does not
@@ -588,7 +642,7 @@ def op_table(torch, ops, dev, only=None, cpu_budget=0.0, profile_launches=0, ker
                     n_ids * (row_bytes + 4 + hidden * 4), n_ids, "rows", make_set,
                     lambda s, dt=dt: ops.embed(s[0], dt, vocab, hidden, s[1], out=s[2]),
                     lambda dt=dt, block=block, nbytes=nbytes, d_off=d_off, nd=nd:
-                        cpu_gather(dt, block, nbytes, d_off, nd, hidden, 1024)))
+                        cpu_gather(dt, block, nbytes, d_off, nd, hidden, 1024), cfg=5 if dt == L.Q4_K else None))
     # C1: Qwen2.5-0.5B layer ops (latency-bound, reported only)
     lrows, tq, vocab_q = latency_rows(torch, ops, dev, orc, nrm, cpu_gather)
     first_latency = len(res)
@@ -627,6 +681,45 @@ def calibration_copies(torch, ops, dev, warmup, steps):
     time_launches(torch, lambda i: ops.add(a[i], zero, out=o[i]), [0, 1], warmup, steps)
     return {"copy_bytes_read": n * 4, "copy_bytes_written": n * 4,
             "calibration_kernels": ["torch copy_", "torch neg", "sph add (a + 0)"]}
+
+
+def reap_children() -> int:
+    """Child processes of this run still alive (there should be none: the kernel-trace child is waited
+    for); any found are terminated and waited for, so none outlives bench.py. Returns how many were found."""
+    import psutil
+    kids = psutil.Process().children(recursive=True)
+    for k in kids:
+        try:
+            k.terminate()
+        except psutil.NoSuchProcess:
+            pass
+    psutil.wait_procs(kids, timeout=5)
+    return len(kids)
+
+
+def cpu_model() -> str:
+    """The host CPU's model name (/proc/cpuinfo), or the platform's processor string."""
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+    return platform.processor() or "unknown CPU"
+
+
+# Keys of an op-table row kept in the final line's compact form (the full rows go to the line before it).
+COMPACT = ("op", "shape", "dtype", "us", "GB/s", "pct_peak", "graph_us", "rotation_bytes", "gpu_vs_cpu")
+
+
+def compact(row: dict) -> dict:
+    """A configuration row as the final line carries it: identity, kernel time, bandwidth, % of peak, the
+    bytes its buffers rotate through (throughput rows) or its graph-replay time (latency rows), and the
+    GPU/CPU rate ratio."""
+    out = {k: row[k] for k in COMPACT if k in row and row[k] is not None}
+    out["cfg"] = row["cfg"]
+    return out
 
 
 def main():
@@ -678,7 +771,8 @@ def main():
         sample_bytes = 4 * n_rows * dim * 4 + dim * 4
         cpu = {"value": round(sample_bytes / sec / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
                "sample": f"oracle add_rms_norm on {n_rows}x{dim} f32 rows (1/8 of the workload), {reps} reps "
-                         f"in {args.cpu_seconds:.0f} s, 1 thread, {os.cpu_count()} host cores visible",
+                         f"in {args.cpu_seconds:.0f} s, 1 thread of {cpu_model()} ({os.cpu_count()} host cores "
+                         f"visible)",
                "rows_per_s": round(n_rows / sec, 1)}
 
     line = {
@@ -708,12 +802,21 @@ def main():
     }
     if not args.no_ops:
         only = set(args.only.split(",")) if args.only else None
-        line["ops"] = op_table(torch, ops, dev, only, 0.0 if args.no_cpu else args.op_cpu_seconds,
-                               kernel_trace=not args.no_kernel_trace)
+        rows = op_table(torch, ops, dev, only, 0.0 if args.no_cpu else args.op_cpu_seconds,
+                        kernel_trace=not args.no_kernel_trace)
+        # Every row in full on a line of its own, before the final line; the final line keeps the rows of
+        # the five benchmark configurations in compact form.
+        extra = {"ops_full": rows}
         if not args.no_cpu:
-            line["ops_cpu"] = ("cpu_*/s: the oracle (the reference's algorithm restated in C, f32, one thread) on "
-                               "cpu_sample rows / tokens / ids of each shape, timed on this host; gpu_vs_cpu = the "
-                               "ratio of the two rates")
+            extra["ops_cpu"] = ("cpu_*/s: the oracle (the reference's algorithm restated in C, f32, one thread) on "
+                                "cpu_sample rows / tokens / ids of each shape, timed on this host; gpu_vs_cpu = the "
+                                "ratio of the two rates")
+        print(json.dumps(extra), flush=True)
+        line["ops"] = [compact(r) for r in rows if r.get("cfg") is not None]
+        line["ops_note"] = ("rows of configurations 1-5; us = kernel time (latency rows: rocprofv3 kernel trace "
+                            "median, beside graph_us per replayed launch), pct_peak of 8 TB/s, gpu_vs_cpu = rate "
+                            "over the one-thread oracle's; every row in full on the line before")
+    line["children_left"] = reap_children()
     print(json.dumps(line), flush=True)
 
 
