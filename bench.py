@@ -668,6 +668,20 @@ def op_table(torch, ops, dev, only=None, cpu_budget=0.0, profile_launches=0, ker
     return res
 
 
+def box_copy(torch, dev, warmup, steps):
+    """This box's streaming speed, for reading the headline across boxes (MI355X boxes differ by a few per
+    cent): torch's `neg` (a kernel this library did not write) over the headline's byte count, 512 MiB read
+    and 512 MiB written per launch, timed like the headline right after it."""
+    n = 2 * 16384 * 4096
+    sets = [(gen(torch, (n,), 90 + i, dev, torch.float32), torch.empty(n, device=dev)) for i in range(2)]
+    ms, _ = time_region(torch, lambda s: torch.neg(s[0], out=s[1]), sets, warmup, steps)
+    gbs = 2 * n * 4 / (ms / steps * 1e-3) / 1e9
+    del sets
+    torch.cuda.empty_cache()
+    return {"kernel": "torch neg, 2 x 16384 x 4096 f32 (read + write)", "GB/s": round(gbs, 1),
+            "pct_peak": round(100 * gbs / PEAK_GBS, 1)}
+
+
 def calibration_copies(torch, ops, dev, warmup, steps):
     """Copies of known size for the HBM counters (2 x 16384 x 4096 f32 = 512 MiB read and 512 MiB
     written per launch): torch's `copy_` and `neg` (kernels this library did not write), then the
@@ -758,6 +772,7 @@ def main():
     avg_ms = region_ms / args.steps
     achieved = alg_bytes / (avg_ms * 1e-3) / 1e9
     value = alg_bytes * args.steps / (region_ms * 1e-3) / 1e9
+    box = box_copy(torch, dev, args.warmup, args.steps)
 
     cpu = None
     if not args.no_cpu:
@@ -796,6 +811,7 @@ def main():
                      "kernel": HEADLINE_KERNEL, "alg_bytes_per_launch": alg_bytes,
                      "avg_launch_us": round(avg_ms * 1e3, 2)},
         "cpu_baseline": cpu,
+        "box_copy": box,
         "timing": {"region_ms": round(region_ms, 3), "host_wall_ms": round(wall * 1e3, 3),
                    "rotation_bytes": rot_bytes,
                    "method": "one HIP event pair around the timed launches on their stream"},
