@@ -80,10 +80,12 @@ def test_f32_activation_every_input(dev, orc, name):
 
 @pytest.mark.parametrize("half", ["f16", "bf16"])
 def test_f32_to_half_every_input(dev, orc, half):
-    """Every kernel that stores f16 / bf16 narrows with the same device helper
-    (v_cvt_f16_f32 / v_cvt_pk_bf16_f32). kv_append from an f32 source into a half
-    cache is that narrowing alone; the oracle's is half's from_f32 (round bit and
-    sticky bits, NaN quieted with 0x40 for bf16). Bar: bit-exact, NaN included."""
+    """Every kernel that stores f16 / bf16 words narrows pairs with the same device
+    helpers, narrow2_f16 (v_cvt_pk_f16_f32) and narrow2_bf16 (v_cvt_pk_bf16_f32).
+    kv_append from an f32 source into a half cache at head_dim 128 (8-element
+    items) is that packed narrowing alone, so this sweep pins the packed
+    conversion over every f32 input; the oracle's is half's from_f32 (round bit
+    and sticky bits, NaN quieted with 0x40 for bf16). Bar: bit-exact, NaN included."""
     tdt = torch.float16 if half == "f16" else torch.bfloat16
     fn = getattr(orc.lib(), "sor_f32_to_f16_n" if half == "f16" else "sor_f32_to_bf16_n")
     nthreads = max(1, min(16, os.cpu_count() or 1))
