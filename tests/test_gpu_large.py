@@ -128,3 +128,29 @@ def test_embed_past_the_token_chunk_and_2g_outputs(dev, orc):
         got = to_np(out[lo:hi])
         want = orc.embed_tokens(table.reshape(-1), Q8_0, vocab, hidden, to_np(ids[lo:hi]).view(np.uint32))
         assert np.array_equal(got.view(np.uint32), want.reshape(hi - lo, hidden).view(np.uint32))
+
+
+@pytest.mark.parametrize("q8", [False, True], ids=["f16", "q8_0"])
+def test_kv_cache_update_past_the_head_chunk(dev, orc, q8):
+    """65535 + 100 heads: the window kernels split heads across launches (grid y holds at most 65535);
+    both forms of the update (in place and into a second cache) match the oracle on every row."""
+    n_kv, hd, max_seq, cur = 65535 + 100, 32, 8, 8
+    code = Q8_0 if q8 else 1
+    row = hd // 32 * 34 if q8 else hd
+    g = torch.Generator(device=dev).manual_seed(21)
+    src = torch.randn(n_kv, 1, hd, generator=g, device=dev)
+    if q8:
+        cache = torch.randint(0, 256, (n_kv, max_seq, row), generator=g, device=dev, dtype=torch.int32).to(torch.uint8)
+    else:
+        cache = torch.randn(n_kv, max_seq, hd, generator=g, device=dev).half()
+    before = to_np(cache).copy()
+    want = before.copy()
+    assert orc.kv_cache_update(to_np(src), want, code, n_kv, 1, hd, max_seq, cur) == max_seq
+    print(f"case kv_cache_update_into {n_kv} heads {'q8_0' if q8 else 'f16'}", flush=True)
+    out = torch.zeros_like(cache)
+    assert ops.kv_cache_update_into(src, cache, out, cur) == max_seq
+    assert np.array_equal(to_np(out).view(np.uint8), want.view(np.uint8))
+    assert np.array_equal(to_np(cache).view(np.uint8), before.view(np.uint8))
+    print(f"case kv_cache_update in place {n_kv} heads {'q8_0' if q8 else 'f16'}", flush=True)
+    assert ops.kv_cache_update(src, cache, cur) == max_seq
+    assert np.array_equal(to_np(cache).view(np.uint8), want.view(np.uint8))
