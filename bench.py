@@ -231,7 +231,7 @@ def gen(torch, shape, seed, dev, dtype, std=1.0, mean=0.0):
     return (torch.randn(shape, generator=g, device=dev) * std + mean).to(dtype)
 
 
-def headline(torch, ops, dev, args):
+def headline(torch, ops, dev, args, clocks=None):
     rows, dim = 16384, 4096
     f32 = torch.float32
     w = gen(torch, (dim,), 3, dev, f32, 0.1, 1.0)
@@ -242,7 +242,11 @@ def headline(torch, ops, dev, args):
     def fn(s):
         ops.add_rms_norm(s[0], s[1], w, 1e-5, out=s[2])
 
-    region_ms, wall = time_region(torch, fn, sets, args.warmup, args.steps)
+    if clocks is not None:
+        with clocks:
+            region_ms, wall = time_region(torch, fn, sets, args.warmup, args.steps)
+    else:
+        region_ms, wall = time_region(torch, fn, sets, args.warmup, args.steps)
     alg_bytes = 4 * rows * dim * 4 + dim * 4  # read x, residual, weight; write y, residual
     return rows, dim, alg_bytes, region_ms, wall, sum(set_bytes(torch, s) for s in sets)
 
@@ -298,11 +302,14 @@ class Row:
     (oracle call, units it covers) for the CPU column."""
 
     def __init__(self, name, shape, dtype, alg_bytes, units, unit_name, make_set, fn, cpu=None, latency=False,
-                 cfg=None):
+                 cfg=None, ref=None):
         self.name, self.shape, self.dtype, self.alg_bytes = name, shape, dtype, alg_bytes
         self.units, self.unit_name, self.make_set, self.fn, self.cpu = units, unit_name, make_set, fn, cpu
         self.latency = latency
         self.cfg = cfg  # the benchmark configuration (1-5) this row measures, or None for an extra row
+        # (label, fn(set)): a torch kernel with the same memory traffic on the same buffers (a copy-like
+        # reference: the same box and buffer placement, a kernel this library did not write), or None
+        self.ref = ref
 
 
 def q_table(torch, dev, g, vocab, hidden, block, nbytes, d_off, nd, dmin=0.0005, dmax=0.02, signed_q=False):
@@ -430,7 +437,7 @@ def latency_child():
     print(json.dumps({"latency_child": True, "launches": C1_LAUNCHES, "rows": [r.name for r in rows]}), flush=True)
 
 
-def op_table(torch, ops, dev, only=None, cpu_budget=0.0, profile_launches=0, kernel_trace=True):
+def op_table(torch, ops, dev, only=None, cpu_budget=0.0, profile_launches=0, kernel_trace=True, clocks=None):
     """Per-op GB/s at each configuration shape (after >= 25 ms of warm-up launches, the median of 5
     regions of back-to-back launches between one event pair, over buffer sets rotating >= 512 MiB;
     latency-bound rows: kernel durations from a rocprofv3 trace, graph replay and one call's latency),
@@ -481,13 +488,30 @@ def op_table(torch, ops, dev, only=None, cpu_budget=0.0, profile_launches=0, ker
             # warm-up then brings the GPU to that row's own steady state.
             torch.cuda.synchronize()
             time.sleep(SETTLE_S)
-            ms = time_regions(torch, r.fn, sets)
+            if clocks is not None and clocks.dir is not None:
+                clocks.samples = []
+                with clocks:
+                    ms = time_regions(torch, r.fn, sets)
+                vals = [v for v in clocks.samples if v is not None]
+                if vals:
+                    row["sclk_mhz"] = median(vals)
+            else:
+                ms = time_regions(torch, r.fn, sets)
             if ms < SHORT_MS:
                 # Python issues a launch in ~10 us: below this the GPU waits on the host between launches,
                 # so time the same launches back to back from a replayed HIP graph instead.
                 row["event_us"] = round(ms * 1e3, 2)
                 ms = time_graph(torch, r.fn, sets)
                 row["us_method"] = "HIP graph replay, per launch"
+            if r.ref is not None:
+                # torch's kernel with the same traffic, timed the same way on the same buffers: where buffers
+                # land in HBM moves a streaming kernel by ~2-3 %, and boxes differ by a few per cent; this
+                # reference shares both with the row.
+                label, rfn = r.ref
+                rms = time_regions(torch, rfn, sets)
+                if rms < SHORT_MS:
+                    rms = time_graph(torch, rfn, sets)
+                row["torch_ref"], row["torch_ref_us"] = label, round(rms * 1e3, 2)
         gbs = r.alg_bytes / (ms * 1e-3) / 1e9
         row.update({"us": round(ms * 1e3, 2), "GB/s": round(gbs, 1), "pct_peak": round(100 * gbs / PEAK_GBS, 1),
                     f"{r.unit_name}/s": round(r.units / (ms * 1e-3), 1), "alg_bytes": r.alg_bytes,
@@ -521,7 +545,8 @@ def op_table(torch, ops, dev, only=None, cpu_budget=0.0, profile_launches=0, ker
         run(Row("rms_norm", f"{rows}x{dim}", tag + " (f32 w)", 2 * rows * dim * es + dim * 4, rows, "rows",
                 lambda i, dt=dt: (gen(torch, (rows, dim), 20 + i, dev, dt), torch.empty(rows, dim, device=dev, dtype=dt)),
                 lambda s, w=w: ops.rms_norm(s[0], w, 1e-5, out=s[1]),
-                lambda: (lambda x=nrm(256, dim), w=nrm(dim, scale=0.1, mean=1.0): orc.rms_norm(x, w, 1e-5), 256)))
+                lambda: (lambda x=nrm(256, dim), w=nrm(dim, scale=0.1, mean=1.0): orc.rms_norm(x, w, 1e-5), 256),
+                ref=("torch neg", lambda s: torch.neg(s[0], out=s[1]))))
     # C3: RoPE, Q 32 + K 8 heads, T 8192, head_dim 128, in place
     T, D = 8192, 128
     pos = torch.arange(T, dtype=torch.int32, device=dev)
@@ -533,7 +558,8 @@ def op_table(torch, ops, dev, only=None, cpu_budget=0.0, profile_launches=0, ker
                     lambda i, dt=dt: (gen(torch, (1, 32, T, D), 50 + i, dev, dt), gen(torch, (1, 8, T, D), 60 + i, dev, dt)),
                     lambda s, il=il: ops.rope_(s[0], s[1], pos, 5e5, interleaved=il),
                     lambda il=il: (lambda x=nrm(1, 40, 32, D), p=np.arange(4000, 4032):
-                                   orc.apply_rope_partial_scaled(x, p, 5e5, D, 1.0, il), 32), cfg=3))
+                                   orc.apply_rope_partial_scaled(x, p, 5e5, D, 1.0, il), 32), cfg=3,
+                    ref=("torch _foreach_neg_ (q and k in place, one launch)", lambda s: torch._foreach_neg_([s[0], s[1]]))))
     # C4: SwiGLU [8192, 14336] f16, GELU-tanh [8192, 10240] f16
     n = 8192 * 14336
     for dt, tag, es, seed in ((f16, "f16", 2, 70), (f32, "f32", 4, 75)):
@@ -543,7 +569,7 @@ def op_table(torch, ops, dev, only=None, cpu_budget=0.0, profile_launches=0, ker
                                              torch.empty(8192, 14336, device=dev, dtype=dt)),
                 lambda s: ops.swiglu(s[0], s[1], out=s[2]),
                 lambda: (lambda g=nrm(64, 14336, scale=2.0), u=nrm(64, 14336, scale=2.0): orc.swiglu(g, u), 64),
-                cfg=4 if dt == f16 else None))
+                cfg=4 if dt == f16 else None, ref=("torch mul", lambda s: torch.mul(s[0], s[1], out=s[2]))))
     if profile_launches == 0 or not only or "gelu_tanh" in only or "gelu_erf" in only:
         ops.init(dev)
     n = 8192 * 10240
@@ -553,7 +579,8 @@ def op_table(torch, ops, dev, only=None, cpu_budget=0.0, profile_launches=0, ker
                 lambda i, dt=dt, seed=seed: (gen(torch, (8192, 10240), seed + i, dev, dt, 2.0),
                                              torch.empty(8192, 10240, device=dev, dtype=dt)),
                 lambda s: ops.gelu_tanh(s[0], out=s[1]),
-                lambda: (lambda x=nrm(64, 10240, scale=2.0): orc.gelu(x), 64), cfg=4 if dt == f16 else None))
+                lambda: (lambda x=nrm(64, 10240, scale=2.0): orc.gelu(x), 64), cfg=4 if dt == f16 else None,
+                ref=("torch neg", lambda s: torch.neg(s[0], out=s[1]))))
     # LayerNorm (+ bias), erf-GELU and the bias add: the encoder-family norm / activation path
     wl, bl = gen(torch, (dim,), 4, dev, f32, 0.1, 1.0), gen(torch, (dim,), 5, dev, f32, 0.1)
     for dt, tag, es in ((f32, "f32", 4), (f16, "f16 (f32 w,b)", 2)):
@@ -562,18 +589,21 @@ def op_table(torch, ops, dev, only=None, cpu_budget=0.0, profile_launches=0, ker
                                   torch.empty(rows, dim, device=dev, dtype=dt)),
                 lambda s: ops.layer_norm(s[0], wl, bl, 1e-5, out=s[1]),
                 lambda: (lambda x=nrm(256, dim, scale=2.0, mean=0.5), w=nrm(dim, scale=0.1, mean=1.0),
-                         b=nrm(dim, scale=0.1): orc.layer_norm(x, w, b, 1e-5), 256)))
+                         b=nrm(dim, scale=0.1): orc.layer_norm(x, w, b, 1e-5), 256),
+                ref=("torch neg", lambda s: torch.neg(s[0], out=s[1]))))
     run(Row("add_bias", f"{rows}x{dim}", "f32", 2 * rows * dim * 4 + dim * 4, rows, "rows",
             lambda i: (gen(torch, (rows, dim), 160 + i, dev, f32), torch.empty(rows, dim, device=dev)),
             lambda s: ops.add_bias(s[0], bl, out=s[1]),
-            lambda: (lambda y=nrm(256, dim), b=nrm(dim, scale=0.1): orc.add_bias_last_dim(y, b), 256)))
+            lambda: (lambda y=nrm(256, dim), b=nrm(dim, scale=0.1): orc.add_bias_last_dim(y, b), 256),
+            ref=("torch add (broadcast bias)", lambda s: torch.add(s[0], bl, out=s[1]))))
     n = 12000 * 5120
     for dt, tag, es in ((f32, "f32", 4), (f16, "f16", 2)):
         run(Row("gelu_erf", "12000x5120", tag, 2 * n * es, 12000, "rows",
                 lambda i, dt=dt: (gen(torch, (12000, 5120), 170 + i, dev, dt, 2.0),
                                   torch.empty(12000, 5120, device=dev, dtype=dt)),
                 lambda s: ops.gelu_erf(s[0], out=s[1]),
-                lambda: (lambda x=nrm(64, 5120, scale=2.0): orc.gelu_erf(x), 64)))
+                lambda: (lambda x=nrm(64, 5120, scale=2.0): orc.gelu_erf(x), 64),
+                ref=("torch neg", lambda s: torch.neg(s[0], out=s[1]))))
     # Decode-chain helpers: head transpose of a Llama-3-8B prefill Q, KV-cache append of its K
     T, H, D = 8192, 32, 128
     for dt, tag, es in ((f32, "f32", 4), (f16, "f16", 2)):
@@ -582,12 +612,14 @@ def op_table(torch, ops, dev, only=None, cpu_budget=0.0, profile_launches=0, ker
                 lambda s: ops.transpose_heads(s[0], out=s[1]),
                 lambda es=es: (lambda x=(nrm(64, H, D) if es == 4 else
                                          crng.integers(0, 65536, (64, H, D), dtype=np.uint16)):
-                               orc.transpose_heads(x, 64, H, D), 64)))
+                               orc.transpose_heads(x, 64, H, D), 64),
+                ref=("torch copy_ of the transposed view", lambda s: s[1].copy_(s[0].transpose(0, 1)))))
     run(Row("kv_append", f"8x{T}x{D} -> cache 8x{T}x{D}", "f32->f16", 8 * T * D * (4 + 2), T, "tokens",
             lambda i: (gen(torch, (8, T, D), 190 + i, dev, f32), torch.empty(8, T, D, device=dev, dtype=f16)),
             lambda s: ops.kv_append(s[0], s[1], 0),
             lambda: (lambda x=nrm(8, 64, D), c=np.zeros((8, T, D), np.uint16):
-                     orc.kv_append(x, c, L.F16, 8, 64, D, T, 0), 64)))
+                     orc.kv_append(x, c, L.F16, 8, 64, D, T, 0), 64),
+            ref=("torch copy_ f32 -> f16", lambda s: s[1].copy_(s[0]))))
     # The trait path's cache update on a full cache (decode step past 8192 positions): the window
     # slides one row — every head's 8191 kept rows move down (read + write) — then the new row lands.
     run(Row("kv_cache_update", f"8x1x{D} -> full cache 8x{T}x{D}", "f32->f16",
@@ -668,6 +700,73 @@ def op_table(torch, ops, dev, only=None, cpu_budget=0.0, profile_launches=0, ker
     return res
 
 
+class ClockSampler:
+    """The GPU's engine clock as the driver reports it (sysfs pp_dpm_sclk, the level marked current),
+    sampled every millisecond on a thread while a timed region runs; plus the memory clock and the board power
+    cap, read once. Boxes differ by a few per cent in speed: this is the clock they ran at."""
+
+    def __init__(self, torch):
+        import ctypes
+        self.dir = None
+        self.samples = []
+        try:
+            hip = ctypes.CDLL("libamdhip64.so")
+            buf = ctypes.create_string_buffer(64)
+            if hip.hipDeviceGetPCIBusId(buf, 64, torch.cuda.current_device()) == 0:
+                d = Path("/sys/bus/pci/devices") / buf.value.decode().lower()
+                if (d / "pp_dpm_sclk").exists():
+                    self.dir = d
+        except OSError:
+            pass
+
+    @staticmethod
+    def _current(text):
+        for line in text.splitlines():
+            if line.rstrip().endswith("*"):
+                m = re.search(r"(\d+)\s*Mhz", line, re.I)
+                return int(m.group(1)) if m else None
+        return None
+
+    def __enter__(self):
+        import threading
+        self._stop = threading.Event()
+
+        def run():
+            while not self._stop.wait(0.001):
+                try:
+                    self.samples.append(self._current((self.dir / "pp_dpm_sclk").read_text()))
+                except OSError:
+                    return
+        self._t = threading.Thread(target=run, daemon=True) if self.dir else None
+        if self._t:
+            self._t.start()
+        return self
+
+    def __exit__(self, *exc):
+        if self._t:
+            self._stop.set()
+            self._t.join()
+
+    def report(self):
+        if self.dir is None:
+            return None
+        out = {"sclk_mhz_during_headline": None, "samples": len(self.samples)}
+        vals = [v for v in self.samples if v is not None]
+        if vals:
+            out["sclk_mhz_during_headline"] = {"median": median(vals), "min": min(vals), "max": max(vals)}
+        for name, f in (("sclk_levels", "pp_dpm_sclk"), ("mclk", "pp_dpm_mclk")):
+            try:
+                out[name] = " ".join((self.dir / f).read_text().split())
+            except OSError:
+                out[name] = None
+        caps = sorted(self.dir.glob("hwmon/hwmon*/power1_cap"))
+        try:
+            out["power_cap_w"] = round(int(caps[0].read_text()) / 1e6) if caps else None
+        except (OSError, ValueError):
+            out["power_cap_w"] = None
+        return out
+
+
 def box_copy(torch, dev, warmup, steps):
     """This box's streaming speed, for reading the headline across boxes (MI355X boxes differ by a few per
     cent): torch's `neg` (a kernel this library did not write) over the headline's byte count, 512 MiB read
@@ -724,7 +823,8 @@ def cpu_model() -> str:
 
 
 # Keys of an op-table row kept in the final line's compact form (the full rows go to the line before it).
-COMPACT = ("op", "shape", "dtype", "us", "GB/s", "pct_peak", "graph_us", "rotation_bytes", "gpu_vs_cpu")
+COMPACT = ("op", "shape", "dtype", "us", "GB/s", "pct_peak", "graph_us", "rotation_bytes", "gpu_vs_cpu", "sclk_mhz",
+           "torch_ref_us")
 
 
 def compact(row: dict) -> dict:
@@ -763,7 +863,8 @@ def main():
         cal = calibration_copies(torch, ops, dev, args.warmup, args.steps)
         print(json.dumps({"profile_run": True, "ops": args.only, "launches_per_row": args.warmup + args.steps, **cal}))
         return
-    rows, dim, alg_bytes, region_ms, wall, rot_bytes = headline(torch, ops, dev, args)
+    clocks = ClockSampler(torch)
+    rows, dim, alg_bytes, region_ms, wall, rot_bytes = headline(torch, ops, dev, args, clocks)
     if args.profile_run:
         cal = calibration_copies(torch, ops, dev, args.warmup, args.steps)
         print(json.dumps({"profile_run": True, "headline_avg_us": round(region_ms / args.steps * 1e3, 2),
@@ -812,6 +913,7 @@ def main():
                      "avg_launch_us": round(avg_ms * 1e3, 2)},
         "cpu_baseline": cpu,
         "box_copy": box,
+        "device_clock": clocks.report(),
         "timing": {"region_ms": round(region_ms, 3), "host_wall_ms": round(wall * 1e3, 3),
                    "rotation_bytes": rot_bytes,
                    "method": "one HIP event pair around the timed launches on their stream"},
@@ -819,7 +921,7 @@ def main():
     if not args.no_ops:
         only = set(args.only.split(",")) if args.only else None
         rows = op_table(torch, ops, dev, only, 0.0 if args.no_cpu else args.op_cpu_seconds,
-                        kernel_trace=not args.no_kernel_trace)
+                        kernel_trace=not args.no_kernel_trace, clocks=ClockSampler(torch))
         # Every row in full on a line of its own, before the final line; the final line keeps the rows of
         # the five benchmark configurations in compact form.
         extra = {"ops_full": rows}
