@@ -339,22 +339,19 @@ def latency_rows(torch, ops, dev, orc, nrm, cpu_gather):
                         lambda s, w=w: ops.rms_norm(s[0], w, 1e-6, out=s[1]),
                         lambda T1=T1: (lambda x=nrm(T1, H), w=nrm(H, scale=0.1, mean=1.0):
                                        orc.rms_norm(x, w, 1e-6), T1), latency=True, cfg=1))
-        # RoPE as the trait path's apply_rope_positions runs it: up to 8192 (token, pair) angles from the
-        # host (cos / sin tables for exactly these positions, device-resident), more evaluated on the
-        # device. Each row's other route is reported beside it as an extra row.
+        # RoPE as the trait path's apply_rope_positions runs it: cos / sin from the backend's angle table
+        # (positions 0 .. 63 at least, resident on the device, as rope_cos_sin_cache lays it out) at
+        # device positions; the device sin/cos route beside it as an extra row.
         pos = torch.arange(T1, dtype=torch.int32, device=dev)
-        cs, sn = (torch.from_numpy(t).to(dev) for t in ops.rope_table(None, 64, 1e6, n=T1))
+        cs, sn = (torch.from_numpy(t).to(dev) for t in ops.rope_table(None, 64, 1e6, n=max(64, T1)))
         qk = (lambda i, T1=T1: (gen(torch, (1, 14, T1, 64), 110 + i, dev, f32),
                                 gen(torch, (1, 2, T1, 64), 120 + i, dev, f32)))
         rope_cpu = (lambda T1=T1: (lambda q=nrm(1, 16, T1, 64), p=np.arange(T1): orc.apply_rope(q, p, 1e6), T1))
-        tab_row = Row(f"rope_neox qwen T={T1}" + (" tables" if T1 > 1 else ""), f"q14+k2 x {T1} x 64", "f32",
-                      2 * 16 * T1 * 64 * 4 + T1 * 32 * 8, T1, "tokens", qk,
-                      lambda s, cs=cs, sn=sn: ops.rope_cached_(s[0], s[1], cs, sn), rope_cpu, latency=True,
-                      cfg=1 if T1 * 32 <= 8192 else None)
-        dev_row = Row(f"rope_neox qwen T={T1}" + (" device-angles" if T1 * 32 <= 8192 else ""), f"q14+k2 x {T1} x 64",
-                      "f32", 2 * 16 * T1 * 64 * 4, T1, "tokens", qk, lambda s, pos=pos: ops.rope_(s[0], s[1], pos, 1e6),
-                      rope_cpu, latency=True, cfg=None if T1 * 32 <= 8192 else 1)
-        rows += [tab_row, dev_row] if tab_row.cfg else [dev_row, tab_row]
+        rows.append(Row(f"rope_neox qwen T={T1}", f"q14+k2 x {T1} x 64", "f32", 2 * 16 * T1 * 64 * 4 + T1 * (4 + 32 * 8),
+                        T1, "tokens", qk, lambda s, cs=cs, sn=sn, pos=pos: ops.rope_cached_(s[0], s[1], cs, sn, pos),
+                        rope_cpu, latency=True, cfg=1))
+        rows.append(Row(f"rope_neox qwen T={T1} device-angles", f"q14+k2 x {T1} x 64", "f32", 2 * 16 * T1 * 64 * 4 + 4 * T1,
+                        T1, "tokens", qk, lambda s, pos=pos: ops.rope_(s[0], s[1], pos, 1e6), rope_cpu, latency=True))
         rows.append(Row(f"swiglu qwen T={T1}", f"{T1}x4864", "f32", 3 * T1 * 4864 * 4, T1, "rows",
                         lambda i, T1=T1: (gen(torch, (T1, 4864), 130 + i, dev, f32),
                                           gen(torch, (T1, 4864), 140 + i, dev, f32), torch.empty(T1, 4864, device=dev)),

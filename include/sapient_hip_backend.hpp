@@ -13,6 +13,7 @@
 
 #include <cstddef>
 #include <cstdint>
+#include <memory>
 #include <mutex>
 #include <stdexcept>
 #include <string>
@@ -177,9 +178,12 @@ class HipLlmBackend final : public LlmBackend {
     // max cache size …", and "Tensor dtype is not F32" for an F16 / BF16 cache, tensor.rs:599-602).
     Tensor update_kv_cache(Tensor& cache, size_t current_seq_len, const Tensor& new_k);
 
-    // RoPE calls with at most this many (token, pair) angles evaluate them on the host
-    // (sph_rope_table → sph_rope_cached); larger ones evaluate them on the device (sph_rope).
-    static constexpr size_t kHostAngleMax = 8192;
+    // RoPE reads its angles from a table of positions 0 .. rows - 1 kept per (base, rotary_dim):
+    // the reference's rope_cos_sin_cache (crates/sapient-backends/cpu/src/kernels/rope.rs:140-153),
+    // evaluated on the host with the libm the reference calls (sph_rope_table), held on the device
+    // and grown (doubling) when a call reaches a later position. Calls with a position at or past
+    // this many rows evaluate sin/cos on the device instead (sph_rope).
+    static constexpr size_t kRopeTableMaxRows = size_t(1) << 18;
 
     // The switches as read at construction.
     bool disabled(const char* op) const;
@@ -220,6 +224,19 @@ class HipLlmBackend final : public LlmBackend {
     Tensor fused_swiglu(const Tensor& gate, const Tensor& up);
     Tensor bias_last_dim(const Tensor& y, const Tensor& bias);
     Tensor gather_rows(const Tensor& weight, const std::vector<uint32_t>& ids);
+
+    // One angle table: `rows` positions of rotary_dim / 2 pairs, cos then sin, on the host and in
+    // one device buffer (cos rows, then sin rows).
+    struct RopeTable {
+        float base = 0.0f;
+        size_t rotary_dim = 0;
+        size_t rows = 0;
+        std::vector<float> cs, sn;
+        void* dev = nullptr;
+    };
+    // The table for (base, rotary_dim) holding at least `rows` positions; called under mu_.
+    const RopeTable& rope_table(float base, size_t rotary_dim, size_t rows);
+    std::vector<std::unique_ptr<RopeTable>> rope_tables_;
 
     void* stream_ = nullptr;
     std::mutex mu_;

@@ -13,6 +13,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cctype>
 #include <cmath>
 #include <cstdio>
@@ -217,7 +218,52 @@ void HipLlmBackend::report(const char* op, int n, const std::pair<Tensor, Tensor
 }
 
 HipLlmBackend::~HipLlmBackend() {
+    if (stream_) (void)hipStreamSynchronize(static_cast<hipStream_t>(stream_));
+    for (auto& t : rope_tables_)
+        if (t->dev) (void)hipFree(t->dev);
     if (stream_) (void)hipStreamDestroy(static_cast<hipStream_t>(stream_));
+}
+
+// Every call ends with a synchronizing download, so no queued work reads a table this replaces.
+const HipLlmBackend::RopeTable& HipLlmBackend::rope_table(float base, size_t rotary_dim, size_t rows) {
+    RopeTable* t = nullptr;
+    for (auto& e : rope_tables_)
+        if (e->rotary_dim == rotary_dim && std::memcmp(&e->base, &base, sizeof base) == 0) t = e.get();
+    if (t == nullptr) {
+        rope_tables_.push_back(std::make_unique<RopeTable>());
+        t = rope_tables_.back().get();
+        t->base = base;
+        t->rotary_dim = rotary_dim;
+    }
+    if (rows <= t->rows) return *t;
+    const size_t half = rotary_dim / 2;
+    size_t target = std::max<size_t>(rows, std::max<size_t>(2 * t->rows, 64));
+    if (target > kRopeTableMaxRows) target = std::max(rows, kRopeTableMaxRows);
+    // Rows t->rows .. target - 1: positions evaluated as the reference does (rope.rs:48-50).
+    std::vector<int64_t> pos(target - t->rows);
+    for (size_t i = 0; i < pos.size(); ++i) pos[i] = (int64_t)(t->rows + i);
+    t->cs.resize(target * half);
+    t->sn.resize(target * half);
+    check(sph_rope_table(pos.data(), (int64_t)pos.size(), (int64_t)rotary_dim, base, 1.0f, t->cs.data() + t->rows * half,
+                         t->sn.data() + t->rows * half),
+          "rope (angle table)");
+    void* dev = nullptr;
+    hip_ok(hipMalloc(&dev, 2 * target * half * sizeof(float)), "malloc");
+    hipStream_t s = static_cast<hipStream_t>(stream_);
+    const hipError_t e1 = hipMemcpyAsync(dev, t->cs.data(), target * half * 4, hipMemcpyHostToDevice, s);
+    const hipError_t e2 = hipMemcpyAsync(static_cast<float*>(dev) + target * half, t->sn.data(), target * half * 4,
+                                         hipMemcpyHostToDevice, s);
+    const hipError_t e3 = hipStreamSynchronize(s);
+    if (e1 != hipSuccess || e2 != hipSuccess || e3 != hipSuccess) {
+        (void)hipFree(dev);
+        t->cs.resize(t->rows * half);
+        t->sn.resize(t->rows * half);
+        hip_ok(e1 != hipSuccess ? e1 : e2 != hipSuccess ? e2 : e3, "upload (angle table)");
+    }
+    if (t->dev) (void)hipFree(t->dev);
+    t->dev = dev;
+    t->rows = target;
+    return *t;
 }
 
 void HipLlmBackend::check(int status, const char* op) const {
@@ -524,29 +570,22 @@ Tensor HipLlmBackend::rope(const Tensor& x0, const std::vector<size_t>& position
         pos[i] = (int32_t)positions[i];
     }
     const Tensor x = f32_input(x0);
-    // Short sequences (decode steps, small chunks) take their angles from the host, evaluated
-    // for exactly these positions by the libm the reference calls (rope.rs:49-50): the kernel
-    // then only reads them. Longer ones evaluate the same sin/cos on the device instead of
-    // spending host time on seq · rotary_dim / 2 of them.
-    const size_t half = rotary_dim / 2;
-    const bool host_angles = seq * half <= kHostAngleMax;
-    std::vector<float> tab;
-    if (host_angles) {
-        std::vector<int64_t> p64(positions.begin(), positions.end());
-        tab.resize(2 * seq * half);
-        check(sph_rope_table(p64.data(), (int64_t)seq, (int64_t)rotary_dim, base, 1.0f, tab.data(),
-                             tab.data() + seq * half),
-              "rope (angles)");
-    }
+    // The angles come from this backend's table of positions 0 .. rows - 1 (the reference's
+    // rope_cos_sin_cache, evaluated with its libm: the kernel only reads them), grown to the call's
+    // last position; a position past the table's cap takes the device sin/cos path.
+    size_t last = 0;
+    for (size_t p : positions) last = std::max(last, p);
+    const bool table = !positions.empty() && last < kRopeTableMaxRows;
     std::lock_guard<std::mutex> lock(mu_);
+    const RopeTable* t = table ? &rope_table(base, rotary_dim, last + 1) : nullptr;
     DeviceBuf xd = upload(x.bytes().data(), x.bytes().size());
-    DeviceBuf pd = host_angles ? upload(tab.data(), tab.size() * 4) : upload(pos.data(), pos.size() * 4);
+    DeviceBuf pd = upload(pos.data(), pos.size() * 4);
     int st;
-    if (host_angles) {
-        const float* cs = static_cast<const float*>(pd.ptr);
-        st = sph_rope_cached(xd.ptr, (int64_t)n_heads, nullptr, 0, SPH_F32, layout, cs, cs + seq * half,
-                             (int64_t)seq, nullptr, (int64_t)batch, (int64_t)seq, (int64_t)head_dim,
-                             (int64_t)rotary_dim, nullptr, stream_);
+    if (table) {
+        const float* cs = static_cast<const float*>(t->dev);
+        st = sph_rope_cached(xd.ptr, (int64_t)n_heads, nullptr, 0, SPH_F32, layout, cs, cs + t->rows * (rotary_dim / 2),
+                             (int64_t)t->rows, static_cast<const int32_t*>(pd.ptr), (int64_t)batch, (int64_t)seq,
+                             (int64_t)head_dim, (int64_t)rotary_dim, nullptr, stream_);
     } else {
         st = sph_rope(xd.ptr, (int64_t)n_heads, nullptr, 0, SPH_F32, layout, static_cast<const int32_t*>(pd.ptr),
                       (int64_t)batch, (int64_t)seq, (int64_t)head_dim, (int64_t)rotary_dim, base, 1.0f, stream_);

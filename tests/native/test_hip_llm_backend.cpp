@@ -286,23 +286,33 @@ static void rope_rejects_bad_arguments(HipLlmBackend& bk) {  // rope.rs:19-35, :
     ASSERT(expect_error([&] { bk.apply_rope_partial(x, {0, 1}, 1e4f, 10); }).find("rotary_dim") != std::string::npos, "rd");
 }
 
-static void rope_host_and_device_angles_agree(HipLlmBackend& bk) {  // rope.rs:48-57
-    // 300 tokens x 32 pairs exceed the host-angle budget (device sin/cos); one token at a time stays
-    // within it (host libm angles): both routes give the reference's bits, so they agree exactly.
-    const size_t H = 2, S = 300, D = 64;
+static void rope_table_and_device_angles_agree(HipLlmBackend& bk) {  // rope.rs:48-57
+    // One call whose positions straddle the angle table's cap takes the device sin/cos path as a
+    // whole; its tokens below the cap, rotated one call each, read the table (grown to them).
+    // Both evaluate the reference's angle and its glibc sin/cos, so they agree bit for bit —
+    // at positions near 2^18, where sinf/cosf take their large-argument reduction.
+    const size_t H = 2, S = 40, D = 64, cap = HipLlmBackend::kRopeTableMaxRows;
     std::vector<float> x(H * S * D);
     for (size_t i = 0; i < x.size(); ++i) x[i] = std::sin(0.37f * (float)i) * 3.0f;
     std::vector<size_t> pos(S);
-    for (size_t s = 0; s < S; ++s) pos[s] = 7919 * s % 100003;
-    ASSERT(S * D / 2 > HipLlmBackend::kHostAngleMax, "the whole call takes the device route");
+    for (size_t s = 0; s < S; ++s) pos[s] = cap - 20 + s;  // 20 below the cap, 20 at or past it
     const std::vector<float> all = bk.apply_rope_positions(Tensor::from_f32(x, {1, H, S, D}), pos, 5e5f).as_f32();
-    for (size_t s = 0; s < S; s += 23) {
+    for (size_t s = 0; s < 20; s += 3) {
         std::vector<float> one(H * D);
         for (size_t h = 0; h < H; ++h) std::memcpy(&one[h * D], &x[(h * S + s) * D], D * 4);
         const std::vector<float> o = bk.apply_rope_positions(Tensor::from_f32(one, {1, H, 1, D}), {pos[s]}, 5e5f).as_f32();
         for (size_t h = 0; h < H; ++h)
             ASSERT(std::memcmp(&o[h * D], &all[(h * S + s) * D], D * 4) == 0, "token rotated alike on both routes");
     }
+    // A partial rotary on the same table machinery (another rotary_dim, another table): channels past
+    // rotary_dim unchanged, and the rotated part equal to a full RoPE of a head of that width.
+    std::vector<float> y(16);
+    for (int i = 0; i < 16; ++i) y[i] = (float)(i + 1) * 0.25f;
+    const std::vector<float> part = bk.apply_rope_partial(Tensor::from_f32(y, {1, 1, 1, 16}), {77}, 1e4f, 8).as_f32();
+    const std::vector<float> head(y.begin(), y.begin() + 8);
+    const std::vector<float> full = bk.apply_rope_positions(Tensor::from_f32(head, {1, 1, 1, 8}), {77}, 1e4f).as_f32();
+    for (int i = 0; i < 8; ++i) ASSERT(std::memcmp(&part[i], &full[i], 4) == 0, "rotated part");
+    for (int i = 8; i < 16; ++i) ASSERT(part[i] == y[i], "tail unchanged");
 }
 
 static void rope_interleaved_is_permuted_neox(HipLlmBackend& bk) {  // gguf_weights.rs:111-115
@@ -579,7 +589,7 @@ int main() {
         {"rope_position_zero_is_identity", rope_position_zero_is_identity},
         {"rope_rejects_bad_arguments", rope_rejects_bad_arguments},
         {"rope_interleaved_is_permuted_neox", rope_interleaved_is_permuted_neox},
-        {"rope_host_and_device_angles_agree", rope_host_and_device_angles_agree},
+        {"rope_table_and_device_angles_agree", rope_table_and_device_angles_agree},
         {"add_rms_norm_is_add_then_rms_norm", add_rms_norm_is_add_then_rms_norm},
         {"embed_row_gather_matches_full_dequant", embed_row_gather_matches_full_dequant},
         {"quant_bytes_are_validated", quant_bytes_are_validated},
