@@ -87,7 +87,10 @@ void sph_engine_destroy(sph_engine* e);
  * next call; the work is enqueued on the engine's stream, not waited for. */
 int sph_engine_forward_token(sph_engine* e, uint32_t tok, const float** hidden);
 /* n ≤ max_chunk tokens at the next positions (WgpuForwardEngine::forward_chunk);
- * *hidden = the final hidden state of the last token. */
+ * *hidden = the final hidden state of the last token. The first chunk to reach
+ * a position beyond the engine's RoPE angle table extends it from the host
+ * and waits for that upload (and so for the stream's earlier work); the table
+ * grows by doubling, so this happens O(log max_seq) times. */
 int sph_engine_forward_chunk(sph_engine* e, const uint32_t* toks, int64_t n, const float** hidden);
 /* Replay forward_token from a captured HIP graph (1) or launch eagerly (0). */
 int sph_engine_use_graph(sph_engine* e, int on);

@@ -859,3 +859,16 @@ extern "C" int sph_rope_kv_append_tokens(const void* q, void* q_out, int64_t n_q
                                     base, pos_scale, kcache, vcache, cache_dtype, max_seq, bq, bk, bv, bias_dtype,
                                     bad_pos_flag, stream);
 }
+
+// Declared in sph_internal.h (not exported).
+extern "C" int sph_rope_kv_append_tokens_angles(const void* q, void* q_out, int64_t n_q_heads, const void* k,
+                                                const void* v, int64_t n_kv_heads, int dtype, int layout,
+                                                const int32_t* positions, const float* angles, int64_t seq,
+                                                int64_t head_dim, void* kcache, void* vcache, int cache_dtype,
+                                                int64_t max_seq, const void* bq, const void* bk, const void* bv,
+                                                int bias_dtype, int32_t* bad_pos_flag, void* stream) {
+    if (angles == nullptr || !sph::aligned(angles, 8)) return SPH_EINVAL;
+    return sph::rope_kv_entry<true>(q, q_out, n_q_heads, k, v, n_kv_heads, dtype, layout, positions, seq, head_dim,
+                                    1.0f, 1.0f, kcache, vcache, cache_dtype, max_seq, bq, bk, bv, bias_dtype,
+                                    bad_pos_flag, stream, angles);
+}

@@ -12,16 +12,20 @@
 //    (sph_rope_kv_append_tokens reads the projections' token-major rows);
 //  - forward_chunk adds the last layer's residual and normalises only the last
 //    row, the one the reference slices out before its final norm (:623-627).
-//  - a one-token step's RoPE angles, cos and sin of position / base^(2i/hd), are
-//    evaluated on the host with the libm the reference calls (the values its
-//    own rope computes) and staged with the token id and position, so the
-//    fused RoPE + KV launch reads them instead of evaluating sin/cos.
+//  - RoPE angles, cos and sin of position / base^(2i/hd), are evaluated on the
+//    host with the libm the reference calls (the values its own rope
+//    computes), so the fused RoPE + KV launch reads them instead of evaluating
+//    sin/cos: a one-token step stages its position's angles with the token id
+//    and position; a chunk reads rows of a per-position table, the reference's
+//    rope_cos_sin_cache (crates/sapient-backends/cpu/src/kernels/rope.rs:140-153)
+//    with (cos, sin) interleaved, filled as positions are first reached.
 // Decode steps can be captured into a HIP graph once and replayed: every
 // per-token value (token id, position, angles) lives in device memory,
 // refreshed by one H2D copy from pinned staging before each launch.
 #include <hip/hip_runtime.h>
 #include <math.h>
 
+#include <algorithm>
 #include <cstring>
 #include <new>
 #include <utility>
@@ -53,6 +57,10 @@ struct sph_engine {
     int32_t* flags = nullptr;  // [0] bad token id, [1] bad cache position (both checked on the host first)
     std::vector<void*> kcache, vcache;
     std::vector<float> dens;  // base^(2i/head_dim), i < head_dim/2, from the host libm
+    // Row r (< max_seq): head_dim/2 (cos, sin) pairs of position r's angles;
+    // rows [0, angle_rows) are filled.
+    float* angles = nullptr;
+    int64_t angle_rows = 0;
 
     uint8_t* staged = nullptr;  // pinned
     hipEvent_t staged_done = nullptr;  // the last H2D copy out of the staging buffer
@@ -138,11 +146,12 @@ int body(sph_engine* e, int64_t T) {
                                               c.kv_dtype, c.max_seq, L.bq, L.bk, L.bv, c.bias_dtype, e->flags + 1,
                                               s));
         } else {
+            // Positions cur .. cur + T - 1: table rows from row cur on.
             qh = e->qt;
-            SPH_TRY(sph_rope_kv_append_tokens(e->q, e->qt, c.n_heads, e->k, e->v, c.n_kv_heads, SPH_F32,
-                                              c.rope_layout, positions, T, c.head_dim, c.rope_theta, 1.0f,
-                                              e->kcache[l], e->vcache[l], c.kv_dtype, c.max_seq, L.bq, L.bk, L.bv,
-                                              c.bias_dtype, e->flags + 1, s));
+            SPH_TRY(sph_rope_kv_append_tokens_angles(e->q, e->qt, c.n_heads, e->k, e->v, c.n_kv_heads, SPH_F32,
+                                                     c.rope_layout, positions, e->angles + e->cur * c.head_dim, T,
+                                                     c.head_dim, e->kcache[l], e->vcache[l], c.kv_dtype, c.max_seq,
+                                                     L.bq, L.bk, L.bv, c.bias_dtype, e->flags + 1, s));
         }
         if (e->attend)
             SPH_TRY(callback_status(e->attend(e->user, l, qh, e->kcache[l], e->vcache[l], c.kv_dtype, positions, T,
@@ -167,6 +176,39 @@ int body(sph_engine* e, int64_t T) {
                             c.hidden, c.rms_eps, s);
 }
 
+// The reference's angle: freq = (f32)pos / base^(2i/d), then cosf / sinf
+// (rope.rs:48-57); pos_scale 1 divides exactly. Writes (cos, sin) pairs.
+void angles_at(const sph_engine* e, int64_t pos, float* out) {
+    const float p = (float)pos;
+    for (size_t i = 0; i < e->dens.size(); ++i) {
+        const float freq = p / e->dens[i];
+        out[2 * i] = cosf(freq);
+        out[2 * i + 1] = sinf(freq);
+    }
+}
+
+// Fill the angle table up to row `need` (<= max_seq). It grows by doubling,
+// at least 256 rows at a time, so a run of chunks uploads O(log max_seq)
+// times; each upload completes before the call returns, and rows already on
+// the device are never rewritten.
+int fill_angles(sph_engine* e, int64_t need) {
+    if (need <= e->angle_rows) return SPH_OK;
+    const int64_t rows = std::min(e->cfg.max_seq, std::max({need, 2 * e->angle_rows, (int64_t)256}));
+    const size_t row = (size_t)e->cfg.head_dim;  // floats per row
+    try {
+        std::vector<float> buf((size_t)(rows - e->angle_rows) * row);
+        for (int64_t r = e->angle_rows; r < rows; ++r) angles_at(e, r, buf.data() + (size_t)(r - e->angle_rows) * row);
+        if (hipMemcpyAsync(e->angles + (size_t)e->angle_rows * row, buf.data(), buf.size() * 4,
+                           hipMemcpyHostToDevice, e->stream) != hipSuccess ||
+            hipStreamSynchronize(e->stream) != hipSuccess)
+            return SPH_EHIP;
+    } catch (...) {
+        return SPH_EHIP;
+    }
+    e->angle_rows = rows;
+    return SPH_OK;
+}
+
 // Copy ids and positions cur .. cur + n - 1 to the device (checked first).
 int stage(sph_engine* e, const uint32_t* toks, int64_t n) {
     if (n <= 0 || n > e->cfg.max_chunk) return SPH_EINVAL;
@@ -179,15 +221,7 @@ int stage(sph_engine* e, const uint32_t* toks, int64_t n) {
     for (int64_t i = 0; i < n; ++i) pos[i] = (int32_t)(e->cur + i);
     size_t bytes = (size_t)n * 8;
     if (n == 1) {
-        // The reference's angle: freq = (f32)pos / base^(2i/d), then sinf / cosf
-        // (rope.rs:48-57); pos_scale 1 divides exactly.
-        float* ang = reinterpret_cast<float*>(e->staged + 8);
-        const float p = (float)e->cur;
-        for (size_t i = 0; i < e->dens.size(); ++i) {
-            const float freq = p / e->dens[i];
-            ang[2 * i] = cosf(freq);
-            ang[2 * i + 1] = sinf(freq);
-        }
+        angles_at(e, e->cur, reinterpret_cast<float*>(e->staged + 8));
         bytes += e->dens.size() * 8;
     }
     if (hipMemcpyAsync(e->inputs, e->staged, bytes, hipMemcpyHostToDevice, e->stream) != hipSuccess ||
@@ -267,7 +301,7 @@ extern "C" int sph_engine_create(const sph_engine_config* cfg, const void* embed
                   dalloc(e, &e->gate, T * c.intermediate * 4) && dalloc(e, &e->up, T * c.intermediate * 4) &&
                   dalloc(e, &e->act, T * c.intermediate * 4) && dalloc(e, &e->down, T * c.hidden * 4) &&
                   dalloc(e, &e->out, (size_t)c.hidden * 4) && dalloc(e, &e->inputs, T * 8 + (size_t)c.head_dim * 4) &&
-                  dalloc(e, &e->flags, 2 * 4);
+                  dalloc(e, &e->flags, 2 * 4) && dalloc(e, &e->angles, (size_t)c.max_seq * (size_t)c.head_dim * 4);
         for (int64_t l = 0; ok && l < c.n_layers; ++l) {
             void *kc = nullptr, *vc = nullptr;
             ok = dalloc(e, &kc, cache_bytes) && dalloc(e, &vc, cache_bytes);
@@ -313,6 +347,7 @@ extern "C" int sph_engine_forward_token(sph_engine* e, uint32_t tok, const float
 extern "C" int sph_engine_forward_chunk(sph_engine* e, const uint32_t* toks, int64_t n, const float** hidden) {
     if (!e || !toks || !hidden) return SPH_EINVAL;
     SPH_TRY(stage(e, toks, n));
+    if (n > 1) SPH_TRY(fill_angles(e, e->cur + n));
     SPH_TRY(body(e, n));
     e->cur += n;
     *hidden = e->out;

@@ -13,8 +13,10 @@ and check, in order:
   2. every op of every layer on the engine's own inputs (the stand-ins record
      what each op received; the residual stream is rebuilt from the records
      with the same f32 adds): the norms to 1e-5 relative, bias + RoPE (NEOX
-     and interleaved; a one-token step's angles come from the host), the
-     KV-cache rows and SwiGLU bit for bit;
+     and interleaved; the angles come from the host: staged per one-token
+     step, rows of a per-position table for a chunk, checked across every
+     fill of that table up to max_seq), the KV-cache rows and SwiGLU bit for
+     bit;
   3. the end-to-end hidden states and caches against the oracle's run of the
      whole reference sequence on its own values, where the norms' last-bit
      differences compound over the layers: 1e-4 of the largest |value|
@@ -223,28 +225,27 @@ def _rel_ok(got, want, what):
     assert np.all(err <= 1e-5 * np.abs(want)), f"{what}: max rel {float((err / np.maximum(np.abs(want), 1e-30)).max())}"
 
 
-@pytest.mark.parametrize("layout", [L.ROPE_NEOX, L.ROPE_INTERLEAVED], ids=["neox", "interleaved"])
-def test_engine_each_op_on_its_own_inputs(dev, orc, model, layout):
-    """Teacher-forced parity: the callbacks record what each op received, the test rebuilds the
-    residual stream x from those records with the same f32 adds (exact), and checks every op of every
-    layer on the engine's own inputs — RMSNorm (input, post-attention, final) to 1e-5 relative,
-    bias + RoPE of q (the attention input) and of k with the v rows (the caches) and SwiGLU bit for
-    bit — so no op's tolerance compounds over the layers. Reference sequence: wgpu_engine.rs:362-629."""
+def _teacher_forced(orc, model, layout, steps, max_seq, max_chunk, what):
+    """Run `steps` (lists of ids: one id = forward_token, more = forward_chunk) through an engine
+    whose stand-ins record what each op received, and check every op of every layer on those
+    inputs: the residual stream x is rebuilt from the records with the same f32 adds (exact);
+    RMSNorm (input, post-attention, final) to 1e-5 relative, bias + RoPE of q (the attention input)
+    and of k with the v rows (the caches) and SwiGLU bit for bit, so no op's tolerance compounds
+    over the layers. Reference sequence: wgpu_engine.rs:362-629."""
     table, layers, final = model
     tab = to_np(table)
     lw = [{k: (None if v is None else widen(v, orc)) for k, v in Lw.items()} for Lw in layers]
     fin = to_np(final)
     rec = _Recorder()
-    t_, l_, f_ = model
-    cfg = L.EngineConfig(H, NQ, NKV, HD, INTER, LAYERS, MAX_SEQ, MAX_CHUNK, EPS, THETA, layout, L.F16, L.F16)
-    eng = Engine(cfg, t_, L.F32, VOCAB, l_, f_, rec.project, rec.attend)
+    cfg = L.EngineConfig(H, NQ, NKV, HD, INTER, LAYERS, max_seq, max_chunk, EPS, THETA, layout, L.F16, L.F16)
+    eng = Engine(cfg, table, L.F32, VOCAB, layers, final, rec.project, rec.attend)
     if layout == L.ROPE_NEOX:
         rope = lambda x, pos: orc.apply_rope(x, pos, THETA)
     else:  # interleaved pairs (the GGUF q/k layout), full rotary dimension
         rope = lambda x, pos: orc.apply_rope_partial_scaled(x, pos, THETA, HD, 1.0, True)
     proj = lambda x, n_out: (0.5 * np.tile(x, (1, -(-n_out // x.shape[1])))[:, :n_out]).astype(np.float32)
-    caches = [(np.zeros((NKV, MAX_SEQ, HD), np.uint16), np.zeros((NKV, MAX_SEQ, HD), np.uint16)) for _ in range(LAYERS)]
-    steps = [PROMPT] + [[t] for t in DECODE]
+    caches = [(np.zeros((NKV, max_seq, HD), np.uint16), np.zeros((NKV, max_seq, HD), np.uint16))
+              for _ in range(LAYERS)]
     pos0 = 0
     for si, ids in enumerate(steps):
         rec.calls.clear()
@@ -255,7 +256,7 @@ def test_engine_each_op_on_its_own_inputs(dev, orc, model, layout):
         got = {}
         for layer, which, t in rec.calls:
             got[(layer, which)] = to_np(t)
-        print(f"case engine teacher-forced layout {layout} step {si} T {T}", flush=True)
+        print(f"case {what} layout {layout} step {si} positions {pos0}..{pos0 + T - 1}", flush=True)
         x = orc.embed_tokens(tab.reshape(-1).view(np.uint8), L.F32, VOCAB, H, np.array(ids, np.uint32)).reshape(T, H)
         down = None
         for l in range(LAYERS):
@@ -269,9 +270,9 @@ def test_engine_each_op_on_its_own_inputs(dev, orc, model, layout):
             qr = rope(np.ascontiguousarray(q.reshape(T, NQ, HD).transpose(1, 0, 2)[None]), pos)[0]
             kr = rope(np.ascontiguousarray(k.reshape(T, NKV, HD).transpose(1, 0, 2)[None]), pos)[0]
             assert np.array_equal(got[(l, "attend")].view(np.uint32), qr.view(np.uint32)), f"step {si} layer {l} rope q"
-            orc.kv_append(kr, caches[l][0], L.F16, NKV, T, HD, MAX_SEQ, pos0)
+            orc.kv_append(kr, caches[l][0], L.F16, NKV, T, HD, max_seq, pos0)
             orc.kv_append(np.ascontiguousarray(v.reshape(T, NKV, HD).transpose(1, 0, 2)), caches[l][1], L.F16, NKV, T,
-                          HD, MAX_SEQ, pos0)
+                          HD, max_seq, pos0)
             attn = got[(l, L.PROJ_O)]
             assert np.array_equal(attn.view(np.uint32), qr.transpose(1, 0, 2).reshape(T, NQ * HD).view(np.uint32))
             x = orc.add(x, proj(attn, H))
@@ -285,6 +286,30 @@ def test_engine_each_op_on_its_own_inputs(dev, orc, model, layout):
         pos0 += T
     for l in range(LAYERS):
         for j, which in enumerate("kv"):
-            g = to_np(eng.cache(l, which)).view(np.uint16).reshape(NKV, MAX_SEQ, HD)
+            g = to_np(eng.cache(l, which)).view(np.uint16).reshape(NKV, max_seq, HD)
             assert np.array_equal(g, caches[l][j]), f"layer {l} {which} cache"
     eng.close()
+
+
+@pytest.mark.parametrize("layout", [L.ROPE_NEOX, L.ROPE_INTERLEAVED], ids=["neox", "interleaved"])
+def test_engine_each_op_on_its_own_inputs(dev, orc, model, layout):
+    """Teacher-forced parity of a prompt chunk and decode steps."""
+    _teacher_forced(orc, model, layout, [PROMPT] + [[t] for t in DECODE], MAX_SEQ, MAX_CHUNK, "engine teacher-forced")
+
+
+def test_engine_chunks_across_angle_table_growth(dev, orc, model):
+    """A chunk's RoPE angles are rows of the engine's per-position table, filled from the host as
+    positions are first reached (256 rows, then doubling up to max_seq = 600). Chunks before, across
+    and after each fill boundary (256, 512, the cap), decode steps between them (their angles are
+    staged per step, outside the table) and a last chunk ending at max_seq, all teacher-forced."""
+    rng = np.random.default_rng(7)
+    ids = lambda n: [int(t) for t in rng.integers(0, VOCAB, n)]
+    steps = [ids(16) for _ in range(15)]                 # 0 .. 239: the first fill covers 256 rows
+    steps += [[t] for t in ids(5)]                        # 240 .. 244 one token at a time
+    steps += [ids(16)]                                    # 245 .. 260: across 256, the table grows to 512
+    steps += [ids(16) for _ in range(15)]                 # 261 .. 500
+    steps += [ids(3), ids(16)]                            # 501 .. 503, then 504 .. 519 across 512: to 600
+    steps += [[t] for t in ids(50)]                       # 520 .. 569
+    steps += [ids(14), ids(16)]                           # 570 .. 583, 584 .. 599: ends at max_seq
+    assert sum(len(s) for s in steps) == 600
+    _teacher_forced(orc, model, L.ROPE_NEOX, steps, 600, 16, "engine angle table")
