@@ -92,7 +92,8 @@ int sph_engine_forward_token(sph_engine* e, uint32_t tok, const float** hidden);
  * and waits for that upload (and so for the stream's earlier work); the table
  * grows by doubling, so this happens O(log max_seq) times. */
 int sph_engine_forward_chunk(sph_engine* e, const uint32_t* toks, int64_t n, const float** hidden);
-/* Replay forward_token from a captured HIP graph (1) or launch eagerly (0). */
+/* Replay forward_token from a captured HIP graph (1) or launch eagerly (0);
+ * forward_chunk always launches eagerly. */
 int sph_engine_use_graph(sph_engine* e, int on);
 /* Start again at position 0 (cached rows are overwritten as positions refill). */
 int sph_engine_reset(sph_engine* e);

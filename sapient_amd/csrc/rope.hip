@@ -361,7 +361,7 @@ __global__ __launch_bounds__(kThreads) void rope_kv_kernel(const T* q, T* qo, in
                                                            int heads_per_group, float pos_scale, TC* kc, TC* vc,
                                                            int64_t max_seq, int32_t* bad_pos_flag, const TB* bq,
                                                            const TB* bk, const TB* bv, DenTable den,
-                                                           const float* __restrict__ ang) {
+                                                           const float* __restrict__ ang, bool ang_by_pos) {
     __shared__ uint32_t inv_pio4[24];
     const int tib = threadIdx.x / lanes_per_tok;
     const int lit = threadIdx.x - tib * lanes_per_tok;
@@ -436,7 +436,7 @@ __global__ __launch_bounds__(kThreads) void rope_kv_kernel(const T* q, T* qo, in
         }                                                                                         \
     } while (0)
     float cs[P], sn[P];
-    if (ang != nullptr) {
+    if (ang != nullptr && !ang_by_pos) {
         // Angles supplied per (token, pair) as (cos, sin): requested with the
         // position and the rows, so the step waits on memory once and computes
         // no sin/cos (the whole block takes this branch; no barrier follows).
@@ -449,6 +449,21 @@ __global__ __launch_bounds__(kThreads) void rope_kv_kernel(const T* q, T* qo, in
             sn[j] = a[2 * j + 1];
         }
         if (h_begin < h_end) SPH_LOAD_HEAD(h_begin);
+    } else if (ang != nullptr) {
+        // Angles read from row pos[s] of a per-position table of max_seq rows
+        // (the first head's rows are requested before the position is waited
+        // on). A position outside [0, max_seq) reads no row: q is rotated by
+        // angle 0 (cos 1, sin 0), the caches are left alone and the flag set.
+        if (!active) return;
+        ps = pos[s];
+        if (h_begin < h_end) SPH_LOAD_HEAD(h_begin);
+        const bool in_table = ps >= 0 && (int64_t)ps < max_seq;
+        const float* a = ang + 2 * ((size_t)(in_table ? ps : 0) * (size_t)half + (size_t)i0);
+#pragma unroll
+        for (int j = 0; j < P; ++j) {
+            cs[j] = in_table ? a[2 * j] : 1.0f;
+            sn[j] = in_table ? a[2 * j + 1] : 0.0f;
+        }
     } else {
         if (active) {
             ps = pos[s];
@@ -577,7 +592,7 @@ inline void fill_dens(DenTable& den, int half, int rotary_dim, float base) {
 template <typename T, typename TC, typename TB, int P, bool IL, bool TM>
 int launch_rope_kv_p(const T* q, T* qo, int nq, const T* k, const T* v, int nkv, const int32_t* pos, int64_t seq, int head_dim,
                      float pos_scale, TC* kc, TC* vc, int64_t max_seq, int32_t* flag, const TB* bq, const TB* bk,
-                     const TB* bv, const DenTable& den, const float* ang, hipStream_t stream) {
+                     const TB* bv, const DenTable& den, const float* ang, bool ang_by_pos, hipStream_t stream) {
     const int half = head_dim / 2;
     const int lanes_per_tok = half / P;
     const int toks_per_block = kThreads / lanes_per_tok;
@@ -595,7 +610,7 @@ int launch_rope_kv_p(const T* q, T* qo, int nq, const T* k, const T* v, int nkv,
     const dim3 grid((unsigned)blocks_x, (unsigned)groups);
     return launch(rope_kv_kernel<T, TC, TB, P, IL, TM>, grid, kThreads, stream, q, qo, nq, k, v, nkv, pos, seq,
                   head_dim, half, lanes_per_tok, toks_per_block, heads_per_group, pos_scale, kc, vc, max_seq, flag, bq,
-                  bk, bv, den, ang);
+                  bk, bv, den, ang, ang_by_pos);
 }
 
 // P: pairs per thread, the widest whose accesses of q/k/v (type T) and of the
@@ -604,7 +619,7 @@ template <typename T, typename TC, typename TB, bool TM>
 int launch_rope_kv(const void* qv, void* qov, int nq, const void* kv, const void* vv, int nkv, int layout,
                    const int32_t* pos, int64_t seq, int head_dim, float base, float pos_scale, void* kcv, void* vcv,
                    int64_t max_seq, int32_t* flag, const void* bqv, const void* bkv, const void* bvv, const float* ang,
-                   hipStream_t stream) {
+                   bool ang_by_pos, hipStream_t stream) {
     const TB* bq = static_cast<const TB*>(bqv);
     const TB* bk = static_cast<const TB*>(bkv);
     const TB* bv = static_cast<const TB*>(bvv);
@@ -635,19 +650,19 @@ int launch_rope_kv(const void* qv, void* qov, int nq, const void* kv, const void
     // so it takes the narrowest runs that stay word-sized: fewer angles per lane.
     const bool few = seq <= 4;
     if (!il) {
-        if (few && ok(V / 2)) return launch_rope_kv_p<T, TC, TB, V / 2, false, TM>(q, qo, nq, k, v, nkv, pos, seq, head_dim, pos_scale, kc, vc, max_seq, flag, bq, bk, bv, den, ang, stream);
-        if (ok(V)) return launch_rope_kv_p<T, TC, TB, V, false, TM>(q, qo, nq, k, v, nkv, pos, seq, head_dim, pos_scale, kc, vc, max_seq, flag, bq, bk, bv, den, ang, stream);
-        if (ok(V / 2)) return launch_rope_kv_p<T, TC, TB, V / 2, false, TM>(q, qo, nq, k, v, nkv, pos, seq, head_dim, pos_scale, kc, vc, max_seq, flag, bq, bk, bv, den, ang, stream);
+        if (few && ok(V / 2)) return launch_rope_kv_p<T, TC, TB, V / 2, false, TM>(q, qo, nq, k, v, nkv, pos, seq, head_dim, pos_scale, kc, vc, max_seq, flag, bq, bk, bv, den, ang, ang_by_pos, stream);
+        if (ok(V)) return launch_rope_kv_p<T, TC, TB, V, false, TM>(q, qo, nq, k, v, nkv, pos, seq, head_dim, pos_scale, kc, vc, max_seq, flag, bq, bk, bv, den, ang, ang_by_pos, stream);
+        if (ok(V / 2)) return launch_rope_kv_p<T, TC, TB, V / 2, false, TM>(q, qo, nq, k, v, nkv, pos, seq, head_dim, pos_scale, kc, vc, max_seq, flag, bq, bk, bv, den, ang, ang_by_pos, stream);
         if constexpr (V / 4 >= 2) {
-            if (ok(V / 4)) return launch_rope_kv_p<T, TC, TB, V / 4, false, TM>(q, qo, nq, k, v, nkv, pos, seq, head_dim, pos_scale, kc, vc, max_seq, flag, bq, bk, bv, den, ang, stream);
+            if (ok(V / 4)) return launch_rope_kv_p<T, TC, TB, V / 4, false, TM>(q, qo, nq, k, v, nkv, pos, seq, head_dim, pos_scale, kc, vc, max_seq, flag, bq, bk, bv, den, ang, ang_by_pos, stream);
         }
     } else {
         if constexpr (V / 4 >= 1) {
-            if (few && ok(V / 4)) return launch_rope_kv_p<T, TC, TB, V / 4, true, TM>(q, qo, nq, k, v, nkv, pos, seq, head_dim, pos_scale, kc, vc, max_seq, flag, bq, bk, bv, den, ang, stream);
+            if (few && ok(V / 4)) return launch_rope_kv_p<T, TC, TB, V / 4, true, TM>(q, qo, nq, k, v, nkv, pos, seq, head_dim, pos_scale, kc, vc, max_seq, flag, bq, bk, bv, den, ang, ang_by_pos, stream);
         }
-        if (ok(V / 2)) return launch_rope_kv_p<T, TC, TB, V / 2, true, TM>(q, qo, nq, k, v, nkv, pos, seq, head_dim, pos_scale, kc, vc, max_seq, flag, bq, bk, bv, den, ang, stream);
+        if (ok(V / 2)) return launch_rope_kv_p<T, TC, TB, V / 2, true, TM>(q, qo, nq, k, v, nkv, pos, seq, head_dim, pos_scale, kc, vc, max_seq, flag, bq, bk, bv, den, ang, ang_by_pos, stream);
         if constexpr (V / 4 >= 1) {
-            if (ok(V / 4)) return launch_rope_kv_p<T, TC, TB, V / 4, true, TM>(q, qo, nq, k, v, nkv, pos, seq, head_dim, pos_scale, kc, vc, max_seq, flag, bq, bk, bv, den, ang, stream);
+            if (ok(V / 4)) return launch_rope_kv_p<T, TC, TB, V / 4, true, TM>(q, qo, nq, k, v, nkv, pos, seq, head_dim, pos_scale, kc, vc, max_seq, flag, bq, bk, bv, den, ang, ang_by_pos, stream);
         }
     }
     return SPH_EINVAL;  // head_dim or alignment the vector paths do not cover
@@ -792,7 +807,7 @@ int rope_kv_entry(const void* q, void* q_out, int64_t n_q_heads, const void* k, 
                   int dtype, int layout, const int32_t* positions, int64_t seq, int64_t head_dim, float base,
                   float pos_scale, void* kcache, void* vcache, int cache_dtype, int64_t max_seq, const void* bq,
                   const void* bk, const void* bv, int bias_dtype, int32_t* bad_pos_flag, void* stream,
-                  const float* angles = nullptr) {
+                  const float* angles = nullptr, bool angles_by_position = false) {
     if (layout != SPH_ROPE_NEOX && layout != SPH_ROPE_INTERLEAVED) return SPH_EINVAL;
     if (!is_float_dtype(dtype) || !is_float_dtype(cache_dtype)) return SPH_EINVAL;
     if ((bq || bk || bv) && !is_float_dtype(bias_dtype)) return SPH_EINVAL;
@@ -818,7 +833,8 @@ int rope_kv_entry(const void* q, void* q_out, int64_t n_q_heads, const void* k, 
                 using TB = decltype(tb);
                 return launch_rope_kv<T, TC, TB, TM>(q, q_out, (int)n_q_heads, k, v, (int)n_kv_heads, layout,
                                                      positions, seq, (int)head_dim, base, pos_scale, kcache, vcache,
-                                                     max_seq, bad_pos_flag, bq, bk, bv, angles, s);
+                                                     max_seq, bad_pos_flag, bq, bk, bv, angles,
+                                                     angles_by_position, s);
             });
         });
     });
@@ -870,5 +886,5 @@ extern "C" int sph_rope_kv_append_tokens_angles(const void* q, void* q_out, int6
     if (angles == nullptr || !sph::aligned(angles, 8)) return SPH_EINVAL;
     return sph::rope_kv_entry<true>(q, q_out, n_q_heads, k, v, n_kv_heads, dtype, layout, positions, seq, head_dim,
                                     1.0f, 1.0f, kcache, vcache, cache_dtype, max_seq, bq, bk, bv, bias_dtype,
-                                    bad_pos_flag, stream, angles);
+                                    bad_pos_flag, stream, angles, true);
 }

@@ -16,10 +16,10 @@ __attribute__((visibility("hidden"))) int sph_rope_kv_append_angles(
     int cache_dtype, int64_t max_seq, const void* bq, const void* bk, const void* bv, int bias_dtype,
     int32_t* bad_pos_flag, void* stream);
 
-// sph_rope_kv_append_tokens with the angles supplied, laid out as above (row s
-// of angles belongs to token s of the chunk). Used by the decode engine's
-// chunks, whose positions are consecutive: it passes row `first position` of
-// its per-position table.
+// sph_rope_kv_append_tokens with the angles read from a per-position table:
+// angles[2 (p·head_dim/2 + i)] and [... + 1] hold cos and sin of p / base^(2i/head_dim)
+// for every position p in [0, max_seq). Token s reads row positions[s], so a
+// captured launch serves any positions. Used by the decode engine's chunks.
 __attribute__((visibility("hidden"))) int sph_rope_kv_append_tokens_angles(
     const void* q, void* q_out, int64_t n_q_heads, const void* k, const void* v, int64_t n_kv_heads, int dtype,
     int layout, const int32_t* positions, const float* angles, int64_t seq, int64_t head_dim, void* kcache,

@@ -8,8 +8,8 @@ stand-ins, enqueued with torch on the engine's stream:
   attention   out = q (the rotated queries, heads-major)
 and check, in order:
   1. graph replay = eager launches, bit for bit, at every decode step (the
-     graph is replayed for several tokens, eager work and synchronizations in
-     between);
+     graph is replayed for several tokens, eager chunks, other work and
+     synchronizations in between, also while the RoPE angle table grows);
   2. every op of every layer on the engine's own inputs (the stand-ins record
      what each op received; the residual stream is rebuilt from the records
      with the same f32 adds): the norms to 1e-5 relative, bias + RoPE (NEOX
@@ -38,6 +38,11 @@ H, NQ, NKV, HD, INTER, LAYERS, MAX_SEQ, MAX_CHUNK, VOCAB = 256, 8, 2, 32, 512, 3
 EPS, THETA = 1e-6, 1e4
 PROMPT = [5, 17, 99, 0, 42, 42, 7]
 DECODE = [3, 64, 11, 98, 1]
+# A prompt, chunks of MAX_CHUNK tokens and single tokens, ending at MAX_SEQ.
+STEPS = ([PROMPT, [(7 * i + 3) % VOCAB for i in range(MAX_CHUNK)]] + [[t] for t in DECODE]
+         + [[(11 * i + 5) % VOCAB for i in range(MAX_CHUNK)], [8], [13], [21],
+            [(13 * i + 1) % VOCAB for i in range(MAX_CHUNK)], [34]])
+assert sum(len(s) for s in STEPS) == MAX_SEQ
 
 
 def _gen(shape, seed, dev, mean=0.0, std=1.0, dtype=torch.float32):
@@ -95,12 +100,11 @@ def _engine(model, kv_dtype=L.F16):
     return Engine(cfg, table, L.F32, VOCAB, layers, final, project, attend)
 
 
-def _run(eng, graph):
+def _run(eng, graph, steps=STEPS):
     eng.use_graph(graph)
-    outs = [eng.forward_chunk(PROMPT).clone()]
-    torch.cuda.synchronize()
-    for t in DECODE:
-        outs.append(eng.forward_token(t).clone())
+    outs = []
+    for ids in steps:
+        outs.append((eng.forward_chunk(ids) if len(ids) > 1 else eng.forward_token(ids[0])).clone())
         torch.cuda.synchronize()
     return [to_np(o) for o in outs]
 
@@ -116,7 +120,7 @@ def test_graph_replay_equals_eager(dev, model):
     for l in range(LAYERS):
         for w in "kv":
             assert torch.equal(eager.cache(l, w), graph.cache(l, w)), f"layer {l} {w} cache"
-    assert eager.position == graph.position == len(PROMPT) + len(DECODE)
+    assert eager.position == graph.position == MAX_SEQ
     eager.close()
     graph.close()
 
@@ -162,13 +166,14 @@ def test_engine_matches_oracle_sequence(dev, orc, model):
     got = _run(eng, True)
     caches = [(np.zeros((NKV, MAX_SEQ, HD), np.uint16), np.zeros((NKV, MAX_SEQ, HD), np.uint16))
               for _ in range(LAYERS)]
-    want = [_oracle_step(orc, model_np, PROMPT, 0, caches)]
-    for i, t in enumerate(DECODE):
-        want.append(_oracle_step(orc, model_np, [t], len(PROMPT) + i, caches))
+    want, pos0 = [], 0
+    for ids in STEPS:
+        want.append(_oracle_step(orc, model_np, ids, pos0, caches))
+        pos0 += len(ids)
     print("case engine vs oracle", flush=True)
     for i, (g, w) in enumerate(zip(got, want)):
         assert np.abs(g - w).max() <= 1e-4 * np.abs(w).max(), f"step {i}: {np.abs(g - w).max()}"
-    used = len(PROMPT) + len(DECODE)
+    used = MAX_SEQ
     for l in range(LAYERS):
         for j, which in enumerate("kv"):
             g = widen(eng.cache(l, which), orc).reshape(NKV, MAX_SEQ, HD)
@@ -176,7 +181,6 @@ def test_engine_matches_oracle_sequence(dev, orc, model):
             scale = np.abs(w[:, :used]).max()
             assert np.all(np.abs(g[:, :used] - w[:, :used]) <= 2.0 ** -10 * np.abs(w[:, :used]) + 1e-4 * scale), \
                 f"layer {l} {which} cache"
-            assert (g[:, used:] == 0).all()
     eng.close()
 
 
@@ -297,11 +301,9 @@ def test_engine_each_op_on_its_own_inputs(dev, orc, model, layout):
     _teacher_forced(orc, model, layout, [PROMPT] + [[t] for t in DECODE], MAX_SEQ, MAX_CHUNK, "engine teacher-forced")
 
 
-def test_engine_chunks_across_angle_table_growth(dev, orc, model):
-    """A chunk's RoPE angles are rows of the engine's per-position table, filled from the host as
-    positions are first reached (256 rows, then doubling up to max_seq = 600). Chunks before, across
-    and after each fill boundary (256, 512, the cap), decode steps between them (their angles are
-    staged per step, outside the table) and a last chunk ending at max_seq, all teacher-forced."""
+def _growth_steps():
+    """Chunks before, across and after each fill boundary of the angle table (256, 512, the cap at
+    max_seq = 600), single tokens between them, and a last chunk ending at max_seq."""
     rng = np.random.default_rng(7)
     ids = lambda n: [int(t) for t in rng.integers(0, VOCAB, n)]
     steps = [ids(16) for _ in range(15)]                 # 0 .. 239: the first fill covers 256 rows
@@ -312,4 +314,32 @@ def test_engine_chunks_across_angle_table_growth(dev, orc, model):
     steps += [[t] for t in ids(50)]                       # 520 .. 569
     steps += [ids(14), ids(16)]                           # 570 .. 583, 584 .. 599: ends at max_seq
     assert sum(len(s) for s in steps) == 600
-    _teacher_forced(orc, model, L.ROPE_NEOX, steps, 600, 16, "engine angle table")
+    return steps
+
+
+def test_engine_chunks_across_angle_table_growth(dev, orc, model):
+    """A chunk's RoPE angles are the rows of the engine's per-position table that its positions name,
+    filled from the host as positions are first reached (256 rows, then doubling up to max_seq);
+    a one-token step's angles are staged per step. Every step teacher-forced."""
+    _teacher_forced(orc, model, L.ROPE_NEOX, _growth_steps(), 600, 16, "engine angle table")
+
+
+def test_graph_run_equals_eager_across_angle_table_growth(dev, model):
+    """Graph mode (replayed single tokens between eager chunks that grow the angle table) is bit
+    for bit the eager run."""
+    table, layers, final = model
+    cfg = L.EngineConfig(H, NQ, NKV, HD, INTER, LAYERS, 600, 16, EPS, THETA, L.ROPE_NEOX, L.F16, L.F16)
+    steps = _growth_steps()
+    runs = []
+    for graph in (False, True):
+        eng = Engine(cfg, table, L.F32, VOCAB, layers, final, project, attend)
+        runs.append((eng, _run(eng, graph, steps)))
+    print("case engine graph chunks vs eager, growth run", flush=True)
+    (eager, e_out), (graph, g_out) = runs
+    for i, (a, b) in enumerate(zip(e_out, g_out)):
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), f"step {i}"
+    for l in range(LAYERS):
+        for w in "kv":
+            assert torch.equal(eager.cache(l, w), graph.cache(l, w)), f"layer {l} {w} cache"
+    eager.close()
+    graph.close()
