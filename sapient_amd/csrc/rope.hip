@@ -630,8 +630,9 @@ int launch_rope_kv(const void* qv, void* qov, int nq, const void* kv, const void
     TC* kc = static_cast<TC*>(kcv);
     TC* vc = static_cast<TC*>(vcv);
     const int half = head_dim / 2;
-    DenTable den;
-    fill_dens(den, half, head_dim, base);
+    // Supplied angles leave the denominators unused: no libm calls per launch.
+    DenTable den{};
+    if (ang == nullptr) fill_dens(den, half, head_dim, base);
     const bool il = layout == SPH_ROPE_INTERLEAVED;
     auto ok = [&](int P) {
         const int run = il ? 2 * P : P;  // contiguous elements per access
