@@ -42,10 +42,16 @@ class Error : public std::runtime_error {
 
 // A contiguous host tensor: shape, dtype and little-endian bytes — the data
 // model of sapient_core::Tensor (crates/sapient-core/src/tensor.rs:22-29).
+// Copies share one byte buffer, as the reference's tensors share one
+// refcounted buffer (an Arc, crates/sapient-core/src/buffer.rs:54): passing
+// or returning a tensor copies no bytes; bytes_mut() first gives this tensor
+// its own bytes when they are shared (copy on write).
 class Tensor {
  public:
     Tensor() = default;
     static Tensor from_f32(const std::vector<float>& data, std::vector<size_t> shape);
+    // Little-endian f32 bytes, taken without a copy (Tensor::from_f32_vec, tensor.rs:51-71).
+    static Tensor from_f32_bytes(std::vector<uint8_t> bytes, std::vector<size_t> shape);
     static Tensor from_f16_bytes(std::vector<uint8_t> bytes, std::vector<size_t> shape);
     static Tensor from_bf16_bytes(std::vector<uint8_t> bytes, std::vector<size_t> shape);
     // Packed GGUF blocks; the byte count must equal byte_count(dt, numel)
@@ -55,20 +61,22 @@ class Tensor {
     const std::vector<size_t>& shape() const { return shape_; }
     DType dtype() const { return dtype_; }
     size_t numel() const;
-    const std::vector<uint8_t>& bytes() const { return bytes_; }
-    // The same bytes under another shape of equal numel (Tensor::reshape).
+    const std::vector<uint8_t>& bytes() const;
+    // The same bytes under another shape of equal numel (Tensor::reshape), shared.
     Tensor reshaped(std::vector<size_t> shape) const;
-    // The bytes, writable in place (Tensor::as_bytes_mut, tensor.rs:590).
-    std::vector<uint8_t>& bytes_mut() { return bytes_; }
+    // The bytes, writable in place (Tensor::as_bytes_mut, tensor.rs:590); shared bytes are copied first.
+    std::vector<uint8_t>& bytes_mut();
     // The values of an F32 tensor (as_f32_slice); throws for other dtypes.
     std::vector<float> as_f32() const;
 
  private:
     Tensor(std::vector<size_t> shape, DType dt, std::vector<uint8_t> bytes)
+        : shape_(std::move(shape)), dtype_(dt), bytes_(std::make_shared<std::vector<uint8_t>>(std::move(bytes))) {}
+    Tensor(std::vector<size_t> shape, DType dt, std::shared_ptr<std::vector<uint8_t>> bytes)
         : shape_(std::move(shape)), dtype_(dt), bytes_(std::move(bytes)) {}
     std::vector<size_t> shape_;
     DType dtype_ = DType::F32;
-    std::vector<uint8_t> bytes_;
+    std::shared_ptr<std::vector<uint8_t>> bytes_;  // null: no bytes
 };
 
 // The op surface of the LlmBackend trait on this path

@@ -79,6 +79,26 @@ Tensor Tensor::from_f32(const std::vector<float>& data, std::vector<size_t> shap
     return Tensor(std::move(shape), DType::F32, std::move(b));
 }
 
+Tensor Tensor::from_f32_bytes(std::vector<uint8_t> bytes, std::vector<size_t> shape) {
+    if (bytes.size() != product(shape) * 4)
+        throw Error("shape mismatch: expected " + std::to_string(product(shape) * 4) + " bytes, got " +
+                    std::to_string(bytes.size()));
+    return Tensor(std::move(shape), DType::F32, std::move(bytes));
+}
+
+const std::vector<uint8_t>& Tensor::bytes() const {
+    static const std::vector<uint8_t> kNone;
+    return bytes_ ? *bytes_ : kNone;
+}
+
+std::vector<uint8_t>& Tensor::bytes_mut() {
+    if (!bytes_)
+        bytes_ = std::make_shared<std::vector<uint8_t>>();
+    else if (bytes_.use_count() > 1)
+        bytes_ = std::make_shared<std::vector<uint8_t>>(*bytes_);
+    return *bytes_;
+}
+
 Tensor Tensor::from_f16_bytes(std::vector<uint8_t> bytes, std::vector<size_t> shape) {
     if (bytes.size() != product(shape) * 2)
         throw Error("shape mismatch: expected " + std::to_string(product(shape) * 2) + " bytes, got " +
@@ -106,13 +126,14 @@ Tensor Tensor::reshaped(std::vector<size_t> shape) const {
     size_t n = 1;
     for (size_t d : shape) n *= d;
     if (n != numel()) throw Error("cannot reshape " + shape_str(shape_) + " to " + shape_str(shape));
-    return Tensor(std::move(shape), dtype_, bytes_);
+    return Tensor(std::move(shape), dtype_, bytes_);  // shares the bytes
 }
 
 std::vector<float> Tensor::as_f32() const {
     if (dtype_ != DType::F32) throw Error(std::string("type mismatch: expected f32, got ") + dtype_name(dtype_));
     std::vector<float> v(numel());
-    if (!v.empty()) std::memcpy(v.data(), bytes_.data(), v.size() * 4);
+    if (bytes().size() != v.size() * 4) throw Error("tensor holds no f32 data for its shape");
+    if (!v.empty()) std::memcpy(v.data(), bytes_->data(), v.size() * 4);
     return v;
 }
 
@@ -353,13 +374,13 @@ Tensor HipLlmBackend::rms_norm(const Tensor& x, const Tensor* weight_t, float ep
     DeviceBuf od = alloc(x.numel() * 4);
     const int st = sph_rms_norm(xd.ptr, (int)x.dtype(), wd.ptr, weight_t ? (int)wt.dtype() : SPH_F32, od.ptr, SPH_F32,
                                 (int64_t)rows, (int64_t)dim, eps, stream_);
-    std::vector<float> out(x.numel());
-    if (st == SPH_OK) download(od, out.data(), out.size() * 4);
+    std::vector<uint8_t> out(x.numel() * 4);
+    if (st == SPH_OK) download(od, out.data(), out.size());
     release(xd);
     release(wd);
     release(od);
     check(st, "rms_norm");
-    return Tensor::from_f32(out, s);
+    return Tensor::from_f32_bytes(std::move(out), s);
 }
 
 std::pair<Tensor, Tensor> HipLlmBackend::add_rms_norm(const Tensor& x, const Tensor& residual, const Tensor& weight_t,
@@ -384,17 +405,17 @@ std::pair<Tensor, Tensor> HipLlmBackend::fused_add_rms_norm(const Tensor& x, con
     DeviceBuf od = alloc(xf.numel() * 4);
     const int st = sph_add_rms_norm(xd.ptr, rd.ptr, SPH_F32, wd.ptr, SPH_F32, od.ptr, SPH_F32, (int64_t)rows,
                                     (int64_t)dim, eps, stream_);
-    std::vector<float> normed(xf.numel()), sum(xf.numel());
+    std::vector<uint8_t> normed(xf.numel() * 4), sum(xf.numel() * 4);
     if (st == SPH_OK) {
-        download(od, normed.data(), normed.size() * 4);
-        download(rd, sum.data(), sum.size() * 4);
+        download(od, normed.data(), normed.size());
+        download(rd, sum.data(), sum.size());
     }
     release(xd);
     release(rd);
     release(wd);
     release(od);
     check(st, "add_rms_norm");
-    return {Tensor::from_f32(normed, xf.shape()), Tensor::from_f32(sum, xf.shape())};
+    return {Tensor::from_f32_bytes(std::move(normed), xf.shape()), Tensor::from_f32_bytes(std::move(sum), xf.shape())};
 }
 
 // binary_f32 (elementwise.rs:27-57): both sides widened to f32; same length or
@@ -412,13 +433,13 @@ Tensor HipLlmBackend::binary(const Tensor& a0, const Tensor& b0, bool mul) {
     DeviceBuf od = alloc(n * 4);
     const int st = mul ? sph_mul(ad.ptr, (int64_t)na, bd.ptr, (int64_t)nb, od.ptr, SPH_F32, stream_)
                        : sph_add(ad.ptr, (int64_t)na, bd.ptr, (int64_t)nb, od.ptr, SPH_F32, stream_);
-    std::vector<float> out(n);
-    if (st == SPH_OK) download(od, out.data(), n * 4);
+    std::vector<uint8_t> out(n * 4);
+    if (st == SPH_OK) download(od, out.data(), out.size());
     release(ad);
     release(bd);
     release(od);
     check(st, mul ? "mul" : "add");
-    return Tensor::from_f32(out, shape);
+    return Tensor::from_f32_bytes(std::move(out), shape);
 }
 
 Tensor HipLlmBackend::add(const Tensor& a, const Tensor& b) {
@@ -439,12 +460,12 @@ Tensor HipLlmBackend::unary_f32(const Tensor& x, const char* op) {
     if (std::strcmp(op, "silu") == 0) st = sph_silu(xd.ptr, od.ptr, SPH_F32, n, stream_);
     else if (std::strcmp(op, "gelu_erf") == 0) st = sph_gelu_erf(xd.ptr, od.ptr, SPH_F32, n, stream_);
     else st = sph_gelu_tanh(xd.ptr, od.ptr, SPH_F32, n, stream_);
-    std::vector<float> out(x.numel());
-    if (st == SPH_OK) download(od, out.data(), out.size() * 4);
+    std::vector<uint8_t> out(x.numel() * 4);
+    if (st == SPH_OK) download(od, out.data(), out.size());
     release(xd);
     release(od);
     check(st, op);
-    return Tensor::from_f32(out, x.shape());
+    return Tensor::from_f32_bytes(std::move(out), x.shape());
 }
 
 Tensor HipLlmBackend::silu(const Tensor& x) {
@@ -488,14 +509,14 @@ Tensor HipLlmBackend::layer_norm(const Tensor& x0, const Tensor* weight0, const 
     DeviceBuf od = alloc(x.numel() * 4);
     const int st = sph_layer_norm(xd.ptr, SPH_F32, wd.ptr, bd.ptr, SPH_F32, od.ptr, SPH_F32, (int64_t)rows,
                                   (int64_t)dim, eps, stream_);
-    std::vector<float> out(x.numel());
-    if (st == SPH_OK) download(od, out.data(), out.size() * 4);
+    std::vector<uint8_t> out(x.numel() * 4);
+    if (st == SPH_OK) download(od, out.data(), out.size());
     release(xd);
     release(wd);
     release(bd);
     release(od);
     check(st, "layer_norm");
-    return Tensor::from_f32(out, s);
+    return Tensor::from_f32_bytes(std::move(out), s);
 }
 
 // common::add_bias_last_dim (common.rs:556-569): y is F32, the bias any float
@@ -518,13 +539,13 @@ Tensor HipLlmBackend::bias_last_dim(const Tensor& y, const Tensor& bias0) {
     DeviceBuf bd = upload(b.bytes().data(), b.bytes().size());
     DeviceBuf od = alloc(y.numel() * 4);
     const int st = sph_add_bias(yd.ptr, bd.ptr, (int)b.dtype(), od.ptr, SPH_F32, (int64_t)y.numel(), (int64_t)n, stream_);
-    std::vector<float> out(y.numel());
-    if (st == SPH_OK) download(od, out.data(), out.size() * 4);
+    std::vector<uint8_t> out(y.numel() * 4);
+    if (st == SPH_OK) download(od, out.data(), out.size());
     release(yd);
     release(bd);
     release(od);
     check(st, "add_bias_last_dim");
-    return Tensor::from_f32(out, y.shape());
+    return Tensor::from_f32_bytes(std::move(out), y.shape());
 }
 
 Tensor HipLlmBackend::swiglu(const Tensor& gate, const Tensor& up) {
@@ -542,13 +563,13 @@ Tensor HipLlmBackend::fused_swiglu(const Tensor& gate, const Tensor& up) {
     DeviceBuf ud = upload(up.bytes().data(), up.bytes().size());
     DeviceBuf od = alloc(gate.numel() * 4);
     const int st = sph_swiglu(gd.ptr, ud.ptr, od.ptr, SPH_F32, (int64_t)gate.numel(), stream_);
-    std::vector<float> out(gate.numel());
-    if (st == SPH_OK) download(od, out.data(), out.size() * 4);
+    std::vector<uint8_t> out(gate.numel() * 4);
+    if (st == SPH_OK) download(od, out.data(), out.size());
     release(gd);
     release(ud);
     release(od);
     check(st, "swiglu");
-    return Tensor::from_f32(out, gate.shape());
+    return Tensor::from_f32_bytes(std::move(out), gate.shape());
 }
 
 // rope.rs:18-62 / :83-136: x [batch, n_heads, seq_len, head_dim] → new f32 tensor.
@@ -590,12 +611,12 @@ Tensor HipLlmBackend::rope(const Tensor& x0, const std::vector<size_t>& position
         st = sph_rope(xd.ptr, (int64_t)n_heads, nullptr, 0, SPH_F32, layout, static_cast<const int32_t*>(pd.ptr),
                       (int64_t)batch, (int64_t)seq, (int64_t)head_dim, (int64_t)rotary_dim, base, 1.0f, stream_);
     }
-    std::vector<float> out(x.numel());
-    if (st == SPH_OK) download(xd, out.data(), out.size() * 4);
+    std::vector<uint8_t> out(x.numel() * 4);
+    if (st == SPH_OK) download(xd, out.data(), out.size());
     release(xd);
     release(pd);
     check(st, "rope");
-    return Tensor::from_f32(out, d);
+    return Tensor::from_f32_bytes(std::move(out), d);
 }
 
 Tensor HipLlmBackend::apply_rope_positions(const Tensor& x, const std::vector<size_t>& positions, float base) {
@@ -635,14 +656,14 @@ Tensor HipLlmBackend::gather_rows(const Tensor& w, const std::vector<uint32_t>& 
     const int st = sph_embed(td.ptr, (int)w.dtype(), (int64_t)vocab, (int64_t)hidden,
                              static_cast<const uint32_t*>(idd.ptr), (int64_t)ids.size(), static_cast<float*>(od.ptr),
                              nullptr, stream_);
-    std::vector<float> out(ids.size() * hidden);
-    if (st == SPH_OK) download(od, out.data(), out.size() * 4);
+    std::vector<uint8_t> out(ids.size() * hidden * 4);
+    if (st == SPH_OK) download(od, out.data(), out.size());
     release(td);
     release(idd);
     release(od);
     if (st == SPH_EINVAL) throw Error(std::string("unsupported embedding dtype ") + dtype_name(w.dtype()));
     check(st, "embed_tokens");
-    return Tensor::from_f32(out, {1, ids.size(), hidden});
+    return Tensor::from_f32_bytes(std::move(out), {1, ids.size(), hidden});
 }
 
 // common.rs:355-434 / :449-528 over sph_kv_cache_update; the Q8_0 prefix is

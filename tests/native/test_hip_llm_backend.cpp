@@ -562,6 +562,29 @@ static void quant_bytes_are_validated(HipLlmBackend&) {  // tensor.rs:143-169
                .find("shape mismatch") != std::string::npos, "byte count");
 }
 
+// Copies share one byte buffer (the reference's Arc'd buffer): no bytes are copied until one copy
+// writes (Arc::make_mut), and then only that copy changes; a reshape shares them too. An op's
+// result owns fresh bytes, and a kv-cache update writes only the tensor it is given.
+static void tensor_copies_share_bytes_until_written(HipLlmBackend& bk) {
+    const Tensor a = Tensor::from_f32({1, 2, 3, 4}, {2, 2});
+    Tensor b = a;
+    const Tensor c = a.reshaped({4});
+    ASSERT(b.bytes().data() == a.bytes().data() && c.bytes().data() == a.bytes().data(), "copies share bytes");
+    float nine = 9.0f;
+    std::memcpy(b.bytes_mut().data(), &nine, 4);
+    ASSERT(b.bytes().data() != a.bytes().data(), "a write gives the copy its own bytes");
+    ASSERT(a.as_f32()[0] == 1.0f && c.as_f32()[0] == 1.0f && b.as_f32()[0] == 9.0f, "only the written copy changed");
+    ASSERT(b.as_f32()[3] == 4.0f, "the rest copied");
+    const Tensor s = bk.silu(a);
+    ASSERT(s.bytes().data() != a.bytes().data() && a.as_f32()[1] == 2.0f, "an op's result owns fresh bytes");
+    // update_kv_cache writes the cache it is given in place, not a copy sharing its bytes
+    Tensor cache = Tensor::from_f32(std::vector<float>(1 * 1 * 4 * 2, 0.0f), {1, 1, 4, 2});
+    const Tensor kept = cache;
+    (void)bk.update_kv_cache(cache, 0, Tensor::from_f32({5, 6}, {1, 1, 1, 2}));
+    ASSERT(cache.as_f32()[0] == 5.0f && cache.as_f32()[1] == 6.0f, "cache row 0 written");
+    ASSERT(kept.as_f32()[0] == 0.0f && kept.as_f32()[1] == 0.0f, "the earlier copy keeps its bytes");
+}
+
 int main() {
     if (!HipLlmBackend::is_available()) {
         std::printf("no gfx950 device\n");
@@ -593,6 +616,7 @@ int main() {
         {"add_rms_norm_is_add_then_rms_norm", add_rms_norm_is_add_then_rms_norm},
         {"embed_row_gather_matches_full_dequant", embed_row_gather_matches_full_dequant},
         {"quant_bytes_are_validated", quant_bytes_are_validated},
+        {"tensor_copies_share_bytes_until_written", tensor_copies_share_bytes_until_written},
         {"kv_cache_update_reference_test", kv_cache_update_reference_test},
         {"kv_cache_update_slides_when_full", kv_cache_update_slides_when_full},
         {"kv_cache_update_q8_0", kv_cache_update_q8_0},
