@@ -131,12 +131,16 @@ def rms_norm(x, weight, eps: float) -> np.ndarray:
 
 
 def add_rms_norm(x, residual, weight, eps: float):
-    """(normed, updated residual) of add (llama.rs:508) then rms_norm (llama.rs:515)."""
+    """(normed, updated residual) of add (llama.rs:508) then rms_norm (llama.rs:515); weight may be
+    None (unit weight, as rms_norm's)."""
     x, r = _f32(x), _f32(residual)
-    w = _f32(weight)
+    w = None if weight is None else _f32(weight)
     dim = x.shape[-1]
+    if r.shape != x.shape or (w is not None and w.size != dim):
+        raise ValueError("residual must match x, and weight the last dimension")
     normed, r_out = np.empty_like(x), np.empty_like(x)
-    lib().sor_add_rms_norm(_p(x), _p(r), _p(w), _p(normed), _p(r_out), x.size // dim, dim, np.float32(eps))
+    lib().sor_add_rms_norm(_p(x), _p(r), None if w is None else _p(w), _p(normed), _p(r_out), x.size // dim, dim,
+                           np.float32(eps))
     return normed, r_out
 
 

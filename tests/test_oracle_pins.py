@@ -231,6 +231,11 @@ def test_add_rms_norm_is_add_then_rms_norm():
     y, r2 = oracle.add_rms_norm(x, r, w, 1e-5)
     assert np.array_equal(_bits(r2), _bits((x + r).astype(np.float32)))
     assert np.array_equal(_bits(y), _bits(oracle.rms_norm(x + r, w, 1e-5)))
+    # no weight is unit weight, as for rms_norm; a weight of the wrong length is refused
+    y1, _ = oracle.add_rms_norm(x, r, None, 1e-5)
+    assert np.array_equal(_bits(y1), _bits(oracle.add_rms_norm(x, r, np.ones(256, np.float32), 1e-5)[0]))
+    with pytest.raises(ValueError):
+        oracle.add_rms_norm(x, r, w[:255], 1e-5)
 
 
 # ─────────────────────────────── add / mul ───────────────────────────────
