@@ -15,6 +15,8 @@ pointer alignment an element offset produces:
   partial, scaled, q + k)
   transpose_heads           resident.rs:420-458
   kv_append                 resident.rs:645-711
+  fused decode step         wgpu_engine.rs:397-432, :525-573 (bias + RoPE + append,
+                            heads-major and token-major)
 
 Bars, as in the fixed tests: RMSNorm f32 outputs ≤ 1e-5 relative and half outputs
 ≤ 1 ulp of the oracle's f32 result rounded to nearest-even (the kernel's Σx² is
@@ -205,3 +207,74 @@ def test_layout_moves_random_shapes(dev, orc, case):
     got = to_np(cache)
     assert np.array_equal(got.view(np.uint32) if got.dtype == np.float32 else got,
                           ref.view(np.uint32) if ref.dtype == np.float32 else ref), f"kv_append case {case}"
+
+
+def _round_to(x32: np.ndarray, dtype, orc) -> np.ndarray:
+    """f32 values rounded to `dtype` (nearest-even) and widened back: a store in that type."""
+    if dtype == torch.float32:
+        return x32.astype(np.float32)
+    bits = narrow_bits(x32, dtype, orc)
+    return orc.f16_bits_to_f32(bits) if dtype == torch.float16 else orc.bf16_bits_to_f32(bits)
+
+
+@pytest.mark.parametrize("case", range(CASES))
+def test_fused_decode_step_random_shapes(dev, orc, case):
+    """sph_rope_kv_append (heads-major, q in place) and sph_rope_kv_append_tokens (token-major in,
+    q out heads-major) against the oracle's unfused sequence, wgpu_engine.rs:397-432 / :525-573:
+    bias added in f32 and stored in the activation type, RoPE over the full head (stored in the
+    activation type again for k), then each token's k and v rows appended at its own position in
+    the cache type. Positions are a random subset of the cache rows, in random order."""
+    rng = np.random.default_rng(6000 + case)
+    dtype = DTYPES[case % 3]
+    cdt = DTYPES[int(rng.integers(0, 3))]
+    bmode = rng.choice(["none", "f32", "same"])
+    bdt = torch.float32 if bmode == "f32" or dtype == torch.float32 else dtype
+    token_major = bool(rng.integers(0, 2))
+    interleaved = bool(rng.integers(0, 2))
+    Hq, Hkv = int(rng.integers(1, 24)), int(rng.integers(1, 9))
+    D = 8 * int(rng.choice([1, 2, 3, 5, 8, 10, 12, 16, 32]))
+    S = int(rng.choice([1, 2, 3, 4, 5, 9, 64, 300]))
+    max_seq = S + int(rng.integers(0, 300))
+    base = float(rng.choice([1e4, 5e5, 1e6]))
+    positions = np.sort(rng.permutation(max_seq)[:S]).astype(np.int32)
+    if rng.integers(0, 2):
+        positions = rng.permutation(positions).astype(np.int32)
+    print(f"case fused {case}: {_name(dtype)} cache {_name(cdt)} bias {bmode} {'tokens' if token_major else 'heads'} "
+          f"{'il' if interleaved else 'neox'} Hq{Hq} Hkv{Hkv} S{S} D{D} max_seq {max_seq}", flush=True)
+    shp = (lambda H: (S, H, D)) if token_major else (lambda H: (H, S, D))
+    q = _tensor(shp(Hq), dtype, dev, 7 * case + 1, 0)
+    k = _tensor(shp(Hkv), dtype, dev, 7 * case + 2, 0)
+    v = _tensor(shp(Hkv), dtype, dev, 7 * case + 3, 0)
+    biases = [None if bmode == "none" else _tensor((H * D,), bdt, dev, 7 * case + 4 + i, 0, 0.1)
+              for i, H in enumerate((Hq, Hkv, Hkv))]
+    kc = _tensor((Hkv, max_seq, D), cdt, dev, 7 * case + 7, 0)
+    vc = _tensor((Hkv, max_seq, D), cdt, dev, 7 * case + 8, 0)
+    kref, vref = to_np(kc).copy(), to_np(vc).copy()
+
+    def heads_major(t, H):  # exact f32 values, [H, S, D]
+        a = widen(t, orc).reshape(shp(H))
+        return np.ascontiguousarray(a.transpose(1, 0, 2) if token_major else a)
+
+    def biased(a, b, H):
+        return a if b is None else _round_to(a + widen(b, orc).reshape(H, 1, D), dtype, orc)
+
+    q32 = biased(heads_major(q, Hq), biases[0], Hq)
+    k32 = biased(heads_major(k, Hkv), biases[1], Hkv)
+    v32 = biased(heads_major(v, Hkv), biases[2], Hkv)
+    pos_t = torch.from_numpy(positions).to(dev)
+    if token_major:
+        q_out = ops.rope_kv_append_tokens(q, k, v, pos_t, base, kc, vc, interleaved=interleaved,
+                                          bq=biases[0], bk=biases[1], bv=biases[2])
+    else:
+        ops.rope_kv_append(q, k, v, pos_t, base, kc, vc, interleaved=interleaved,
+                           bq=biases[0], bk=biases[1], bv=biases[2])
+        q_out = q
+    rope = lambda a: orc.apply_rope_partial_scaled(a[None], positions, base, D, 1.0, interleaved)[0]
+    _same_bits(q_out, rope(q32), orc, f"fused q case {case}")
+    kr = _round_to(rope(k32), dtype, orc)
+    for s, p in enumerate(positions.tolist()):
+        orc.kv_append(np.ascontiguousarray(kr[:, s:s + 1]), kref, CODE[cdt], Hkv, 1, D, max_seq, p)
+        orc.kv_append(np.ascontiguousarray(v32[:, s:s + 1]), vref, CODE[cdt], Hkv, 1, D, max_seq, p)
+    for got, want, what in ((to_np(kc), kref, "k cache"), (to_np(vc), vref, "v cache")):
+        eq = got.view(np.uint32) == want.view(np.uint32) if got.dtype == np.float32 else got == want
+        assert eq.all(), f"fused {what} case {case}: {int((~eq).sum())} elements differ"
