@@ -101,3 +101,37 @@ def assert_ulp16(got: np.ndarray, want: np.ndarray, dtype, max_ulp: int, what: s
         worst = bad[np.argsort(-d[bad])][:6]
         ex = ", ".join(f"[{i}] got {g[i]:#06x} want {w[i]:#06x} ({int(d[i])} ulp)" for i in worst)
         raise AssertionError(f"{what}: {bad.size} of {g.size} beyond {max_ulp} ulp: {ex}")
+
+
+def layer_norm_bound(x32: np.ndarray, w, b, ref: np.ndarray) -> np.ndarray:
+    """Per-element bound on |kernel - oracle| for LayerNorm: the kernel sums Σx and Σ(x − mean)² in
+    another order than the reference's serial folds, which moves the mean and the variance by about
+    2^-24·√n·(|mean| + σ) (8× that as the margin); everything else rounds alike."""
+    x64 = x32.astype(np.float64)
+    n = x64.shape[-1]
+    mu = x64.mean(axis=-1, keepdims=True)
+    sd = np.maximum(x64.std(axis=-1, keepdims=True), 1e-30)
+    normed = np.abs(x64 - mu) / sd
+    wa = 1.0 if w is None else np.abs(w.astype(np.float64))
+    rel = 8 * 2.0 ** -24 * np.sqrt(n) * (np.abs(mu) + sd) / sd
+    return wa * (1 + normed) * rel + 2.0 ** -22 * np.abs(ref.astype(np.float64)) + 1e-30
+
+
+def check_layer_norm(out: torch.Tensor, ref: np.ndarray, x32, w, b, orc, what: str):
+    """LayerNorm parity: f32 outputs within layer_norm_bound of the oracle; half outputs within 1 ulp
+    of its f32 result rounded to nearest-even, or within that bound plus half an ulp."""
+    bound = layer_norm_bound(x32, w, b, ref)
+    if out.dtype == torch.float32:
+        got = to_np(out).astype(np.float64)
+        bad = ~(np.abs(got - ref) <= bound)
+        assert not bad.any(), f"{what}: {int(bad.sum())} beyond bound; worst {np.max(np.abs(got - ref) / bound):.2f}x"
+    else:
+        got16 = to_np(out)
+        want16 = narrow_bits(ref, out.dtype, orc)
+        d = ulp_diff16(got16, want16, out.dtype).reshape(ref.shape)
+        g32 = widen(out, orc).astype(np.float64)
+        mant = 10 if out.dtype == torch.float16 else 7
+        e = np.floor(np.log2(np.maximum(np.abs(ref.astype(np.float64)), 2.0 ** -14)))
+        half_ulp = 0.5 * 2.0 ** (e - mant)
+        ok = (d <= 1) | (np.abs(g32 - ref) <= bound + half_ulp)
+        assert ok.all(), f"{what}: {int((~ok).sum())} of {ok.size} beyond 1 ulp and the f32 bound"

@@ -17,7 +17,7 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import assert_ulp16, max_rel, narrow_bits, to_np, ulp_diff16, widen
+from helpers import assert_ulp16, check_layer_norm, max_rel, narrow_bits, to_np, ulp_diff16, widen
 from refvec import WgpuLcg
 
 import sapient_amd.ops as ops
@@ -32,35 +32,6 @@ def _gen(shape, seed, dev, mean=0.0, std=1.0, dtype=torch.float32):
     return (torch.randn(shape, generator=g, device=dev) * std + mean).to(dtype)
 
 
-def _bound(x32: np.ndarray, w, b, ref: np.ndarray) -> np.ndarray:
-    x64 = x32.astype(np.float64)
-    n = x64.shape[-1]
-    mu = x64.mean(axis=-1, keepdims=True)
-    sd = np.maximum(x64.std(axis=-1, keepdims=True), 1e-30)
-    normed = np.abs(x64 - mu) / sd
-    wa = 1.0 if w is None else np.abs(w.astype(np.float64))
-    rel = 8 * 2.0 ** -24 * np.sqrt(n) * (np.abs(mu) + sd) / sd
-    return wa * (1 + normed) * rel + 2.0 ** -22 * np.abs(ref.astype(np.float64)) + 1e-30
-
-
-def _check(out: torch.Tensor, ref: np.ndarray, x32, w, b, orc, what: str):
-    bound = _bound(x32, w, b, ref)
-    if out.dtype == torch.float32:
-        got = to_np(out).astype(np.float64)
-        bad = ~(np.abs(got - ref) <= bound)
-        assert not bad.any(), f"{what}: {int(bad.sum())} beyond bound; worst {np.max(np.abs(got - ref) / bound):.2f}x"
-    else:
-        got16 = to_np(out)
-        want16 = narrow_bits(ref, out.dtype, orc)
-        d = ulp_diff16(got16, want16, out.dtype).reshape(ref.shape)
-        g32 = widen(out, orc).astype(np.float64)
-        mant = 10 if out.dtype == torch.float16 else 7
-        e = np.floor(np.log2(np.maximum(np.abs(ref.astype(np.float64)), 2.0 ** -14)))
-        half_ulp = 0.5 * 2.0 ** (e - mant)
-        ok = (d <= 1) | (np.abs(g32 - ref) <= bound + half_ulp)
-        assert ok.all(), f"{what}: {int((~ok).sum())} of {ok.size} beyond 1 ulp and the f32 bound"
-
-
 def test_layer_norm_matches_wgpu_test_vectors(dev, orc):
     """wgpu tests/resident.rs:860-886: 7 x 1536, lcg, x·3, w = 0.5 + |next()|, b = next()·0.1,
     eps 1e-5; the reference test's own bound is 1e-4 absolute."""
@@ -72,7 +43,7 @@ def test_layer_norm_matches_wgpu_test_vectors(dev, orc):
     print(f"case layer_norm wgpu-vectors {rows}x{dim}", flush=True)
     out = ops.layer_norm(torch.from_numpy(x).to(dev), torch.from_numpy(w).to(dev), torch.from_numpy(b).to(dev), 1e-5)
     ref = orc.layer_norm(x, w, b, 1e-5)
-    _check(out, ref, x, w, b, orc, "wgpu vectors")
+    check_layer_norm(out, ref, x, w, b, orc, "wgpu vectors")
     x64 = x.astype(np.float64)
     mu, var = x64.mean(axis=1, keepdims=True), x64.var(axis=1, keepdims=True)
     assert np.abs(to_np(out) - ((x64 - mu) / np.sqrt(var + 1e-5) * w + b)).max() < 1e-4
@@ -88,7 +59,7 @@ def _run(dev, orc, dtype, rows, dim, mode, wbt, od):
     w32 = None if w is None else widen(w, orc)
     b32 = None if b is None else widen(b, orc)
     ref = orc.layer_norm(x32, w32, b32, 1e-5)
-    _check(out, ref, x32, w32, b32, orc, f"layer_norm {dtype} {rows}x{dim} {mode}")
+    check_layer_norm(out, ref, x32, w32, b32, orc, f"layer_norm {dtype} {rows}x{dim} {mode}")
 
 
 @pytest.mark.parametrize("dtype", DTYPES, ids=IDS)
@@ -121,7 +92,7 @@ def test_layer_norm_full(dev, orc, dtype, rows, dim):
     torch.cuda.synchronize()
     x32 = widen(x, orc)
     ref = orc.layer_norm(x32, to_np(w), to_np(b), 1e-5)
-    _check(out, ref, x32, to_np(w), to_np(b), orc, f"layer_norm full {dtype}")
+    check_layer_norm(out, ref, x32, to_np(w), to_np(b), orc, f"layer_norm full {dtype}")
 
 
 @pytest.mark.parametrize("dtype", DTYPES, ids=IDS)
@@ -178,7 +149,7 @@ def test_layer_norm_unaligned_views_take_generic_path(dev, orc):
     b = _gen((768,), 93, dev, 0.0, 0.1)
     ops.layer_norm(x, w, b, 1e-5, out=out)
     ref = orc.layer_norm(to_np(x), to_np(w), to_np(b), 1e-5)
-    _check(out, ref, to_np(x), to_np(w), to_np(b), orc, "unaligned")
+    check_layer_norm(out, ref, to_np(x), to_np(w), to_np(b), orc, "unaligned")
 
 
 def test_layer_norm_rejects_bad_arguments(dev):

@@ -8,6 +8,7 @@ aligned fallbacks — meet odd dimensions, small and large row counts and every
 pointer alignment an element offset produces:
 
   rms_norm / add_rms_norm   layernorm.rs:75-106, llama.rs:508→515
+  layer_norm                layernorm.rs:17-69
   silu, swiglu, gelu_tanh,  elementwise.rs:15-69, :120-143, :163-174
   gelu_erf, add, mul
   add_bias                  common.rs:556-569
@@ -20,14 +21,16 @@ pointer alignment an element offset produces:
 
 Bars, as in the fixed tests: RMSNorm f32 outputs ≤ 1e-5 relative and half outputs
 ≤ 1 ulp of the oracle's f32 result rounded to nearest-even (the kernel's Σx² is
-summed in another order); the fused residual, the element-wise ops, the bias, RoPE
-and the layout moves bit for bit.
+summed in another order); LayerNorm within the fixed tests' summation-order bound
+(helpers.layer_norm_bound); the fused residual, the element-wise ops, the bias,
+RoPE and the layout moves bit for bit.
 """
 import numpy as np
 import pytest
 import torch
 
-from helpers import assert_bits16_equal, assert_bits_equal, assert_ulp16, max_rel, narrow_bits, to_np, widen
+from helpers import (assert_bits16_equal, assert_bits_equal, assert_ulp16, check_layer_norm, max_rel, narrow_bits,
+                     to_np, widen)
 
 import sapient_amd.ops as ops
 from sapient_amd._lib import BF16, F16, F32
@@ -107,6 +110,30 @@ def test_norms_random_shapes(dev, orc, case):
     ref_y, ref_r = orc.add_rms_norm(x32, r32, w32, eps)
     _same_bits(r, ref_r, orc, f"add_rms_norm residual case {case}")
     _norm_close(y, ref_y, orc, f"add_rms_norm case {case}")
+
+
+@pytest.mark.parametrize("case", range(CASES))
+def test_layer_norm_random_shapes(dev, orc, case):
+    rng = np.random.default_rng(1500 + case)
+    dtype = DTYPES[case % 3]
+    rows = int(rng.choice([1, 2, 3, 7, 16, 33, 100, 257]))
+    dim = _dim(rng, 20000)
+    while rows * dim > 600_000:
+        rows = max(1, rows // 2)
+    mode = rng.choice(["wb", "w", "b", "none"])
+    wbdt = torch.float32 if rng.integers(0, 2) or dtype == torch.float32 else dtype
+    odt = torch.float32 if rng.integers(0, 2) else dtype
+    offs = [int(o) for o in rng.integers(0, 4, 3)]
+    print(f"case layer_norm {case}: {_name(dtype)} {rows}x{dim} {mode} wb {_name(wbdt)} out {_name(odt)} "
+          f"offsets={offs}", flush=True)
+    x = _tensor((rows, dim), dtype, dev, 3 * case + 1, offs[0], 1.5, 0.5)
+    w = _tensor((dim,), wbdt, dev, 3 * case + 2, offs[1], 0.2, 1.0) if "w" in mode else None
+    b = _tensor((dim,), wbdt, dev, 3 * case + 3, offs[2], 0.1) if "b" in mode else None
+    x32 = widen(x, orc)
+    w32 = None if w is None else widen(w, orc)
+    b32 = None if b is None else widen(b, orc)
+    out = ops.layer_norm(x, w, b, 1e-5, out_dtype=odt)
+    check_layer_norm(out, orc.layer_norm(x32, w32, b32, 1e-5), x32, w32, b32, orc, f"layer_norm case {case}")
 
 
 @pytest.mark.parametrize("case", range(CASES))
