@@ -903,7 +903,8 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
-        "data": "synthetic (seeded torch.randn ~N(0,1) inputs/residual, weight ~N(1,0.1))",
+        "data": "synthetic (seeded torch.randn ~N(0,1) inputs/residual, weight ~N(1,0.1); torch.Generator "
+                "seeds: x 10 and 11, residual 20 and 21 (two rotating sets), weight 3)",
         "config": {"workload": "fused residual-add + RMSNorm, Llama-3-8B width", "rows": rows, "dim": dim,
                    "eps": 1e-5, "io": "x, residual in; normed + updated residual out (f32)",
                    "rows_per_s": round(rows / (avg_ms * 1e-3), 1), "pct_of_peak": round(100 * value / PEAK_GBS, 1)},
