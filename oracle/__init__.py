@@ -2,7 +2,7 @@
 ``oracle/sapient_oracle.c`` by ``oracle/Makefile``).
 
 Test infrastructure only: the test suite, the smoke check and the benchmark's
-CPU-baseline leg use it as the checker. It is never part of the product path.
+CPU-baseline leg use it as the reference for results. It is never part of the product path.
 Every wrapper takes and returns numpy arrays; dtypes follow the reference's
 CPU kernels (f32 compute, f32 outputs).
 """

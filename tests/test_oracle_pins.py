@@ -1,4 +1,4 @@
-"""Pins the CPU oracle before it is trusted as the checker (no GPU needed).
+"""Pins the CPU oracle before the GPU results are held to it (no GPU needed).
 
 Each oracle function is held to something it was not written from:
   - the known-answer tests in the reference's own test modules,
