@@ -311,7 +311,7 @@ class Row:
         self.latency = latency
         self.cfg = cfg  # the benchmark configuration (1-5) this row measures, or None for an extra row
         # (label, fn(set)): a torch kernel with the same memory traffic on the same buffers (a copy-like
-        # reference: the same box and buffer placement, a kernel this library did not write), or None
+        # reference: the same machine and buffer placement, a kernel this library did not write), or None
         self.ref = ref
 
 
@@ -505,7 +505,7 @@ def op_table(torch, ops, dev, only=None, cpu_budget=0.0, profile_launches=0, ker
                 row["us_method"] = "HIP graph replay, per launch"
             if r.ref is not None:
                 # torch's kernel with the same traffic, timed the same way on the same buffers: where buffers
-                # land in HBM moves a streaming kernel by ~2-3 %, and boxes differ by a few per cent; this
+                # land in HBM moves a streaming kernel by ~2-3 %, and machines differ by a few per cent; this
                 # reference shares both with the row.
                 label, rfn = r.ref
                 rms = time_regions(torch, rfn, sets)
@@ -703,7 +703,7 @@ def op_table(torch, ops, dev, only=None, cpu_budget=0.0, profile_launches=0, ker
 class ClockSampler:
     """The GPU's engine clock as the driver reports it (sysfs pp_dpm_sclk, the level marked current),
     sampled every millisecond on a thread while a timed region runs; plus the memory clock and the board power
-    cap, read once. Boxes differ by a few per cent in speed: this is the clock they ran at."""
+    cap, read once. Machines differ by a few per cent in speed: this is the clock they ran at."""
 
     def __init__(self, torch):
         import ctypes
@@ -767,8 +767,8 @@ class ClockSampler:
         return out
 
 
-def box_copy(torch, dev, warmup, steps):
-    """This box's streaming speed, for reading the headline across boxes (MI355X boxes differ by a few per
+def plain_copy(torch, dev, warmup, steps):
+    """This machine's streaming speed, for reading the headline across machines (MI355X machines differ by a few per
     cent): torch's `neg` (a kernel this library did not write) over the headline's byte count, 512 MiB read
     and 512 MiB written per launch, timed like the headline right after it."""
     n = 2 * 16384 * 4096
@@ -873,7 +873,7 @@ def main():
     avg_ms = region_ms / args.steps
     achieved = alg_bytes / (avg_ms * 1e-3) / 1e9
     value = alg_bytes * args.steps / (region_ms * 1e-3) / 1e9
-    box = box_copy(torch, dev, args.warmup, args.steps)
+    plain = plain_copy(torch, dev, args.warmup, args.steps)
 
     cpu = None
     if not args.no_cpu:
@@ -913,7 +913,7 @@ def main():
                      "kernel": HEADLINE_KERNEL, "alg_bytes_per_launch": alg_bytes,
                      "avg_launch_us": round(avg_ms * 1e3, 2)},
         "cpu_baseline": cpu,
-        "box_copy": box,
+        "plain_copy": plain,
         "device_clock": clocks.report(),
         "timing": {"region_ms": round(region_ms, 3), "host_wall_ms": round(wall * 1e3, 3),
                    "rotation_bytes": rot_bytes,

@@ -324,7 +324,7 @@ int launch_shape(const TX* xp, TX* rp, const TW* wp, const TW* bp, TO* op, int64
 }
 
 // Launch shapes, measured at 16384 x 4096 on MI355X (round-robin medians on
-// two boxes; one-block-per-row shapes listed as VPT):
+// two machines; one-block-per-row shapes listed as VPT):
 //  - fused add + RMSNorm: row-looping blocks, one vector per lane, 16 (f32)
 //    or 8 (half) resident waves per CU: f32 171.8 µs (one block per row,
 //    VPT 2: 175.0), f16 85.4 µs (VPT 1: 87.6), bf16 85.8 µs (84.9);

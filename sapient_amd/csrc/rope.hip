@@ -135,7 +135,7 @@ __device__ __forceinline__ void store_run(T* p, const float (&v)[L]) {
 // reduction. Per-thread angles (pairs i0 .. i0+P of one token) put low pairs
 // in every wave, which made every wave pay for both reductions. sin and cos
 // reach the threads that apply them through LDS. Measured at 32 + 8 heads x
-// 8192 tokens x 128 on MI355X (one box): f16 NEOX 31.5 us per-thread, 28.4 us
+// 8192 tokens x 128 on MI355X (one machine): f16 NEOX 31.5 us per-thread, 28.4 us
 // with no angles at all, 28.6 us pair-major with two batches in flight. f32,
 // whose angles are shared by all 40 heads of a thread, is ~0.5 us faster
 // per-thread (the two block barriers cost about what the reductions save).
@@ -529,7 +529,7 @@ __global__ __launch_bounds__(kThreads) void rope_kv_kernel(const T* q, T* qo, in
 // Launch shape of rope_kernel per storage type and layout, chosen by
 // round-robin timing at the Llama-3-8B shape on MI355X (32 + 8 heads × 8192
 // tokens × 128, in place), beside an in-place 16-byte copy of the same bytes
-// (two launches, q and k) as the ceiling; medians of 12 rounds on one box:
+// (two launches, q and k) as the ceiling; medians of 12 rounds on one machine:
 //  - half types: NEOX P = 4 (8-byte runs), interleaved split with P = 2
 //    (two 8-byte runs), U = 2, pair-major angles, 2048 units in all (four
 //    head groups, each recomputing its angles: more waves in flight outweigh
@@ -539,7 +539,7 @@ __global__ __launch_bounds__(kThreads) void rope_kv_kernel(const T* q, T* qo, in
 //  - f32: P = 4 NEOX, interleaved split with P = 2 (16-byte runs), U = 1,
 //    per-thread angles, 512 units (one group holds all 40 heads). NEOX
 //    57.5 µs, interleaved 58.0 µs (one 16-byte run: 61.2 µs), copy 56.3 µs.
-// Boxes differ by up to ±5 % in absolute speed; the ordering held on each.
+// Machines differ by up to ±5 % in absolute speed; the ordering held on each.
 template <typename T, bool IL>
 struct RopeShape {
     static constexpr bool kHalf = sizeof(T) == 2;

@@ -54,7 +54,7 @@ def test_final_line_fits_a_log_tail():
             "cpu_baseline": {"value": 11.9, "unit": "GB/s", "cores": 1, "kind": "port",
                              "sample": "oracle add_rms_norm on 2048x4096 f32 rows (1/8 of the workload), 889 reps in "
                                        "10 s, 1 thread of AMD EPYC 9575F 64-Core Processor (16 host cores visible)"},
-            "box_copy": {"kernel": "torch neg, 2 x 16384 x 4096 f32 (read + write)", "GB/s": 6120.2, "pct_peak": 76.5},
+            "plain_copy": {"kernel": "torch neg, 2 x 16384 x 4096 f32 (read + write)", "GB/s": 6120.2, "pct_peak": 76.5},
             "device_clock": {"sclk_mhz_during_headline": {"median": 825.0, "min": 711, "max": 893}, "samples": 14,
                              "sclk_levels": "0: 500Mhz 1: 1412Mhz * 2: 2400Mhz", "mclk": "0: 2000Mhz *",
                              "power_cap_w": 1400},
