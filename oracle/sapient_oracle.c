@@ -34,8 +34,8 @@ static inline float u2f(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
 
 /* ───────────────────────── half-precision conversions ─────────────────────────
  * The reference widens with crate `half` 2.7.1 (tensor.rs:348-361,
- * common.rs:192-203); widening is exact, NaNs come out quiet. Narrowing (the outputs this build
- * stores as f16/bf16) follows half's from_f32: IEEE round-to-nearest-even,
+ * common.rs:192-203); widening is exact, NaNs come out quiet. Narrowing (the outputs the HIP
+ * library stores as f16/bf16) follows half's from_f32: IEEE round-to-nearest-even,
  * NaN kept quiet with the top mantissa bits. */
 
 float sor_f16_to_f32(uint16_t h) {
