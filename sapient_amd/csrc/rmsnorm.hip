@@ -340,6 +340,8 @@ int launch_shape(const TX* xp, TX* rp, const TW* wp, const TW* bp, TO* op, int64
 // A row too wide for the looping shape takes the one-block-per-row kernel
 // (twice the values per lane past 16 waves); unaligned rows, or rows wider
 // than that, the generic kernel.
+constexpr int64_t kFewValues = int64_t(1) << 21;
+
 template <typename TX, typename TW, typename TO, int KIND>
 int launch_rms(const void* x, void* residual, const void* w, const void* bias, void* out, int64_t rows, int64_t dim,
                float eps, hipStream_t stream) {
@@ -371,9 +373,19 @@ int launch_rms(const void* x, void* residual, const void* w, const void* bias, v
         TO* op = static_cast<TO*>(out) + off;
         int st = kNoShape;
         if (vec_ok) {
+            // Launches of up to 2^21 values (a decode step, a prefill chunk at small widths): one
+            // vector per lane and twice the waves per row, so each wave's chain is one load
+            // before its reduction. Back-to-back per launch on MI355X, against the shapes below:
+            // 1 x 896 f32 1.87 -> 1.65 µs, f16 2.10 -> 1.65; 512 x 896 f32 2.73 -> 2.36-2.46,
+            // f16 2.89 -> 2.34; 512 x 4096 f16 3.6 -> 2.9, f32 3.83 -> 3.63; at 2048 x 4096 it
+            // lost (f16 6.7 -> 7.9, f32 12.9 -> 13.7), hence the bound.
+            if constexpr ((KIND == K_RMS || KIND == K_LAYER) && VPT > 1)
+                if (nr * dim <= kFewValues)
+                    st = launch_shape<TX, TW, TO, KIND, 1, false>(xp, rp, wp, bp, op, nr, (int)dim, eps, 16, stream);
             if constexpr (VPT_L > 0)
-                st = launch_shape<TX, TW, TO, KIND, VPT_L, true>(xp, rp, wp, bp, op, nr, (int)dim, eps, kLoopWaves,
-                                                                 stream);
+                if (st == kNoShape)
+                    st = launch_shape<TX, TW, TO, KIND, VPT_L, true>(xp, rp, wp, bp, op, nr, (int)dim, eps,
+                                                                     kLoopWaves, stream);
             if (st == kNoShape)
                 st = launch_shape<TX, TW, TO, KIND, VPT, kLoop>(xp, rp, wp, bp, op, nr, (int)dim, eps, 16, stream);
             if (st == kNoShape)  // wider than 16 waves at VPT: twice the values per lane, one block per row
