@@ -93,9 +93,9 @@ def test_add_mul_scalar_broadcast(dev, orc):
 
 
 @pytest.mark.parametrize("dtype", DTYPES, ids=IDS)
-# 16384 * 4 and 16384 * 4 + 4 straddle the one-vector-per-thread launch of small
-# element-wise calls (up to 16384 16-byte vectors; f32 holds 4 values per vector).
-@pytest.mark.parametrize("n", [1, 5, 4864, 16384 * 4, 16384 * 4 + 4, 512 * 4864, 1 << 20])
+# 2^22 / 2^22 + 4 (f32) and 2^23 / 2^23 + 8 (half types) straddle the one-vector-per-thread launch of
+# small and mid-size element-wise calls (up to 2^20 16-byte vectors; a vector holds 4 f32 or 8 half values).
+@pytest.mark.parametrize("n", [1, 5, 4864, 512 * 4864, 1 << 22, (1 << 22) + 4, 1 << 23, (1 << 23) + 8])
 def test_silu_swiglu(dev, orc, dtype, n):
     print(f"case silu/swiglu {dtype} n={n}", flush=True)
     g, u = _gen((n,), 6, dev, 2.0, dtype), _gen((n,), 7, dev, 2.0, dtype)
