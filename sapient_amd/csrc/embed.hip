@@ -20,7 +20,8 @@
 //
 // Design (write-dominated: 16 KiB of f32 out per 2.3 KiB Q4_K row in):
 //  - One wave64 per token (16 tokens per 1024-thread block; 8 per 512-thread
-//    block in embed_staged, whose LDS footprint that keeps small); each lane produces
+//    block in embed_staged, whose LDS footprint that keeps small, and 2 per
+//    block when there are too few ids to give every CU a block); each lane produces
 //    4 consecutive outputs per step, so every store instruction writes 1 KiB
 //    contiguous (16 bytes per lane), non-temporal (non-temporal stores and the
 //    larger block measured 4.8 → 6.5 TB/s on the Q4_K gather).
@@ -232,6 +233,7 @@ __global__ __launch_bounds__(kThreads) void embed_rows(const uint8_t* __restrict
 constexpr int kStageBytes = 4608;
 constexpr int kStagedThreads = 512;
 constexpr int kStagedTokPerBlock = kStagedThreads / kWave;
+constexpr int kFewTokPerBlock = 2;
 
 template <int W> struct StageWord;
 template <> struct StageWord<16> { using type = u32x4; };
@@ -250,17 +252,18 @@ template <> struct StageUnit<SPH_Q5_K> { static constexpr int bytes = 176, elems
 template <> struct StageUnit<SPH_Q6_K> { static constexpr int bytes = 210, elems = 256; };
 
 // chunk_units: units per chunk, chunk_units * bytes <= kStageBytes and a multiple of W.
-template <int DT, int W>
-__global__ __launch_bounds__(kStagedThreads) void embed_staged(const uint8_t* __restrict__ table, int64_t vocab, int hidden,
-                                                         int64_t row_bytes, const uint32_t* __restrict__ ids,
-                                                         int64_t n_ids, float* __restrict__ out, int32_t* bad_id_flag,
-                                                         int chunk_units) {
+// TPB: tokens (waves) per block.
+template <int DT, int W, int TPB>
+__global__ __launch_bounds__(TPB * kWave) void embed_staged(const uint8_t* __restrict__ table, int64_t vocab, int hidden,
+                                                      int64_t row_bytes, const uint32_t* __restrict__ ids,
+                                                      int64_t n_ids, float* __restrict__ out, int32_t* bad_id_flag,
+                                                      int chunk_units) {
     using Word = typename StageWord<W>::type;
     using U = StageUnit<DT>;
-    __shared__ __align__(16) uint8_t stage[kStagedTokPerBlock][kStageBytes];
+    __shared__ __align__(16) uint8_t stage[TPB][kStageBytes];
     const int lane = threadIdx.x & (kWave - 1);
     const int wv = threadIdx.x / kWave;
-    const int64_t t = (int64_t)blockIdx.x * kStagedTokPerBlock + wv;
+    const int64_t t = (int64_t)blockIdx.x * TPB + wv;
     const bool active = t < n_ids;
     const uint32_t id = active ? __builtin_amdgcn_readfirstlane(ids[t]) : 0u;
     const bool valid = active && (int64_t)id < vocab;
@@ -375,8 +378,20 @@ int launch_staged(const void* table, int64_t vocab, int64_t hidden, int64_t row_
     constexpr int64_t kChunk = int64_t(1) << 24;  // tokens per launch
     for (int64_t t0 = 0; t0 < n_ids; t0 += kChunk) {
         const int64_t nt = n_ids - t0 < kChunk ? n_ids - t0 : kChunk;
+        // Too few ids for one 8-wave block per CU (a decode step, a prefill chunk): 2-wave
+        // blocks, four times as many CUs. Per launch, back to back on MI355X: Q8_0 151936 x 896,
+        // 512 ids 2.49 -> 2.38-2.42 µs; F16 51200 x 2560, 64 ids 3.22 -> 2.93, 512 ids 3.57 ->
+        // 3.17-3.29 (one and four waves per block measured between the two).
+        if (nt <= (int64_t)kStagedTokPerBlock * device_cu_count()) {
+            const dim3 g2((unsigned)((nt + kFewTokPerBlock - 1) / kFewTokPerBlock));
+            const int st2 = launch(embed_staged<DT, W, kFewTokPerBlock>, g2, kFewTokPerBlock * kWave, stream,
+                                   static_cast<const uint8_t*>(table), vocab, (int)hidden, row_bytes, ids + t0, nt,
+                                   out + (size_t)t0 * (size_t)hidden, flag, cu);
+            if (st2 != SPH_OK) return st2;
+            continue;
+        }
         const dim3 grid((unsigned)((nt + kStagedTokPerBlock - 1) / kStagedTokPerBlock));
-        const int st = launch(embed_staged<DT, W>, grid, kStagedThreads, stream, static_cast<const uint8_t*>(table), vocab,
+        const int st = launch(embed_staged<DT, W, kStagedTokPerBlock>, grid, kStagedThreads, stream, static_cast<const uint8_t*>(table), vocab,
                               (int)hidden, row_bytes, ids + t0, nt, out + (size_t)t0 * (size_t)hidden, flag, cu);
         if (st != SPH_OK) return st;
     }
