@@ -669,6 +669,8 @@ int launch_rope_kv(const void* qv, void* qov, int nq, const void* kv, const void
     return SPH_EINVAL;  // head_dim or alignment the vector paths do not cover
 }
 
+constexpr int64_t kFewRopeRows = int64_t(1) << 15;
+
 // den: the denominators (DenTable) or the angle tables (TableArgs).
 template <typename T, typename A>
 int launch_rope(void* qv, int nq, void* kv, int nk, int layout, const int32_t* pos, int64_t batch, int64_t seq,
@@ -686,6 +688,15 @@ int launch_rope(void* qv, int nq, void* kv, int nk, int layout, const int32_t* p
     if (layout == SPH_ROPE_NEOX) {
         // The preferred P (a run of P elements per access), then narrower runs.
         constexpr int PN = RopeShape<T, false>::P;
+        // In-kernel angles at up to 2^15 (token, head) rows (a decode step, a small prefill chunk):
+        // one pair per run, so each lane evaluates one sin/cos — the long pole of a small launch.
+        // Per launch, back to back on MI355X, Qwen2.5-0.5B's 14 + 2 heads x 64: T = 1 f32 3.0 -> 2.25
+        // µs, f16 4.0 -> 2.57; T = 512 f32 3.96 -> 3.03, f16 4.37 -> 3.61; T = 2048 f32 5.0 -> 4.7,
+        // f16 6.3 -> 5.9. Table angles gain nothing from it (T = 512 f32 2.44 -> 2.66).
+        if constexpr (std::is_same<A, DenTable>::value) {
+            if (ntok * (int64_t)(nq + nk) <= kFewRopeRows && ok(1, 1))
+                return launch_rope_p<T, 1, false>(q, nq, k, nk, pos, ntok, seq, head_dim, half, pos_scale, den, stream);
+        }
         if (ok(PN, PN)) return launch_rope_p<T, PN, false>(q, nq, k, nk, pos, ntok, seq, head_dim, half, pos_scale, den, stream);
         if constexpr (PN / 2 >= 2) {
             if (ok(PN / 2, PN / 2)) return launch_rope_p<T, PN / 2, false>(q, nq, k, nk, pos, ntok, seq, head_dim, half, pos_scale, den, stream);
@@ -699,6 +710,12 @@ int launch_rope(void* qv, int nq, void* kv, int nk, int layout, const int32_t* p
     // Interleaved: split runs (two per thread, from both halves of the pairs)
     // when half divides into them, else one run per thread.
     constexpr int PI = RopeShape<T, true>::P;
+    // In-kernel angles at small launches: one pair per run, as for NEOX (T = 1 f32 3.05 -> 2.24 µs,
+    // f16 4.0 -> 2.5; T = 512 f32 3.85 -> 3.02, f16 4.37 -> 3.65; T = 2048 f16 6.33 -> 5.71).
+    if constexpr (std::is_same<A, DenTable>::value) {
+        if (ntok * (int64_t)(nq + nk) <= kFewRopeRows && ok(1, 2))
+            return launch_rope_p<T, 1, true, false>(q, nq, k, nk, pos, ntok, seq, head_dim, half, pos_scale, den, stream);
+    }
     if (half % (2 * PI) == 0 && ok(PI, 2 * PI))
         return launch_rope_p<T, PI, true, true>(q, nq, k, nk, pos, ntok, seq, head_dim, half, pos_scale, den, stream);
     constexpr int V = vec16<T>::n;  // elements per 16-byte access
