@@ -342,6 +342,14 @@ def latency_rows(torch, ops, dev, orc, nrm, cpu_gather):
                         lambda s, w=w: ops.rms_norm(s[0], w, 1e-6, out=s[1]),
                         lambda T1=T1: (lambda x=nrm(T1, H), w=nrm(H, scale=0.1, mean=1.0):
                                        orc.rms_norm(x, w, 1e-6), T1), latency=True, cfg=1))
+        # The residual add fused into the next RMSNorm (llama.rs:508 -> :515): x and the residual read,
+        # the normed rows and the updated residual written.
+        rows.append(Row(f"add_rms_norm qwen T={T1}", f"{T1}x{H}", "f32", T1 * H * 16 + H * 4, T1, "rows",
+                        lambda i, T1=T1: (gen(torch, (T1, H), 150 + i, dev, f32), gen(torch, (T1, H), 160 + i, dev, f32),
+                                          torch.empty(T1, H, device=dev)),
+                        lambda s, w=w: ops.add_rms_norm(s[0], s[1], w, 1e-6, out=s[2]),
+                        lambda T1=T1: (lambda x=nrm(T1, H), r=nrm(T1, H), w=nrm(H, scale=0.1, mean=1.0):
+                                       orc.add_rms_norm(x, r, w, 1e-6), T1), latency=True, cfg=1))
         # RoPE as the trait path's apply_rope_positions runs it: cos / sin from the backend's angle table
         # (positions 0 .. 63 at least, resident on the device, as rope_cos_sin_cache lays it out) at
         # device positions; the device sin/cos route beside it as an extra row.
