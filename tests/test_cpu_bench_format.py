@@ -34,7 +34,7 @@ def test_compact_rows_keep_identity_and_measurements():
 
 
 def test_final_line_fits_a_log_tail():
-    """Eighteen configuration rows (the count the default run prints) plus a headline line of the
+    """Twenty configuration rows (the count the default run prints) plus a headline line of the
     real field set stay under 7 KB."""
     b = _bench()
     rows = ([_row("add_rms_norm", dt, 2) for dt in ("f16 (f32 w)", "bf16 (f32 w)")] +
@@ -42,11 +42,12 @@ def test_final_line_fits_a_log_tail():
             [_row("swiglu", "f16", 4), _row("gelu_tanh", "f16", 4)] +
             [_row("embed_q4_k " + d, "q4_k->f32", 5) for d in ("uniform", "zipf1.1")] +
             [_row(f"{op} qwen T={t}", "f32", 1, latency=True) for t in (1, 512)
-             for op in ("rms_norm", "rope_neox", "swiglu", "embed_q8_0")])
-    assert len(rows) == 18
+             for op in ("rms_norm", "add_rms_norm", "rope_neox", "swiglu", "embed_q8_0")])
+    assert len(rows) == 20
     line = {"metric": b.METRIC, "value": 6113.8, "unit": "GB/s", "n_gpus": 1, "steps": 20, "warmup": 5,
             "ms_per_step": 0.1752, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
-            "data": "synthetic (seeded torch.randn ~N(0,1) inputs/residual, weight ~N(1,0.1))",
+            "data": "synthetic (seeded torch.randn ~N(0,1) inputs/residual, weight ~N(1,0.1); torch.Generator "
+                    "seeds: x 10 and 11, residual 20 and 21 (two rotating sets), weight 3)",
             "config": {"workload": "fused residual-add + RMSNorm, Llama-3-8B width", "rows": 16384, "dim": 4096},
             "roofline": {"bound": "hbm", "achieved": 6113.8, "peak": 8000.0, "unit": "GB/s", "frac": 0.7642,
                          "traffic": 1073887092.0, "kernel": b.HEADLINE_KERNEL, "alg_bytes_per_launch": 1073758208,
