@@ -70,6 +70,7 @@ class Tensor {
     std::vector<float> as_f32() const;
 
  private:
+    friend class HipLlmBackend;  // builds results on recycled byte buffers
     Tensor(std::vector<size_t> shape, DType dt, std::vector<uint8_t> bytes)
         : shape_(std::move(shape)), dtype_(dt), bytes_(std::make_shared<std::vector<uint8_t>>(std::move(bytes))) {}
     Tensor(std::vector<size_t> shape, DType dt, std::shared_ptr<std::vector<uint8_t>> bytes)
@@ -214,6 +215,15 @@ class HipLlmBackend final : public LlmBackend {
     DeviceBuf alloc(size_t bytes);
     void release(DeviceBuf& b);
     void download(const DeviceBuf& b, void* host, size_t bytes);
+    // Host bytes for a result of n bytes. Large ones come from a pool that takes back buffers of
+    // dropped results (the last tensor sharing them gone) with their pages still mapped: first touch
+    // of fresh host memory, more than the transfer, is what a large host-tensor call spends its time
+    // on. The pool is shared with the tensors whose bytes it lent, so it outlives the backend when
+    // they do. Contents are unspecified; every result writes all of its bytes.
+    class ResultPool;
+    std::shared_ptr<ResultPool> pool_;
+    std::shared_ptr<std::vector<uint8_t>> result_bytes(size_t n);
+    Tensor f32_result(std::shared_ptr<std::vector<uint8_t>> bytes, std::vector<size_t> shape) const;
     Tensor f32_input(const Tensor& t) const;  // exact widening of f16/bf16 (tensor.rs:331-361)
     Tensor binary(const Tensor& a, const Tensor& b, bool mul);
     Tensor unary_f32(const Tensor& x, const char* op);

@@ -19,6 +19,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <map>
 #include <string>
 
 namespace sapient_hip {
@@ -176,11 +177,75 @@ static std::vector<std::string> disable_list() {
     return out;
 }
 
+// Freed result buffers of at least kMinBytes, kept (at most kMaxHeld bytes in all) and handed to
+// later results needing between half and all of a buffer's capacity.
+class HipLlmBackend::ResultPool : public std::enable_shared_from_this<ResultPool> {
+ public:
+    static constexpr size_t kMinBytes = size_t(1) << 20;
+    static constexpr size_t kMaxHeld = size_t(4) << 30;
+
+    std::shared_ptr<std::vector<uint8_t>> take(size_t n) {
+        std::vector<uint8_t>* v = nullptr;
+        if (n >= kMinBytes) {
+            std::lock_guard<std::mutex> lock(mu_);
+            auto it = free_.lower_bound(n);
+            if (it != free_.end() && it->first / 2 <= n) {
+                v = it->second;
+                held_ -= it->first;
+                free_.erase(it);
+            }
+        }
+        if (v == nullptr) {
+            v = new std::vector<uint8_t>(n);
+        } else {
+            v->resize(n);  // within its capacity: no reallocation
+        }
+        if (n < kMinBytes) return std::shared_ptr<std::vector<uint8_t>>(v);
+        std::shared_ptr<ResultPool> self = shared_from_this();
+        return std::shared_ptr<std::vector<uint8_t>>(v, [self](std::vector<uint8_t>* b) { self->give(b); });
+    }
+
+    ~ResultPool() {
+        for (auto& e : free_) delete e.second;
+    }
+
+ private:
+    void give(std::vector<uint8_t>* v) noexcept {
+        const size_t cap = v->capacity();
+        {
+            std::lock_guard<std::mutex> lock(mu_);
+            if (held_ + cap <= kMaxHeld) {
+                try {
+                    free_.emplace(cap, v);
+                    held_ += cap;
+                    return;
+                } catch (...) {
+                }
+            }
+        }
+        delete v;
+    }
+
+    std::mutex mu_;
+    std::multimap<size_t, std::vector<uint8_t>*> free_;  // by capacity
+    size_t held_ = 0;
+};
+
+std::shared_ptr<std::vector<uint8_t>> HipLlmBackend::result_bytes(size_t n) { return pool_->take(n); }
+
+Tensor HipLlmBackend::f32_result(std::shared_ptr<std::vector<uint8_t>> bytes, std::vector<size_t> shape) const {
+    if (bytes->size() != product(shape) * 4)
+        throw Error("shape mismatch: expected " + std::to_string(product(shape) * 4) + " bytes, got " +
+                    std::to_string(bytes->size()));
+    return Tensor(std::move(shape), DType::F32, std::move(bytes));
+}
+
 HipLlmBackend::HipLlmBackend(LlmBackend* cpu) : cpu_(cpu) {
     if (!is_available()) throw Error("hip: no gfx950 device available");
     hipStream_t s = nullptr;
     hip_ok(hipStreamCreate(&s), "stream create");  // default priority
     stream_ = s;
+    pool_ = std::make_shared<ResultPool>();
     disabled_ = disable_list();
     const char* v = std::getenv("SAPIENT_HIP_VERIFY");
     verify_ = v != nullptr && std::strcmp(v, "1") == 0;
@@ -374,13 +439,13 @@ Tensor HipLlmBackend::rms_norm(const Tensor& x, const Tensor* weight_t, float ep
     DeviceBuf od = alloc(x.numel() * 4);
     const int st = sph_rms_norm(xd.ptr, (int)x.dtype(), wd.ptr, weight_t ? (int)wt.dtype() : SPH_F32, od.ptr, SPH_F32,
                                 (int64_t)rows, (int64_t)dim, eps, stream_);
-    std::vector<uint8_t> out(x.numel() * 4);
-    if (st == SPH_OK) download(od, out.data(), out.size());
+    auto out = result_bytes(x.numel() * 4);
+    if (st == SPH_OK) download(od, out->data(), out->size());
     release(xd);
     release(wd);
     release(od);
     check(st, "rms_norm");
-    return Tensor::from_f32_bytes(std::move(out), s);
+    return f32_result(std::move(out), s);
 }
 
 std::pair<Tensor, Tensor> HipLlmBackend::add_rms_norm(const Tensor& x, const Tensor& residual, const Tensor& weight_t,
@@ -405,17 +470,18 @@ std::pair<Tensor, Tensor> HipLlmBackend::fused_add_rms_norm(const Tensor& x, con
     DeviceBuf od = alloc(xf.numel() * 4);
     const int st = sph_add_rms_norm(xd.ptr, rd.ptr, SPH_F32, wd.ptr, SPH_F32, od.ptr, SPH_F32, (int64_t)rows,
                                     (int64_t)dim, eps, stream_);
-    std::vector<uint8_t> normed(xf.numel() * 4), sum(xf.numel() * 4);
+    auto normed = result_bytes(xf.numel() * 4);
+    auto sum = result_bytes(xf.numel() * 4);
     if (st == SPH_OK) {
-        download(od, normed.data(), normed.size());
-        download(rd, sum.data(), sum.size());
+        download(od, normed->data(), normed->size());
+        download(rd, sum->data(), sum->size());
     }
     release(xd);
     release(rd);
     release(wd);
     release(od);
     check(st, "add_rms_norm");
-    return {Tensor::from_f32_bytes(std::move(normed), xf.shape()), Tensor::from_f32_bytes(std::move(sum), xf.shape())};
+    return {f32_result(std::move(normed), xf.shape()), f32_result(std::move(sum), xf.shape())};
 }
 
 // binary_f32 (elementwise.rs:27-57): both sides widened to f32; same length or
@@ -433,13 +499,13 @@ Tensor HipLlmBackend::binary(const Tensor& a0, const Tensor& b0, bool mul) {
     DeviceBuf od = alloc(n * 4);
     const int st = mul ? sph_mul(ad.ptr, (int64_t)na, bd.ptr, (int64_t)nb, od.ptr, SPH_F32, stream_)
                        : sph_add(ad.ptr, (int64_t)na, bd.ptr, (int64_t)nb, od.ptr, SPH_F32, stream_);
-    std::vector<uint8_t> out(n * 4);
-    if (st == SPH_OK) download(od, out.data(), out.size());
+    auto out = result_bytes(n * 4);
+    if (st == SPH_OK) download(od, out->data(), out->size());
     release(ad);
     release(bd);
     release(od);
     check(st, mul ? "mul" : "add");
-    return Tensor::from_f32_bytes(std::move(out), shape);
+    return f32_result(std::move(out), shape);
 }
 
 Tensor HipLlmBackend::add(const Tensor& a, const Tensor& b) {
@@ -460,12 +526,12 @@ Tensor HipLlmBackend::unary_f32(const Tensor& x, const char* op) {
     if (std::strcmp(op, "silu") == 0) st = sph_silu(xd.ptr, od.ptr, SPH_F32, n, stream_);
     else if (std::strcmp(op, "gelu_erf") == 0) st = sph_gelu_erf(xd.ptr, od.ptr, SPH_F32, n, stream_);
     else st = sph_gelu_tanh(xd.ptr, od.ptr, SPH_F32, n, stream_);
-    std::vector<uint8_t> out(x.numel() * 4);
-    if (st == SPH_OK) download(od, out.data(), out.size());
+    auto out = result_bytes(x.numel() * 4);
+    if (st == SPH_OK) download(od, out->data(), out->size());
     release(xd);
     release(od);
     check(st, op);
-    return Tensor::from_f32_bytes(std::move(out), x.shape());
+    return f32_result(std::move(out), x.shape());
 }
 
 Tensor HipLlmBackend::silu(const Tensor& x) {
@@ -509,14 +575,14 @@ Tensor HipLlmBackend::layer_norm(const Tensor& x0, const Tensor* weight0, const 
     DeviceBuf od = alloc(x.numel() * 4);
     const int st = sph_layer_norm(xd.ptr, SPH_F32, wd.ptr, bd.ptr, SPH_F32, od.ptr, SPH_F32, (int64_t)rows,
                                   (int64_t)dim, eps, stream_);
-    std::vector<uint8_t> out(x.numel() * 4);
-    if (st == SPH_OK) download(od, out.data(), out.size());
+    auto out = result_bytes(x.numel() * 4);
+    if (st == SPH_OK) download(od, out->data(), out->size());
     release(xd);
     release(wd);
     release(bd);
     release(od);
     check(st, "layer_norm");
-    return Tensor::from_f32_bytes(std::move(out), s);
+    return f32_result(std::move(out), s);
 }
 
 // common::add_bias_last_dim (common.rs:556-569): y is F32, the bias any float
@@ -539,13 +605,13 @@ Tensor HipLlmBackend::bias_last_dim(const Tensor& y, const Tensor& bias0) {
     DeviceBuf bd = upload(b.bytes().data(), b.bytes().size());
     DeviceBuf od = alloc(y.numel() * 4);
     const int st = sph_add_bias(yd.ptr, bd.ptr, (int)b.dtype(), od.ptr, SPH_F32, (int64_t)y.numel(), (int64_t)n, stream_);
-    std::vector<uint8_t> out(y.numel() * 4);
-    if (st == SPH_OK) download(od, out.data(), out.size());
+    auto out = result_bytes(y.numel() * 4);
+    if (st == SPH_OK) download(od, out->data(), out->size());
     release(yd);
     release(bd);
     release(od);
     check(st, "add_bias_last_dim");
-    return Tensor::from_f32_bytes(std::move(out), y.shape());
+    return f32_result(std::move(out), y.shape());
 }
 
 Tensor HipLlmBackend::swiglu(const Tensor& gate, const Tensor& up) {
@@ -563,13 +629,13 @@ Tensor HipLlmBackend::fused_swiglu(const Tensor& gate, const Tensor& up) {
     DeviceBuf ud = upload(up.bytes().data(), up.bytes().size());
     DeviceBuf od = alloc(gate.numel() * 4);
     const int st = sph_swiglu(gd.ptr, ud.ptr, od.ptr, SPH_F32, (int64_t)gate.numel(), stream_);
-    std::vector<uint8_t> out(gate.numel() * 4);
-    if (st == SPH_OK) download(od, out.data(), out.size());
+    auto out = result_bytes(gate.numel() * 4);
+    if (st == SPH_OK) download(od, out->data(), out->size());
     release(gd);
     release(ud);
     release(od);
     check(st, "swiglu");
-    return Tensor::from_f32_bytes(std::move(out), gate.shape());
+    return f32_result(std::move(out), gate.shape());
 }
 
 // rope.rs:18-62 / :83-136: x [batch, n_heads, seq_len, head_dim] → new f32 tensor.
@@ -611,12 +677,12 @@ Tensor HipLlmBackend::rope(const Tensor& x0, const std::vector<size_t>& position
         st = sph_rope(xd.ptr, (int64_t)n_heads, nullptr, 0, SPH_F32, layout, static_cast<const int32_t*>(pd.ptr),
                       (int64_t)batch, (int64_t)seq, (int64_t)head_dim, (int64_t)rotary_dim, base, 1.0f, stream_);
     }
-    std::vector<uint8_t> out(x.numel() * 4);
-    if (st == SPH_OK) download(xd, out.data(), out.size());
+    auto out = result_bytes(x.numel() * 4);
+    if (st == SPH_OK) download(xd, out->data(), out->size());
     release(xd);
     release(pd);
     check(st, "rope");
-    return Tensor::from_f32_bytes(std::move(out), d);
+    return f32_result(std::move(out), d);
 }
 
 Tensor HipLlmBackend::apply_rope_positions(const Tensor& x, const std::vector<size_t>& positions, float base) {
@@ -656,14 +722,14 @@ Tensor HipLlmBackend::gather_rows(const Tensor& w, const std::vector<uint32_t>& 
     const int st = sph_embed(td.ptr, (int)w.dtype(), (int64_t)vocab, (int64_t)hidden,
                              static_cast<const uint32_t*>(idd.ptr), (int64_t)ids.size(), static_cast<float*>(od.ptr),
                              nullptr, stream_);
-    std::vector<uint8_t> out(ids.size() * hidden * 4);
-    if (st == SPH_OK) download(od, out.data(), out.size());
+    auto out = result_bytes(ids.size() * hidden * 4);
+    if (st == SPH_OK) download(od, out->data(), out->size());
     release(td);
     release(idd);
     release(od);
     if (st == SPH_EINVAL) throw Error(std::string("unsupported embedding dtype ") + dtype_name(w.dtype()));
     check(st, "embed_tokens");
-    return Tensor::from_f32_bytes(std::move(out), {1, ids.size(), hidden});
+    return f32_result(std::move(out), {1, ids.size(), hidden});
 }
 
 // common.rs:355-434 / :449-528 over sph_kv_cache_update; the Q8_0 prefix is

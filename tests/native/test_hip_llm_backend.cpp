@@ -585,6 +585,38 @@ static void tensor_copies_share_bytes_until_written(HipLlmBackend& bk) {
     ASSERT(kept.as_f32()[0] == 0.0f && kept.as_f32()[1] == 0.0f, "the earlier copy keeps its bytes");
 }
 
+// Large results (>= 1 MiB) take the bytes of dropped results of a fitting size back from the
+// backend's pool, pages already mapped; a live result's bytes are never handed out again, and a
+// result outlives the backend that made it.
+static void results_recycle_dropped_buffers(HipLlmBackend&) {
+    HipLlmBackend bk;  // an empty pool
+    const size_t n = size_t(1) << 19;  // 2 MiB of f32
+    std::vector<float> xs(n);
+    for (size_t i = 0; i < n; ++i) xs[i] = (float)(int)(i % 97) * 0.125f - 6.0f;
+    const Tensor x = Tensor::from_f32(xs, {n});
+    const uint8_t* first = nullptr;
+    std::vector<float> want;
+    {
+        const Tensor a = bk.silu(x);
+        first = a.bytes().data();
+        want = a.as_f32();
+    }
+    const Tensor b = bk.silu(x);
+    ASSERT(b.bytes().data() == first, "a dropped result's buffer is reused");
+    ASSERT(b.as_f32() == want, "the reused buffer holds the new result");
+    const Tensor c = bk.gelu(x);
+    ASSERT(c.bytes().data() != b.bytes().data(), "a live result's buffer is not handed out");
+    const Tensor small = bk.silu(Tensor::from_f32({1.0f, -2.0f}, {2}));
+    ASSERT(small.as_f32().size() == 2, "small results are plain allocations");
+    Tensor kept;
+    {
+        HipLlmBackend other;
+        kept = other.silu(x);
+    }
+    ASSERT(kept.as_f32() == want, "a result outlives its backend");
+    kept = Tensor();  // its bytes go back to the departed backend's pool, which it keeps alive
+}
+
 int main() {
     if (!HipLlmBackend::is_available()) {
         std::printf("no gfx950 device\n");
@@ -617,6 +649,7 @@ int main() {
         {"embed_row_gather_matches_full_dequant", embed_row_gather_matches_full_dequant},
         {"quant_bytes_are_validated", quant_bytes_are_validated},
         {"tensor_copies_share_bytes_until_written", tensor_copies_share_bytes_until_written},
+        {"results_recycle_dropped_buffers", results_recycle_dropped_buffers},
         {"kv_cache_update_reference_test", kv_cache_update_reference_test},
         {"kv_cache_update_slides_when_full", kv_cache_update_slides_when_full},
         {"kv_cache_update_q8_0", kv_cache_update_q8_0},
