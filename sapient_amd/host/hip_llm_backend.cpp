@@ -21,6 +21,7 @@
 #include <cstring>
 #include <map>
 #include <string>
+#include <unordered_map>
 
 namespace sapient_hip {
 
@@ -75,46 +76,46 @@ Tensor Tensor::from_f32(const std::vector<float>& data, std::vector<size_t> shap
     if (product(shape) != data.size())
         throw Error("shape mismatch: expected " + std::to_string(product(shape)) + " elements, got " +
                     std::to_string(data.size()));
-    std::vector<uint8_t> b(data.size() * 4);
+    Bytes b(data.size() * 4);
     if (!data.empty()) std::memcpy(b.data(), data.data(), b.size());
     return Tensor(std::move(shape), DType::F32, std::move(b));
 }
 
-Tensor Tensor::from_f32_bytes(std::vector<uint8_t> bytes, std::vector<size_t> shape) {
+Tensor Tensor::from_f32_bytes(Bytes bytes, std::vector<size_t> shape) {
     if (bytes.size() != product(shape) * 4)
         throw Error("shape mismatch: expected " + std::to_string(product(shape) * 4) + " bytes, got " +
                     std::to_string(bytes.size()));
     return Tensor(std::move(shape), DType::F32, std::move(bytes));
 }
 
-const std::vector<uint8_t>& Tensor::bytes() const {
-    static const std::vector<uint8_t> kNone;
+const Bytes& Tensor::bytes() const {
+    static const Bytes kNone;
     return bytes_ ? *bytes_ : kNone;
 }
 
-std::vector<uint8_t>& Tensor::bytes_mut() {
+Bytes& Tensor::bytes_mut() {
     if (!bytes_)
-        bytes_ = std::make_shared<std::vector<uint8_t>>();
+        bytes_ = std::make_shared<Bytes>();
     else if (bytes_.use_count() > 1)
-        bytes_ = std::make_shared<std::vector<uint8_t>>(*bytes_);
+        bytes_ = std::make_shared<Bytes>(*bytes_);
     return *bytes_;
 }
 
-Tensor Tensor::from_f16_bytes(std::vector<uint8_t> bytes, std::vector<size_t> shape) {
+Tensor Tensor::from_f16_bytes(Bytes bytes, std::vector<size_t> shape) {
     if (bytes.size() != product(shape) * 2)
         throw Error("shape mismatch: expected " + std::to_string(product(shape) * 2) + " bytes, got " +
                     std::to_string(bytes.size()));
     return Tensor(std::move(shape), DType::F16, std::move(bytes));
 }
 
-Tensor Tensor::from_bf16_bytes(std::vector<uint8_t> bytes, std::vector<size_t> shape) {
+Tensor Tensor::from_bf16_bytes(Bytes bytes, std::vector<size_t> shape) {
     if (bytes.size() != product(shape) * 2)
         throw Error("shape mismatch: expected " + std::to_string(product(shape) * 2) + " bytes, got " +
                     std::to_string(bytes.size()));
     return Tensor(std::move(shape), DType::BF16, std::move(bytes));
 }
 
-Tensor Tensor::from_quant_bytes(std::vector<uint8_t> bytes, std::vector<size_t> shape, DType dt) {
+Tensor Tensor::from_quant_bytes(Bytes bytes, std::vector<size_t> shape, DType dt) {
     if (!is_quantized(dt))
         throw Error(std::string("type mismatch: expected a quantized dtype (Q4_0, Q8_0, Q4_K, Q5_K, Q6_K), got ") + dtype_name(dt));
     const size_t expected = byte_count(dt, product(shape));
@@ -177,63 +178,121 @@ static std::vector<std::string> disable_list() {
     return out;
 }
 
-// Freed result buffers of at least kMinBytes, kept (at most kMaxHeld bytes in all) and handed to
-// later results needing between half and all of a buffer's capacity.
-class HipLlmBackend::ResultPool : public std::enable_shared_from_this<ResultPool> {
- public:
-    static constexpr size_t kMinBytes = size_t(1) << 20;
-    static constexpr size_t kMaxHeld = size_t(4) << 30;
+// ─────────────────────────── host byte blocks ───────────────────────────
+namespace {
 
-    std::shared_ptr<std::vector<uint8_t>> take(size_t n) {
-        std::vector<uint8_t>* v = nullptr;
-        if (n >= kMinBytes) {
+constexpr size_t kLargeBlock = size_t(1) << 20;  // page-locked and recycled from this size on
+constexpr size_t kMaxHeld = size_t(4) << 30;      // freed bytes kept for reuse, at most
+
+// Large host blocks: handed out, and freed ones kept (by size) for the next request needing between
+// half and all of one. Process-wide, and never destroyed: tensors may outlive every backend, and
+// blocks still held at exit go back to the system with the process.
+class HostBlocks {
+ public:
+    void* take(size_t n) {
+        {
             std::lock_guard<std::mutex> lock(mu_);
             auto it = free_.lower_bound(n);
             if (it != free_.end() && it->first / 2 <= n) {
-                v = it->second;
+                it = std::prev(free_.upper_bound(it->first));  // the most recently freed of that size
+                const Block b = it->second;
                 held_ -= it->first;
                 free_.erase(it);
+                live_.emplace(b.ptr, b);
+                return b.ptr;
             }
         }
-        if (v == nullptr) {
-            v = new std::vector<uint8_t>(n);
+        Block b{nullptr, n, false};
+        if (pinnable() && hipHostMalloc(&b.ptr, n, hipHostMallocDefault) == hipSuccess && b.ptr != nullptr) {
+            b.pinned = true;
         } else {
-            v->resize(n);  // within its capacity: no reallocation
+            (void)hipGetLastError();  // a refused page-locked allocation falls back to the heap
+            b.ptr = ::operator new(n);
         }
-        if (n < kMinBytes) return std::shared_ptr<std::vector<uint8_t>>(v);
-        std::shared_ptr<ResultPool> self = shared_from_this();
-        return std::shared_ptr<std::vector<uint8_t>>(v, [self](std::vector<uint8_t>* b) { self->give(b); });
+        try {
+            std::lock_guard<std::mutex> lock(mu_);
+            live_.emplace(b.ptr, b);
+        } catch (...) {
+            release(b);
+            throw;
+        }
+        return b.ptr;
     }
 
-    ~ResultPool() {
-        for (auto& e : free_) delete e.second;
-    }
-
- private:
-    void give(std::vector<uint8_t>* v) noexcept {
-        const size_t cap = v->capacity();
+    void give(void* p) noexcept {
+        Block b{};
         {
             std::lock_guard<std::mutex> lock(mu_);
-            if (held_ + cap <= kMaxHeld) {
+            auto it = live_.find(p);
+            if (it == live_.end()) return;  // not handed out here: nothing to do
+            b = it->second;
+            live_.erase(it);
+            if (held_ + b.size <= kMaxHeld) {
                 try {
-                    free_.emplace(cap, v);
-                    held_ += cap;
+                    free_.emplace(b.size, b);
+                    held_ += b.size;
                     return;
                 } catch (...) {
                 }
             }
         }
-        delete v;
+        release(b);
+    }
+
+ private:
+    struct Block {
+        void* ptr;
+        size_t size;
+        bool pinned;
+    };
+
+    static void release(const Block& b) noexcept {
+        if (b.pinned)
+            (void)hipHostFree(b.ptr);
+        else
+            ::operator delete(b.ptr);
+    }
+
+    // A HIP device is present (checked once): page-locked memory is only worth its cost then.
+    static bool pinnable() {
+        static const bool yes = [] {
+            int n = 0;
+            const bool ok = hipGetDeviceCount(&n) == hipSuccess && n > 0;
+            (void)hipGetLastError();
+            return ok;
+        }();
+        return yes;
     }
 
     std::mutex mu_;
-    std::multimap<size_t, std::vector<uint8_t>*> free_;  // by capacity
+    std::unordered_map<void*, Block> live_;
+    std::multimap<size_t, Block> free_;  // by size; equal sizes in the order freed
     size_t held_ = 0;
 };
 
-std::shared_ptr<std::vector<uint8_t>> HipLlmBackend::result_bytes(size_t n) { return pool_->take(n); }
+HostBlocks& host_blocks() {
+    static HostBlocks* blocks = new HostBlocks;
+    return *blocks;
+}
 
-Tensor HipLlmBackend::f32_result(std::shared_ptr<std::vector<uint8_t>> bytes, std::vector<size_t> shape) const {
+}  // namespace
+
+void* host_bytes_alloc(size_t n) {
+    if (n < kLargeBlock) return ::operator new(n == 0 ? 1 : n);
+    return host_blocks().take(n);
+}
+
+void host_bytes_free(void* p, size_t n) noexcept {
+    if (p == nullptr) return;
+    if (n < kLargeBlock)
+        ::operator delete(p);
+    else
+        host_blocks().give(p);
+}
+
+std::shared_ptr<Bytes> HipLlmBackend::result_bytes(size_t n) { return std::make_shared<Bytes>(n); }
+
+Tensor HipLlmBackend::f32_result(std::shared_ptr<Bytes> bytes, std::vector<size_t> shape) const {
     if (bytes->size() != product(shape) * 4)
         throw Error("shape mismatch: expected " + std::to_string(product(shape) * 4) + " bytes, got " +
                     std::to_string(bytes->size()));
@@ -245,7 +304,6 @@ HipLlmBackend::HipLlmBackend(LlmBackend* cpu) : cpu_(cpu) {
     hipStream_t s = nullptr;
     hip_ok(hipStreamCreate(&s), "stream create");  // default priority
     stream_ = s;
-    pool_ = std::make_shared<ResultPool>();
     disabled_ = disable_list();
     const char* v = std::getenv("SAPIENT_HIP_VERIFY");
     verify_ = v != nullptr && std::strcmp(v, "1") == 0;
@@ -390,9 +448,12 @@ Tensor HipLlmBackend::f32_input(const Tensor& t) const {
     if (t.dtype() == DType::F32) return t;
     if (t.dtype() != DType::F16 && t.dtype() != DType::BF16)
         throw Error(std::string("type mismatch: expected a float tensor, got ") + dtype_name(t.dtype()));
-    std::vector<float> v(t.numel());
+    const size_t n = t.numel();
+    if (t.bytes().size() != n * 2) throw Error("tensor holds no half-precision data for its shape");
+    std::shared_ptr<Bytes> out = result_bytes(n * 4);
     const uint8_t* b = t.bytes().data();
-    for (size_t i = 0; i < v.size(); ++i) {
+    uint8_t* o = out->data();
+    for (size_t i = 0; i < n; ++i) {
         const uint16_t h = (uint16_t)(b[2 * i] | (b[2 * i + 1] << 8));
         uint32_t u;
         if (t.dtype() == DType::BF16) {
@@ -409,9 +470,9 @@ Tensor HipLlmBackend::f32_input(const Tensor& t) const {
                 u = sign | ((exp + 112u) << 23) | (man << 13);
             }
         }
-        std::memcpy(&v[i], &u, 4);
+        std::memcpy(o + 4 * i, &u, 4);
     }
-    return Tensor::from_f32(v, t.shape());
+    return f32_result(std::move(out), t.shape());
 }
 
 Tensor HipLlmBackend::rms_norm(const Tensor& x, const Tensor& weight_t, float eps) {

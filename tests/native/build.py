@@ -17,8 +17,10 @@ OUT = HERE / "_build"
 def build() -> None:
     gxx = shutil.which("g++") or "g++"
     OUT.mkdir(exist_ok=True)
-    subprocess.run([gxx, "-std=c++17", "-O1", "-Wall", f"-I{ROOT / 'include'}", str(HERE / "test_hip_llm_backend.cpp"),
+    subprocess.run([gxx, "-std=c++17", "-O1", "-Wall", "-D__HIP_PLATFORM_AMD__", "-I/opt/rocm/include",
+                    f"-I{ROOT / 'include'}", str(HERE / "test_hip_llm_backend.cpp"),
                     "-o", str(OUT / "test_hip_llm_backend"), f"-L{ROOT / 'sapient_amd'}", "-lsapient_hip",
+                    "-L/opt/rocm/lib", "-lamdhip64",
                     "-Wl,-rpath,$ORIGIN/../../../sapient_amd", "-Wl,-rpath,/opt/rocm/lib"], check=True)
     for check in ("check_glibc_tanhf", "check_glibc_expf", "check_glibc_sincosf"):
         subprocess.run([gxx, "-O2", "-std=c++17", "-ffp-contract=off", "-fno-fast-math", "-D__HIP_PLATFORM_AMD__",

@@ -6,6 +6,7 @@
 //   crates/sapient-backends/cpu/src/backend.rs:239-487, the trait's validation errors (rope.rs:19-35,
 //   elementwise.rs:15-21, common.rs:171-173), and the debug switches of backend.rs:191-216.
 // Prints "test <name> ... ok|FAILED: <why>" per test; exits 1 if any failed.
+#include <algorithm>
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
@@ -14,8 +15,11 @@
 #include <string>
 #include <vector>
 
+#include <hip/hip_runtime.h>
+
 #include "sapient_hip_backend.hpp"
 
+using sapient_hip::Bytes;
 using sapient_hip::DType;
 using sapient_hip::Error;
 using sapient_hip::HipLlmBackend;
@@ -38,6 +42,10 @@ static std::string expect_error(F&& f) {
         return e.what();
     }
     throw Failure{"expected an error"};
+}
+
+static bool same_bytes(const Bytes& a, const std::vector<uint8_t>& b) {
+    return a.size() == b.size() && std::equal(a.begin(), a.end(), b.begin());
 }
 
 // ── helpers the reference tests use ──────────────────────────────────────────
@@ -105,7 +113,7 @@ static void rmsnorm_identity_weight(HipLlmBackend& bk) {  // layernorm.rs:125-14
 }
 
 static void rmsnorm_half_input_outputs_f32(HipLlmBackend& bk) {  // to_f32_cow upcast, f32 result
-    std::vector<uint8_t> b;
+    Bytes b;
     for (float v : {3.0f, 4.0f}) {
         const uint16_t h = f16_from_f32(v);
         b.push_back((uint8_t)(h & 0xFF));
@@ -139,7 +147,7 @@ static void add_bias_last_dim_broadcasts(HipLlmBackend& bk) {  // common.rs:556-
     const Tensor y = Tensor::from_f32({1.0f, 2.0f, 3.0f, 4.0f, 5.0f, 6.0f}, {2, 3});
     const std::vector<float> o = bk.add_bias_last_dim(y, Tensor::from_f32({10.0f, 20.0f, 30.0f}, {3})).as_f32();
     ASSERT(o == std::vector<float>({11.0f, 22.0f, 33.0f, 14.0f, 25.0f, 36.0f}), "f32 bias");
-    std::vector<uint8_t> hb;
+    Bytes hb;
     for (float v : {0.5f, -1.0f, 2.0f}) {
         const uint16_t h = f16_from_f32(v);
         hb.push_back((uint8_t)(h & 0xFF));
@@ -348,7 +356,7 @@ static void embed_row_gather_matches_full_dequant(HipLlmBackend& bk) {  // commo
         v = ((float)(s >> 40) / (float)(1u << 24)) * 2.0f - 1.0f;
     }
     const Tensor f32_t = Tensor::from_f32(data, {vocab, hidden});
-    std::vector<uint8_t> f16b;
+    Bytes f16b;
     std::vector<float> f16_full;
     for (float v : data) {
         const uint16_t h = f16_from_f32(v);
@@ -363,7 +371,7 @@ static void embed_row_gather_matches_full_dequant(HipLlmBackend& bk) {  // commo
         const float d = f16_to_f32((uint16_t)(q8[b * 34] | (q8[b * 34 + 1] << 8)));
         for (int j = 0; j < 32; ++j) q8_full.push_back((float)(int8_t)q8[b * 34 + 2 + j] * d);
     }
-    const Tensor q8_t = Tensor::from_quant_bytes(q8, {vocab, hidden}, DType::Q8_0);
+    const Tensor q8_t = Tensor::from_quant_bytes(Bytes(q8.begin(), q8.end()), {vocab, hidden}, DType::Q8_0);
     const std::vector<uint32_t> ids = {0, 7, 16, 3};
     const std::pair<const Tensor*, const std::vector<float>*> tables[] = {{&f32_t, &data}, {&f16_t, &f16_full}, {&q8_t, &q8_full}};
     for (const auto& [table, full] : tables) {
@@ -494,10 +502,10 @@ static void kv_cache_update_slides_when_full(HipLlmBackend& bk) {  // common.rs:
 
 static void kv_cache_update_refuses_half_caches(HipLlmBackend& bk) {  // common.rs:378 → tensor.rs:599-602
     // The float path writes through as_f32_slice_mut, which refuses every dtype but F32.
-    Tensor cache = Tensor::from_f16_bytes(std::vector<uint8_t>(32, 0), {1, 2, 4, 2});
+    Tensor cache = Tensor::from_f16_bytes(Bytes(32, 0), {1, 2, 4, 2});
     ASSERT(expect_error([&] { bk.update_kv_cache(cache, 0, Tensor::from_f32({1, 1, 2, 2}, {1, 2, 1, 2})); })
                .find("Tensor dtype is not F32") != std::string::npos, "f16 cache");
-    Tensor cache_bf = Tensor::from_bf16_bytes(std::vector<uint8_t>(32, 0), {1, 2, 4, 2});
+    Tensor cache_bf = Tensor::from_bf16_bytes(Bytes(32, 0), {1, 2, 4, 2});
     ASSERT(expect_error([&] { bk.update_kv_cache(cache_bf, 0, Tensor::from_f32({1, 1, 2, 2}, {1, 2, 1, 2})); })
                .find("Tensor dtype is not F32") != std::string::npos, "bf16 cache");
 }
@@ -537,16 +545,16 @@ static void kv_cache_update_q8_0(HipLlmBackend& bk) {  // update_kv_cache_q8, co
     }
     std::vector<uint8_t> bytes = quantize_q8_0(r0);
     bytes.resize(68, 0);
-    Tensor cache = Tensor::from_quant_bytes(bytes, {1, 1, 2, 32}, DType::Q8_0);
+    Tensor cache = Tensor::from_quant_bytes(Bytes(bytes.begin(), bytes.end()), {1, 1, 2, 32}, DType::Q8_0);
     const Tensor v1 = bk.update_kv_cache(cache, 1, Tensor::from_f32(r1, {1, 1, 1, 32}));
     std::vector<uint8_t> want = quantize_q8_0(r0), q1 = quantize_q8_0(r1);
     want.insert(want.end(), q1.begin(), q1.end());
-    ASSERT(cache.bytes() == want, "second row quantized in place");
+    ASSERT(same_bytes(cache.bytes(), want), "second row quantized in place");
     const Tensor v2 = bk.update_kv_cache(cache, 2, Tensor::from_f32(r2, {1, 1, 1, 32}));
     std::vector<uint8_t> q2 = quantize_q8_0(r2);
     want.assign(q1.begin(), q1.end());
     want.insert(want.end(), q2.begin(), q2.end());
-    ASSERT(cache.bytes() == want, "window slid by one block row");
+    ASSERT(same_bytes(cache.bytes(), want), "window slid by one block row");
     ASSERT((v2.shape() == std::vector<size_t>{1, 1, 2, 32}), "prefix shape");
     const std::vector<float> y = v2.as_f32();
     for (int s = 0; s < 2; ++s) {
@@ -558,7 +566,7 @@ static void kv_cache_update_q8_0(HipLlmBackend& bk) {  // update_kv_cache_q8, co
 }
 
 static void quant_bytes_are_validated(HipLlmBackend&) {  // tensor.rs:143-169
-    ASSERT(expect_error([] { Tensor::from_quant_bytes(std::vector<uint8_t>(33), {32}, DType::Q8_0); })
+    ASSERT(expect_error([] { Tensor::from_quant_bytes(Bytes(33), {32}, DType::Q8_0); })
                .find("shape mismatch") != std::string::npos, "byte count");
 }
 
@@ -585,36 +593,47 @@ static void tensor_copies_share_bytes_until_written(HipLlmBackend& bk) {
     ASSERT(kept.as_f32()[0] == 0.0f && kept.as_f32()[1] == 0.0f, "the earlier copy keeps its bytes");
 }
 
-// Large results (>= 1 MiB) take the bytes of dropped results of a fitting size back from the
-// backend's pool, pages already mapped; a live result's bytes are never handed out again, and a
-// result outlives the backend that made it.
-static void results_recycle_dropped_buffers(HipLlmBackend&) {
-    HipLlmBackend bk;  // an empty pool
+// Tensor bytes of 1 MiB or more are page-locked host memory (so transfers run as direct DMA), and a
+// dropped tensor's block goes to the next one of a fitting size, pages already mapped; a live
+// tensor's bytes are never handed out again, and a result outlives the backend that made it.
+static bool page_locked(const void* p) {
+    hipPointerAttribute_t a{};
+    const bool yes = hipPointerGetAttributes(&a, p) == hipSuccess && a.type == hipMemoryTypeHost;
+    (void)hipGetLastError();  // plain heap memory is an error to the query
+    return yes;
+}
+
+static void large_tensor_bytes_are_page_locked_and_recycled(HipLlmBackend& bk) {
     const size_t n = size_t(1) << 19;  // 2 MiB of f32
     std::vector<float> xs(n);
     for (size_t i = 0; i < n; ++i) xs[i] = (float)(int)(i % 97) * 0.125f - 6.0f;
     const Tensor x = Tensor::from_f32(xs, {n});
+    ASSERT(page_locked(x.bytes().data()), "a large input tensor's bytes are page-locked");
     const uint8_t* first = nullptr;
     std::vector<float> want;
     {
         const Tensor a = bk.silu(x);
+        ASSERT(page_locked(a.bytes().data()), "a large result's bytes are page-locked");
         first = a.bytes().data();
         want = a.as_f32();
     }
     const Tensor b = bk.silu(x);
-    ASSERT(b.bytes().data() == first, "a dropped result's buffer is reused");
-    ASSERT(b.as_f32() == want, "the reused buffer holds the new result");
+    ASSERT(b.bytes().data() == first, "a dropped result's block is reused");
+    ASSERT(b.as_f32() == want, "the reused block holds the new result");
     const Tensor c = bk.gelu(x);
-    ASSERT(c.bytes().data() != b.bytes().data(), "a live result's buffer is not handed out");
+    ASSERT(c.bytes().data() != b.bytes().data(), "a live result's block is not handed out");
     const Tensor small = bk.silu(Tensor::from_f32({1.0f, -2.0f}, {2}));
-    ASSERT(small.as_f32().size() == 2, "small results are plain allocations");
+    ASSERT(!page_locked(small.bytes().data()), "small tensors are plain heap memory");
+    Bytes grown{1, 2, 3, 4, 5, 6, 7, 8};
+    grown.resize(size_t(3) << 20);  // reallocated into a large block
+    ASSERT(page_locked(grown.data()), "a grown byte buffer is page-locked");
+    ASSERT(grown[0] == 1 && grown[7] == 8, "growing keeps the contents");
     Tensor kept;
     {
         HipLlmBackend other;
         kept = other.silu(x);
     }
     ASSERT(kept.as_f32() == want, "a result outlives its backend");
-    kept = Tensor();  // its bytes go back to the departed backend's pool, which it keeps alive
 }
 
 int main() {
@@ -649,7 +668,7 @@ int main() {
         {"embed_row_gather_matches_full_dequant", embed_row_gather_matches_full_dequant},
         {"quant_bytes_are_validated", quant_bytes_are_validated},
         {"tensor_copies_share_bytes_until_written", tensor_copies_share_bytes_until_written},
-        {"results_recycle_dropped_buffers", results_recycle_dropped_buffers},
+        {"large_tensor_bytes_are_page_locked_and_recycled", large_tensor_bytes_are_page_locked_and_recycled},
         {"kv_cache_update_reference_test", kv_cache_update_reference_test},
         {"kv_cache_update_slides_when_full", kv_cache_update_slides_when_full},
         {"kv_cache_update_q8_0", kv_cache_update_q8_0},
