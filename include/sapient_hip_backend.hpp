@@ -253,6 +253,9 @@ class HipLlmBackend final : public LlmBackend {
     DeviceBuf alloc(size_t bytes);
     void release(DeviceBuf& b);
     void download(const DeviceBuf& b, void* host, size_t bytes);
+    // One call's host operands as device addresses: page-locked tensor bytes in place, others
+    // through device buffers.
+    class Operands;
     // Uninitialised host bytes for a result of n bytes (every result writes all of them); large
     // ones are page-locked blocks freed by dropped tensors, pages already mapped, when one fits.
     static std::shared_ptr<Bytes> result_bytes(size_t n);

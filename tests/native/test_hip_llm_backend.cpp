@@ -20,6 +20,7 @@
 #include "sapient_hip_backend.hpp"
 
 using sapient_hip::Bytes;
+using sapient_hip::byte_count;
 using sapient_hip::DType;
 using sapient_hip::Error;
 using sapient_hip::HipLlmBackend;
@@ -636,6 +637,105 @@ static void large_tensor_bytes_are_page_locked_and_recycled(HipLlmBackend& bk) {
     ASSERT(kept.as_f32() == want, "a result outlives its backend");
 }
 
+// Large tensors (page-locked bytes) are read and written by the kernels in place, over the host
+// link; small ones go through device buffers. Every row of a large call must be what a small call
+// on those rows gives: bit for bit for the element-wise ops, the bias, RoPE, the gather and the
+// residual sum, and within 1e-5 relative for the normalized rows (the row reduction's order can
+// follow the launch shape).
+static Tensor rows_of(const Tensor& t, size_t r0, size_t n) {
+    std::vector<size_t> shape = t.shape();
+    const size_t row = t.numel() / shape[0];
+    shape[0] = n;
+    const size_t rb = byte_count(t.dtype(), row);
+    Bytes b(t.bytes().begin() + r0 * rb, t.bytes().begin() + (r0 + n) * rb);
+    return t.dtype() == DType::F32 ? Tensor::from_f32_bytes(std::move(b), shape)
+                                   : Tensor::from_quant_bytes(std::move(b), shape, t.dtype());
+}
+
+static bool rows_match(const Tensor& big, size_t r0, const Tensor& part, float rel) {
+    const std::vector<float> a = big.as_f32(), b = part.as_f32();
+    const size_t row = big.numel() / big.shape()[0];
+    for (size_t i = 0; i < b.size(); ++i) {
+        const float x = a[r0 * row + i], y = b[i];
+        if (rel == 0.0f ? std::memcmp(&x, &y, 4) != 0 : std::fabs(x - y) > rel * std::max(1.0f, std::fabs(y))) return false;
+    }
+    return true;
+}
+
+static void large_calls_equal_small_calls(HipLlmBackend& bk) {
+    const size_t R = 4096, D = 2048;  // 32 MiB per f32 operand: several chunks
+    std::vector<float> xv(R * D), rv(R * D), wv(D), bv(D);
+    uint64_t st = 0x9E3779B97F4A7C15ull;
+    auto rnd = [&] {
+        st = st * 6364136223846793005ull + 1442695040888963407ull;
+        return ((float)(st >> 40) / (float)(1u << 24)) * 4.0f - 2.0f;
+    };
+    for (auto& v : xv) v = rnd();
+    for (auto& v : rv) v = rnd();
+    for (auto& v : wv) v = 1.0f + 0.1f * rnd();
+    for (auto& v : bv) v = rnd();
+    const Tensor x = Tensor::from_f32(xv, {R, D}), r = Tensor::from_f32(rv, {R, D});
+    const Tensor w = Tensor::from_f32(wv, {D}), b = Tensor::from_f32(bv, {D});
+    const Tensor two = Tensor::from_f32({2.5f}, {1});
+    const size_t S = 8, HD = 128, NH = R * D / (S * HD);  // RoPE over 8192 heads of 8 x 128
+    std::vector<size_t> positions(S);
+    for (size_t i = 0; i < S; ++i) positions[i] = 1000 + 37 * i;
+    const auto ar = bk.add_rms_norm(x, r, w, 1e-5f);
+    const Tensor rn = bk.rms_norm(x, w, 1e-5f), ln = bk.layer_norm(x, w, &b, 1e-5f);
+    const Tensor si = bk.silu(x), ge = bk.gelu(x), ml = bk.mul(x, two), ad = bk.add(x, r), sw = bk.swiglu(x, r);
+    const Tensor bi = bk.add_bias_last_dim(x, b);
+    const Tensor ro = bk.apply_rope_positions(x.reshaped({1, NH, S, HD}), positions, 10000.0f).reshaped({NH, S * HD});
+    const size_t slices[][2] = {{0, 10}, {1000, 100}, {2040, 16}, {R - 6, 6}};
+    for (const auto& sl : slices) {
+        const size_t r0 = sl[0], n = sl[1];
+        const Tensor xs = rows_of(x, r0, n), rs = rows_of(r, r0, n);
+        const auto p = bk.add_rms_norm(xs, rs, w, 1e-5f);
+        ASSERT(rows_match(ar.second, r0, p.second, 0.0f), "add_rms_norm sum");
+        ASSERT(rows_match(ar.first, r0, p.first, 1e-5f), "add_rms_norm normed");
+        ASSERT(rows_match(rn, r0, bk.rms_norm(xs, w, 1e-5f), 1e-5f), "rms_norm");
+        ASSERT(rows_match(ln, r0, bk.layer_norm(xs, w, &b, 1e-5f), 1e-5f), "layer_norm");
+        ASSERT(rows_match(si, r0, bk.silu(xs), 0.0f), "silu");
+        ASSERT(rows_match(ge, r0, bk.gelu(xs), 0.0f), "gelu");
+        ASSERT(rows_match(ml, r0, bk.mul(xs, two), 0.0f), "mul by a length-1 side");
+        ASSERT(rows_match(ad, r0, bk.add(xs, rs), 0.0f), "add");
+        ASSERT(rows_match(sw, r0, bk.swiglu(xs, rs), 0.0f), "swiglu");
+        ASSERT(rows_match(bi, r0, bk.add_bias_last_dim(xs, b), 0.0f), "add_bias_last_dim");
+    }
+    for (const auto& sl : {std::pair<size_t, size_t>{0, 10}, {4090, 16}, {NH - 6, 6}}) {
+        const Tensor heads = rows_of(x.reshaped({NH, S * HD}), sl.first, sl.second).reshaped({1, sl.second, S, HD});
+        const Tensor rot = bk.apply_rope_positions(heads, positions, 10000.0f).reshaped({sl.second, S * HD});
+        ASSERT(rows_match(ro, sl.first, rot, 0.0f), "rope");
+    }
+    // the gather: 70000 ids of a 4096 x 64 Q8_0 table (17.9 MB of output; the table itself, 278 KB,
+    // goes through a device buffer) and of a 65536 x 64 one read in place (4.5 MB)
+    const size_t V = 4096, H = 64, N = 70000;
+    std::vector<float> tv(V * H);
+    for (auto& v : tv) v = rnd();
+    const std::vector<uint8_t> q8 = quantize_q8_0(tv);
+    const Tensor table = Tensor::from_quant_bytes(Bytes(q8.begin(), q8.end()), {V, H}, DType::Q8_0);
+    std::vector<uint32_t> ids(N);
+    for (size_t i = 0; i < N; ++i) ids[i] = (uint32_t)((i * 2654435761u) % V);
+    const Tensor all = bk.embed_tokens(table, ids).reshaped({N, H});
+    for (size_t i0 : {size_t(0), size_t(34000), N - 5}) {
+        const std::vector<uint32_t> part(ids.begin() + i0, ids.begin() + std::min(N, i0 + 200));
+        ASSERT(rows_match(all, i0, bk.embed_tokens(table, part).reshaped({part.size(), H}), 0.0f), "embed_tokens");
+    }
+    const size_t V2 = 65536;
+    std::vector<float> tv2(V2 * H);
+    for (auto& v : tv2) v = rnd();
+    const std::vector<uint8_t> q82 = quantize_q8_0(tv2);
+    const Tensor big_table = Tensor::from_quant_bytes(Bytes(q82.begin(), q82.end()), {V2, H}, DType::Q8_0);
+    const Tensor small_table = rows_of(big_table, V2 - 4096, 4096);  // 278 KB: through a device buffer
+    std::vector<uint32_t> hi(300), lo(300);
+    for (size_t i = 0; i < hi.size(); ++i) {
+        lo[i] = (uint32_t)((i * 40503u) % 4096);
+        hi[i] = (uint32_t)(V2 - 4096) + lo[i];
+    }
+    ASSERT(rows_match(bk.embed_tokens(big_table, hi).reshaped({hi.size(), H}), 0,
+                      bk.embed_tokens(small_table, lo).reshaped({lo.size(), H}), 0.0f),
+           "embed_tokens from a table read in place");
+}
+
 int main() {
     if (!HipLlmBackend::is_available()) {
         std::printf("no gfx950 device\n");
@@ -669,6 +769,7 @@ int main() {
         {"quant_bytes_are_validated", quant_bytes_are_validated},
         {"tensor_copies_share_bytes_until_written", tensor_copies_share_bytes_until_written},
         {"large_tensor_bytes_are_page_locked_and_recycled", large_tensor_bytes_are_page_locked_and_recycled},
+        {"large_calls_equal_small_calls", large_calls_equal_small_calls},
         {"kv_cache_update_reference_test", kv_cache_update_reference_test},
         {"kv_cache_update_slides_when_full", kv_cache_update_slides_when_full},
         {"kv_cache_update_q8_0", kv_cache_update_q8_0},
