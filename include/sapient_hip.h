@@ -87,6 +87,18 @@ int sph_rms_norm(const void* x, int x_dtype, const void* weight, int w_dtype, vo
 int sph_add_rms_norm(const void* x, void* residual, int dtype, const void* weight, int w_dtype,
                      void* out, int out_dtype, int64_t rows, int64_t dim, float eps, void* stream);
 
+/* sph_add_rms_norm with the sum written to `sum` and `residual` only read:
+ * the pair as the trait returns it, LlmBackend::add producing a new tensor
+ * (crates/sapient-backends/cpu/src/kernels/elementwise.rs:27-57, called at
+ * llama.rs:508) that LlmBackend::rms_norm then reads (:515). For callers whose
+ * inputs must survive the call (host-tensor backends, whose kernels can then
+ * read and write host memory in place). sum == residual is sph_add_rms_norm;
+ * otherwise `sum` must not alias x, and `out` none of x, residual and sum.
+ * Results equal sph_add_rms_norm's bit for bit. */
+int sph_add_rms_norm_to(const void* x, const void* residual, void* sum, int dtype, const void* weight,
+                        int w_dtype, void* out, int out_dtype, int64_t rows, int64_t dim, float eps,
+                        void* stream);
+
 /* LayerNorm over the last dimension, two-pass mean then variance:
  *   mean = sum(x) / dim;  var = sum((x - mean)^2) / dim;
  *   y = ((x - mean) * (1 / sqrt(var + eps))) * weight + bias.

@@ -48,6 +48,7 @@ SIGNATURES = {
     "sph_init": (_i32, [_vp]),
     "sph_rms_norm": (_i32, [_vp, _i32, _vp, _i32, _vp, _i32, _i64, _i64, _f, _vp]),
     "sph_add_rms_norm": (_i32, [_vp, _vp, _i32, _vp, _i32, _vp, _i32, _i64, _i64, _f, _vp]),
+    "sph_add_rms_norm_to": (_i32, [_vp, _vp, _vp, _i32, _vp, _i32, _vp, _i32, _i64, _i64, _f, _vp]),
     "sph_layer_norm": (_i32, [_vp, _i32, _vp, _vp, _i32, _vp, _i32, _i64, _i64, _f, _vp]),
     "sph_add": (_i32, [_vp, _i64, _vp, _i64, _vp, _i32, _vp]),
     "sph_mul": (_i32, [_vp, _i64, _vp, _i64, _vp, _i32, _vp]),

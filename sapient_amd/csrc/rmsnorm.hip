@@ -3,8 +3,8 @@
 // Reference math (crates/sapient-backends/cpu/src/kernels/layernorm.rs:93-103):
 //   ms = (Σ x_i²) / dim;  inv = 1 / sqrt(ms + eps);  y_i = (x_i · inv) · w_i
 // The fused variant replaces `add` (llama.rs:508) followed by `rms_norm`
-// (llama.rs:515): r = x + residual is written back to `residual` and y is the
-// RMSNorm of the f32 sum. LayerNorm (layernorm.rs:17-69, last axis):
+// (llama.rs:515): r = x + residual is written back to `residual` (or, in the
+// out-of-place form, to a separate `sum`) and y is the RMSNorm of the f32 sum. LayerNorm (layernorm.rs:17-69, last axis):
 //   mean = Σx / n;  var = Σ(x − mean)² / n;  y = ((x − mean) · 1/sqrt(var + eps)) · w + b
 //
 // Design (HBM-bound, ≈0.2 flop/byte):
@@ -35,7 +35,11 @@ namespace {
 
 constexpr int kWave = 64;
 
-enum Kind { K_RMS = 0, K_ADD_RMS = 1, K_LAYER = 2 };
+// K_ADD_RMS writes the sum back into `residual`; K_ADD_RMS_TO writes it to `sum` and only reads
+// `residual`.
+enum Kind { K_RMS = 0, K_ADD_RMS = 1, K_LAYER = 2, K_ADD_RMS_TO = 3 };
+
+constexpr bool adds(int kind) { return kind == K_ADD_RMS || kind == K_ADD_RMS_TO; }
 
 // y for one element: RMSNorm (r·inv)·w; LayerNorm (d·inv)·w + b, where the
 // caller passes the centred value d = r − mean for LayerNorm. An absent weight
@@ -87,8 +91,9 @@ __device__ __forceinline__ void unpack16(const u32x4& q, float (&v)[E]) {
 //    row would (LayerNorm: weight and bias rows).
 template <typename TX, typename TW, typename TO, int KIND, int W, int VPT, bool LOOP>
 __global__ __launch_bounds__(W >= 4 ? 64 * W : 256) void rms_rows_vec(const TX* __restrict__ x, TX* __restrict__ residual,
-                                                                   const TW* __restrict__ w, const TW* __restrict__ bias,
-                                                                   TO* __restrict__ out, int64_t rows, int dim, float eps) {
+                                                                   TX* __restrict__ sum, const TW* __restrict__ w,
+                                                                   const TW* __restrict__ bias, TO* __restrict__ out,
+                                                                   int64_t rows, int dim, float eps) {
     constexpr int E = vec16<TX>::n;  // elements per 16-byte access of x
     constexpr int WPB = W >= 4 ? W : 4;
     constexpr int RPB = WPB / W;
@@ -124,7 +129,7 @@ __global__ __launch_bounds__(W >= 4 ? 64 * W : 256) void rms_rows_vec(const TX* 
             const int v = (sub * VPT + j) * kWave + lane;
             if (v < nvec) {
                 vx[j] = vload<true>(reinterpret_cast<const u32x4*>(x + base + (size_t)v * E));
-                if constexpr (KIND == K_ADD_RMS)
+                if constexpr (adds(KIND))
                     vres[j] = vload<true>(reinterpret_cast<const u32x4*>(residual + base + (size_t)v * E));
             }
         }
@@ -143,12 +148,12 @@ __global__ __launch_bounds__(W >= 4 ? 64 * W : 256) void rms_rows_vec(const TX* 
                 const int v = (sub * VPT + j) * kWave + lane;
                 if (v < nvec) {
                     unpack16<TX, E>(cx[j], r[j]);
-                    if constexpr (KIND == K_ADD_RMS) {
+                    if constexpr (adds(KIND)) {
                         float b[E];
                         unpack16<TX, E>(cres[j], b);
 #pragma unroll
                         for (int e = 0; e < E; ++e) r[j][e] = r[j][e] + b[e];
-                        store_f32<TX, E, true>(residual + base + (size_t)v * E, r[j]);
+                        store_f32<TX, E, true>((KIND == K_ADD_RMS_TO ? sum : residual) + base + (size_t)v * E, r[j]);
                     }
 #pragma unroll
                     for (int e = 0; e < E; ++e) {
@@ -238,7 +243,7 @@ __global__ __launch_bounds__(W >= 4 ? 64 * W : 256) void rms_rows_vec(const TX* 
 // half variants normalise the unrounded f32 sum; each thread owns the same
 // elements in every pass, so the in-place residual update cannot race.
 template <typename TX, typename TW, typename TO, int KIND>
-__global__ __launch_bounds__(256) void rms_rows_generic(const TX* __restrict__ x, TX* residual,
+__global__ __launch_bounds__(256) void rms_rows_generic(const TX* __restrict__ x, TX* residual, TX* __restrict__ sum,
                                                        const TW* __restrict__ w, const TW* __restrict__ bias,
                                                        TO* __restrict__ out, int64_t rows, int64_t dim, float eps) {
     __shared__ float partial[2][256 / kWave];
@@ -248,7 +253,7 @@ __global__ __launch_bounds__(256) void rms_rows_generic(const TX* __restrict__ x
     const size_t base = (size_t)row * (size_t)dim;
     auto value = [&](int64_t i) {
         float r = widen(x[base + i]);
-        if constexpr (KIND == K_ADD_RMS) r = r + widen(residual[base + i]);
+        if constexpr (adds(KIND)) r = r + widen(residual[base + i]);
         return r;
     };
     float ss = 0.0f;
@@ -275,6 +280,7 @@ __global__ __launch_bounds__(256) void rms_rows_generic(const TX* __restrict__ x
     for (int64_t i = threadIdx.x; i < dim; i += blockDim.x) {
         const float r = value(i);
         if constexpr (KIND == K_ADD_RMS) residual[base + i] = narrow<TX>(r);
+        if constexpr (KIND == K_ADD_RMS_TO) sum[base + i] = narrow<TX>(r);
         const float wv_ = has_w ? widen(w[i]) : 1.0f;
         const float bv = (KIND == K_LAYER && has_b) ? widen(bias[i]) : -0.0f;
         out[base + i] = narrow<TO>(norm_out<KIND>(KIND == K_LAYER ? r - mean : r, inv, wv_, bv));
@@ -282,14 +288,14 @@ __global__ __launch_bounds__(256) void rms_rows_generic(const TX* __restrict__ x
 }
 
 template <typename TX, typename TW, typename TO, int KIND, int VPT, bool LOOP>
-int launch_vec(int W, dim3 grid, int threads, const TX* xp, TX* rp, const TW* wp, const TW* bp, TO* op, int64_t nr, int d,
-               float eps, hipStream_t stream) {
+int launch_vec(int W, dim3 grid, int threads, const TX* xp, TX* rp, TX* sp, const TW* wp, const TW* bp, TO* op,
+               int64_t nr, int d, float eps, hipStream_t stream) {
     switch (W) {
-    case 1: return launch(rms_rows_vec<TX, TW, TO, KIND, 1, VPT, LOOP>, grid, threads, stream, xp, rp, wp, bp, op, nr, d, eps);
-    case 2: return launch(rms_rows_vec<TX, TW, TO, KIND, 2, VPT, LOOP>, grid, threads, stream, xp, rp, wp, bp, op, nr, d, eps);
-    case 4: return launch(rms_rows_vec<TX, TW, TO, KIND, 4, VPT, LOOP>, grid, threads, stream, xp, rp, wp, bp, op, nr, d, eps);
-    case 8: return launch(rms_rows_vec<TX, TW, TO, KIND, 8, VPT, LOOP>, grid, threads, stream, xp, rp, wp, bp, op, nr, d, eps);
-    default: return launch(rms_rows_vec<TX, TW, TO, KIND, 16, VPT, LOOP>, grid, threads, stream, xp, rp, wp, bp, op, nr, d, eps);
+    case 1: return launch(rms_rows_vec<TX, TW, TO, KIND, 1, VPT, LOOP>, grid, threads, stream, xp, rp, sp, wp, bp, op, nr, d, eps);
+    case 2: return launch(rms_rows_vec<TX, TW, TO, KIND, 2, VPT, LOOP>, grid, threads, stream, xp, rp, sp, wp, bp, op, nr, d, eps);
+    case 4: return launch(rms_rows_vec<TX, TW, TO, KIND, 4, VPT, LOOP>, grid, threads, stream, xp, rp, sp, wp, bp, op, nr, d, eps);
+    case 8: return launch(rms_rows_vec<TX, TW, TO, KIND, 8, VPT, LOOP>, grid, threads, stream, xp, rp, sp, wp, bp, op, nr, d, eps);
+    default: return launch(rms_rows_vec<TX, TW, TO, KIND, 16, VPT, LOOP>, grid, threads, stream, xp, rp, sp, wp, bp, op, nr, d, eps);
     }
 }
 
@@ -301,7 +307,7 @@ constexpr int kNoShape = 1;
 // resident waves per CU (at least one block). Returns the launch's status, or
 // kNoShape, launching nothing, when a row is wider than 16 waves cover.
 template <typename TX, typename TW, typename TO, int KIND, int VPT, bool LOOP>
-int launch_shape(const TX* xp, TX* rp, const TW* wp, const TW* bp, TO* op, int64_t nr, int dim, float eps,
+int launch_shape(const TX* xp, TX* rp, TX* sp, const TW* wp, const TW* bp, TO* op, int64_t nr, int dim, float eps,
                   int waves_per_cu, hipStream_t stream) {
     constexpr int E = vec16<TX>::n;
     const int64_t nvec = dim / E;
@@ -319,7 +325,7 @@ int launch_shape(const TX* xp, TX* rp, const TW* wp, const TW* bp, TO* op, int64
             if (nb > cap) nb = cap;
         }
     }
-    return launch_vec<TX, TW, TO, KIND, VPT, LOOP>(W, dim3((unsigned)nb), threads, xp, rp, wp, bp, op, nr, dim, eps,
+    return launch_vec<TX, TW, TO, KIND, VPT, LOOP>(W, dim3((unsigned)nb), threads, xp, rp, sp, wp, bp, op, nr, dim, eps,
                                                    stream);
 }
 
@@ -343,14 +349,14 @@ int launch_shape(const TX* xp, TX* rp, const TW* wp, const TW* bp, TO* op, int64
 constexpr int64_t kFewValues = int64_t(1) << 21;
 
 template <typename TX, typename TW, typename TO, int KIND>
-int launch_rms(const void* x, void* residual, const void* w, const void* bias, void* out, int64_t rows, int64_t dim,
-               float eps, hipStream_t stream) {
+int launch_rms(const void* x, void* residual, void* sum, const void* w, const void* bias, void* out, int64_t rows,
+               int64_t dim, float eps, hipStream_t stream) {
     if (rows == 0 || dim == 0) return SPH_OK;
     constexpr int E = vec16<TX>::n;
-    constexpr bool FUSED = KIND == K_ADD_RMS;
+    constexpr bool FUSED = adds(KIND);
     constexpr bool HALF = sizeof(TX) == 2;
     // One-block-per-row (or LayerNorm's looping) shape: values per lane.
-    constexpr int VPT = (HALF && KIND != K_ADD_RMS) ? 2 : 8 / E;
+    constexpr int VPT = (HALF && !FUSED) ? 2 : 8 / E;
     constexpr bool kLoop = KIND == K_LAYER;
     // The row-looping shape tried first (VPT_L values per lane, 0: none) and its
     // resident waves per CU.
@@ -358,7 +364,8 @@ int launch_rms(const void* x, void* residual, const void* w, const void* bias, v
     constexpr int kLoopWaves = FUSED && !HALF ? 16 : 8;
     const int64_t nvec = dim / E;
     const bool vec_ok = dim % E == 0 && aligned(x, 16) && aligned(out, 16) &&
-                        (!FUSED || aligned(residual, 16)) && (w == nullptr || aligned(w, 16)) &&
+                        (!FUSED || aligned(residual, 16)) && (KIND != K_ADD_RMS_TO || aligned(sum, 16)) &&
+                        (w == nullptr || aligned(w, 16)) &&
                         (bias == nullptr || aligned(bias, 16)) && nvec <= (int64_t)kWave * 2 * VPT * 16 &&
                         dim <= INT32_MAX;
     // A launch covers at most 2^22 rows, keeping grid x block below 2^32 work-items.
@@ -368,6 +375,7 @@ int launch_rms(const void* x, void* residual, const void* w, const void* bias, v
         const size_t off = (size_t)r0 * (size_t)dim;
         const TX* xp = static_cast<const TX*>(x) + off;
         TX* rp = FUSED ? static_cast<TX*>(residual) + off : nullptr;
+        TX* sp = KIND == K_ADD_RMS_TO ? static_cast<TX*>(sum) + off : nullptr;
         const TW* wp = static_cast<const TW*>(w);
         const TW* bp = static_cast<const TW*>(bias);
         TO* op = static_cast<TO*>(out) + off;
@@ -381,19 +389,19 @@ int launch_rms(const void* x, void* residual, const void* w, const void* bias, v
             // lost (f16 6.7 -> 7.9, f32 12.9 -> 13.7), hence the bound.
             if constexpr ((KIND == K_RMS || KIND == K_LAYER) && VPT > 1)
                 if (nr * dim <= kFewValues)
-                    st = launch_shape<TX, TW, TO, KIND, 1, false>(xp, rp, wp, bp, op, nr, (int)dim, eps, 16, stream);
+                    st = launch_shape<TX, TW, TO, KIND, 1, false>(xp, rp, sp, wp, bp, op, nr, (int)dim, eps, 16, stream);
             if constexpr (VPT_L > 0)
                 if (st == kNoShape)
-                    st = launch_shape<TX, TW, TO, KIND, VPT_L, true>(xp, rp, wp, bp, op, nr, (int)dim, eps,
+                    st = launch_shape<TX, TW, TO, KIND, VPT_L, true>(xp, rp, sp, wp, bp, op, nr, (int)dim, eps,
                                                                      kLoopWaves, stream);
             if (st == kNoShape)
-                st = launch_shape<TX, TW, TO, KIND, VPT, kLoop>(xp, rp, wp, bp, op, nr, (int)dim, eps, 16, stream);
+                st = launch_shape<TX, TW, TO, KIND, VPT, kLoop>(xp, rp, sp, wp, bp, op, nr, (int)dim, eps, 16, stream);
             if (st == kNoShape)  // wider than 16 waves at VPT: twice the values per lane, one block per row
-                st = launch_shape<TX, TW, TO, KIND, 2 * VPT, false>(xp, rp, wp, bp, op, nr, (int)dim, eps, 16, stream);
+                st = launch_shape<TX, TW, TO, KIND, 2 * VPT, false>(xp, rp, sp, wp, bp, op, nr, (int)dim, eps, 16, stream);
             if (st == kNoShape) return SPH_EINVAL;  // unreachable: vec_ok bounds the width
         } else {
-            st = launch(rms_rows_generic<TX, TW, TO, KIND>, dim3((unsigned)nr), 256, stream, xp, rp, wp, bp, op, nr,
-                        dim, eps);
+            st = launch(rms_rows_generic<TX, TW, TO, KIND>, dim3((unsigned)nr), 256, stream, xp, rp, sp, wp, bp, op,
+                        nr, dim, eps);
         }
         if (st != SPH_OK) return st;
     }
@@ -402,7 +410,7 @@ int launch_rms(const void* x, void* residual, const void* w, const void* bias, v
 
 // Resolve (x, weight/bias, out) storage types: weight/bias and out are each f32 or x's type.
 template <int KIND>
-int dispatch_rms(const void* x, void* residual, int x_dt, const void* w, const void* b, int w_dt, void* out,
+int dispatch_rms(const void* x, void* residual, void* sum, int x_dt, const void* w, const void* b, int w_dt, void* out,
                  int out_dt, int64_t rows, int64_t dim, float eps, hipStream_t stream) {
     if (!is_float_dtype(x_dt)) return SPH_EINVAL;
     if ((w != nullptr || b != nullptr) && w_dt != SPH_F32 && w_dt != x_dt) return SPH_EINVAL;
@@ -412,12 +420,12 @@ int dispatch_rms(const void* x, void* residual, int x_dt, const void* w, const v
     return with_float_type(x_dt, [&](auto tx) -> int {
         using TX = decltype(tx);
         if constexpr (sizeof(TX) == 4) {
-            return launch_rms<float, float, float, KIND>(x, residual, w, b, out, rows, dim, eps, stream);
+            return launch_rms<float, float, float, KIND>(x, residual, sum, w, b, out, rows, dim, eps, stream);
         } else {
-            if (w32 && o32) return launch_rms<TX, float, float, KIND>(x, residual, w, b, out, rows, dim, eps, stream);
-            if (w32 && !o32) return launch_rms<TX, float, TX, KIND>(x, residual, w, b, out, rows, dim, eps, stream);
-            if (!w32 && o32) return launch_rms<TX, TX, float, KIND>(x, residual, w, b, out, rows, dim, eps, stream);
-            return launch_rms<TX, TX, TX, KIND>(x, residual, w, b, out, rows, dim, eps, stream);
+            if (w32 && o32) return launch_rms<TX, float, float, KIND>(x, residual, sum, w, b, out, rows, dim, eps, stream);
+            if (w32 && !o32) return launch_rms<TX, float, TX, KIND>(x, residual, sum, w, b, out, rows, dim, eps, stream);
+            if (!w32 && o32) return launch_rms<TX, TX, float, KIND>(x, residual, sum, w, b, out, rows, dim, eps, stream);
+            return launch_rms<TX, TX, TX, KIND>(x, residual, sum, w, b, out, rows, dim, eps, stream);
         }
     });
 }
@@ -429,7 +437,7 @@ extern "C" int sph_rms_norm(const void* x, int x_dtype, const void* weight, int 
                             int out_dtype, int64_t rows, int64_t dim, float eps, void* stream) {
     if (rows < 0 || dim < 0) return SPH_EINVAL;
     if ((rows > 0 && dim > 0) && (x == nullptr || out == nullptr)) return SPH_EINVAL;
-    return sph::dispatch_rms<sph::K_RMS>(x, nullptr, x_dtype, weight, nullptr, w_dtype, out, out_dtype, rows, dim, eps,
+    return sph::dispatch_rms<sph::K_RMS>(x, nullptr, nullptr, x_dtype, weight, nullptr, w_dtype, out, out_dtype, rows, dim, eps,
                                          static_cast<hipStream_t>(stream));
 }
 
@@ -438,14 +446,26 @@ extern "C" int sph_add_rms_norm(const void* x, void* residual, int dtype, const 
     if (rows < 0 || dim < 0) return SPH_EINVAL;
     if ((rows > 0 && dim > 0) && (x == nullptr || residual == nullptr || out == nullptr)) return SPH_EINVAL;
     if (out == x || out == residual) return SPH_EINVAL;
-    return sph::dispatch_rms<sph::K_ADD_RMS>(x, residual, dtype, weight, nullptr, w_dtype, out, out_dtype, rows, dim,
-                                             eps, static_cast<hipStream_t>(stream));
+    return sph::dispatch_rms<sph::K_ADD_RMS>(x, residual, nullptr, dtype, weight, nullptr, w_dtype, out, out_dtype, rows,
+                                             dim, eps, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int sph_add_rms_norm_to(const void* x, const void* residual, void* sum, int dtype, const void* weight,
+                                   int w_dtype, void* out, int out_dtype, int64_t rows, int64_t dim, float eps,
+                                   void* stream) {
+    if (sum == residual) return sph_add_rms_norm(x, sum, dtype, weight, w_dtype, out, out_dtype, rows, dim, eps, stream);
+    if (rows < 0 || dim < 0) return SPH_EINVAL;
+    if ((rows > 0 && dim > 0) && (x == nullptr || residual == nullptr || sum == nullptr || out == nullptr))
+        return SPH_EINVAL;
+    if (out == x || out == residual || out == sum || sum == x) return SPH_EINVAL;
+    return sph::dispatch_rms<sph::K_ADD_RMS_TO>(x, const_cast<void*>(residual), sum, dtype, weight, nullptr, w_dtype,
+                                                out, out_dtype, rows, dim, eps, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int sph_layer_norm(const void* x, int x_dtype, const void* weight, const void* bias, int wb_dtype,
                               void* out, int out_dtype, int64_t rows, int64_t dim, float eps, void* stream) {
     if (rows < 0 || dim < 0) return SPH_EINVAL;
     if ((rows > 0 && dim > 0) && (x == nullptr || out == nullptr)) return SPH_EINVAL;
-    return sph::dispatch_rms<sph::K_LAYER>(x, nullptr, x_dtype, weight, bias, wb_dtype, out, out_dtype, rows, dim,
+    return sph::dispatch_rms<sph::K_LAYER>(x, nullptr, nullptr, x_dtype, weight, bias, wb_dtype, out, out_dtype, rows, dim,
                                            eps, static_cast<hipStream_t>(stream));
 }

@@ -609,11 +609,13 @@ std::pair<Tensor, Tensor> HipLlmBackend::fused_add_rms_norm(const Tensor& x, con
     auto sum = result_bytes(xf.numel() * 4);
     Operands ops(*this);
     const void* xd = ops.in(xf.bytes().data(), xf.bytes().size());
-    void* rd = ops.staged(rf.bytes().data(), sum->data(), sum->size());  // the kernel adds into it in place
+    const void* rd = ops.in(rf.bytes().data(), rf.bytes().size());
+    void* sd = ops.out(sum->data(), sum->size());
     const void* wd = ops.in(wt.bytes().data(), wt.bytes().size());
     void* od = ops.out(normed->data(), normed->size());
     const int st = ops.run([&] {
-        return sph_add_rms_norm(xd, rd, SPH_F32, wd, SPH_F32, od, SPH_F32, (int64_t)rows, (int64_t)dim, eps, stream_);
+        return sph_add_rms_norm_to(xd, rd, sd, SPH_F32, wd, SPH_F32, od, SPH_F32, (int64_t)rows, (int64_t)dim, eps,
+                                   stream_);
     });
     check(st, "add_rms_norm");
     return {f32_result(std::move(normed), xf.shape()), f32_result(std::move(sum), xf.shape())};

@@ -104,23 +104,35 @@ def layer_norm(x: torch.Tensor, weight: Optional[torch.Tensor], bias: Optional[t
 
 def add_rms_norm(x: torch.Tensor, residual: torch.Tensor, weight: Optional[torch.Tensor], eps: float,
                  out: Optional[torch.Tensor] = None,
-                 out_dtype: Optional[torch.dtype] = None) -> Tuple[torch.Tensor, torch.Tensor]:
+                 out_dtype: Optional[torch.dtype] = None,
+                 sum_out: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, torch.Tensor]:
     """Fused add (llama.rs:508) + rms_norm (llama.rs:515). `residual` is
-    updated in place with x + residual; returns (normed, residual)."""
+    updated in place with x + residual, or, given `sum_out`, left as it is while
+    the sum goes to `sum_out` (as the trait's add returns a new tensor); returns
+    (normed, sum)."""
     _dev(x, "x")
     _dev(residual, "residual")
     if residual.shape != x.shape or residual.dtype != x.dtype:
         raise ValueError("x and residual must share shape and dtype")
+    if sum_out is not None:
+        _dev(sum_out, "sum_out")
+        if sum_out.shape != x.shape or sum_out.dtype != x.dtype:
+            raise ValueError("sum_out must share x's shape and dtype")
     dim = x.shape[-1]
     rows = x.numel() // dim if dim else 0
     od = out_dtype or (out.dtype if out is not None else x.dtype)
     out = _out(out, x.shape, od, x.device)
     w = _vec(weight, dim, "weight")
-    check(lib().sph_add_rms_norm(x.data_ptr(), residual.data_ptr(), dtype_code(x.dtype),
-                                 None if w is None else w.data_ptr(), dtype_code(w.dtype) if w is not None else 0,
-                                 out.data_ptr(), dtype_code(out.dtype), rows, dim, float(eps), _stream(x)),
+    wp, wd = (None, 0) if w is None else (w.data_ptr(), dtype_code(w.dtype))
+    if sum_out is None:
+        check(lib().sph_add_rms_norm(x.data_ptr(), residual.data_ptr(), dtype_code(x.dtype), wp, wd,
+                                     out.data_ptr(), dtype_code(out.dtype), rows, dim, float(eps), _stream(x)),
+              "add_rms_norm")
+        return out, residual
+    check(lib().sph_add_rms_norm_to(x.data_ptr(), residual.data_ptr(), sum_out.data_ptr(), dtype_code(x.dtype), wp,
+                                    wd, out.data_ptr(), dtype_code(out.dtype), rows, dim, float(eps), _stream(x)),
           "add_rms_norm")
-    return out, residual
+    return out, sum_out
 
 
 def _binary(fn, name, a, b, out):

@@ -94,6 +94,55 @@ def test_add_rms_norm_shapes(dev, orc, dtype, rows, dim):
         assert_bits16_equal(to_np(r_new), narrow_bits(ref_r, dtype, orc), "updated residual")
 
 
+def _same_bits(a: torch.Tensor, b: torch.Tensor) -> bool:
+    return torch.equal(a.contiguous().view(torch.uint8), b.contiguous().view(torch.uint8))
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: str(d).split(".")[-1])
+@pytest.mark.parametrize("rows,dim", [(1, 896), (512, 896), (33, 4096), (2, 12288), (2, 16384), (3, 100),
+                                      (16384, 4096)])
+def test_add_rms_norm_to_equals_in_place(dev, orc, dtype, rows, dim):
+    """The out-of-place form (sph_add_rms_norm_to): the residual is left as it was, and the sum and
+    the normed rows are the in-place form's bit for bit, across the launch shapes and at the full
+    16384 x 4096 shape (the sum also against the oracle)."""
+    print(f"case add_rms_norm_to {dtype} {rows}x{dim}", flush=True)
+    x = _gen((rows, dim), 51 + dim, dev, dtype=dtype)
+    r = _gen((rows, dim), 53 + dim, dev, dtype=dtype)
+    w = _gen((dim,), 57, dev, 1.0, 0.1)
+    r_before = r.clone()
+    out_to, s = ops.add_rms_norm(x, r, w, 1e-5, sum_out=torch.empty_like(r))
+    torch.cuda.synchronize()
+    assert _same_bits(r, r_before), "residual left as it was"
+    out_in, r_in = ops.add_rms_norm(x, r.clone(), w, 1e-5)
+    torch.cuda.synchronize()
+    assert _same_bits(s, r_in), "sum equals the in-place residual"
+    assert _same_bits(out_to, out_in), "normed rows equal the in-place form's"
+    if rows * dim <= 1 << 20:
+        ref_r = orc.add_rms_norm(widen(x, orc), widen(r_before, orc), widen(w, orc), 1e-5)[1]
+        if dtype == torch.float32:
+            assert_bits_equal(to_np(s), ref_r, "sum")
+        else:
+            assert_bits16_equal(to_np(s), narrow_bits(ref_r, dtype, orc), "sum")
+
+
+def test_add_rms_norm_to_unaligned_and_half_outputs(dev, orc):
+    """The generic kernel (a 4-byte offset view) and an f16 output with an f16 weight, out of place."""
+    base = _gen((4 * 896 + 1,), 61, dev)
+    x = base[1:].view(4, 896)
+    r = _gen((4, 896), 62, dev)
+    s = torch.empty(4 * 896 + 1, device=dev)[1:].view(4, 896)
+    w = _gen((896,), 63, dev, 1.0, 0.1)
+    out, _ = ops.add_rms_norm(x, r, w, 1e-6, sum_out=s)
+    ref, ref_r = orc.add_rms_norm(to_np(x), to_np(r), to_np(w), 1e-6)
+    assert_bits_equal(to_np(s), ref_r, "unaligned sum")
+    assert max_rel(to_np(out), ref) <= RTOL
+    xh, rh, wh = (_gen((8, 1024), 64 + i, dev, dtype=torch.float16) for i in range(3))
+    outh, sh = ops.add_rms_norm(xh, rh, wh[0], 1e-5, sum_out=torch.empty_like(rh))
+    refh, refh_r = orc.add_rms_norm(widen(xh, orc), widen(rh, orc), widen(wh[0], orc), 1e-5)
+    assert_bits16_equal(to_np(sh), narrow_bits(refh_r, torch.float16, orc), "f16 sum")
+    _check_out(outh, refh, orc, "f16 out of place")
+
+
 @pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: str(d).split(".")[-1])
 def test_add_rms_norm_llama3_8b_full(dev, orc, dtype):
     """Fused add + RMSNorm at Llama-3-8B width, 16384 x 4096, eps 1e-5, the full benchmark shape."""
@@ -150,4 +199,15 @@ def test_rms_norm_rejects_bad_arguments(dev):
     assert L.sph_rms_norm(x.data_ptr(), 5, None, 0, x.data_ptr(), 0, 4, 8, 1e-5, s) == EINVAL  # dtype
     assert L.sph_rms_norm(None, 0, None, 0, x.data_ptr(), 0, 4, 8, 1e-5, s) == EINVAL        # null x
     assert L.sph_add_rms_norm(x.data_ptr(), x.data_ptr(), 0, None, 0, x.data_ptr(), 0, 4, 8, 1e-5, s) == EINVAL
+    r, y, t = torch.zeros(4, 8, device=dev), torch.zeros(4, 8, device=dev), torch.zeros(4, 8, device=dev)
+    to = L.sph_add_rms_norm_to
+    assert to(x.data_ptr(), r.data_ptr(), x.data_ptr(), 0, None, 0, y.data_ptr(), 0, 4, 8, 1e-5, s) == EINVAL  # sum = x
+    assert to(x.data_ptr(), r.data_ptr(), t.data_ptr(), 0, None, 0, t.data_ptr(), 0, 4, 8, 1e-5, s) == EINVAL  # out = sum
+    assert to(x.data_ptr(), r.data_ptr(), None, 0, None, 0, y.data_ptr(), 0, 4, 8, 1e-5, s) == EINVAL  # null sum
+    assert to(x.data_ptr(), r.data_ptr(), t.data_ptr(), 7, None, 0, y.data_ptr(), 0, 4, 8, 1e-5, s) == EINVAL  # dtype
+    # sum = residual is the in-place form
+    x1 = torch.ones(4, 8, device=dev)
+    assert to(x1.data_ptr(), r.data_ptr(), r.data_ptr(), 0, None, 0, y.data_ptr(), 0, 4, 8, 1e-5, s) == 0
+    torch.cuda.synchronize()
+    assert torch.equal(r, x1) and torch.allclose(y, torch.ones_like(y))
     assert L.sph_rms_norm(x.data_ptr(), 1, x.data_ptr(), 0, x.data_ptr(), 30, 4, 8, 1e-5, s) == EINVAL  # out dtype
