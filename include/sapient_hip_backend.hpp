@@ -3,8 +3,10 @@
 //
 // The reference trait (crates/sapient-models/src/forward/backend.rs:57-115)
 // takes host tensors and returns new host tensors; this class does the same —
-// upload, run the HIP kernels through the C ABI on its own stream, download —
-// with the reference's argument meaning, validation and error messages. It is
+// the HIP kernels, through the C ABI on its own stream, read the inputs and
+// write the results in host memory (page-locked bytes in place, small ones
+// through device buffers) — with the reference's argument meaning, validation
+// and error messages. It is
 // what a Rust `HipLlmBackend` wrapper does over FFI, written in C++ because the
 // reference is compiled code. There is no CPU fallback: a failed HIP call
 // raises sapient_hip::Error (the debug switches below route an op elsewhere

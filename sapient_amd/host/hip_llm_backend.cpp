@@ -1,14 +1,17 @@
 // hip_llm_backend.cpp — the C++ host-side mirror of sapient's LlmBackend op
 // surface (crates/sapient-models/src/forward/backend.rs:57-115) over the C ABI.
 //
-// Each op uploads its host inputs, runs the HIP kernels on this backend's
-// stream, waits, and downloads a new host tensor — the round trip the
-// reference's MLX backend makes per op (backend.rs:520-600). Weights are
-// uploaded per call too: a host tensor's address can be reused once it is
-// freed, so caching by pointer (as the MLX backend does, backend.rs:483-508,
-// where Arc lifetimes make it safe) would risk a stale device copy here.
-// Output dtypes, validation and error messages follow the reference's CPU
-// kernels.
+// Each op runs the HIP kernels on this backend's stream over its host inputs,
+// waits, and returns a new host tensor — the round trip the reference's MLX
+// backend makes per op (backend.rs:520-600). Tensor bytes of 1 MiB or more are
+// page-locked host memory, which the kernels read and write in place through
+// its device mapping (both directions of the host link at once, and a gather
+// reads only the table rows it needs); smaller operands are copied through
+// device buffers. Nothing is cached on the device between calls: a host
+// tensor's address can be reused once it is freed, so caching by pointer (as
+// the MLX backend does, backend.rs:483-508, where Arc lifetimes make it safe)
+// would risk a stale copy. Output dtypes, validation and error messages follow
+// the reference's CPU kernels.
 #include "sapient_hip_backend.hpp"
 
 #include <hip/hip_runtime.h>
