@@ -94,7 +94,10 @@ int sph_add_rms_norm(const void* x, void* residual, int dtype, const void* weigh
  * inputs must survive the call (host-tensor backends, whose kernels can then
  * read and write host memory in place). sum == residual is sph_add_rms_norm;
  * otherwise `sum` must not alias x, and `out` none of x, residual and sum.
- * Results equal sph_add_rms_norm's bit for bit. */
+ * The sum is sph_add_rms_norm's bit for bit; so is `out` when sum and
+ * residual share their 16-byte alignment (the launch shape follows the
+ * pointers' alignment, and shapes differ only in the order of a row's sum of
+ * squares). */
 int sph_add_rms_norm_to(const void* x, const void* residual, void* sum, int dtype, const void* weight,
                         int w_dtype, void* out, int out_dtype, int64_t rows, int64_t dim, float eps,
                         void* stream);

@@ -105,11 +105,23 @@ def test_norms_random_shapes(dev, orc, case):
     w32 = None if w is None else widen(w, orc)
     out = ops.rms_norm(x, w, eps, out_dtype=odt)
     _norm_close(out, orc.rms_norm(x32, w32, eps), orc, f"rms_norm case {case}")
+    # out of place first (the residual must come back unchanged), then in place; the sum buffer is
+    # as aligned as the residual in odd cases (then the launch is the in-place one's, bit for bit)
+    so = offs[1] if case % 2 else (offs[1] + 1) % 4
+    sm = torch.empty(rows * dim + so, dtype=dtype, device=dev)[so:].view(rows, dim)
+    y_to = torch.empty(rows * dim + offs[3], dtype=odt, device=dev)[offs[3]:].view(rows, dim)
+    r_before = r.clone()
+    ops.add_rms_norm(x, r, w, eps, out=y_to, sum_out=sm)
+    assert np.array_equal(to_np(r).view(np.uint8), to_np(r_before).view(np.uint8)), f"residual kept, case {case}"
     y = torch.empty(rows * dim + offs[3], dtype=odt, device=dev)[offs[3]:].view(rows, dim)
     ops.add_rms_norm(x, r, w, eps, out=y)
     ref_y, ref_r = orc.add_rms_norm(x32, r32, w32, eps)
     _same_bits(r, ref_r, orc, f"add_rms_norm residual case {case}")
     _norm_close(y, ref_y, orc, f"add_rms_norm case {case}")
+    _same_bits(sm, ref_r, orc, f"add_rms_norm_to sum case {case}")
+    _norm_close(y_to, ref_y, orc, f"add_rms_norm_to case {case}")
+    if so == offs[1]:
+        assert np.array_equal(to_np(y_to).view(np.uint8), to_np(y).view(np.uint8)), f"add_rms_norm_to output case {case}"
 
 
 @pytest.mark.parametrize("case", range(CASES))
