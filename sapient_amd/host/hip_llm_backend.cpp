@@ -17,6 +17,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cctype>
 #include <cmath>
 #include <cstdio>
@@ -206,7 +207,8 @@ class HostBlocks {
             }
         }
         Block b{nullptr, n, false, nullptr};
-        if (pinnable() && hipHostMalloc(&b.ptr, n, hipHostMallocDefault) == hipSuccess && b.ptr != nullptr) {
+        // Portable: mapped for every device, whichever is current when a kernel reads it.
+        if (pinnable() && hipHostMalloc(&b.ptr, n, hipHostMallocPortable) == hipSuccess && b.ptr != nullptr) {
             b.pinned = true;
             if (hipHostGetDevicePointer(&b.dev, b.ptr, 0) != hipSuccess) {
                 b.dev = nullptr;  // usable for transfers, not in place
@@ -264,10 +266,17 @@ class HostBlocks {
     };
 
     static void release(const Block& b) noexcept {
-        if (b.pinned)
-            (void)hipHostFree(b.ptr);
-        else
+        if (!b.pinned)
             ::operator delete(b.ptr);
+        else if (!exiting())  // at exit the runtime may be gone; the system takes the pages back
+            (void)hipHostFree(b.ptr);
+    }
+
+    // Set by an exit handler registered after the runtime's set-up (at the first page-locked
+    // allocation), so it runs before the runtime's own teardown.
+    static std::atomic<bool>& exiting() {
+        static std::atomic<bool> flag{false};
+        return flag;
     }
 
     // A HIP device is present (checked once): page-locked memory is only worth its cost then.
@@ -276,6 +285,7 @@ class HostBlocks {
             int n = 0;
             const bool ok = hipGetDeviceCount(&n) == hipSuccess && n > 0;
             (void)hipGetLastError();
+            if (ok) std::atexit([] { exiting().store(true); });
             return ok;
         }();
         return yes;
