@@ -75,6 +75,8 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU-baseline time budget")
     p.add_argument("--op-cpu-seconds", type=float, default=0.3, help="CPU time budget per op-table row")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    p.add_argument("--no-host-tensor", action="store_true",
+                   help="skip the C++ trait mirror's host-tensor rate (a child process)")
     p.add_argument("--no-kernel-trace", action="store_true",
                    help="latency-bound rows: skip the rocprofv3 child (us = graph replay per launch)")
     p.add_argument("--profile-run", action="store_true",
@@ -804,6 +806,28 @@ def calibration_copies(torch, ops, dev, warmup, steps):
             "calibration_kernels": ["torch copy_", "torch neg", "sph add (a + 0)"]}
 
 
+def host_tensor_rate():
+    """The C++ trait mirror's host-tensor rate (tests/native/bench_host_tensor, built by build()): the
+    fused add + RMSNorm at the headline shape on host tensors, the host link crossed both ways as the
+    reference's trait calls do. Runs as a child process in its own group; returns its JSON object, or
+    a dict naming why there is none."""
+    exe = ROOT / "tests" / "native" / "_build" / "bench_host_tensor"
+    if not exe.exists():
+        return {"skipped": "tests/native/_build/bench_host_tensor not built"}
+    child = subprocess.Popen([str(exe)], stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True,
+                             start_new_session=True)
+    try:
+        out, _ = child.communicate(timeout=120)
+    except subprocess.TimeoutExpired:
+        os.killpg(child.pid, signal.SIGKILL)
+        child.communicate()
+        return {"skipped": "host-tensor child timed out"}
+    for ln in out.splitlines():
+        if ln.startswith('{"host_tensor"'):
+            return json.loads(ln)["host_tensor"]
+    return {"skipped": f"host-tensor child failed (rc {child.returncode})"}
+
+
 def reap_children() -> int:
     """Child processes of this run still alive (there should be none: the kernel-trace child is waited
     for); any found are terminated and waited for, so none outlives bench.py. Returns how many were found."""
@@ -943,6 +967,8 @@ def main():
         line["ops_note"] = ("rows of configurations 1-5; us = kernel time (latency rows: rocprofv3 kernel trace "
                             "median, beside graph_us per replayed launch), pct_peak of 8 TB/s, gpu_vs_cpu = rate "
                             "over the one-thread oracle's; every row in full on the line before")
+    if not args.no_host_tensor:
+        line["host_tensor"] = host_tensor_rate()
     line["children_left"] = reap_children()
     print(json.dumps(line), flush=True)
 

@@ -35,7 +35,7 @@ def test_compact_rows_keep_identity_and_measurements():
 
 def test_final_line_fits_a_log_tail():
     """Twenty configuration rows (the count the default run prints) plus a headline line of the
-    real field set stay under 7 KB."""
+    real field set (the host-tensor rate included) stay under 7 KB."""
     b = _bench()
     rows = ([_row("add_rms_norm", dt, 2) for dt in ("f16 (f32 w)", "bf16 (f32 w)")] +
             [_row(op, dt, 3) for op in ("rope_neox", "rope_interleaved") for dt in ("f32", "f16")] +
@@ -62,7 +62,10 @@ def test_final_line_fits_a_log_tail():
             "timing": {"region_ms": 3.505, "host_wall_ms": 3.747, "rotation_bytes": 1610612736,
                        "method": "one HIP event pair around the timed launches on their stream"},
             "ops": [b.compact(r) for r in rows],
-            "ops_note": "x" * 300, "children_left": 0}
+            "ops_note": "x" * 300,
+            "host_tensor": {"op": "add_rms_norm", "shape": "16384x4096 f32", "ms": 12.301, "GB/s": 87.3,
+                            "first_call_ms": 32.55, "embed_one_id_ms": 0.0431, "how": "y" * 170},
+            "children_left": 0}
     text = json.dumps(line)
     assert len(text) < 7000, len(text)
     assert all(r["cfg"] in (1, 2, 3, 4, 5) for r in line["ops"])
