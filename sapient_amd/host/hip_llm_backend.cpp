@@ -887,46 +887,70 @@ Tensor HipLlmBackend::update_kv_cache(Tensor& cache, size_t current_seq_len, con
     if (current_seq_len > max_seq) throw Error("current length " + std::to_string(current_seq_len) + " exceeds the cache");
     const Tensor src = f32_input(new_k);
     std::lock_guard<std::mutex> lock(mu_);
-    DeviceBuf cdev = upload(cache.bytes().data(), cache.bytes().size());
-    DeviceBuf sdev = upload(src.bytes().data(), src.bytes().size());
-    int64_t total = 0;
-    // When the window slides, the kept rows move once into a second buffer (the in-place shift
-    // moves them twice), which then becomes the cache; the first is freed after the download.
+    // The cache's own bytes (copied first if another tensor shares them), written as the reference
+    // writes through as_f32_slice_mut. Page-locked bytes are updated where they lie: an append
+    // writes only the new rows; a slide moves the kept rows once into a fresh block, which then
+    // becomes the cache's storage. Other caches go through device buffers.
+    Bytes& cb = cache.bytes_mut();
+    const size_t cbytes = cb.size();
+    void* cmap = mapped(cb.data(), cbytes);
     const bool slides = current_seq_len + new_seq > max_seq;
-    DeviceBuf next = slides ? alloc(cache.bytes().size()) : DeviceBuf();
-    int st;
-    if (slides) {
-        st = sph_kv_cache_update_into(sdev.ptr, SPH_F32, cdev.ptr, next.ptr, (int)cdt, (int64_t)(b * h),
-                                      (int64_t)new_seq, (int64_t)hd, (int64_t)max_seq, (int64_t)current_seq_len,
-                                      &total, stream_);
-        if (st == SPH_OK) std::swap(cdev.ptr, next.ptr);
-    } else {
-        st = sph_kv_cache_update(sdev.ptr, SPH_F32, cdev.ptr, (int)cdt, (int64_t)(b * h), (int64_t)new_seq,
-                                 (int64_t)hd, (int64_t)max_seq, (int64_t)current_seq_len, &total, stream_);
+    std::shared_ptr<Bytes> fresh = (cmap && slides) ? result_bytes(cbytes) : nullptr;
+    void* fmap = fresh ? mapped(fresh->data(), cbytes) : nullptr;
+    if (fresh && !fmap) {  // no page-locked block for the slide: go through device buffers
+        fresh.reset();
+        cmap = nullptr;
     }
-    if (st == SPH_OK) download(cdev, cache.bytes_mut().data(), cache.bytes().size());
-    release(sdev);
+    int64_t total = 0;
+    int st;
+    {
+        Operands ops(*this);
+        const void* sd = ops.in(src.bytes().data(), src.bytes().size());
+        // Not page-locked: the whole cache goes up and comes back.
+        void* cd = cmap ? cmap : ops.staged(cb.data(), cb.data(), cbytes);
+        // A slide there moves the kept rows once into a second device buffer, then back into the
+        // staged one for its download.
+        DeviceBuf next = (slides && !cmap) ? alloc(cbytes) : DeviceBuf();
+        st = ops.run([&] {
+            if (!slides)
+                return sph_kv_cache_update(sd, SPH_F32, cd, (int)cdt, (int64_t)(b * h), (int64_t)new_seq,
+                                           (int64_t)hd, (int64_t)max_seq, (int64_t)current_seq_len, &total, stream_);
+            const int r = sph_kv_cache_update_into(sd, SPH_F32, cd, fmap ? fmap : next.ptr, (int)cdt,
+                                                   (int64_t)(b * h), (int64_t)new_seq, (int64_t)hd, (int64_t)max_seq,
+                                                   (int64_t)current_seq_len, &total, stream_);
+            if (r == SPH_OK && !fmap &&
+                hipMemcpyAsync(cd, next.ptr, cbytes, hipMemcpyDeviceToDevice, static_cast<hipStream_t>(stream_)) !=
+                    hipSuccess)
+                return (int)SPH_EHIP;
+            return r;
+        });
+    }
     check(st, "update_kv_cache");
+    if (fresh) cache.bytes_ = std::move(fresh);
+    const Bytes& now = cache.bytes();
     const size_t n = (size_t)total;
-    std::vector<float> out(b * h * n * hd);
     if (cdt == DType::Q8_0) {
+        // The live prefix dequantized by the gather kernel, the cache rows read as a table.
         std::vector<uint32_t> ids(b * h * n);
         for (size_t r = 0; r < b * h; ++r)
             for (size_t s = 0; s < n; ++s) ids[r * n + s] = (uint32_t)(r * max_seq + s);
-        DeviceBuf idd = upload(ids.data(), ids.size() * 4);
-        DeviceBuf od = alloc(out.size() * 4);
-        st = sph_embed(cdev.ptr, SPH_Q8_0, (int64_t)(b * h * max_seq), (int64_t)hd,
-                       static_cast<const uint32_t*>(idd.ptr), (int64_t)ids.size(), static_cast<float*>(od.ptr),
-                       nullptr, stream_);
-        if (st == SPH_OK) download(od, out.data(), out.size() * 4);
+        auto out = result_bytes(ids.size() * hd * 4);
+        Operands ops(*this);
+        const void* td = ops.in(now.data(), now.size());
+        const uint32_t* idd = static_cast<const uint32_t*>(ops.in(ids.data(), ids.size() * 4));
+        float* od = static_cast<float*>(ops.out(out->data(), out->size()));
+        st = ops.run([&] {
+            return sph_embed(td, SPH_Q8_0, (int64_t)(b * h * max_seq), (int64_t)hd, idd, (int64_t)ids.size(), od,
+                             nullptr, stream_);
+        });
         check(st, "update_kv_cache (dequantize)");
-    } else {
-        const Tensor all = f32_input(cache);
-        const std::vector<float> v = all.as_f32();
-        for (size_t r = 0; r < b * h; ++r)
-            std::memcpy(out.data() + r * n * hd, v.data() + r * max_seq * hd, n * hd * 4);
+        return f32_result(std::move(out), {b, h, n, hd});
     }
-    return Tensor::from_f32(out, {b, h, n, hd});
+    // The live prefix [b, h, n, hd] of the F32 cache, head by head.
+    auto out = result_bytes(b * h * n * hd * 4);
+    for (size_t r = 0; r < b * h; ++r)
+        if (n) std::memcpy(out->data() + r * n * hd * 4, now.data() + r * max_seq * hd * 4, n * hd * 4);
+    return f32_result(std::move(out), {b, h, n, hd});
 }
 
 // ── graph-side dispatch ─────────────────────────────────────────────────────

@@ -566,6 +566,61 @@ static void kv_cache_update_q8_0(HipLlmBackend& bk) {  // update_kv_cache_q8, co
     (void)v1;
 }
 
+// Caches of 1 MiB or more are page-locked and updated where they lie (an append writes only the
+// new rows; a slide moves the kept rows once into a fresh block that becomes the cache's storage):
+// appends of 1 to 700 tokens into an F32 [1, 4, 1024, 128] and a Q8_0 [1, 8, 1024, 128] cache,
+// sliding several times, each checked against the reference's update (common.rs:381-412,
+// :449-528) restated on the host, cache bytes and returned prefix alike.
+static void kv_cache_update_in_place_on_large_caches(HipLlmBackend& bk) {
+    const size_t steps[] = {1, 1, 300, 1, 700, 50, 1, 1, 200, 1, 513, 1, 1024, 3};
+    for (const bool q8 : {false, true}) {
+        const size_t H = q8 ? 8 : 4, S = 1024, D = 128;
+        const size_t row = q8 ? D / 32 * 34 : D * 4;  // bytes per cache row
+        std::vector<uint8_t> want(H * S * row, 0);
+        Tensor cache = q8 ? Tensor::from_quant_bytes(Bytes(want.size(), 0), {1, H, S, D}, DType::Q8_0)
+                          : Tensor::from_f32(std::vector<float>(H * S * D, 0.0f), {1, H, S, D});
+        size_t cur = 0, t = 0;
+        for (size_t ns : steps) {
+            std::vector<float> nk(H * ns * D);
+            for (size_t i = 0; i < nk.size(); ++i) nk[i] = (float)(int)((i * 7 + t * 131) % 2001) * 0.01f - 10.0f;
+            t += ns;
+            const Tensor view = bk.update_kv_cache(cache, cur, Tensor::from_f32(nk, {1, H, ns, D}));
+            const size_t shift = cur + ns > S ? cur + ns - S : 0, keep = cur - shift;
+            for (size_t hh = 0; hh < H; ++hh) {
+                uint8_t* base = want.data() + hh * S * row;
+                std::memmove(base, base + shift * row, keep * row);
+                for (size_t s = 0; s < ns; ++s) {
+                    const float* src = nk.data() + (hh * ns + s) * D;
+                    if (q8) {
+                        const std::vector<uint8_t> q = quantize_q8_0(std::vector<float>(src, src + D));
+                        std::memcpy(base + (keep + s) * row, q.data(), row);
+                    } else {
+                        std::memcpy(base + (keep + s) * row, src, row);
+                    }
+                }
+            }
+            cur = std::min(S, cur + ns);
+            ASSERT(view.shape()[2] == cur, "prefix length");
+            ASSERT(same_bytes(cache.bytes(), want), q8 ? "q8_0 cache bytes" : "f32 cache bytes");
+            const std::vector<float> got = view.as_f32();
+            for (size_t hh = 0; hh < H; ++hh)
+                for (size_t s = 0; s < cur; ++s) {
+                    const uint8_t* r = want.data() + (hh * S + s) * row;
+                    for (size_t d = 0; d < D; ++d) {
+                        float v;
+                        if (q8) {
+                            const uint8_t* blk = r + d / 32 * 34;
+                            v = (float)(int8_t)blk[2 + d % 32] * f16_to_f32((uint16_t)(blk[0] | (blk[1] << 8)));
+                        } else {
+                            std::memcpy(&v, r + d * 4, 4);
+                        }
+                        if (std::memcmp(&v, &got[(hh * cur + s) * D + d], 4) != 0) throw Failure{"prefix value"};
+                    }
+                }
+        }
+    }
+}
+
 static void quant_bytes_are_validated(HipLlmBackend&) {  // tensor.rs:143-169
     ASSERT(expect_error([] { Tensor::from_quant_bytes(Bytes(33), {32}, DType::Q8_0); })
                .find("shape mismatch") != std::string::npos, "byte count");
@@ -775,6 +830,7 @@ int main() {
         {"kv_cache_update_q8_0", kv_cache_update_q8_0},
         {"kv_cache_update_refuses_half_caches", kv_cache_update_refuses_half_caches},
         {"kv_cache_update_long_decode", kv_cache_update_long_decode},
+        {"kv_cache_update_in_place_on_large_caches", kv_cache_update_in_place_on_large_caches},
         {"disable_routes_listed_ops", disable_routes_listed_ops},
         {"disable_without_backend_raises", disable_without_backend_raises},
         {"verify_returns_the_device_result", verify_returns_the_device_result},
