@@ -255,9 +255,26 @@ class HipLlmBackend final : public LlmBackend {
     DeviceBuf alloc(size_t bytes);
     void release(DeviceBuf& b);
     void download(const DeviceBuf& b, void* host, size_t bytes);
-    // One call's host operands as device addresses: page-locked tensor bytes in place, others
-    // through device buffers.
+    // One call's host operands as device addresses: page-locked tensor bytes in place, small ones
+    // through page-locked staging, others through device buffers.
     class Operands;
+    // Page-locked staging for a call's small operands, which the kernels read and write in place:
+    // chunks kept for the backend's lifetime and reused by every call (calls hold mu_ and wait for
+    // their work). stage() returns a slot of `bytes` (host and device addresses; null when no
+    // page-locked memory could be had); stage_reset() frees every slot.
+    struct StageSlot {
+        void* host;
+        void* dev;
+    };
+    struct StageChunk {
+        void* host;
+        void* dev;
+        size_t cap;
+    };
+    StageSlot stage(size_t bytes);
+    void stage_reset() { stage_chunk_ = stage_used_ = 0; }
+    std::vector<StageChunk> stage_chunks_;
+    size_t stage_chunk_ = 0, stage_used_ = 0;  // the chunk being filled, and its bytes handed out
     // Uninitialised host bytes for a result of n bytes (every result writes all of them); large
     // ones are page-locked blocks freed by dropped tensors, pages already mapped, when one fits.
     static std::shared_ptr<Bytes> result_bytes(size_t n);
