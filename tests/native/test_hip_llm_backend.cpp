@@ -12,7 +12,9 @@
 #include <cstdlib>
 #include <cstring>
 #include <functional>
+#include <memory>
 #include <string>
+#include <thread>
 #include <vector>
 
 #include <hip/hip_runtime.h>
@@ -791,6 +793,59 @@ static void large_calls_equal_small_calls(HipLlmBackend& bk) {
            "embed_tokens from a table read in place");
 }
 
+// Threads share the process-wide cache of page-locked blocks and, when they share a backend, its
+// staging (calls serialise on the backend's lock): four threads, two on a shared backend and two on
+// backends of their own, each run large (in place) and small (staged) calls on their own data many
+// times; every result must equal the single-threaded one, bit for bit.
+static void threads_share_blocks_and_staging(HipLlmBackend& shared) {
+    const size_t big = size_t(1) << 19, small = 4096;  // 2 MiB and 16 KiB of f32
+    auto make = [](size_t n, int seed) {
+        std::vector<float> v(n);
+        for (size_t i = 0; i < n; ++i) v[i] = (float)(int)((i * 2654435761u + (size_t)seed * 97u) % 4001) * 0.001f - 2.0f;
+        return v;
+    };
+    struct Case {
+        Tensor xb, rb, xs, rs, w;
+    };
+    std::vector<Case> cases;
+    for (int t = 0; t < 4; ++t)
+        cases.push_back({Tensor::from_f32(make(big, t), {big / 4096, 4096}), Tensor::from_f32(make(big, t + 10), {big / 4096, 4096}),
+                         Tensor::from_f32(make(small, t + 20), {1, small}), Tensor::from_f32(make(small, t + 30), {1, small}),
+                         Tensor::from_f32(make(4096, 40), {4096})});
+    auto run = [](HipLlmBackend& bk, const Case& c) {
+        std::vector<std::vector<float>> out;
+        const auto p = bk.add_rms_norm(c.xb, c.rb, c.w, 1e-5f);
+        out.push_back(p.first.as_f32());
+        out.push_back(p.second.as_f32());
+        out.push_back(bk.silu(c.xb).as_f32());
+        out.push_back(bk.add(c.xs, c.rs).as_f32());
+        out.push_back(bk.swiglu(c.xs, c.rs).as_f32());
+        out.push_back(bk.rms_norm(c.xs.reshaped({1, small}), Tensor::from_f32(std::vector<float>(small, 1.0f), {small}), 1e-6f).as_f32());
+        return out;
+    };
+    std::vector<std::vector<std::vector<float>>> want;
+    for (const Case& c : cases) want.push_back(run(shared, c));
+    std::vector<std::string> errors(4);
+    std::vector<std::thread> threads;
+    for (int t = 0; t < 4; ++t)
+        threads.emplace_back([&, t] {
+            try {
+                std::unique_ptr<HipLlmBackend> own;
+                if (t >= 2) own = std::make_unique<HipLlmBackend>();
+                HipLlmBackend& bk = own ? *own : shared;
+                for (int round = 0; round < 10; ++round)
+                    if (run(bk, cases[t]) != want[t]) {
+                        errors[t] = "thread " + std::to_string(t) + " round " + std::to_string(round) + " differs";
+                        return;
+                    }
+            } catch (const std::exception& e) {
+                errors[t] = e.what();
+            }
+        });
+    for (auto& th : threads) th.join();
+    for (const std::string& e : errors) ASSERT(e.empty(), e);
+}
+
 int main() {
     if (!HipLlmBackend::is_available()) {
         std::printf("no gfx950 device\n");
@@ -825,6 +880,7 @@ int main() {
         {"tensor_copies_share_bytes_until_written", tensor_copies_share_bytes_until_written},
         {"large_tensor_bytes_are_page_locked_and_recycled", large_tensor_bytes_are_page_locked_and_recycled},
         {"large_calls_equal_small_calls", large_calls_equal_small_calls},
+        {"threads_share_blocks_and_staging", threads_share_blocks_and_staging},
         {"kv_cache_update_reference_test", kv_cache_update_reference_test},
         {"kv_cache_update_slides_when_full", kv_cache_update_slides_when_full},
         {"kv_cache_update_q8_0", kv_cache_update_q8_0},
