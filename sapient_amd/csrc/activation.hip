@@ -59,6 +59,19 @@ constexpr int64_t kMaxGrid = 65536;  // ~one loop trip per thread at the configu
 // (1.8 M vectors) 14.2 -> 16.1, and at larger launches both shapes run alike.
 constexpr int64_t kFewVecs = int64_t(1) << 20;
 
+// Launches of up to 2^18 elements (decode steps, small prefill chunks) take one element per thread
+// instead, for every op whose per-element work is long (half-precision I/O, GELU) and for f32 from
+// 2048 elements on: a thread's chain is then one element's, and half-precision GELU reads its
+// table from cache rather than staging it per block. Per launch (replayed graph, back to back) on
+// MI355X, against the vector shapes: SwiGLU and SiLU f16 / bf16 -21 to -36 % (SwiGLU 1 x 4864 f16
+// 2.58 -> 1.83 µs), GELU-tanh f16 / bf16 -16 to -40 % (1 x 10240 f16 2.90 -> 1.79 µs), GELU-tanh
+// f32 -16 to -23 %, SwiGLU f32 -4 to -6 % from 4864 elements (1.92 -> 1.82 µs); below 2048 f32
+// elements the light ops measured level or 0.3 % slower, and at 2^19 elements both shapes ran
+// alike (bf16 GELU 5.9 % slower one element per thread), hence the bounds. Results are the same
+// bits either way.
+constexpr int64_t kFewElems = int64_t(1) << 18;
+constexpr int64_t kFewF32LightMin = 2048;
+
 enum Op { OP_ADD = 0, OP_MUL = 1, OP_SILU = 2, OP_SWIGLU = 3, OP_GELU = 4, OP_GELU_ERF = 5 };
 
 // 2^(i/32) for the expf restatement, staged per block into LDS by the kernels that need it.
@@ -227,6 +240,9 @@ int launch_ew(const void* a, const void* b, void* out, int64_t n, hipStream_t st
     const T* ap = static_cast<const T*>(a);
     const T* bp = static_cast<const T*>(b);
     T* op = static_cast<T*>(out);
+    constexpr bool kLongChain = sizeof(T) == 2 || OP == OP_GELU || OP == OP_GELU_ERF;
+    if (n <= kFewElems && (kLongChain || n >= kFewF32LightMin))
+        return launch(ew_scalar<T, OP, BC>, grid_for(n, kThreads, 4096), kThreads, stream, ap, bp, op, (int64_t)0, n);
     const bool vec_ok = aligned(out, 16) && (BC == B_SCALAR_A || aligned(a, 16)) &&
                         (!binary_op<OP>() || BC == B_SCALAR_B || aligned(b, 16));
     int64_t done = 0;
@@ -446,6 +462,9 @@ int gelu_half(const uint16_t* x, uint16_t* out, int which, int64_t n, hipStream_
     int cus = 0;
     int st = ensure_device_ready(stream, &cus);
     if (st != SPH_OK) return st;
+    if (n <= kFewElems)  // one element per thread, the table read from cache (see kFewElems)
+        return launch(gelu_lut_apply_scalar<T>, grid_for(n, kThreads, 4096), kThreads, stream, x, out, (int64_t)0, n,
+                      which);
     int64_t done = 0;
     if (aligned(x, 16) && aligned(out, 16)) {
         const int64_t nvec = n / 8;
