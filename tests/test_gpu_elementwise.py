@@ -94,8 +94,10 @@ def test_add_mul_scalar_broadcast(dev, orc):
 
 @pytest.mark.parametrize("dtype", DTYPES, ids=IDS)
 # 2^22 / 2^22 + 4 (f32) and 2^23 / 2^23 + 8 (half types) straddle the one-vector-per-thread launch of
-# small and mid-size element-wise calls (up to 2^20 16-byte vectors; a vector holds 4 f32 or 8 half values).
-@pytest.mark.parametrize("n", [1, 5, 4864, 512 * 4864, 1 << 22, (1 << 22) + 4, 1 << 23, (1 << 23) + 8])
+# small and mid-size element-wise calls (up to 2^20 16-byte vectors; a vector holds 4 f32 or 8 half values);
+# 2047 / 2048 and 2^18 / 2^18 + 1 the one-element-per-thread launch of small ones.
+@pytest.mark.parametrize("n", [1, 5, 2047, 2048, 4864, 1 << 18, (1 << 18) + 1, 512 * 4864, 1 << 22, (1 << 22) + 4,
+                               1 << 23, (1 << 23) + 8])
 def test_silu_swiglu(dev, orc, dtype, n):
     print(f"case silu/swiglu {dtype} n={n}", flush=True)
     g, u = _gen((n,), 6, dev, 2.0, dtype), _gen((n,), 7, dev, 2.0, dtype)
@@ -116,6 +118,19 @@ def _exact(out: torch.Tensor, ref32: np.ndarray, orc, what: str):
         assert (ulp_diff16(got[nan], want[nan], out.dtype) == 0).all(), what + " NaN"
 
 
+# Launches of up to 2^18 elements run one element per thread (half-precision GELU reading its table
+# from cache); larger ones take the vector kernels (16-byte accesses, the half types' certified fast
+# paths, GELU's table staged per block). The exhaustive tests check the small form against the oracle
+# over every 16-bit pattern and then the vector form against it over the same patterns tiled past
+# that bound.
+TILES = 5  # 5 x 65536 = 327680 > 2^18
+
+
+def _tiled_same(fn, x: torch.Tensor, got_small: np.ndarray, what: str):
+    big = to_np(fn(x.repeat(TILES)))
+    assert np.array_equal(big, np.tile(got_small, TILES)), what + " (vector kernels)"
+
+
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=IDS)
 def test_silu_swiglu_half_exhaustive_bit_exact(dev, orc, dtype):
     """Every 16-bit gate pattern: SiLU, and SwiGLU with up = 1, −3.7, ~N(0, 2), ~N(0, 300) and
@@ -123,12 +138,17 @@ def test_silu_swiglu_half_exhaustive_bit_exact(dev, orc, dtype):
     g = torch.arange(0, 65536, dtype=torch.int32).to(torch.int16).view(dtype).to(dev)
     g32 = widen(g, orc)
     print(f"case silu/swiglu exhaustive {dtype}", flush=True)
-    _exact(ops.silu(g), orc.silu(g32), orc, f"silu {dtype}")
+    s = ops.silu(g)
+    _exact(s, orc.silu(g32), orc, f"silu {dtype}")
+    _tiled_same(ops.silu, g, to_np(s), f"silu {dtype}")
     ups = [torch.ones(65536, device=dev), torch.full((65536,), -3.7, device=dev),
            _gen((65536,), 31, dev, 2.0), _gen((65536,), 32, dev, 300.0), _gen((65536,), 33, dev, 1e-30)]
     for i, u in enumerate(ups):
         u = u.to(dtype)
-        _exact(ops.swiglu(g, u), orc.swiglu(g32, widen(u, orc)), orc, f"swiglu {dtype} up #{i}")
+        y = ops.swiglu(g, u)
+        _exact(y, orc.swiglu(g32, widen(u, orc)), orc, f"swiglu {dtype} up #{i}")
+        big = to_np(ops.swiglu(g.repeat(TILES), u.repeat(TILES)))
+        assert np.array_equal(big, np.tile(to_np(y), TILES)), f"swiglu {dtype} up #{i} (vector kernels)"
 
 
 def test_silu_special_values(dev, orc):
@@ -195,6 +215,7 @@ def test_gelu_half_exhaustive_bit_exact(dev, orc, dtype):
     # unaligned / tail path gives the same bits
     got2 = to_np(ops.gelu_tanh(x[3:]))
     assert np.array_equal(got2, got[3:])
+    _tiled_same(ops.gelu_tanh, x, got, f"gelu {dtype}")
 
 
 def test_gelu_phi2_full(dev, orc):
@@ -243,6 +264,7 @@ def test_gelu_erf_half_exhaustive_bit_exact(dev, orc, dtype):
     assert (ulp_diff16(got[nan], want[nan], dtype) == 0).all()
     got2 = to_np(ops.gelu_erf(x[3:]))
     assert np.array_equal(got2, got[3:])
+    _tiled_same(ops.gelu_erf, x, got, f"gelu_erf {dtype}")
 
 
 @pytest.mark.parametrize("dtype", DTYPES, ids=IDS)
