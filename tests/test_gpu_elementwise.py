@@ -198,7 +198,11 @@ def test_gelu_f32_bit_exact(dev, orc):
     """f32 GELU reproduces glibc's tanhf bits, so the result equals the oracle exactly."""
     x = torch.cat([_gen((1 << 20,), 10, dev, 2.0), _gen((1 << 16,), 11, dev, 8.0), torch.from_numpy(SPECIALS).to(dev)])
     print("case gelu f32", flush=True)
-    assert_bits_equal(to_np(ops.gelu_tanh(x)), orc.gelu(to_np(x)), "gelu f32")
+    want = orc.gelu(to_np(x))
+    assert_bits_equal(to_np(ops.gelu_tanh(x)), want, "gelu f32")
+    # the one-element-per-thread launch of small calls (up to 2^18 elements), on slices of the same inputs
+    for lo, hi in ((0, 4864), (5, 1 << 18), ((1 << 20) - 7, (1 << 20) + 70000)):
+        assert_bits_equal(to_np(ops.gelu_tanh(x[lo:hi])), want[lo:hi], f"gelu f32 [{lo}:{hi}]")
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=IDS)
