@@ -6,6 +6,10 @@
  * function:
  *   - takes raw DEVICE pointers, explicit sizes and a HIP stream
  *     (`stream` is a hipStream_t passed as void*; NULL = the default stream);
+ *     a device pointer is any address the kernels can reach: device memory,
+ *     or page-locked host memory through its device mapping
+ *     (hipHostGetDevicePointer), which they then read and write in place
+ *     over the host link (the C++ trait mirror passes large host tensors so);
  *   - enqueues its kernels on that stream and returns without synchronizing;
  *   - never allocates or frees memory (all buffers are caller-owned and must
  *     outlive the queued work);
