@@ -3,8 +3,9 @@
 // reports beside its device-resident figures: the fused residual add + RMSNorm
 // on 16384 x 4096 f32 HOST tensors (the trait's calling convention,
 // crates/sapient-models/src/forward/backend.rs:57-115: inputs and results in
-// host memory, so every call crosses the host link both ways), and the
-// embedding gather of one token id from a 128256 x 4096 Q8_0 host table.
+// host memory, so every call crosses the host link both ways), the same call
+// on one 4096-wide row (a decode step), and the embedding gather of one token
+// id from a 128256 x 4096 Q8_0 host table.
 // Prints one JSON line: {"host_tensor": {...}} (null with a reason when no
 // gfx950 device answers).
 #include <algorithm>
@@ -19,6 +20,12 @@ using sapient_hip::Bytes;
 using sapient_hip::DType;
 using sapient_hip::HipLlmBackend;
 using sapient_hip::Tensor;
+
+static std::vector<float> xv1(size_t n) {
+    std::vector<float> v(n);
+    for (size_t i = 0; i < n; ++i) v[i] = (float)(int)((i * 2654435761u) % 2001) * 0.001f - 1.0f;
+    return v;
+}
 
 template <typename F>
 static double ms_of(F&& f) {
@@ -64,6 +71,13 @@ int main() {
         tb[34 * b + 1] = 0x1c;  // d = 2^-8 (f16)
         for (int j = 0; j < 32; ++j) tb[34 * b + 2 + j] = (uint8_t)((b * 7 + (size_t)j * 13) & 0xFF);
     }
+    // a decode step's fused add + RMSNorm: one 4096-wide row (operands through page-locked staging)
+    const Tensor x1 = Tensor::from_f32(std::vector<float>(xv1(D)), {1, D});
+    const Tensor r1 = Tensor::from_f32(std::vector<float>(xv1(D)), {1, D});
+    for (int i = 0; i < 5; ++i) (void)bk.add_rms_norm(x1, r1, w, 1e-5f);
+    std::vector<double> td;
+    for (int i = 0; i < 51; ++i) td.push_back(ms_of([&] { (void)bk.add_rms_norm(x1, r1, w, 1e-5f); }));
+
     const Tensor table = Tensor::from_quant_bytes(std::move(tb), {V, H}, DType::Q8_0);
     const std::vector<uint32_t> one = {12345};
     (void)bk.embed_tokens(table, one);
@@ -71,9 +85,9 @@ int main() {
     for (int i = 0; i < 7; ++i) te.push_back(ms_of([&] { (void)bk.embed_tokens(table, one); }));
 
     std::printf("{\"host_tensor\": {\"op\": \"add_rms_norm\", \"shape\": \"16384x4096 f32\", \"ms\": %.3f, "
-                "\"GB/s\": %.1f, \"first_call_ms\": %.2f, \"embed_one_id_ms\": %.4f, "
+                "\"GB/s\": %.1f, \"first_call_ms\": %.2f, \"embed_one_id_ms\": %.4f, \"decode_row_us\": %.1f, "
                 "\"how\": \"C++ LlmBackend mirror on host tensors: page-locked bytes read and written in place "
-                "by the kernels over the host link (median of 7 calls after one)\"}}\n",
-                ms, alg / ms / 1e6, first, median(te));
+                "by the kernels over the host link (medians: 7 calls after one; the decode row 51 after 5)\"}}\n",
+                ms, alg / ms / 1e6, first, median(te), median(td) * 1e3);
     return 0;
 }

@@ -64,7 +64,8 @@ def test_final_line_fits_a_log_tail():
             "ops": [b.compact(r) for r in rows],
             "ops_note": "x" * 300,
             "host_tensor": {"op": "add_rms_norm", "shape": "16384x4096 f32", "ms": 12.301, "GB/s": 87.3,
-                            "first_call_ms": 32.55, "embed_one_id_ms": 0.0431, "how": "y" * 170},
+                            "first_call_ms": 32.55, "embed_one_id_ms": 0.0431, "decode_row_us": 16.7,
+                            "how": "y" * 190},
             "children_left": 0}
     text = json.dumps(line)
     assert len(text) < 7000, len(text)
