@@ -10,6 +10,10 @@ NATIVE = Path(__file__).resolve().parent / "native"
 def test_tensor_host_program():
     exe = NATIVE / "_build" / "test_tensor_host"
     if not exe.exists():
+        import sapient_amd
+        if not sapient_amd.LIB_PATH.exists():  # the program links the library
+            from sapient_amd import build
+            build.build()
         import importlib.util
         spec = importlib.util.spec_from_file_location("native_build", NATIVE / "build.py")
         mod = importlib.util.module_from_spec(spec)
