@@ -5,8 +5,8 @@
 // takes host tensors and returns new host tensors; this class does the same —
 // the HIP kernels, through the C ABI on its own stream, read the inputs and
 // write the results in host memory (page-locked bytes in place, small ones
-// through device buffers) — with the reference's argument meaning, validation
-// and error messages. It is
+// through page-locked staging) — with the reference's argument meaning,
+// validation and error messages. It is
 // what a Rust `HipLlmBackend` wrapper does over FFI, written in C++ because the
 // reference is compiled code. There is no CPU fallback: a failed HIP call
 // raises sapient_hip::Error (the debug switches below route an op elsewhere
@@ -44,13 +44,13 @@ class Error : public std::runtime_error {
 };
 
 // Host memory for tensor bytes. Blocks of 1 MiB or more are page-locked
-// (hipHostMalloc) when a HIP device is present, so a tensor's upload and
-// download run as direct DMA (~4.7 ms per 256 MiB each way) rather than
-// through the runtime's staging of pageable memory (9-21 ms), and are kept
-// for reuse when freed (up to 4 GiB in all, process-wide): a freed block goes
-// to the next request needing between half and all of it, most recently
-// freed first, with its pages already mapped. Smaller blocks are plain heap
-// memory.
+// (hipHostMalloc) when a HIP device is present, so the kernels read and write
+// them in place through their device mapping (and any copy of them runs as
+// direct DMA, ~4.7 ms per 256 MiB each way, rather than through the runtime's
+// staging of pageable memory, 9-21 ms), and are kept for reuse when freed (up
+// to 4 GiB in all, process-wide): a freed block goes to the next request
+// needing between half and all of it, most recently freed first, with its
+// pages already mapped. Smaller blocks are plain heap memory.
 void* host_bytes_alloc(size_t n);
 void host_bytes_free(void* p, size_t n) noexcept;
 
