@@ -472,10 +472,11 @@ void HipLlmBackend::download(const DeviceBuf& b, void* host, size_t bytes) {
 // Page-locked tensor bytes are used where they lie, through their device mapping: the kernels
 // then read and write host memory over the host link, both directions at once (on the test
 // machine a streaming kernel reading two 256 MiB host tensors and writing two took 11.9 ms, the
-// four copies alone 18.8 ms). Other bytes (small tensors, host vectors) go through device buffers,
-// uploaded before the kernels or downloaded after them. run() enqueues the uploads, the kernels and,
-// when the kernels were accepted, the downloads on the backend's stream, and waits for them: the
-// host bytes must stay untouched until it returns.
+// four copies alone 18.8 ms). Other large bytes (where page-locked memory was refused, or host
+// vectors) go through device buffers, uploaded before the kernels or downloaded after them; small
+// ones through staging (below). run() enqueues the uploads, the kernels and, when the kernels were
+// accepted, the downloads on the backend's stream, waits for them, then copies staged results out:
+// the host bytes must stay untouched until it returns.
 //
 // Small operands (up to kStageMax bytes: weights, ids, positions, decode-step rows) are copied on
 // the host into the backend's page-locked staging, which the kernels also use in place: a call then
