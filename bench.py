@@ -548,6 +548,14 @@ def op_table(torch, ops, dev, only=None, cpu_budget=0.0, profile_launches=0, ker
                 lambda s, w=w: ops.add_rms_norm(s[0], s[1], w, 1e-5, out=s[2]),
                 lambda: (lambda x=nrm(256, dim), r=nrm(256, dim), w=nrm(dim, scale=0.1, mean=1.0):
                          orc.add_rms_norm(x, r, w, 1e-5), 256), cfg=2))
+    # The out-of-place form (the sum to its own buffer, the residual only read), f32 at the headline shape
+    w = gen(torch, (dim,), 3, dev, f32, 0.1, 1.0)
+    run(Row("add_rms_norm_to", f"{rows}x{dim}", "f32 (f32 w)", 4 * rows * dim * 4 + dim * 4, rows, "rows",
+            lambda i: (gen(torch, (rows, dim), 10 + i, dev, f32), gen(torch, (rows, dim), 20 + i, dev, f32),
+                       torch.empty(rows, dim, device=dev, dtype=f32), torch.empty(rows, dim, device=dev, dtype=f32)),
+            lambda s, w=w: ops.add_rms_norm(s[0], s[1], w, 1e-5, out=s[2], sum_out=s[3]),
+            lambda: (lambda x=nrm(256, dim), r=nrm(256, dim), w=nrm(dim, scale=0.1, mean=1.0):
+                     orc.add_rms_norm(x, r, w, 1e-5), 256)))
     # Plain RMSNorm at the same width (the norm the fused kernel's second half is)
     for dt, tag in ((f32, "f32"), (f16, "f16"), (bf16, "bf16")):
         w = gen(torch, (dim,), 3, dev, f32, 0.1, 1.0)
