@@ -485,6 +485,8 @@ void HipLlmBackend::download(const DeviceBuf& b, void* host, size_t bytes) {
 // 15 µs, swiglu of 1 × 14336 97 -> 17 µs).
 constexpr size_t kStageMax = size_t(1) << 20;
 
+// One Operands per backend at a time (it hands out the backend's staging from the start): each op
+// makes one under the backend's lock, and ends it before making another.
 class HipLlmBackend::Operands {
  public:
     explicit Operands(HipLlmBackend& bk) : bk_(bk) { bk_.stage_reset(); }
