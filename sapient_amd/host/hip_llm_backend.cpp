@@ -7,7 +7,8 @@
 // page-locked host memory, which the kernels read and write in place through
 // its device mapping (both directions of the host link at once, and a gather
 // reads only the table rows it needs); smaller operands are copied through
-// device buffers. Nothing is cached on the device between calls: a host
+// page-locked staging. No tensor is cached on the device between calls (only
+// the RoPE angle tables, which depend on nothing but (base, rotary_dim)): a host
 // tensor's address can be reused once it is freed, so caching by pointer (as
 // the MLX backend does, backend.rs:483-508, where Arc lifetimes make it safe)
 // would risk a stale copy. Output dtypes, validation and error messages follow
